@@ -1,0 +1,155 @@
+/*
+ * libmixmoe -- MI355X (gfx950) executor for mixlab's MoE feed-forward op
+ * (IR op 74, OP_MOE_FEED_FORWARD).
+ *
+ * This is the C ABI that replaces, for op 74 only, the path
+ *   gpu/lower.go:117-170 (LowerIRProgram)  ->  mlx_ir_program_create/add_op
+ *   gpu/mlx_bridge.h:83-90                  ->  mlx_ir_eval_program_named_outputs
+ *   gpu/mlx_bridge.h:172-181                ->  ir_interpret_outputs
+ *   gpu/ir.cpp:4816-4824 (case OP_MOE_FEED_FORWARD) -> moe_feed_forward
+ *   gpu/ir.cpp:1073-1164.
+ * The op keeps the reference encoding (arch/ir.go:692-698):
+ *   IntParams   = [B, T, D, E, topK, expertType, ffn, activation]
+ *   FloatParams = [leakySlope]
+ *   Inputs      = [x, router_w, then per expert (gate, up, down) or (up, down)]
+ *   Outputs     = [delta [B*T, D] fp32, aux [1] fp32, entropy [1] fp32]
+ *
+ * Conventions follow gpu/mlx_bridge.h: opaque int64 handles with 0 meaning
+ * failure (gpu/mlx_bridge.h:70-83), int status codes with 0 = OK and -1 =
+ * failure (gpu/mlx_bridge.cpp:814-823), and no C++ exception ever crosses the
+ * boundary (gpu/mlx_bridge.cpp:64-82): the message of the last failure on the
+ * calling thread is available from mxm_last_error.  Tensor dtype codes extend
+ * mlx_tensor_input's (0 = int32, 1 = float32; gpu/mlx_bridge.h:92-99).
+ *
+ * Every call on one op handle is serialised by the caller (one HIP stream per
+ * handle); distinct handles are independent.
+ */
+#ifndef MIXMOE_H
+#define MIXMOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXM_OK 0
+#define MXM_ERR -1
+#define MXM_ERR_ARGS -10 /* gpu/mlx_bridge.cpp:814-823: argument error */
+#define MXM_ERR_INIT -11 /* runtime / device not initialised */
+#define MXM_ERR_OP -12   /* bad op handle */
+
+#define MXM_DTYPE_INT32 0 /* gpu/mlx_bridge.h:94 */
+#define MXM_DTYPE_F32 1   /* gpu/mlx_bridge.h:94 */
+#define MXM_DTYPE_BF16 2  /* compute_dtype "bf16" (gpu/ir_trainer.cpp:1395-1412) */
+#define MXM_DTYPE_I8 3    /* symmetric int8 weights with fp32 per-output-channel scales */
+
+#define MXM_OP_MOE_FEED_FORWARD 74 /* arch/ir.go:67, gpu/ir.h:81 */
+
+/* mxm_moe_create flags */
+#define MXM_FLAG_FORCE_SIMT 1 /* use the exact-order SIMT expert kernels even where MFMA tiles fit */
+#define MXM_FLAG_DEBUG_PROBS 2 /* keep the router probabilities of the last forward */
+
+/* Stages timed by mxm_moe_stage_times, in launch order. */
+#define MXM_STAGE_ROUTER 0
+#define MXM_STAGE_SCAN 1
+#define MXM_STAGE_SCATTER 2
+#define MXM_STAGE_GEMM_UP 3
+#define MXM_STAGE_GEMM_DOWN 4
+#define MXM_STAGE_COMBINE 5
+#define MXM_NUM_STAGES 6
+
+/* Initialise the HIP runtime on the current device.  Replaces mlx_init
+ * (gpu/mlx_bridge.h:15).  0 on success, -1 on failure. */
+int mxm_init(void);
+
+/* Device name ("AMD Instinct MI355X ..."); replaces mlx_device_name
+ * (gpu/mlx_bridge.h:53).  Never NULL. */
+const char* mxm_device_name(void);
+
+/* Copy the last failure message of the calling thread into buf (NUL
+ * terminated, truncated to n bytes).  Returns the full message length.
+ * Replaces the stderr logging of log_bridge_exception
+ * (gpu/mlx_bridge.cpp:80-82). */
+int mxm_last_error(char* buf, int n);
+
+/* Device memory for callers that hold inputs and outputs in HBM (the cgo
+ * side keeps these instead of MLX array handles, gpu/mlx_bridge.h:70-80). */
+int mxm_malloc(void** ptr, int64_t bytes);
+int mxm_free(void* ptr);
+int mxm_memcpy_h2d(void* dst, const void* src, int64_t bytes);
+int mxm_memcpy_d2h(void* dst, const void* src, int64_t bytes);
+int mxm_memcpy_d2d(void* dst, const void* src, int64_t bytes);
+int mxm_device_synchronize(void);
+
+/* Create an op-74 executor.  Replaces mlx_ir_program_create(n_weights) +
+ * mlx_ir_program_add_op(prog, 74, ...) (gpu/mlx_bridge.h:83-90) for one MoE
+ * op.  int_params/float_params are the op's IntParams/FloatParams
+ * (arch/ir.go:697); n_inputs is len(Op.Inputs).  Parameter checks and their
+ * messages are those of gpu/ir.cpp:1076-1104.  compute_dtype is
+ * MXM_DTYPE_F32 or MXM_DTYPE_BF16 (weights are cast to it, as
+ * gpu/ir_trainer.cpp:1395-1412 does).  Returns a handle, 0 on failure. */
+int64_t mxm_moe_create(const float* float_params, int n_float_params, const int32_t* int_params,
+                       int n_int_params, int n_inputs, int compute_dtype, int flags);
+
+/* Release an executor and its device memory; replaces
+ * mlx_ir_program_destroy + mlx_free_handles (gpu/mlx_bridge.h:79-90). */
+int mxm_moe_destroy(int64_t op);
+
+/* Bind weight input `input_index` (position in Op.Inputs: 1 = router_w
+ * [D, E], then expert e's matrices at 2 + e*wpe + j, in x.W layout
+ * [in, out] as arch/moe.go:126-142 declares them).  dtype is MXM_DTYPE_F32
+ * or MXM_DTYPE_BF16; data is host memory (on_device = 0) or device memory
+ * (on_device = 1), copied and converted, so the caller keeps ownership.
+ * Replaces mlx_from_data_shape (gpu/mlx_bridge.h:71) plus the w<i> name
+ * lookup of gpu/ir.cpp:3730-3734; shape checks and messages are those of
+ * gpu/ir.cpp:1098-1140. */
+int mxm_moe_set_input(int64_t op, int input_index, int dtype, const int64_t* shape, int ndim,
+                      const void* data, int on_device);
+
+/* Run the op on x [rows = B*T, D] (dtype MXM_DTYPE_BF16 or MXM_DTYPE_F32;
+ * fp32 x is rounded to bf16 first under bf16 compute), writing delta
+ * [rows, D] fp32, aux [1] fp32 and entropy [1] fp32.  All pointers are
+ * device memory; the call is asynchronous on the op's stream.  aux and
+ * entropy may be NULL.  Replaces the case OP_MOE_FEED_FORWARD dispatch
+ * (gpu/ir.cpp:4816-4824) of moe_feed_forward (gpu/ir.cpp:1073-1164). */
+int mxm_moe_forward(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
+                    float* aux, float* entropy);
+
+/* Same with host buffers; synchronous (copies in, runs, copies out).  This
+ * is the shape of mlx_ir_eval_program_named_outputs (gpu/mlx_bridge.h:172-181)
+ * for the three outputs of op 74. */
+int mxm_moe_forward_host(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
+                         float* aux, float* entropy);
+
+/* Wait for all work queued on the op's stream. */
+int mxm_moe_synchronize(int64_t op);
+
+/* Routing of the last forward (synchronous copy): top_idx [rows, K] int32
+ * (argsort(-probs)[:, :K], gpu/ir.cpp:1108-1109), gates [rows, K] fp32
+ * (top_norm, gpu/ir.cpp:1110-1111), counts [E], offsets [E+1] and perm
+ * [rows*K] (expert-grouped token ids).  Any pointer may be NULL.  to_host
+ * selects host (1) or device (0) destinations. */
+int mxm_moe_routing(int64_t op, int32_t* top_idx, float* gates, int32_t* counts,
+                    int32_t* offsets, int32_t* perm, int to_host);
+
+/* Router probabilities [rows, E] of the last forward; requires
+ * MXM_FLAG_DEBUG_PROBS.  Host destination. */
+int mxm_moe_probs(int64_t op, float* probs);
+
+/* Per-stage HIP-event timing.  When enabled, every forward records events
+ * between its kernels; mxm_moe_stage_times waits for the last forward and
+ * writes MXM_NUM_STAGES durations in milliseconds. */
+int mxm_moe_set_profiling(int64_t op, int enable);
+int mxm_moe_stage_times(int64_t op, float* ms, int n);
+
+/* Executor facts: info[0] = 1 if the MFMA expert kernels are used, info[1] =
+ * workspace bytes, info[2] = row-tile height of the grouped GEMM, info[3] =
+ * number of router tiles.  Returns the number of entries written. */
+int mxm_moe_info(int64_t op, int64_t* info, int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIXMOE_H */

@@ -1,0 +1,635 @@
+// C ABI of libmixmoe (declared in include/mixmoe.h): handle table, weight
+// upload, and the op-74 forward as a sequence of six kernels on one stream.
+//
+// Mirrors the reference bridge's conventions (gpu/mlx_bridge.cpp): a
+// process-global mutex over the handle table (gpu/mlx_bridge.cpp:39-42,105),
+// int64 handles with 0 = failure, and an exception fence around every entry
+// point (gpu/mlx_bridge.cpp:64-82) that turns failures into status codes and
+// a per-thread message.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/mixmoe.h"
+#include "mxm_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+std::mutex g_mu;
+std::map<int64_t, std::unique_ptr<struct MoeOp>> g_ops;
+int64_t g_next_handle = 1;
+std::string g_device_name = "uninitialised";
+
+[[noreturn]] void fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  throw std::runtime_error(buf);
+}
+
+#define HIPCK(expr)                                                                    \
+  do {                                                                                 \
+    hipError_t _e = (expr);                                                            \
+    if (_e != hipSuccess) fail("HIP error %s at %s:%d", hipGetErrorString(_e), __FILE__, __LINE__); \
+  } while (0)
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { reset(); }
+  void alloc(size_t n) {
+    reset();
+    if (n == 0) n = 256;
+    HIPCK(hipMalloc(&p, n));
+    bytes = n;
+  }
+  void reset() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  template <typename T>
+  T* as() const { return static_cast<T*>(p); }
+};
+
+bool hidden_is_bf16(int etype, int act) {
+  if (etype == MXM_EXPERT_SWIGLU) return true;
+  if (etype == MXM_EXPERT_GEGLU) return false;
+  return act == MXM_ACT_SILU || act == MXM_ACT_RELU;
+}
+
+struct MoeOp {
+  // op parameters (arch/ir.go:697)
+  int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
+  float slope = 0.0f;
+  int N = 0, wpe = 0, n_inputs = 0;
+  bool bf16 = false, mfma = false, debug_probs = false;
+  hipStream_t stream = nullptr;
+
+  // weights.  SIMT family: w1 = gate (GLU) or up (MLP) fp32 [E][D][F], w1b =
+  // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
+  // bf16 [E][2F or F][D] (GLU interleaved), w2 = bf16 [E][D][F].
+  DevBuf router, w1, w1b, w2;
+  std::vector<char> have;
+
+  // workspace, sized for N at the first forward
+  bool ws_ready = false;
+  int ntiles = 0, bm = 0, max_mtiles = 0;
+  DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
+      tile_base, counts, offsets, mstart, aux, ent, H, Y, probs;
+  size_t ws_bytes = 0;
+
+  // profiling
+  bool profiling = false, have_timing = false;
+  hipEvent_t ev[MXM_NUM_STAGES + 1] = {};
+
+  ~MoeOp() {
+    if (stream) {
+      (void)hipStreamSynchronize(stream);
+      (void)hipStreamDestroy(stream);
+    }
+    for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
+  }
+};
+
+MoeOp* get_op(int64_t h) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_ops.find(h);
+  if (it == g_ops.end()) return nullptr;
+  return it->second.get();
+}
+
+template <typename F>
+int fenced(F&& f) {
+  try {
+    return f();
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return MXM_ERR;
+  } catch (...) {
+    g_last_error = "unknown exception";
+    return MXM_ERR;
+  }
+}
+
+#define OP_OR_RETURN(h)                                 \
+  MoeOp* op = get_op(h);                                \
+  if (!op) {                                            \
+    g_last_error = "OP_MOE_FEED_FORWARD invalid handle"; \
+    return MXM_ERR_OP;                                  \
+  }
+
+void alloc_workspace(MoeOp& o) {
+  const size_t N = (size_t)o.N, K = (size_t)o.K, E = (size_t)o.E, NK = N * K;
+  o.ntiles = (int)((N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
+  o.bm = o.mfma ? mxm_mfma_bm() : mxm_simt_bm();
+  o.max_mtiles = (int)((NK + o.bm - 1) / o.bm) + o.E;
+  const size_t T = (size_t)o.ntiles;
+  size_t total = 0;
+  auto A = [&](DevBuf& b, size_t bytes) {
+    b.alloc(bytes);
+    total += b.bytes;
+  };
+  if (o.bf16) A(o.xcast, N * o.D * 2);
+  A(o.top_idx, NK * 4);
+  A(o.gates, NK * 4);
+  A(o.slot_rank, NK * 4);
+  A(o.slot_pos, NK * 4);
+  A(o.perm, NK * 4);
+  A(o.tile_counts, E * T * 4);
+  A(o.tile_psum, E * T * 4);
+  A(o.tile_ent, T * 4);
+  A(o.tile_base, E * T * 4);
+  A(o.counts, E * 4);
+  A(o.offsets, (E + 1) * 4);
+  A(o.mstart, (E + 1) * 4);
+  A(o.aux, 4);
+  A(o.ent, 4);
+  const size_t esz = o.mfma ? 2 : 4;
+  A(o.H, NK * (size_t)o.F * esz);
+  A(o.Y, NK * (size_t)o.D * esz);
+  if (o.debug_probs) A(o.probs, N * E * 4);
+  o.ws_bytes = total;
+  o.ws_ready = true;
+}
+
+void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent) {
+  for (int i = 1; i < o.n_inputs; ++i)
+    if (!o.have[i]) fail("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
+  if (!o.ws_ready) alloc_workspace(o);
+  hipStream_t st = o.stream;
+  const void* xin = x;
+  if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
+    mxm_launch_to_bf16(x, MXM_DTYPE_F32, o.xcast.as<uint16_t>(), (int64_t)o.N * o.D, st);
+    xin = o.xcast.p;
+  } else if ((o.bf16 && x_dtype != MXM_DTYPE_BF16) || (!o.bf16 && x_dtype != MXM_DTYPE_F32)) {
+    fail("OP_MOE_FEED_FORWARD unsupported x dtype %d for this compute dtype", x_dtype);
+  }
+  float* aux_p = aux ? aux : o.aux.as<float>();
+  float* ent_p = ent ? ent : o.ent.as<float>();
+  auto mark = [&](int i) {
+    if (o.profiling) HIPCK(hipEventRecord(o.ev[i], st));
+  };
+
+  mark(0);
+  RouterArgs ra{};
+  ra.x = xin;
+  ra.wr = o.router.p;
+  ra.N = o.N;
+  ra.D = o.D;
+  ra.E = o.E;
+  ra.K = o.K;
+  ra.top_idx = o.top_idx.as<int32_t>();
+  ra.gates = o.gates.as<float>();
+  ra.slot_rank = o.slot_rank.as<int32_t>();
+  ra.tile_counts = o.tile_counts.as<int32_t>();
+  ra.tile_psum = o.tile_psum.as<float>();
+  ra.tile_ent = o.tile_ent.as<float>();
+  ra.probs_out = o.debug_probs ? o.probs.as<float>() : nullptr;
+  mxm_launch_router(ra, o.bf16, st);
+  HIPCK(hipGetLastError());
+
+  mark(1);
+  ScanArgs sa{};
+  sa.tile_counts = ra.tile_counts;
+  sa.tile_psum = ra.tile_psum;
+  sa.tile_ent = ra.tile_ent;
+  sa.N = o.N;
+  sa.E = o.E;
+  sa.K = o.K;
+  sa.ntiles = o.ntiles;
+  sa.bm1 = o.bm;
+  sa.bm2 = o.bm;
+  sa.counts = o.counts.as<int32_t>();
+  sa.offsets = o.offsets.as<int32_t>();
+  sa.tile_base = o.tile_base.as<int32_t>();
+  sa.mstart1 = o.mstart.as<int32_t>();
+  sa.mstart2 = o.mstart.as<int32_t>();
+  sa.aux = aux_p;
+  sa.entropy = ent_p;
+  mxm_launch_scan(sa, o.bf16, st);
+  HIPCK(hipGetLastError());
+
+  mark(2);
+  ScatterArgs sc{};
+  sc.top_idx = ra.top_idx;
+  sc.slot_rank = ra.slot_rank;
+  sc.tile_base = sa.tile_base;
+  sc.N = o.N;
+  sc.K = o.K;
+  sc.ntiles = o.ntiles;
+  sc.perm = o.perm.as<int32_t>();
+  sc.slot_pos = o.slot_pos.as<int32_t>();
+  mxm_launch_scatter(sc, st);
+  HIPCK(hipGetLastError());
+
+  mark(3);
+  const bool glu = o.etype != MXM_EXPERT_MLP;
+  GemmArgs g1{};
+  g1.mode = glu ? MXM_GEMM_GLU : MXM_GEMM_MLP;
+  g1.a = xin;
+  g1.perm = sc.perm;
+  g1.b0 = o.w1.p;
+  g1.b1 = o.w1b.p;
+  g1.out = o.H.p;
+  g1.offsets = sa.offsets;
+  g1.mstart = sa.mstart1;
+  g1.E = o.E;
+  g1.Kd = o.D;
+  g1.Ncols = (o.mfma && glu) ? 2 * o.F : o.F;
+  g1.max_mtiles = o.max_mtiles;
+  g1.expert_type = o.etype;
+  g1.activation = o.act;
+  g1.slope = o.slope;
+  if (o.mfma)
+    mxm_launch_gemm_mfma(g1, st);
+  else
+    mxm_launch_gemm_simt(g1, o.bf16, st);
+  HIPCK(hipGetLastError());
+
+  mark(4);
+  GemmArgs g2{};
+  g2.mode = MXM_GEMM_DOWN;
+  g2.a = o.H.p;
+  g2.b0 = o.w2.p;
+  g2.out = o.Y.p;
+  g2.offsets = sa.offsets;
+  g2.mstart = sa.mstart2;
+  g2.E = o.E;
+  g2.Kd = o.F;
+  g2.Ncols = o.D;
+  g2.max_mtiles = o.max_mtiles;
+  g2.expert_type = o.etype;
+  g2.activation = o.act;
+  g2.slope = o.slope;
+  g2.y_bf16 = o.bf16 && hidden_is_bf16(o.etype, o.act);
+  if (o.mfma)
+    mxm_launch_gemm_mfma(g2, st);
+  else
+    mxm_launch_gemm_simt(g2, o.bf16, st);
+  HIPCK(hipGetLastError());
+
+  mark(5);
+  CombineArgs ca{};
+  ca.y = o.Y.p;
+  ca.top_idx = ra.top_idx;
+  ca.gates = ra.gates;
+  ca.slot_pos = sc.slot_pos;
+  ca.N = o.N;
+  ca.D = o.D;
+  ca.K = o.K;
+  ca.delta = delta;
+  mxm_launch_combine(ca, o.mfma, st);
+  HIPCK(hipGetLastError());
+  mark(6);
+  o.have_timing = o.profiling;
+}
+
+void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, const void* data,
+                int on_device) {
+  if (idx < 1 || idx >= o.n_inputs)
+    fail("OP_MOE_FEED_FORWARD input index %d out of range [1,%d)", idx, o.n_inputs);
+  if (dtype != MXM_DTYPE_F32 && dtype != MXM_DTYPE_BF16)
+    fail("OP_MOE_FEED_FORWARD weight dtype %d unsupported (want fp32 or bf16)", dtype);
+  if (!data) fail("OP_MOE_FEED_FORWARD input w%d has no data", idx - 1);
+  int rows, cols;
+  int e = -1, j = -1;
+  if (idx == 1) {
+    rows = o.D;
+    cols = o.E;
+    if (ndim != 2 || shape[0] != o.D || shape[1] != o.E)
+      fail("OP_MOE_FEED_FORWARD expects router_w shape [D,num_experts]");
+  } else {
+    e = (idx - 2) / o.wpe;
+    j = (idx - 2) % o.wpe;
+    const bool down = (j == o.wpe - 1);
+    rows = down ? o.F : o.D;
+    cols = down ? o.D : o.F;
+    if (ndim != 2 || shape[0] != rows || shape[1] != cols) {
+      if (o.wpe == 3) fail("OP_MOE_FEED_FORWARD expert GLU weights have invalid shapes");
+      fail("OP_MOE_FEED_FORWARD expert MLP weights have invalid shapes");
+    }
+  }
+  const size_t n = (size_t)rows * cols;
+  const size_t src_bytes = n * (dtype == MXM_DTYPE_BF16 ? 2 : 4);
+  hipStream_t st = o.stream;
+  DevBuf staging;
+  const void* src = data;
+  if (!on_device) {
+    staging.alloc(src_bytes);
+    HIPCK(hipMemcpyAsync(staging.p, data, src_bytes, hipMemcpyHostToDevice, st));
+    src = staging.p;
+  }
+  if (idx == 1) {
+    if (o.bf16)
+      mxm_launch_to_bf16(src, dtype, o.router.as<uint16_t>(), (int64_t)n, st);
+    else
+      mxm_launch_to_f32(src, dtype, o.router.as<float>(), (int64_t)n, st);
+  } else if (o.mfma) {
+    const bool glu = o.wpe == 3;
+    if (j == o.wpe - 1) {
+      uint16_t* dst = o.w2.as<uint16_t>() + (size_t)e * o.D * o.F;
+      mxm_launch_transpose_bf16(src, dtype, o.F, o.D, -1, dst, st);
+    } else {
+      const size_t ncols1 = glu ? 2 * (size_t)o.F : (size_t)o.F;
+      uint16_t* dst = o.w1.as<uint16_t>() + (size_t)e * ncols1 * o.D;
+      mxm_launch_transpose_bf16(src, dtype, o.D, o.F, glu ? j : -1, dst, st);
+    }
+  } else {
+    // SIMT family keeps the reference layout in fp32 storage, values rounded
+    // to bf16 first under bf16 compute.
+    float* dst;
+    if (j == o.wpe - 1)
+      dst = o.w2.as<float>() + (size_t)e * o.F * o.D;
+    else if (o.wpe == 3 && j == 1)
+      dst = o.w1b.as<float>() + (size_t)e * o.D * o.F;
+    else
+      dst = o.w1.as<float>() + (size_t)e * o.D * o.F;
+    if (o.bf16) {
+      DevBuf tmp;
+      tmp.alloc(n * 2);
+      mxm_launch_to_bf16(src, dtype, tmp.as<uint16_t>(), (int64_t)n, st);
+      mxm_launch_to_f32(tmp.p, MXM_DTYPE_BF16, dst, (int64_t)n, st);
+      HIPCK(hipStreamSynchronize(st));
+    } else {
+      mxm_launch_to_f32(src, dtype, dst, (int64_t)n, st);
+    }
+  }
+  HIPCK(hipGetLastError());
+  HIPCK(hipStreamSynchronize(st));
+  o.have[idx] = 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mxm_init(void) {
+  return fenced([&] {
+    int n = 0;
+    HIPCK(hipGetDeviceCount(&n));
+    if (n <= 0) fail("no HIP device");
+    int dev = 0;
+    HIPCK(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HIPCK(hipGetDeviceProperties(&prop, dev));
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_device_name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
+                    std::to_string(prop.multiProcessorCount) + " CUs)";
+    return MXM_OK;
+  });
+}
+
+const char* mxm_device_name(void) { return g_device_name.c_str(); }
+
+int mxm_last_error(char* buf, int n) {
+  if (buf && n > 0) {
+    std::strncpy(buf, g_last_error.c_str(), (size_t)n - 1);
+    buf[n - 1] = '\0';
+  }
+  return (int)g_last_error.size();
+}
+
+int mxm_malloc(void** ptr, int64_t bytes) {
+  return fenced([&] {
+    if (!ptr || bytes < 0) fail("mxm_malloc: bad arguments");
+    HIPCK(hipMalloc(ptr, bytes > 0 ? (size_t)bytes : 256));
+    return MXM_OK;
+  });
+}
+
+int mxm_free(void* ptr) {
+  return fenced([&] {
+    if (ptr) HIPCK(hipFree(ptr));
+    return MXM_OK;
+  });
+}
+
+int mxm_memcpy_h2d(void* dst, const void* src, int64_t bytes) {
+  return fenced([&] {
+    if (bytes > 0) HIPCK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    return MXM_OK;
+  });
+}
+
+int mxm_memcpy_d2h(void* dst, const void* src, int64_t bytes) {
+  return fenced([&] {
+    if (bytes > 0) HIPCK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+    return MXM_OK;
+  });
+}
+
+int mxm_memcpy_d2d(void* dst, const void* src, int64_t bytes) {
+  return fenced([&] {
+    if (bytes > 0) HIPCK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice));
+    return MXM_OK;
+  });
+}
+
+int mxm_device_synchronize(void) {
+  return fenced([&] {
+    HIPCK(hipDeviceSynchronize());
+    return MXM_OK;
+  });
+}
+
+int64_t mxm_moe_create(const float* float_params, int n_float_params, const int32_t* int_params,
+                       int n_int_params, int n_inputs, int compute_dtype, int flags) {
+  int64_t handle = 0;
+  const int rc = fenced([&] {
+    // gpu/ir.cpp:1076-1104
+    if (!int_params || n_int_params < 8)
+      fail("OP_MOE_FEED_FORWARD requires B,T,D,E,topK,expertType,ffn,activation");
+    auto o = std::make_unique<MoeOp>();
+    o->B = int_params[0];
+    o->T = int_params[1];
+    o->D = int_params[2];
+    o->E = int_params[3];
+    o->K = int_params[4];
+    o->etype = int_params[5];
+    o->F = int_params[6];
+    o->act = int_params[7];
+    o->slope = (float_params && n_float_params > 0) ? float_params[0] : 0.0f;
+    if (o->B <= 0 || o->T <= 0 || o->D <= 0 || o->E <= 0 || o->K <= 0 || o->K > o->E || o->F <= 0)
+      fail("OP_MOE_FEED_FORWARD invalid dimensions");
+    if ((int64_t)o->B * o->T > (int64_t)1 << 30) fail("OP_MOE_FEED_FORWARD invalid dimensions");
+    if (o->etype < MXM_EXPERT_SWIGLU || o->etype > MXM_EXPERT_MLP)
+      fail("OP_MOE_FEED_FORWARD unsupported expert type");
+    if (o->etype == MXM_EXPERT_MLP && (o->act < MXM_ACT_SILU || o->act > MXM_ACT_LEAKY_RELU_SQ))
+      fail("OP_MOE_FEED_FORWARD unsupported activation");
+    o->wpe = (o->etype == MXM_EXPERT_MLP) ? 2 : 3;
+    if (n_inputs != 2 + o->E * o->wpe)
+      fail("OP_MOE_FEED_FORWARD unexpected expert weight input count");
+    if (o->E > MXM_MAX_EXPERTS)
+      fail("OP_MOE_FEED_FORWARD supports at most %d experts (got %d)", MXM_MAX_EXPERTS, o->E);
+    if (compute_dtype != MXM_DTYPE_F32 && compute_dtype != MXM_DTYPE_BF16)
+      fail("OP_MOE_FEED_FORWARD compute dtype %d unsupported", compute_dtype);
+    o->N = o->B * o->T;
+    o->n_inputs = n_inputs;
+    o->bf16 = compute_dtype == MXM_DTYPE_BF16;
+    o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && (o->D % 128 == 0) && (o->F % 128 == 0);
+    o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
+    o->have.assign((size_t)n_inputs, 0);
+    HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
+    for (auto& e : o->ev) HIPCK(hipEventCreate(&e));
+    const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
+    o->router.alloc(DE * (o->bf16 ? 2 : 4));
+    if (o->mfma) {
+      o->w1.alloc(EE * DF * 2 * (o->wpe == 3 ? 2 : 1));
+      o->w2.alloc(EE * DF * 2);
+    } else {
+      o->w1.alloc(EE * DF * 4);
+      if (o->wpe == 3) o->w1b.alloc(EE * DF * 4);
+      o->w2.alloc(EE * DF * 4);
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    handle = g_next_handle++;
+    g_ops[handle] = std::move(o);
+    return MXM_OK;
+  });
+  return rc == MXM_OK ? handle : 0;
+}
+
+int mxm_moe_destroy(int64_t h) {
+  return fenced([&] {
+    std::unique_ptr<MoeOp> victim;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      auto it = g_ops.find(h);
+      if (it == g_ops.end()) {
+        g_last_error = "OP_MOE_FEED_FORWARD invalid handle";
+        return MXM_ERR_OP;
+      }
+      victim = std::move(it->second);
+      g_ops.erase(it);
+    }
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_set_input(int64_t h, int input_index, int dtype, const int64_t* shape, int ndim,
+                      const void* data, int on_device) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!shape && ndim > 0) fail("OP_MOE_FEED_FORWARD shape is NULL");
+    set_weight(*op, input_index, dtype, shape, ndim, data, on_device);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_forward(int64_t h, const void* x, int x_dtype, int64_t rows, float* delta, float* aux,
+                    float* entropy) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
+    run_forward(*op, x, x_dtype, delta, aux, entropy);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_forward_host(int64_t h, const void* x, int x_dtype, int64_t rows, float* delta,
+                         float* aux, float* entropy) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
+    const size_t xe = (x_dtype == MXM_DTYPE_BF16) ? 2 : 4;
+    DevBuf dx, dd;
+    dx.alloc((size_t)op->N * op->D * xe);
+    dd.alloc((size_t)op->N * op->D * 4);
+    HIPCK(hipMemcpyAsync(dx.p, x, dx.bytes, hipMemcpyHostToDevice, op->stream));
+    if (!op->ws_ready) alloc_workspace(*op);
+    run_forward(*op, dx.p, x_dtype, dd.as<float>(), op->aux.as<float>(), op->ent.as<float>());
+    HIPCK(hipMemcpyAsync(delta, dd.p, (size_t)op->N * op->D * 4, hipMemcpyDeviceToHost, op->stream));
+    if (aux) HIPCK(hipMemcpyAsync(aux, op->aux.p, 4, hipMemcpyDeviceToHost, op->stream));
+    if (entropy) HIPCK(hipMemcpyAsync(entropy, op->ent.p, 4, hipMemcpyDeviceToHost, op->stream));
+    HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_synchronize(int64_t h) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_routing(int64_t h, int32_t* top_idx, float* gates, int32_t* counts, int32_t* offsets,
+                    int32_t* perm, int to_host) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!op->ws_ready) fail("OP_MOE_FEED_FORWARD routing requested before any forward");
+    const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    const size_t NK = (size_t)op->N * op->K;
+    auto cp = [&](void* dst, const DevBuf& src, size_t bytes) {
+      if (dst) HIPCK(hipMemcpyAsync(dst, src.p, bytes, kind, op->stream));
+    };
+    cp(top_idx, op->top_idx, NK * 4);
+    cp(gates, op->gates, NK * 4);
+    cp(counts, op->counts, (size_t)op->E * 4);
+    cp(offsets, op->offsets, ((size_t)op->E + 1) * 4);
+    cp(perm, op->perm, NK * 4);
+    HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_probs(int64_t h, float* probs) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!op->debug_probs) fail("OP_MOE_FEED_FORWARD probabilities need MXM_FLAG_DEBUG_PROBS");
+    if (!op->ws_ready) fail("OP_MOE_FEED_FORWARD probabilities requested before any forward");
+    HIPCK(hipMemcpyAsync(probs, op->probs.p, (size_t)op->N * op->E * 4, hipMemcpyDeviceToHost,
+                         op->stream));
+    HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_set_profiling(int64_t h, int enable) {
+  OP_OR_RETURN(h);
+  op->profiling = enable != 0;
+  op->have_timing = false;
+  return MXM_OK;
+}
+
+int mxm_moe_stage_times(int64_t h, float* ms, int n) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!op->have_timing) fail("OP_MOE_FEED_FORWARD no profiled forward yet");
+    HIPCK(hipEventSynchronize(op->ev[MXM_NUM_STAGES]));
+    for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i)
+      HIPCK(hipEventElapsedTime(&ms[i], op->ev[i], op->ev[i + 1]));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_info(int64_t h, int64_t* info, int n) {
+  OP_OR_RETURN(h);
+  const int64_t vals[4] = {op->mfma ? 1 : 0, (int64_t)op->ws_bytes,
+                           op->mfma ? mxm_mfma_bm() : mxm_simt_bm(),
+                           (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM)};
+  int w = 0;
+  for (; w < n && w < 4; ++w) info[w] = vals[w];
+  return w;
+}
+
+}  // extern "C"

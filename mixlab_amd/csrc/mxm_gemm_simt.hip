@@ -1,0 +1,175 @@
+// Grouped expert FFN, SIMT family.  Used for the fp32 flow and for bf16
+// shapes the MFMA family does not tile (D or F not a multiple of 128).
+//
+// Each output is accumulated by fmaf over k = 0..Kd-1 in ascending order, the
+// order of the CPU restatement, and the epilogue follows the dtype flow of
+// gpu/ir.cpp:1126-1145 (projections rounded to bf16 in the bf16 flow, the
+// hidden activation per mxm_hidden, y rounded to bf16 when the reference's
+// down projection produces bf16).  H and Y are kept in fp32 storage.
+//
+// Row tiles are ragged per expert: blockIdx.y indexes the concatenation of
+// every expert's ceil(count/BM) row tiles (prefix `mstart`), so no host sync
+// is needed between dispatch and the GEMM.
+#include "mxm_kernels.h"
+
+namespace {
+
+constexpr int BM = 64, BN = 64, BK = 16, NT = 256;
+constexpr int LDA = BM + 4, LDB = BN + 4;
+
+__device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mtile) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (mstart[mid] <= mtile)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename TA>
+__device__ __forceinline__ float lda_f32(const TA* p);
+template <>
+__device__ __forceinline__ float lda_f32<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float lda_f32<uint16_t>(const uint16_t* p) { return mxm_bf2f(*p); }
+
+template <typename TA, bool BF16, int MODE>
+__global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
+  constexpr int NB = (MODE == MXM_GEMM_GLU) ? 2 : 1;
+  __shared__ float As[BK][LDA];
+  __shared__ float Bs[NB][BK][LDB];
+
+  const int mtile = blockIdx.y;
+  if (mtile >= a.mstart[a.E]) return;
+  const int e = find_expert(a.mstart, a.E, mtile);
+  const int row0 = a.offsets[e] + (mtile - a.mstart[e]) * BM;
+  const int rows = min(BM, a.offsets[e + 1] - row0);
+  const int n0 = blockIdx.x * BN;
+  const int Kd = a.Kd, NC = a.Ncols;
+  const int tid = threadIdx.x;
+  const int ty = tid >> 4, tx = tid & 15;
+
+  const TA* A = static_cast<const TA*>(a.a);
+  const float* B0 = static_cast<const float*>(a.b0) + (size_t)e * Kd * NC;
+  const float* B1 = (NB == 2) ? static_cast<const float*>(a.b1) + (size_t)e * Kd * NC : nullptr;
+
+  // A-tile rows this thread loads: idx = tid + 256*r -> row idx/BK, k idx%BK
+  const TA* arow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = (tid + NT * r) / BK;
+    if (row < rows) {
+      const int p = row0 + row;
+      const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
+      arow[r] = A + (size_t)src * Kd;
+    } else {
+      arow[r] = nullptr;
+    }
+  }
+
+  float acc[NB][4][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[b][i][j] = 0.0f;
+
+  for (int k0 = 0; k0 < Kd; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int idx = tid + NT * r;
+      const int row = idx / BK, kk = idx % BK;
+      const int k = k0 + kk;
+      As[kk][row] = (arow[r] != nullptr && k < Kd) ? lda_f32<TA>(arow[r] + k) : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float* Bm = (b == 0) ? B0 : B1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = tid + NT * r;
+        const int kk = idx / BN, col = idx % BN;
+        const int k = k0 + kk, c = n0 + col;
+        Bs[b][kk][col] = (k < Kd && c < NC) ? Bm[(size_t)k * NC + c] : 0.0f;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; ++kk) {
+      const float4 av = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
+      const float ar[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float4 bv = *reinterpret_cast<const float4*>(&Bs[b][kk][tx * 4]);
+        const float br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[b][i][j] = __builtin_fmaf(ar[i], br[j], acc[b][i][j]);
+      }
+    }
+  }
+
+  float* out = static_cast<float*>(a.out);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = ty * 4 + i;
+    if (row >= rows) continue;
+    const size_t orow = (size_t)(row0 + row) * NC;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = n0 + tx * 4 + j;
+      if (c >= NC) continue;
+      float v;
+      if (MODE == MXM_GEMM_GLU) {
+        float g = acc[0][i][j], u = acc[NB - 1][i][j];
+        if (BF16) {
+          g = mxm_rbf(g);
+          u = mxm_rbf(u);
+        }
+        v = mxm_hidden<BF16>(a.expert_type, a.activation, a.slope, g, u);
+      } else if (MODE == MXM_GEMM_MLP) {
+        float u = acc[0][i][j];
+        if (BF16) u = mxm_rbf(u);
+        v = mxm_hidden<BF16>(MXM_EXPERT_MLP, a.activation, a.slope, 0.0f, u);
+      } else {
+        v = acc[0][i][j];
+        if (a.y_bf16) v = mxm_rbf(v);
+      }
+      out[orow + c] = v;
+    }
+  }
+}
+
+template <typename TA, bool BF16>
+void launch_t(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.Ncols + BN - 1) / BN, a.max_mtiles);
+  switch (a.mode) {
+    case MXM_GEMM_GLU:
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU>), grid, dim3(NT), 0, s, a);
+      break;
+    case MXM_GEMM_MLP:
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP>), grid, dim3(NT), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN>), grid, dim3(NT), 0, s, a);
+      break;
+  }
+}
+
+}  // namespace
+
+int mxm_simt_bm() { return BM; }
+
+void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s) {
+  if (a.max_mtiles <= 0) return;
+  if (bf16)
+    launch_t<uint16_t, true>(a, s);
+  else
+    launch_t<float, false>(a, s);
+}

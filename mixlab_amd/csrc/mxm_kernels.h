@@ -1,0 +1,103 @@
+// Launchers of the libmixmoe kernels (one HIP stream per call).  Host code in
+// mxm_abi.cpp owns every buffer; these structs carry raw device pointers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mxm_numerics.h"
+
+// Tokens per router tile; the dispatch bitmasks are two 32-bit words per
+// expert and tile, so this is fixed at 64.
+#define MXM_ROUTER_TM 64
+// Largest expert count the router supports (4 experts per lane).
+#define MXM_MAX_EXPERTS 256
+
+struct RouterArgs {
+  const void* x;   // [N, D], bf16 bits or fp32
+  const void* wr;  // [D, E], same dtype
+  int N, D, E, K;
+  int32_t* top_idx;      // [N, K]
+  float* gates;          // [N, K]
+  int32_t* slot_rank;    // [N, K] rank of the slot among the tile's tokens on that expert
+  int32_t* tile_counts;  // [E, ntiles]
+  float* tile_psum;      // [E, ntiles] sum of probabilities over the tile
+  float* tile_ent;       // [ntiles] sum over the tile of sum_e p log max(p, 1e-12)
+  float* probs_out;      // optional [N, E]
+};
+void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s);
+
+struct ScanArgs {
+  const int32_t* tile_counts;  // [E, ntiles]
+  const float* tile_psum;      // [E, ntiles]
+  const float* tile_ent;       // [ntiles]
+  int N, E, K, ntiles;
+  int bm1, bm2;         // row-tile heights of the two grouped GEMMs
+  int32_t* counts;      // [E]
+  int32_t* offsets;     // [E + 1]
+  int32_t* tile_base;   // [E, ntiles] first permuted position of the tile's rows on e
+  int32_t* mstart1;     // [E + 1] prefix of ceil(counts / bm1)
+  int32_t* mstart2;     // [E + 1] prefix of ceil(counts / bm2)
+  float* aux;           // [1]
+  float* entropy;       // [1]
+};
+void mxm_launch_scan(const ScanArgs& a, bool bf16, hipStream_t s);
+
+struct ScatterArgs {
+  const int32_t* top_idx;
+  const int32_t* slot_rank;
+  const int32_t* tile_base;
+  int N, K, ntiles;
+  int32_t* perm;      // [N*K] permuted position -> token
+  int32_t* slot_pos;  // [N*K] slot (n, k) -> permuted position
+};
+void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s);
+
+// Grouped expert FFN.  mode: 0 = gate+up with GLU epilogue, 1 = up with MLP
+// activation, 2 = down projection.
+enum { MXM_GEMM_GLU = 0, MXM_GEMM_MLP = 1, MXM_GEMM_DOWN = 2 };
+
+struct GemmArgs {
+  int mode;
+  const void* a;          // mode 0/1: x [N, Kd]; mode 2: H [N*K, Kd]
+  const int32_t* perm;    // mode 0/1: permuted position -> token
+  const void* b0;         // weights, layout depends on the kernel family
+  const void* b1;         // second weight (SIMT GLU up-projection)
+  const float* scale0;    // int8 weights: per-output-channel scales
+  const float* scale1;
+  void* out;              // mode 0/1: H [N*K, F]; mode 2: Y [N*K, D]
+  const int32_t* offsets; // [E + 1]
+  const int32_t* mstart;  // [E + 1]
+  int E, Kd, Ncols;       // reduction length, output columns (per matrix)
+  int max_mtiles;         // grid bound on row tiles
+  int expert_type, activation;
+  float slope;
+  bool y_bf16;            // SIMT down: round y to bf16
+};
+// SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
+// fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
+void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s);
+// MFMA family: bf16 weights stored transposed ([out, in]); GLU gate/up rows
+// interleaved in groups of 32; H and Y are bf16.
+void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s);
+int mxm_mfma_bm();  // row-tile height used by the MFMA kernels
+int mxm_simt_bm();
+
+struct CombineArgs {
+  const void* y;          // [N*K, D], fp32 or bf16
+  const int32_t* top_idx; // [N, K]
+  const float* gates;     // [N, K]
+  const int32_t* slot_pos;
+  int N, D, K;
+  float* delta;           // [N, D]
+};
+void mxm_launch_combine(const CombineArgs& a, bool y_bf16, hipStream_t s);
+
+// Weight preparation (run once at upload).
+void mxm_launch_to_f32(const void* src, int src_dtype, float* dst, int64_t n, hipStream_t s);
+void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n, hipStream_t s);
+// Transposed bf16 copy of one weight matrix src [Kd, C] (x.W layout):
+// dst[q, k] = bf16(src[k, c]) with q = c (slot < 0), or, for the GLU
+// interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up.
+void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
+                               uint16_t* dst, hipStream_t s);

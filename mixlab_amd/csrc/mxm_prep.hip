@@ -1,0 +1,65 @@
+// Weight preparation, run once when weights are uploaded: dtype conversion
+// to the flow's storage type and the transposed / GLU-interleaved layout of
+// the MFMA family.  Source dtypes: 1 = fp32, 2 = bf16 bits.
+#include "mxm_kernels.h"
+
+namespace {
+
+__device__ __forceinline__ float src_at(const void* p, int dtype, size_t i) {
+  return dtype == 2 ? mxm_bf2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+__global__ void to_f32_kernel(const void* src, int dtype, float* dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = src_at(src, dtype, (size_t)i);
+}
+
+__global__ void to_bf16_kernel(const void* src, int dtype, uint16_t* dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = mxm_f2bf(src_at(src, dtype, (size_t)i));
+}
+
+// 32x32 LDS transpose: block (32, 8) covers source cols c0..c0+31 and
+// k0..k0+31; the 32 destination rows of an aligned group of 32 source
+// columns are consecutive in both layouts.
+__global__ void transpose_kernel(const void* src, int dtype, int Kd, int C, int slot,
+                                 uint16_t* dst) {
+  __shared__ uint16_t tile[32][33];
+  const int c0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
+  for (int yy = threadIdx.y; yy < 32; yy += 8) {
+    const int k = k0 + yy, c = c0 + threadIdx.x;
+    tile[yy][threadIdx.x] = (k < Kd && c < C) ? mxm_f2bf(src_at(src, dtype, (size_t)k * C + c)) : 0;
+  }
+  __syncthreads();
+  for (int yy = threadIdx.y; yy < 32; yy += 8) {
+    const int c = c0 + yy, k = k0 + threadIdx.x;
+    if (c < C && k < Kd) {
+      const int q = slot < 0 ? c : (c >> 5) * 64 + slot * 32 + (c & 31);
+      dst[(size_t)q * Kd + k] = tile[threadIdx.x][yy];
+    }
+  }
+}
+
+int grid_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  return (int)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+void mxm_launch_to_f32(const void* src, int src_dtype, float* dst, int64_t n, hipStream_t s) {
+  if (n > 0) hipLaunchKernelGGL(to_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, dst, n);
+}
+
+void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n, hipStream_t s) {
+  if (n > 0) hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, dst, n);
+}
+
+void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
+                               uint16_t* dst, hipStream_t s) {
+  const dim3 grid((C + 31) / 32, (Kd + 31) / 32);
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, s, src, src_dtype, Kd, C, slot, dst);
+}

@@ -1,0 +1,196 @@
+"""GPU parity: libmixmoe (HIP, gfx950) against the CPU restatement of
+gpu/ir.cpp:1073-1164 on the same seeded inputs.
+
+Bars: top-k indices, gates, dispatch counts/offsets/permutation bit-exact;
+delta within 1e-5 relative L2 in fp32 and 2e-2 in bf16 (the tolerances of the
+benchmark plan); the exact-order SIMT kernels are additionally bit-exact.
+"""
+import numpy as np
+import pytest
+
+from mixlab_amd import _lib
+from mixlab_amd.workloads import CONFIGS, make_workload, round_bf16
+from tests.moe_testutil import (assert_routing_equal, random_case, rel_l2, run_gpu, run_oracle,
+                                same_bits)
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _patterned(n, scale):
+    i = np.arange(n, dtype=np.float64)
+    return (scale * (np.sin(i + 1) * 0.7 + np.cos((i + 3) % 11) * 0.3)).astype(np.float32)
+
+
+@pytest.mark.parametrize("top_k", [1, 2])
+def test_reference_known_answer_case(gpu_lib, top_k):
+    """gpu/moe_feed_forward_test.go:19-79: B=1, T=4, D=3, E=3, FFN=4, swiglu."""
+    B, T, D, E, F = 1, 4, 3, 3, 4
+    x = _patterned(B * T * D, 0.17).reshape(B * T, D)
+    wr = _patterned(D * E, 0.23).reshape(D, E)
+    experts = [[_patterned(D * F, 0.09 + e * 0.03).reshape(D, F),
+                _patterned(D * F, 0.11 + e * 0.03).reshape(D, F),
+                _patterned(F * D, 0.13 + e * 0.03).reshape(F, D)] for e in range(E)]
+    delta, aux, ent, routing, _ = run_gpu(x, wr, experts, B=B, T=T, K=top_k)
+    want = run_oracle(x, wr, experts, K=top_k)
+    assert_routing_equal(routing, want)
+    assert same_bits(delta, want["delta"])
+    assert abs(aux - want["aux"]) <= 2e-5
+    assert abs(ent - want["entropy"]) <= 2e-5
+
+
+def test_c1_fp32(gpu_lib):
+    cfg = CONFIGS["C1"]
+    w = make_workload(cfg)
+    delta, aux, ent, routing, info = run_gpu(w.x, w.router_w, w.experts, B=cfg.B, T=cfg.T, K=cfg.K)
+    want = run_oracle(w.x, w.router_w, w.experts, K=cfg.K)
+    assert not info["mfma"]
+    assert_routing_equal(routing, want)
+    assert rel_l2(delta, want["delta"]) <= FP32_TOL
+    assert same_bits(delta, want["delta"])
+    assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
+    assert abs(ent - want["entropy"]) <= 1e-5 * abs(want["entropy"])
+
+
+def test_c2_bf16_mfma(gpu_lib):
+    cfg = CONFIGS["C2"]
+    w = make_workload(cfg)
+    delta, aux, ent, routing, info = run_gpu(w.x, w.router_w, w.experts, B=cfg.B, T=cfg.T,
+                                             K=cfg.K, bf16=True)
+    want = run_oracle(w.x, w.router_w, w.experts, K=cfg.K, bf16=True)
+    assert info["mfma"]
+    assert_routing_equal(routing, want)
+    err = rel_l2(delta, want["delta"])
+    print(f"C2 bf16 delta rel L2 = {err:.3e}")
+    assert err <= BF16_TOL
+    assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+    assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"])
+
+
+def test_bf16_simt_bit_exact(gpu_lib):
+    """The exact-order SIMT kernels reproduce the bf16 dtype flow bit for bit."""
+    x, wr, experts = random_case(11, 512, 256, 8, 256)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(m) for m in ws] for ws in experts]
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=2, T=256, K=2, bf16=True,
+                                             flags=_lib.MXM_FLAG_FORCE_SIMT)
+    want = run_oracle(x, wr, experts, K=2, bf16=True)
+    assert not info["mfma"]
+    assert_routing_equal(routing, want)
+    assert same_bits(delta, want["delta"])
+
+
+EXPERTS = [
+    ("swiglu", 0, 0, 0.0),
+    ("geglu", 1, 1, 0.0),
+    ("mlp_silu", 2, 0, 0.0),
+    ("mlp_gelu", 2, 1, 0.0),
+    ("mlp_relu", 2, 2, 0.0),
+    ("mlp_leaky_relu_sq", 2, 3, 0.2),
+]
+
+
+@pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
+@pytest.mark.parametrize("flow", ["fp32", "bf16_mfma", "bf16_simt"])
+def test_expert_types(gpu_lib, name, etype, act, slope, flow):
+    bf16 = flow != "fp32"
+    x, wr, experts = random_case(7 + etype * 4 + act, 320, 256, 8, 256, expert_type=etype)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(m) for m in ws] for ws in experts]
+    flags = _lib.MXM_FLAG_FORCE_SIMT if flow == "bf16_simt" else 0
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=320, K=2, expert_type=etype,
+                                             activation=act, slope=slope, bf16=bf16, flags=flags)
+    want = run_oracle(x, wr, experts, K=2, expert_type=etype, activation=act, slope=slope,
+                      bf16=bf16)
+    assert info["mfma"] == (flow == "bf16_mfma")
+    assert_routing_equal(routing, want)
+    if flow == "bf16_mfma":
+        err = rel_l2(delta, want["delta"])
+        print(f"{name} bf16 mfma rel L2 = {err:.3e}")
+        assert err <= BF16_TOL
+    else:
+        assert same_bits(delta, want["delta"])
+
+
+def test_ties_go_to_lower_expert(gpu_lib):
+    """Duplicate router columns give equal probabilities; a stable argsort
+    (train/export_hf_ffn_oracle_test.go:40-42) keeps the lower expert first."""
+    x, wr, experts = random_case(5, 256, 64, 8, 128)
+    wr[:, 5] = wr[:, 2]
+    wr[:, 7] = wr[:, 2]
+    wr[:, 6] = wr[:, 1]
+    for flow in (False, True):
+        xx, ww = (round_bf16(x), round_bf16(wr)) if flow else (x, wr)
+        ee = [[round_bf16(m) for m in ws] for ws in experts] if flow else experts
+        delta, aux, ent, routing, _ = run_gpu(xx, ww, ee, B=1, T=256, K=3, bf16=flow,
+                                              flags=_lib.MXM_FLAG_FORCE_SIMT)
+        want = run_oracle(xx, ww, ee, K=3, bf16=flow)
+        assert_routing_equal(routing, want)
+        top = routing["top_idx"]
+        # expert 2 always precedes its copies 5 and 7, expert 1 precedes 6
+        for n in range(top.shape[0]):
+            row = list(top[n])
+            for lo, hi in ((2, 5), (2, 7), (5, 7), (1, 6)):
+                if lo in row and hi in row:
+                    assert row.index(lo) < row.index(hi)
+
+
+@pytest.mark.parametrize("B,T", [(3, 37), (1, 1), (1, 65), (2, 200)])
+def test_ragged_token_counts(gpu_lib, B, T):
+    x, wr, experts = random_case(B * 100 + T, B * T, 128, 6, 128)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(m) for m in ws] for ws in experts]
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=B, T=T, K=2, bf16=True)
+    want = run_oracle(x, wr, experts, K=2, bf16=True)
+    assert info["mfma"]
+    assert_routing_equal(routing, want)
+    assert rel_l2(delta, want["delta"]) <= BF16_TOL
+
+
+def test_k_equals_e_and_k1(gpu_lib):
+    x, wr, experts = random_case(21, 128, 128, 4, 128)
+    for K in (1, 4):
+        delta, aux, ent, routing, _ = run_gpu(x, wr, experts, B=1, T=128, K=K)
+        want = run_oracle(x, wr, experts, K=K)
+        assert_routing_equal(routing, want)
+        assert same_bits(delta, want["delta"])
+        if K == 1:
+            assert np.all(routing["gates"] == 1.0)
+
+
+def _check_large(name, sample_rows=256):
+    cfg = CONFIGS[name]
+    w = make_workload(cfg)
+    delta, aux, ent, routing, info = run_gpu(w.x, w.router_w, w.experts, B=cfg.B, T=cfg.T,
+                                             K=cfg.K, bf16=True)
+    rng = np.random.default_rng(1)
+    rows = np.sort(rng.choice(cfg.N, size=sample_rows, replace=False)).astype(np.int32)
+    want = run_oracle(w.x, w.router_w, w.experts, K=cfg.K, bf16=True, rows=rows)
+    assert info["mfma"]
+    assert_routing_equal(routing, want)
+    # size-independent invariants of the dispatch
+    assert routing["counts"].sum() == cfg.N * cfg.K
+    perm = routing["perm"]
+    off = routing["offsets"]
+    for e in range(cfg.E):
+        seg = perm[off[e]:off[e + 1]]
+        assert np.all(np.diff(seg) > 0)
+    err = rel_l2(delta[rows], want["delta"][rows])
+    print(f"{name} sampled delta rel L2 = {err:.3e}; counts = {routing['counts'].tolist()}")
+    assert err <= BF16_TOL
+    assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+    assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"])
+    return routing
+
+
+def test_c3_zipf_full(gpu_lib):
+    routing = _check_large("C3")
+    c = routing["counts"].astype(np.float64)
+    assert c[0] > 4 * c[-1]  # skewed
+
+
+def test_c4_full(gpu_lib):
+    _check_large("C4")
