@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""MoE layer forward throughput on one MI355X (libmixmoe, op 74).
+
+A step is one forward of the MoE feed-forward op (router, dispatch, grouped
+expert FFN, combine) over the whole batch, with inputs and weights resident
+in HBM.  Default workload: d_model 2048, 64 experts, top-8, gated expert
+hidden 1024, 65,536 tokens, bf16 (the configuration the headline metric is
+quoted on).  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "MoE layer tokens/sec at d=2048,64e top-8; grouped-GEMM % MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (AMD published)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def stage_bytes(cfg) -> dict:
+    """Algorithmic HBM bytes per launch of the memory-bound stages."""
+    N, D, E, K, F = cfg.N, cfg.D, cfg.E, cfg.K, cfg.F
+    xb = 2 if cfg.dtype == "bf16" else 4
+    NK = N * K
+    tiles = (N + 63) // 64
+    return {
+        # x read, router weights, top_idx + gates + ranks written, tile partials
+        "router": N * D * xb + D * E * xb + NK * 12 + tiles * E * 8,
+        # top_idx, ranks, tile bases read; perm, slot_pos written
+        "scatter": NK * 4 * 2 + NK * 4 * 2,
+        # K rows of y per token, gates + idx + pos, delta written fp32
+        "combine": NK * D * (2 if cfg.dtype == "bf16" else 4) + NK * 12 + N * D * 4,
+    }
+
+
+def cpu_baseline(w, cfg, target_s: float) -> dict:
+    """Time the dense fp32 BLAS restatement of the reference algorithm on a
+    bounded prefix of the same tokens (oracle/dense_blas.py)."""
+    from threadpoolctl import threadpool_info
+
+    from oracle.dense_blas import dense_forward
+
+    cores = max((p.get("num_threads", 1) for p in threadpool_info()
+                 if p.get("user_api") == "blas"), default=1)
+    mats = {}
+
+    def mat(e, j):
+        if (e, j) not in mats:
+            mats[(e, j)] = np.ascontiguousarray(w.matrix(e, j), dtype=np.float32)
+        return mats[(e, j)]
+
+    def run(n):
+        t0 = time.perf_counter()
+        dense_forward(w.x[:n], w.router_w, mat, cfg.E, cfg.K, cfg.expert_type, cfg.activation,
+                      cfg.leaky_slope)
+        return time.perf_counter() - t0
+
+    n = min(cfg.N, 64)
+    t = run(n)  # warm-up (also converts the weights once)
+    t = run(n)
+    while t < target_s / 4 and n < cfg.N:
+        n = min(cfg.N, n * 4)
+        t = run(n)
+    times = [t] + [run(n) for _ in range(2)]
+    med = float(np.median(times))
+    return {"value": n / med, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": (f"first {n} of {cfg.N} tokens, dense fp32 (all {cfg.E} experts on every "
+                       f"token, gpu/ir.cpp:1118-1148) with numpy/OpenBLAS sgemm; median of 3 "
+                       f"runs of {med:.2f} s after warm-up")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C4", help="C1..C4 (C4 is the headline configuration)")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="target seconds per timed run of the CPU baseline (0 disables it)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(data parallelism over tokens would shard N with no collective; "
+              "expert parallelism needs an all-to-all). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from mixlab_amd import _lib
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import CONFIGS, make_workload
+
+    cfg = CONFIGS[args.config]
+    log(f"device: {_lib.device_name()}")
+    t0 = time.time()
+    w = make_workload(cfg)
+    log(f"workload {cfg.name} generated in {time.time() - t0:.1f}s ({cfg.note})")
+
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype)
+    op.set_input(1, w.router_upload())
+    idx = 2
+    for e in range(cfg.E):
+        for j in range(cfg.wpe):
+            op.set_input(idx, w.matrix_upload(e, j))
+            idx += 1
+    xdev = _lib.DeviceBuffer.from_array(w.x_upload())
+    delta = _lib.DeviceBuffer(cfg.N * cfg.D * 4)
+    aux = _lib.DeviceBuffer(4)
+    ent = _lib.DeviceBuffer(4)
+    xcode = _lib.MXM_DTYPE_BF16 if cfg.dtype == "bf16" else _lib.MXM_DTYPE_F32
+    log(f"weights uploaded; executor {op.info()}")
+
+    def step():
+        op.forward(xdev.value, xcode, cfg.N, delta.value, aux.value, ent.value)
+
+    for _ in range(args.warmup):
+        step()
+    op.synchronize()
+    log(f"warmup {args.warmup} done")
+
+    op.set_profiling(True)
+    op.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    op.synchronize()
+    elapsed = time.perf_counter() - t0
+    stages = op.stage_times()
+    op.set_profiling(False)
+    ms_per_step = elapsed * 1e3 / args.steps
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; stages {stages}")
+
+    fl = cfg.flops()
+    up_tflops = fl["up"] / (stages["gemm_up"] * 1e-3) / 1e12
+    down_tflops = fl["down"] / (stages["gemm_down"] * 1e-3) / 1e12
+    gg_ms = stages["gemm_up"] + stages["gemm_down"]
+    gg_tflops = fl["experts"] / (gg_ms * 1e-3) / 1e12
+    sb = stage_bytes(cfg)
+    hbm = {k: sb[k] / (stages[k] * 1e-3) / 1e9 for k in sb}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(w, cfg, args.cpu_seconds)
+        log(f"cpu baseline {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": cfg.N / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights)",
+        "config": {"workload": cfg.name, "tokens": cfg.N, "d_model": cfg.D, "experts": cfg.E,
+                   "top_k": cfg.K, "expert_hidden": cfg.F,
+                   "expert": "sigmoid-GLU (swiglu)" if cfg.expert_type == 0 else str(cfg.expert_type),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_up (gate+up grouped GEMM, GLU epilogue)",
+                     "achieved": up_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": up_tflops / PEAK_BF16_TFLOPS, "traffic": None},
+        "grouped_gemm": {"ms": gg_ms, "tflops": gg_tflops, "frac": gg_tflops / PEAK_BF16_TFLOPS,
+                         "up_tflops": up_tflops, "down_tflops": down_tflops},
+        "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
+        "hbm_gbs": hbm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    op.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -137,9 +137,11 @@ int mxm_moe_routing(int64_t op, int32_t* top_idx, float* gates, int32_t* counts,
  * MXM_FLAG_DEBUG_PROBS.  Host destination. */
 int mxm_moe_probs(int64_t op, float* probs);
 
-/* Per-stage HIP-event timing.  When enabled, every forward records events
- * between its kernels; mxm_moe_stage_times waits for the last forward and
- * writes MXM_NUM_STAGES durations in milliseconds. */
+/* Per-stage HIP-event timing on the op's stream.  mxm_moe_set_profiling
+ * (re)starts a recording: every later forward records events between its
+ * kernels.  mxm_moe_stage_times waits for the recorded forwards and writes
+ * the mean duration of each of the MXM_NUM_STAGES stages in milliseconds;
+ * it returns the number of forwards averaged (> 0) or an error code. */
 int mxm_moe_set_profiling(int64_t op, int enable);
 int mxm_moe_stage_times(int64_t op, float* ms, int n);
 

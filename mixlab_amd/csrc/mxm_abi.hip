@@ -8,6 +8,7 @@
 // a per-thread message.
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -93,17 +94,19 @@ struct MoeOp {
       tile_base, counts, offsets, mstart, aux, ent, H, Y, probs;
   size_t ws_bytes = 0;
 
-  // profiling
-  bool profiling = false, have_timing = false;
-  hipEvent_t ev[MXM_NUM_STAGES + 1] = {};
+  // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
+  bool profiling = false;
+  std::vector<std::array<hipEvent_t, MXM_NUM_STAGES + 1>> ev_sets;
+  size_t ev_used = 0;
 
   ~MoeOp() {
     if (stream) {
       (void)hipStreamSynchronize(stream);
       (void)hipStreamDestroy(stream);
     }
-    for (auto& e : ev)
-      if (e) (void)hipEventDestroy(e);
+    for (auto& set : ev_sets)
+      for (auto& e : set)
+        if (e) (void)hipEventDestroy(e);
   }
 };
 
@@ -182,8 +185,17 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   }
   float* aux_p = aux ? aux : o.aux.as<float>();
   float* ent_p = ent ? ent : o.ent.as<float>();
+  hipEvent_t* evs = nullptr;
+  if (o.profiling) {
+    if (o.ev_used == o.ev_sets.size()) {
+      std::array<hipEvent_t, MXM_NUM_STAGES + 1> set{};
+      for (auto& e : set) HIPCK(hipEventCreate(&e));
+      o.ev_sets.push_back(set);
+    }
+    evs = o.ev_sets[o.ev_used++].data();
+  }
   auto mark = [&](int i) {
-    if (o.profiling) HIPCK(hipEventRecord(o.ev[i], st));
+    if (evs) HIPCK(hipEventRecord(evs[i], st));
   };
 
   mark(0);
@@ -297,7 +309,6 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   mxm_launch_combine(ca, o.mfma, st);
   HIPCK(hipGetLastError());
   mark(6);
-  o.have_timing = o.profiling;
 }
 
 void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, const void* data,
@@ -486,7 +497,6 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
-    for (auto& e : o->ev) HIPCK(hipEventCreate(&e));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
     if (o->mfma) {
@@ -606,20 +616,34 @@ int mxm_moe_probs(int64_t h, float* probs) {
 
 int mxm_moe_set_profiling(int64_t h, int enable) {
   OP_OR_RETURN(h);
-  op->profiling = enable != 0;
-  op->have_timing = false;
-  return MXM_OK;
+  return fenced([&] {
+    HIPCK(hipStreamSynchronize(op->stream));
+    op->profiling = enable != 0;
+    op->ev_used = 0;
+    return MXM_OK;
+  });
 }
 
 int mxm_moe_stage_times(int64_t h, float* ms, int n) {
   OP_OR_RETURN(h);
-  return fenced([&] {
-    if (!op->have_timing) fail("OP_MOE_FEED_FORWARD no profiled forward yet");
-    HIPCK(hipEventSynchronize(op->ev[MXM_NUM_STAGES]));
-    for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i)
-      HIPCK(hipEventElapsedTime(&ms[i], op->ev[i], op->ev[i + 1]));
+  int count = 0;
+  const int rc = fenced([&] {
+    if (op->ev_used == 0) fail("OP_MOE_FEED_FORWARD no profiled forward yet");
+    for (int i = 0; i < n; ++i) ms[i] = 0.0f;
+    for (size_t f = 0; f < op->ev_used; ++f) {
+      auto& set = op->ev_sets[f];
+      HIPCK(hipEventSynchronize(set[MXM_NUM_STAGES]));
+      for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i) {
+        float t = 0.0f;
+        HIPCK(hipEventElapsedTime(&t, set[i], set[i + 1]));
+        ms[i] += t;
+      }
+    }
+    for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i) ms[i] /= (float)op->ev_used;
+    count = (int)op->ev_used;
     return MXM_OK;
   });
+  return rc == MXM_OK ? count : rc;
 }
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {

@@ -136,10 +136,14 @@ class MoEFeedForward:
         _lib.check(self._lib.mxm_moe_set_profiling(self.handle, int(enable)), "set_profiling")
 
     def stage_times(self) -> dict:
+        """Mean per-stage milliseconds over the forwards since set_profiling(True)."""
         ms = (ctypes.c_float * _lib.MXM_NUM_STAGES)()
-        _lib.check(self._lib.mxm_moe_stage_times(self.handle, ms, _lib.MXM_NUM_STAGES),
-                   "mxm_moe_stage_times")
-        return {name: float(ms[i]) for i, name in enumerate(_lib.STAGE_NAMES)}
+        count = self._lib.mxm_moe_stage_times(self.handle, ms, _lib.MXM_NUM_STAGES)
+        if count <= 0:
+            _lib.check(count if count < 0 else -1, "mxm_moe_stage_times")
+        out = {name: float(ms[i]) for i, name in enumerate(_lib.STAGE_NAMES)}
+        out["forwards"] = count
+        return out
 
     def info(self) -> dict:
         arr = (ctypes.c_int64 * 4)()

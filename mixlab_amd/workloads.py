@@ -13,6 +13,8 @@ the seed so that top-k loads follow p_e ~ (e+1)^-1.2.
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -73,9 +75,13 @@ CONFIGS = {
 
 
 def round_bf16(a: np.ndarray) -> np.ndarray:
+    """Round finite fp32 values to the nearest bf16 (ties to even), as fp32."""
     a = np.ascontiguousarray(a, dtype=np.float32)
     u = a.view(np.uint32)
-    r = ((u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)
+    r &= np.uint32(0xFFFF0000)
     return r.view(np.float32)
 
 
@@ -83,74 +89,132 @@ def bf16_bits(a: np.ndarray) -> np.ndarray:
     return (round_bf16(a).view(np.uint32) >> 16).astype(np.uint16)
 
 
+def from_bits(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b).astype(np.uint32) << 16).view(np.float32)
+
+
 def quantize_int8(w: np.ndarray):
     """Symmetric per-output-channel int8 of a [in, out] matrix:
     s_j = max_k |w[k, j]| / 127, q = clamp(round(w / s), -127, 127)."""
     amax = np.abs(w).max(axis=0)
-    s = np.where(amax > 0, amax / 127.0, 1.0).astype(np.float32)
+    s = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
     q = np.clip(np.rint(w / s), -127, 127).astype(np.int8)
     return q, s
 
 
 @dataclass
 class Workload:
+    """Seeded inputs of one configuration.  Expert matrices are stored once:
+    as bf16 bit patterns (bf16 configs) or fp32 (fp32 configs), shaped
+    [E, wpe, rows*cols] in the x.W layout of arch/moe.go:126-142."""
+
     cfg: MoEConfig
-    x: np.ndarray            # [N, D] fp32 values (bf16-representable for bf16 configs)
-    router_w: np.ndarray     # [D, E]
-    experts: list            # per expert [w_gate, w_up, w_down] (fp32 values)
-    q8: list = field(default_factory=list)  # per expert [(q, s), ...] for int8 configs
+    x: np.ndarray                   # [N, D] fp32 values (bf16-representable for bf16)
+    router_w: np.ndarray            # [D, E]
+    store: np.ndarray               # [E, wpe, D*F] uint16 bits or fp32
+    q8: list = field(default_factory=list)  # per expert [(q [in,out] int8, s [out] fp32), ...]
     zipf_bias: np.ndarray = None
 
-    def x_bits(self) -> np.ndarray:
-        return bf16_bits(self.x)
+    def shape(self, j: int) -> tuple:
+        D, F = self.cfg.D, self.cfg.F
+        return (F, D) if j == self.cfg.wpe - 1 else (D, F)
+
+    def matrix(self, e: int, j: int) -> np.ndarray:
+        """Expert e's j-th matrix as fp32 values."""
+        m = self.store[e, j]
+        if m.dtype == np.uint16:
+            m = from_bits(m)
+        return m.reshape(self.shape(j))
+
+    def matrix_upload(self, e: int, j: int) -> np.ndarray:
+        """Expert e's j-th matrix in the form uploaded to the device."""
+        return self.store[e, j].reshape(self.shape(j))
+
+    @property
+    def experts(self) -> list:
+        return [[self.matrix(e, j) for j in range(self.cfg.wpe)] for e in range(self.cfg.E)]
+
+    def packed_f32(self) -> np.ndarray:
+        """All expert matrices as one flat fp32 array (the oracle's packing)."""
+        return from_bits(self.store).ravel() if self.store.dtype == np.uint16 else self.store.ravel()
+
+    def x_upload(self) -> np.ndarray:
+        return bf16_bits(self.x) if self.cfg.dtype == "bf16" else self.x
+
+    def router_upload(self) -> np.ndarray:
+        return bf16_bits(self.router_w) if self.cfg.dtype == "bf16" else self.router_w
 
 
-def _zipf_bias(rng, x, wr, cfg: MoEConfig, iters: int = 40) -> np.ndarray:
-    """Per-expert logit bias so that top-k loads follow p_e ~ (e+1)^-s."""
+def _zipf_bias(x, wr, cfg: MoEConfig, iters: int = 200) -> np.ndarray:
+    """Per-expert logit bias so that top-k loads follow p_e ~ (e+1)^-s
+    (damped multiplicative fitting of the realised loads on a token sample)."""
     E, K = cfg.E, cfg.K
     target = (np.arange(1, E + 1, dtype=np.float64)) ** (-cfg.zipf_s)
     target = target / target.sum()
     sample = x[: min(len(x), 16384)].astype(np.float64)
     base = sample[:, :-1] @ wr[:-1].astype(np.float64)
-    b = np.log(target) - np.log(target).mean()
+    b = np.zeros(E)
     for _ in range(iters):
         bb = round_bf16(b.astype(np.float32)).astype(np.float64) if cfg.dtype == "bf16" else b
         logits = base + bb[None, :]
         top = np.argpartition(-logits, K - 1, axis=1)[:, :K]
         load = np.bincount(top.ravel(), minlength=E) / top.size
-        b = b + 0.8 * (np.log(target) - np.log(np.maximum(load, 1e-6)))
+        step = np.clip(np.log(target) - np.log(np.maximum(load, 0.5 / top.size)), -0.5, 0.5)
+        b = b + 0.5 * step
         b -= b.mean()
     return b.astype(np.float32)
 
 
-def make_workload(cfg: MoEConfig, n_tokens: int = None) -> Workload:
-    rng = np.random.default_rng(cfg.seed)
+_X_CHUNK = 4096
+
+
+def make_workload(cfg: MoEConfig, n_tokens: int = None, threads: int = None) -> Workload:
+    """Seeded inputs; independent child streams per expert and per 4096-row
+    block of x (numpy SeedSequence.spawn), generated on a thread pool."""
     N = cfg.N if n_tokens is None else n_tokens
-    D, E, F = cfg.D, cfg.E, cfg.F
-    x = rng.standard_normal((N, D), dtype=np.float32)
-    wr = (rng.standard_normal((D, E), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-    experts = []
-    for _ in range(E):
-        mats = []
-        for j in range(cfg.wpe):
-            shape = (F, D) if j == cfg.wpe - 1 else (D, F)
-            mats.append((rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)))
-        experts.append(mats)
+    D, E, F, wpe = cfg.D, cfg.E, cfg.F, cfg.wpe
+    root = np.random.SeedSequence(cfg.seed)
+    s_x, s_r, s_e = root.spawn(3)
+    x_seeds = s_x.spawn((N + _X_CHUNK - 1) // _X_CHUNK)
+    e_seeds = s_e.spawn(E)
+    threads = threads or min(16, os.cpu_count() or 1)
+    bf16 = cfg.dtype == "bf16"
+
+    x = np.empty((N, D), np.float32)
+
+    def gen_x(i):
+        r0, r1 = i * _X_CHUNK, min(N, (i + 1) * _X_CHUNK)
+        np.random.default_rng(x_seeds[i]).standard_normal(out=x[r0:r1], dtype=np.float32)
+
+    wr = np.random.default_rng(s_r).standard_normal((D, E), dtype=np.float32) * np.float32(0.02)
+    store = np.empty((E, wpe, D * F), np.uint16 if bf16 else np.float32)
+    q8 = [None] * E
+
+    def gen_e(e):
+        rng = np.random.default_rng(e_seeds[e])
+        buf = np.empty(D * F, np.float32)
+        qs = []
+        for j in range(wpe):
+            rng.standard_normal(out=buf, dtype=np.float32)
+            buf *= np.float32(0.02)
+            w = buf
+            if cfg.int8_weights:
+                q, s = quantize_int8(buf.reshape((F, D) if j == wpe - 1 else (D, F)))
+                qs.append((q, s))
+                w = (q.astype(np.float32) * s[None, :]).ravel()
+            store[e, j] = bf16_bits(w) if bf16 else w
+        if cfg.int8_weights:
+            q8[e] = qs
+
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(gen_x, range(len(x_seeds))))
+        list(ex.map(gen_e, range(E)))
     bias = None
     if cfg.zipf_s > 0:
         x[:, D - 1] = 1.0
-        bias = _zipf_bias(rng, x, wr, cfg)
+        bias = _zipf_bias(x, wr, cfg)
         wr[D - 1, :] = bias
-    q8 = []
-    if cfg.int8_weights:
-        deq = []
-        for mats in experts:
-            qs = [quantize_int8(w) for w in mats]
-            q8.append(qs)
-            deq.append([q.astype(np.float32) * s[None, :] for q, s in qs])
-        experts = deq
-    if cfg.dtype == "bf16":
+    if bf16:
         x = round_bf16(x)
         wr = round_bf16(wr)
-        experts = [[round_bf16(w) for w in mats] for mats in experts]
-    return Workload(cfg, x, wr, experts, q8, bias)
+    return Workload(cfg, x, wr, store, q8 if cfg.int8_weights else [], bias)

@@ -78,10 +78,14 @@ def _p(a, ctype=ctypes.c_float):
 def round_bf16(a: np.ndarray) -> np.ndarray:
     """Round fp32 values to the nearest bf16 (ties to even), returned as fp32."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
-    r = np.where(nan, (u.astype(np.uint32) | 0x00400000) & 0xFFFF0000, r).astype(np.uint32)
+    u = a.view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)
+    r &= np.uint32(0xFFFF0000)
+    nan = np.isnan(a)
+    if nan.any():
+        r[nan] = (u[nan] | np.uint32(0x00400000)) & np.uint32(0xFFFF0000)
     return r.view(np.float32)
 
 
@@ -118,7 +122,8 @@ def pack_experts(expert_weights) -> np.ndarray:
 
 def moe_forward(x, router_w, expert_weights, *, top_k: int, expert_type: int = 0,
                 activation: int = 0, leaky_slope: float = 0.0, bf16: bool = False,
-                dense: bool = False, rows=None, want_delta: bool = True) -> dict:
+                dense: bool = False, rows=None, want_delta: bool = True,
+                prerounded: bool = False) -> dict:
     """Run the restatement.  x [N, D]; router_w [D, E]; expert_weights as in
     pack_experts (or already packed).  In the bf16 flow inputs are rounded to
     bf16 here.  Returns delta, aux, entropy, top_idx, gates, probs, logits,
@@ -136,7 +141,7 @@ def moe_forward(x, router_w, expert_weights, *, top_k: int, expert_type: int = 0
     F = packed.size // (E * wpe * D)
     if F * E * wpe * D != packed.size:
         raise ValueError("expert weight sizes do not match D, E and the expert type")
-    if bf16:
+    if bf16 and not prerounded:
         x, router_w, packed = round_bf16(x), round_bf16(router_w), round_bf16(packed)
     K = top_k
     delta = np.zeros((N, D), np.float32) if want_delta else None

@@ -70,3 +70,30 @@ def random_case(seed, N, D, E, F, expert_type=0, wscale=0.02):
         experts.append([rng.standard_normal(((F, D) if j == wpe - 1 else (D, F)), dtype=np.float32)
                         * np.float32(wscale) for j in range(wpe)])
     return x, wr, experts
+
+
+def run_gpu_workload(w, flags=0):
+    """Forward of a generated Workload, uploading its stored bits directly."""
+    from mixlab_amd.op import MoEFeedForward
+
+    cfg = w.cfg
+    with MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype,
+                        flags=flags) as op:
+        op.set_input(1, w.router_upload())
+        idx = 2
+        for e in range(cfg.E):
+            for j in range(cfg.wpe):
+                op.set_input(idx, w.matrix_upload(e, j))
+                idx += 1
+        delta, aux, ent = op.forward_host(w.x_upload())
+        routing = op.routing()
+        info = op.info()
+    return delta, aux, ent, routing, info
+
+
+def run_oracle_workload(w, rows=None):
+    cfg = w.cfg
+    return oracle.moe_forward(w.x, w.router_w, w.packed_f32(), top_k=cfg.K,
+                              expert_type=cfg.expert_type, activation=cfg.activation,
+                              leaky_slope=cfg.leaky_slope, bf16=cfg.dtype == "bf16", rows=rows,
+                              prerounded=True)
