@@ -86,6 +86,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4", help="C1..C4 (C4 is the headline configuration)")
+    ap.add_argument("--flags", type=int, default=0, help="mxm_moe_create flags (include/mixmoe.h)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
     args = ap.parse_args()
@@ -107,7 +108,8 @@ def main() -> int:
     w = make_workload(cfg)
     log(f"workload {cfg.name} generated in {time.time() - t0:.1f}s ({cfg.note})")
 
-    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype)
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype,
+                        flags=args.flags)
     op.set_input(1, w.router_upload())
     idx = 2
     for e in range(cfg.E):

@@ -49,6 +49,7 @@ extern "C" {
 /* mxm_moe_create flags */
 #define MXM_FLAG_FORCE_SIMT 1 /* use the exact-order SIMT expert kernels even where MFMA tiles fit */
 #define MXM_FLAG_DEBUG_PROBS 2 /* keep the router probabilities of the last forward */
+#define MXM_FLAG_MFMA_TILE128 4 /* use the 128x128 MFMA tiles even where 256x256 tiles fit */
 
 /* Stages timed by mxm_moe_stage_times, in launch order. */
 #define MXM_STAGE_ROUTER 0

@@ -20,6 +20,7 @@ MXM_DTYPE_BF16 = 2
 MXM_DTYPE_I8 = 3
 MXM_FLAG_FORCE_SIMT = 1
 MXM_FLAG_DEBUG_PROBS = 2
+MXM_FLAG_MFMA_TILE128 = 4
 MXM_NUM_STAGES = 6
 STAGE_NAMES = ("router", "scan", "scatter", "gemm_up", "gemm_down", "combine")
 

@@ -33,6 +33,7 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-ffp-contract=off",
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]

@@ -78,7 +78,7 @@ struct MoeOp {
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
   float slope = 0.0f;
   int N = 0, wpe = 0, n_inputs = 0;
-  bool bf16 = false, mfma = false, debug_probs = false;
+  bool bf16 = false, mfma = false, debug_probs = false, tile128 = false;
   hipStream_t stream = nullptr;
 
   // weights.  SIMT family: w1 = gate (GLU) or up (MLP) fp32 [E][D][F], w1b =
@@ -89,9 +89,9 @@ struct MoeOp {
 
   // workspace, sized for N at the first forward
   bool ws_ready = false;
-  int ntiles = 0, bm = 0, max_mtiles = 0;
+  int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
-      tile_base, counts, offsets, mstart, aux, ent, H, Y, probs;
+      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs;
   size_t ws_bytes = 0;
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
@@ -140,8 +140,15 @@ int fenced(F&& f) {
 void alloc_workspace(MoeOp& o) {
   const size_t N = (size_t)o.N, K = (size_t)o.K, E = (size_t)o.E, NK = N * K;
   o.ntiles = (int)((N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
-  o.bm = o.mfma ? mxm_mfma_bm() : mxm_simt_bm();
-  o.max_mtiles = (int)((NK + o.bm - 1) / o.bm) + o.E;
+  const bool glu = o.etype != MXM_EXPERT_MLP;
+  if (o.mfma) {
+    o.bm1 = mxm_mfma_tile_rows(glu ? 2 * o.F : o.F, o.D, o.tile128);
+    o.bm2 = mxm_mfma_tile_rows(o.D, o.F, o.tile128);
+  } else {
+    o.bm1 = o.bm2 = mxm_simt_bm();
+  }
+  o.max_mtiles1 = (int)((NK + o.bm1 - 1) / o.bm1) + o.E;
+  o.max_mtiles2 = (int)((NK + o.bm2 - 1) / o.bm2) + o.E;
   const size_t T = (size_t)o.ntiles;
   size_t total = 0;
   auto A = [&](DevBuf& b, size_t bytes) {
@@ -160,7 +167,8 @@ void alloc_workspace(MoeOp& o) {
   A(o.tile_base, E * T * 4);
   A(o.counts, E * 4);
   A(o.offsets, (E + 1) * 4);
-  A(o.mstart, (E + 1) * 4);
+  A(o.mstart1, (E + 1) * 4);
+  A(o.mstart2, (E + 1) * 4);
   A(o.aux, 4);
   A(o.ent, 4);
   const size_t esz = o.mfma ? 2 : 4;
@@ -225,13 +233,13 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   sa.E = o.E;
   sa.K = o.K;
   sa.ntiles = o.ntiles;
-  sa.bm1 = o.bm;
-  sa.bm2 = o.bm;
+  sa.bm1 = o.bm1;
+  sa.bm2 = o.bm2;
   sa.counts = o.counts.as<int32_t>();
   sa.offsets = o.offsets.as<int32_t>();
   sa.tile_base = o.tile_base.as<int32_t>();
-  sa.mstart1 = o.mstart.as<int32_t>();
-  sa.mstart2 = o.mstart.as<int32_t>();
+  sa.mstart1 = o.mstart1.as<int32_t>();
+  sa.mstart2 = o.mstart2.as<int32_t>();
   sa.aux = aux_p;
   sa.entropy = ent_p;
   mxm_launch_scan(sa, o.bf16, st);
@@ -264,7 +272,8 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g1.E = o.E;
   g1.Kd = o.D;
   g1.Ncols = (o.mfma && glu) ? 2 * o.F : o.F;
-  g1.max_mtiles = o.max_mtiles;
+  g1.max_mtiles = o.max_mtiles1;
+  g1.tile128 = o.tile128;
   g1.expert_type = o.etype;
   g1.activation = o.act;
   g1.slope = o.slope;
@@ -285,7 +294,8 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g2.E = o.E;
   g2.Kd = o.F;
   g2.Ncols = o.D;
-  g2.max_mtiles = o.max_mtiles;
+  g2.max_mtiles = o.max_mtiles2;
+  g2.tile128 = o.tile128;
   g2.expert_type = o.etype;
   g2.activation = o.act;
   g2.slope = o.slope;
@@ -495,6 +505,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->bf16 = compute_dtype == MXM_DTYPE_BF16;
     o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && (o->D % 128 == 0) && (o->F % 128 == 0);
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
+    o->tile128 = (flags & MXM_FLAG_MFMA_TILE128) != 0;
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
@@ -648,8 +659,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t vals[4] = {op->mfma ? 1 : 0, (int64_t)op->ws_bytes,
-                           op->mfma ? mxm_mfma_bm() : mxm_simt_bm(),
+  const int64_t vals[4] = {op->mfma ? 1 : 0, (int64_t)op->ws_bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM)};
   int w = 0;
   for (; w < n && w < 4; ++w) info[w] = vals[w];

@@ -73,6 +73,7 @@ struct GemmArgs {
   int expert_type, activation;
   float slope;
   bool y_bf16;            // SIMT down: round y to bf16
+  bool tile128;           // MFMA: force the 128x128 tile family
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
@@ -80,7 +81,9 @@ void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s);
 // MFMA family: bf16 weights stored transposed ([out, in]); GLU gate/up rows
 // interleaved in groups of 32; H and Y are bf16.
 void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s);
-int mxm_mfma_bm();  // row-tile height used by the MFMA kernels
+int mxm_mfma_bm();  // row-tile height of the 128-tile MFMA kernel
+// Row-tile height the MFMA launcher uses for a GEMM with these dimensions.
+int mxm_mfma_tile_rows(int Ncols, int Kd, bool tile128);
 int mxm_simt_bm();
 
 struct CombineArgs {

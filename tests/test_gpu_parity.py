@@ -93,21 +93,23 @@ EXPERTS = [
 
 
 @pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
-@pytest.mark.parametrize("flow", ["fp32", "bf16_mfma", "bf16_simt"])
+@pytest.mark.parametrize("flow", ["fp32", "bf16_mfma", "bf16_mfma128", "bf16_simt"])
 def test_expert_types(gpu_lib, name, etype, act, slope, flow):
     bf16 = flow != "fp32"
     x, wr, experts = random_case(7 + etype * 4 + act, 320, 256, 8, 256, expert_type=etype)
     if bf16:
         x, wr = round_bf16(x), round_bf16(wr)
         experts = [[round_bf16(m) for m in ws] for ws in experts]
-    flags = _lib.MXM_FLAG_FORCE_SIMT if flow == "bf16_simt" else 0
+    flags = {"bf16_simt": _lib.MXM_FLAG_FORCE_SIMT,
+             "bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128}.get(flow, 0)
     delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=320, K=2, expert_type=etype,
                                              activation=act, slope=slope, bf16=bf16, flags=flags)
     want = run_oracle(x, wr, experts, K=2, expert_type=etype, activation=act, slope=slope,
                       bf16=bf16)
-    assert info["mfma"] == (flow == "bf16_mfma")
+    assert info["mfma"] == flow.startswith("bf16_mfma")
+    assert info["gemm_bm"] == {"bf16_mfma": 256, "bf16_mfma128": 128}.get(flow, 64)
     assert_routing_equal(routing, want)
-    if flow == "bf16_mfma":
+    if flow.startswith("bf16_mfma"):
         err = rel_l2(delta, want["delta"])
         print(f"{name} bf16 mfma rel L2 = {err:.3e}")
         assert err <= BF16_TOL
@@ -138,9 +140,10 @@ def test_ties_go_to_lower_expert(gpu_lib):
                     assert row.index(lo) < row.index(hi)
 
 
-@pytest.mark.parametrize("B,T", [(3, 37), (1, 1), (1, 65), (2, 200)])
-def test_ragged_token_counts(gpu_lib, B, T):
-    x, wr, experts = random_case(B * 100 + T, B * T, 128, 6, 128)
+@pytest.mark.parametrize("D,F", [(128, 128), (256, 256)])
+@pytest.mark.parametrize("B,T", [(3, 37), (1, 1), (1, 65), (2, 200), (5, 333)])
+def test_ragged_token_counts(gpu_lib, B, T, D, F):
+    x, wr, experts = random_case(B * 100 + T, B * T, D, 6, F)
     x, wr = round_bf16(x), round_bf16(wr)
     experts = [[round_bf16(m) for m in ws] for ws in experts]
     delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=B, T=T, K=2, bf16=True)
