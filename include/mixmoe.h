@@ -49,7 +49,12 @@ extern "C" {
 /* mxm_moe_create flags */
 #define MXM_FLAG_FORCE_SIMT 1 /* use the exact-order SIMT expert kernels even where MFMA tiles fit */
 #define MXM_FLAG_DEBUG_PROBS 2 /* keep the router probabilities of the last forward */
-#define MXM_FLAG_MFMA_TILE128 4 /* use the 128x128 MFMA tiles even where 256x256 tiles fit */
+/* MFMA tile family (bits 2-3); 0 picks 256x256 where the dimensions allow,
+ * else 128x128 */
+#define MXM_FLAG_MFMA_TILE128 4       /* 128 x 128 x 64 tiles, 4 waves, 2 LDS stages */
+#define MXM_FLAG_MFMA_TILE256x128 8   /* 256 x 128 x 32 tiles, 4 waves, 3 LDS stages */
+#define MXM_FLAG_MFMA_TILE256x256 12  /* 256 x 256 x 64 tiles, 8 waves, 2 LDS stages */
+#define MXM_FLAG_MFMA_TILE_MASK 12
 
 /* Stages timed by mxm_moe_stage_times, in launch order. */
 #define MXM_STAGE_ROUTER 0

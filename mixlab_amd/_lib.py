@@ -21,6 +21,8 @@ MXM_DTYPE_I8 = 3
 MXM_FLAG_FORCE_SIMT = 1
 MXM_FLAG_DEBUG_PROBS = 2
 MXM_FLAG_MFMA_TILE128 = 4
+MXM_FLAG_MFMA_TILE256x128 = 8
+MXM_FLAG_MFMA_TILE256x256 = 12
 MXM_NUM_STAGES = 6
 STAGE_NAMES = ("router", "scan", "scatter", "gemm_up", "gemm_down", "combine")
 

@@ -36,6 +36,7 @@ HIP_FLAGS = [
     "-mllvm", "-disable-promote-alloca-to-lds",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    "-Wno-inline-asm",  # the direct-to-LDS load names M0 in its clobber list
 ]
 
 

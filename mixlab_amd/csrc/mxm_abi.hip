@@ -78,7 +78,8 @@ struct MoeOp {
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
   float slope = 0.0f;
   int N = 0, wpe = 0, n_inputs = 0;
-  bool bf16 = false, mfma = false, debug_probs = false, tile128 = false;
+  bool bf16 = false, mfma = false, debug_probs = false;
+  int family = MXM_TILE_AUTO;
   hipStream_t stream = nullptr;
 
   // weights.  SIMT family: w1 = gate (GLU) or up (MLP) fp32 [E][D][F], w1b =
@@ -142,8 +143,8 @@ void alloc_workspace(MoeOp& o) {
   o.ntiles = (int)((N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
   const bool glu = o.etype != MXM_EXPERT_MLP;
   if (o.mfma) {
-    o.bm1 = mxm_mfma_tile_rows(glu ? 2 * o.F : o.F, o.D, o.tile128);
-    o.bm2 = mxm_mfma_tile_rows(o.D, o.F, o.tile128);
+    o.bm1 = mxm_mfma_tile_rows(glu ? 2 * o.F : o.F, o.D, o.family);
+    o.bm2 = mxm_mfma_tile_rows(o.D, o.F, o.family);
   } else {
     o.bm1 = o.bm2 = mxm_simt_bm();
   }
@@ -273,7 +274,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g1.Kd = o.D;
   g1.Ncols = (o.mfma && glu) ? 2 * o.F : o.F;
   g1.max_mtiles = o.max_mtiles1;
-  g1.tile128 = o.tile128;
+  g1.family = o.family;
   g1.expert_type = o.etype;
   g1.activation = o.act;
   g1.slope = o.slope;
@@ -295,7 +296,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g2.Kd = o.F;
   g2.Ncols = o.D;
   g2.max_mtiles = o.max_mtiles2;
-  g2.tile128 = o.tile128;
+  g2.family = o.family;
   g2.expert_type = o.etype;
   g2.activation = o.act;
   g2.slope = o.slope;
@@ -503,9 +504,14 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->N = o->B * o->T;
     o->n_inputs = n_inputs;
     o->bf16 = compute_dtype == MXM_DTYPE_BF16;
-    o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && (o->D % 128 == 0) && (o->F % 128 == 0);
+    {
+      const int f = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
+      const int n1 = o->etype == MXM_EXPERT_MLP ? o->F : 2 * o->F;
+      o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && mxm_mfma_tile_rows(n1, o->D, f) > 0 &&
+                mxm_mfma_tile_rows(o->D, o->F, f) > 0;
+    }
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
-    o->tile128 = (flags & MXM_FLAG_MFMA_TILE128) != 0;
+    o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;

@@ -36,9 +36,21 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // scalar replacement of the prefetch registers).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 64;            // k per LDS stage
-constexpr int CH = BK / 8;        // 16-byte chunks per tile row
 constexpr int GM = 4;             // row tiles per scheduling group
+
+// Physical 16-byte chunk of logical chunk kc in tile row `row` (CH chunks per
+// row).  ds_read_b128 is serviced 16 lanes (16 consecutive rows, one chunk)
+// at a time over 64 four-byte banks = 16 groups of 16 bytes; rows r and
+// r + 16/CH fall in the same groups, so the CH rows of a phase that share
+// them get distinct chunks.
+template <int CH>
+__device__ __forceinline__ int swz_phys(int row, int kc) {
+  return kc ^ ((row / (16 / CH)) % CH);
+}
+template <int CH>
+__device__ __forceinline__ int swz(int row, int kc) {
+  return row * CH + swz_phys<CH>(row, kc);
+}
 
 __device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mtile) {
   int lo = 0, hi = E - 1;
@@ -52,13 +64,34 @@ __device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mti
   return lo;
 }
 
-// 16-byte chunk kc of tile row `row`, XOR-swizzled by (row & 7).
-__device__ __forceinline__ int swz(int row, int kc) { return row * CH + (kc ^ (row & 7)); }
+// Direct global->LDS load of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's data lands at LDS address `lds` + 16*l.  Issued as inline asm so
+// the compiler does not track it: its conservative tracking of LDS DMA would
+// otherwise drain every in-flight stage before the next LDS read.  The caller
+// waits with explicit vmcnt counts (stage_barrier) before reading.  M0 holds
+// the LDS base; nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(base)
+               : "memory", "m0");
+}
+
+// Wait until at most N of this thread's direct-to-LDS loads are in flight and
+// its LDS reads are done, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
 
 // Tile family: BM x BN workgroup tile, WM x WN waves, each wave
 // (BM/WM) x (BN/WN) = TM x TN MFMA 32x32 tiles.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int WAVES_PER_SIMD, int NSTAGE, int BKK>
 struct Tile {
+  static constexpr int NS = NSTAGE;
+  static constexpr int BK = BKK;      // k per LDS stage
+  static constexpr int CH = BKK / 8;  // 16-byte chunks per tile row
   static constexpr int NT = 64 * WM * WN;
   static constexpr int TM = BM / WM / 32;
   static constexpr int TN = BN / WN / 32;
@@ -67,7 +100,8 @@ struct Tile {
   static constexpr int BUF = A_CH + B_CH;
   static constexpr int LA = A_CH / NT;
   static constexpr int LB = B_CH / NT;
-  static_assert(TN == 2, "GLU epilogue pairs gate and up in a wave's two column tiles");
+  static constexpr int WPS = WAVES_PER_SIMD;
+  static_assert(TN % 2 == 0, "GLU epilogue pairs gate and up column tiles");
   static_assert(A_CH % NT == 0 && B_CH % NT == 0, "whole chunks per thread");
 };
 
@@ -91,11 +125,15 @@ struct Epi {
 };
 
 template <class TL, int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
+__global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(GemmArgs a,
+                                                                            int ngroups) {
   constexpr int MODE = Epi<EPI>::MODE;
-  constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN, LA = TL::LA, LB = TL::LB;
+  constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN;
   constexpr int A_CH = TL::A_CH, BUF = TL::BUF;
-  __shared__ u32x4_t lds[2][BUF];
+  constexpr int NW = NT / 64;
+  constexpr int NS = TL::NS;  // LDS stages in the ring (NS-1 in flight)
+  constexpr int BK = TL::BK, CH = TL::CH;
+  __shared__ u32x4_t lds[NS * BUF];
 
   // XCD-aware grouped schedule (see the file comment).
   const int ntile_n = a.Ncols / BN;
@@ -123,21 +161,60 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
   const uint16_t* __restrict__ B =
       static_cast<const uint16_t*>(a.b0) + (size_t)e * a.Ncols * Kd;
 
-  // Global->LDS assignment: chunk c = tid + NT*i -> tile row c/8, k-chunk c%8.
-  const int kc_ld = tid & (CH - 1);
-  const int r_ld = tid / CH;  // + i * NT/CH
-  size_t aoff[LA];
+  // Global->LDS: global_load_lds_dwordx4 writes lane l's 16 bytes to
+  // LDS base + 16*l, so one wave-load fills 1 KB = 64/CH consecutive tile
+  // rows.  Lane l lands in row (l/CH) of its group at physical chunk l%CH and
+  // fetches the logical k-chunk stored there -- the swizzle is applied on the
+  // global address.
+  constexpr int RPW = 64 / CH;     // tile rows per wave-load
+  constexpr int QA = BM / RPW / NW;  // A wave-loads per wave per stage
+  constexpr int QB = BN / RPW / NW;
+  constexpr int LDPS = QA + QB;      // direct-to-LDS loads per thread per stage
+  static_assert(QA * RPW * NW == BM && QB * RPW * NW == BN, "whole wave-loads");
+  const int lrow = lane / CH;  // row within the wave-load group
+  // Logical chunk of this lane's physical slot (the swizzle is an involution).
+  // It depends on the tile row modulo 16; the row of load i is
+  // (wave + NW*i)*RPW + lrow, which is the same modulo 16 for every i because
+  // NW*RPW is a multiple of 16.
+  static_assert((NW * RPW) % 16 == 0, "swizzle phase is the same for every wave-load of a lane");
+  const int lkc = swz_phys<CH>(wave * RPW + lrow, lane % CH);
+  size_t aoff[QA];
 #pragma unroll
-  for (int i = 0; i < LA; ++i) {
-    const int r = r_ld + i * (NT / CH);
+  for (int i = 0; i < QA; ++i) {
+    const int r = (wave + NW * i) * RPW + lrow;
     const int p = row0 + min(r, rows - 1);  // rows past the segment reload a valid row
     const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
-    aoff[i] = (size_t)src * Kd + kc_ld * 8;
+    aoff[i] = (size_t)src * Kd + lkc * 8;
   }
-  const size_t boff = (size_t)(n0 + r_ld) * Kd + kc_ld * 8;
-  const size_t bstep = (size_t)(NT / CH) * Kd;
+  const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kd + lkc * 8;
+  const size_t bstep = (size_t)(NW * RPW) * Kd;
 
-  u32x4_t ra[LA], rb[LB];
+#define MXM_DMA(STAGE, K0)                                                                    \
+  do {                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < QA; ++i) {                                         \
+      const uint16_t* g_ = A + aoff[i] + (K0);                                                \
+      dma16(g_, STAGE + (wave + NW * i) * 64);                                                \
+    }                                                                                         \
+    _Pragma("unroll") for (int i = 0; i < QB; ++i) {                                         \
+      const uint16_t* g_ = bsrc + i * bstep + (K0);                                           \
+      dma16(g_, STAGE + A_CH + (wave + NW * i) * 64);                                         \
+    }                                                                                         \
+  } while (0)
+  // Stage barrier: this thread's loads of the current stage have landed (at
+  // most AHEAD later stages still in flight), then the workgroup barrier --
+  // the stage is complete for every wave and the stage consumed in the
+  // previous step is free.
+#define MXM_STAGE_BARRIER(AHEAD)              \
+  do {                                        \
+    if ((AHEAD) >= 2)                         \
+      stage_barrier<2 * LDPS>();              \
+    else if ((AHEAD) == 1)                    \
+      stage_barrier<LDPS>();                  \
+    else                                      \
+      stage_barrier<0>();                     \
+  } while (0)
+  static_assert(NS >= 2 && NS <= 4, "stage barrier counts cover up to two stages ahead");
+
   f32x16_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -146,63 +223,69 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // Fragment registers are double-buffered across the 16-wide k steps: the
+  // reads for step ks+1 are issued before the MFMAs of step ks.
+  const int arow = wm * TM * 32 + (lane & 31);
+  const int brow = wn * TN * 32 + (lane & 31);
+  bf16x8_t af[2][TM], bfm[2][TN];
+
+#define MXM_FRAGS(STAGE, P, KS)                                                               \
+  do {                                                                                        \
+    const int kc_ = (KS) * 2 + (lane >> 5);                                                   \
+    _Pragma("unroll") for (int i = 0; i < TM; ++i) af[P][i] =                                 \
+        __builtin_bit_cast(bf16x8_t, STAGE[swz<CH>(arow + i * 32, kc_)]);                         \
+    _Pragma("unroll") for (int j = 0; j < TN; ++j) bfm[P][j] =                                \
+        __builtin_bit_cast(bf16x8_t, STAGE[A_CH + swz<CH>(brow + j * 32, kc_)]);                  \
+  } while (0)
+// Per 16-wide k step: the fragment reads of the next step are interleaved
+// one by one between the MFMAs of this step (sched_group_barrier pins the
+// order: 1 MFMA, 1 LDS read, ...), so LDS latency hides behind MFMAs.
+#define MXM_COMPUTE(STAGE)                                                                    \
+  do {                                                                                        \
+    MXM_FRAGS(STAGE, 0, 0);                                                                   \
+    _Pragma("unroll") for (int ks = 0; ks < BK / 16; ++ks) {                                  \
+      if (ks + 1 < BK / 16) MXM_FRAGS(STAGE, (ks + 1) & 1, ks + 1);                           \
+      _Pragma("unroll") for (int i = 0; i < TM; ++i)                                          \
+          _Pragma("unroll") for (int j = 0; j < TN; ++j) acc[i][j] =                          \
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfm[ks & 1][j],          \
+                                                      acc[i][j], 0, 0, 0);                    \
+      if (ks + 1 < BK / 16) {                                                                 \
+        _Pragma("unroll") for (int q = 0; q < TM * TN; ++q) {                                 \
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  \
+          if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 \
+        }                                                                                     \
+      }                                                                                       \
+    }                                                                                         \
+  } while (0)
+
   const int nk = Kd / BK;
 #pragma unroll
-  for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4_t*>(A + aoff[i]);
-#pragma unroll
-  for (int i = 0; i < LB; ++i) rb[i] = *reinterpret_cast<const u32x4_t*>(B + boff + i * bstep);
-#pragma unroll
-  for (int i = 0; i < LA; ++i) lds[0][swz(r_ld + i * (NT / CH), kc_ld)] = ra[i];
-#pragma unroll
-  for (int i = 0; i < LB; ++i) lds[0][A_CH + swz(r_ld + i * (NT / CH), kc_ld)] = rb[i];
-  __syncthreads();
-
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < nk) MXM_DMA(lds + st * BUF, st * BK);
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int k0 = (kt + 1) * BK;
-#pragma unroll
-      for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4_t*>(A + aoff[i] + k0);
-#pragma unroll
-      for (int i = 0; i < LB; ++i)
-        rb[i] = *reinterpret_cast<const u32x4_t*>(B + boff + i * bstep + k0);
-    }
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int kc = ks * 2 + (lane >> 5);
-      bf16x8_t af[TM], bfm[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = __builtin_bit_cast(bf16x8_t,
-                                   lds[cur][swz(wm * TM * 32 + i * 32 + (lane & 31), kc)]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bfm[j] = __builtin_bit_cast(
-            bf16x8_t, lds[cur][A_CH + swz(wn * TN * 32 + j * 32 + (lane & 31), kc)]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfm[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < LA; ++i) lds[cur ^ 1][swz(r_ld + i * (NT / CH), kc_ld)] = ra[i];
-#pragma unroll
-      for (int i = 0; i < LB; ++i) lds[cur ^ 1][A_CH + swz(r_ld + i * (NT / CH), kc_ld)] = rb[i];
-    }
-    __syncthreads();
+    // stage kt is complete, the stage consumed at kt-1 is free and receives
+    // stage kt+NS-1, then the MFMAs of stage kt
+    MXM_STAGE_BARRIER(min(NS - 2, nk - 1 - kt));
+    if (kt + NS - 1 < nk) MXM_DMA(lds + ((kt + NS - 1) % NS) * BUF, (kt + NS - 1) * BK);
+    const u32x4_t* cur = lds + (kt % NS) * BUF;
+    MXM_COMPUTE(cur);
   }
+  MXM_STAGE_BARRIER(0);  // every wave is done reading before the staging reuse
+#undef MXM_DMA
+#undef MXM_STAGE_BARRIER
+#undef MXM_FRAGS
+#undef MXM_COMPUTE
 
   // ---- epilogue: activation, bf16, per-wave LDS staging, 16-byte stores ----
   // 32x32 accumulator layout: register r of lane l holds
   // C[(r/4)*8 + (l/32)*4 + r%4][l%32].
   constexpr int WROWS = TM * 32;
-  constexpr int C = (MODE == MXM_GEMM_GLU) ? 32 : 64;  // output columns per wave
+  constexpr int C = (MODE == MXM_GEMM_GLU) ? TN * 16 : TN * 32;  // output columns per wave
   constexpr int CPR = C / 8;
-  static_assert(WM * WN * WROWS * 64 * 2 <= (int)sizeof(u32x4_t) * 2 * BUF, "staging fits in LDS");
-  uint16_t* stage = reinterpret_cast<uint16_t*>(&lds[0][0]) + (size_t)wave * WROWS * 64;
+  constexpr int SW = CPR < 8 ? CPR : 8;  // chunk swizzle width
+  // Per-wave staging in the (now idle) stage ring.
+  static_assert(NW * WROWS * C * 2 <= (int)sizeof(u32x4_t) * NS * BUF, "staging fits in LDS");
+  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + (size_t)wave * WROWS * C;
   const int col = lane & 31;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -210,10 +293,14 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
     for (int r = 0; r < 16; ++r) {
       const int row = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
       if (MODE == MXM_GEMM_GLU) {
-        const float gg = mxm_rbf(acc[i][0][r]);
-        const float u = mxm_rbf(acc[i][1][r]);
-        const float h = mxm_hidden<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
-        stage[row * C + (((col >> 3) ^ (row & (CPR - 1))) << 3) + (col & 7)] = mxm_f2bf(h);
+#pragma unroll
+        for (int pj = 0; pj < TN / 2; ++pj) {
+          const float gg = mxm_rbf(acc[i][2 * pj][r]);
+          const float u = mxm_rbf(acc[i][2 * pj + 1][r]);
+          const float h = mxm_hidden<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
+          const int c = pj * 32 + col;
+          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf(h);
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -221,7 +308,7 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
           if (MODE == MXM_GEMM_MLP)
             v = mxm_hidden<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf(v));
           const int c = j * 32 + col;
-          stage[row * C + (((c >> 3) ^ (row & (CPR - 1))) << 3) + (c & 7)] = mxm_f2bf(v);
+          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf(v);
         }
       }
     }
@@ -230,7 +317,7 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int ldo = (MODE == MXM_GEMM_GLU) ? a.Ncols / 2 : a.Ncols;
-  const int c0 = (MODE == MXM_GEMM_GLU) ? n0 / 2 + wn * 32 : n0 + wn * 64;
+  const int c0 = n0 / (MODE == MXM_GEMM_GLU ? 2 : 1) + wn * C;
   uint16_t* __restrict__ out = static_cast<uint16_t*>(a.out);
 #pragma unroll
   for (int it = 0; it < WROWS * CPR / 64; ++it) {
@@ -239,44 +326,44 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmArgs a, int ngroups) {
     const int grow = wm * WROWS + row;
     if (grow < rows) {
       const u32x4_t v =
-          *reinterpret_cast<const u32x4_t*>(stage + row * C + ((cc ^ (row & (CPR - 1))) << 3));
+          *reinterpret_cast<const u32x4_t*>(stage + row * C + ((cc ^ (row & (SW - 1))) << 3));
       *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow) * ldo + c0 + cc * 8) = v;
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK, int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
-  using TL = Tile<BM, BN, WM, WN>;
+  using TL = Tile<BM, BN, WM, WN, WPS, NSTG, BKK>;
   hipLaunchKernelGGL((gemm_kernel<TL, BM, BN, WM, WN, EPI>), dim3(blocks), dim3(TL::NT), 0, s, a,
                      ngroups);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK>
 void launch_family(const GemmArgs& a, hipStream_t s) {
   const int ngroups = (a.max_mtiles + GM - 1) / GM;
   const int per_group = GM * (a.Ncols / BN);
   const int blocks = ((ngroups + 7) / 8) * 8 * per_group;
   if (a.mode == MXM_GEMM_DOWN) {
-    launch_epi<BM, BN, WM, WN, EPI_DOWN>(a, s, blocks, ngroups);
+    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
   } else if (a.mode == MXM_GEMM_GLU) {
     if (a.expert_type == MXM_EXPERT_GEGLU)
-      launch_epi<BM, BN, WM, WN, EPI_GEGLU>(a, s, blocks, ngroups);
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_GEGLU>(a, s, blocks, ngroups);
     else
-      launch_epi<BM, BN, WM, WN, EPI_SWIGLU>(a, s, blocks, ngroups);
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SWIGLU>(a, s, blocks, ngroups);
   } else {
     switch (a.activation) {
       case MXM_ACT_GELU:
-        launch_epi<BM, BN, WM, WN, EPI_MLP_GELU>(a, s, blocks, ngroups);
+        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_GELU>(a, s, blocks, ngroups);
         break;
       case MXM_ACT_RELU:
-        launch_epi<BM, BN, WM, WN, EPI_MLP_RELU>(a, s, blocks, ngroups);
+        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_RELU>(a, s, blocks, ngroups);
         break;
       case MXM_ACT_LEAKY_RELU_SQ:
-        launch_epi<BM, BN, WM, WN, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
+        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
         break;
       default:
-        launch_epi<BM, BN, WM, WN, EPI_MLP_SILU>(a, s, blocks, ngroups);
+        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_SILU>(a, s, blocks, ngroups);
         break;
     }
   }
@@ -284,16 +371,38 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
-int mxm_mfma_bm() { return 128; }
+int mxm_mfma_tile_rows(int Ncols, int Kd, int family) {
+  if (Kd % 64 != 0) return 0;
+  const bool f256 = Ncols % 256 == 0, f128 = Ncols % 128 == 0;
+  switch (family) {
+    case MXM_TILE_256x128:
+      return f128 ? 256 : 0;
+    case MXM_TILE_128x128:
+      return f128 ? 128 : 0;
+    case MXM_TILE_256x256:
+      return f256 ? 256 : 0;
+    default:  // auto: 256 x 256 where it tiles, else 128 x 128
+      return f256 ? 256 : f128 ? 128 : 0;
+  }
+}
 
-int mxm_mfma_tile_rows(int Ncols, int Kd, bool tile128) {
-  return (!tile128 && Ncols % 256 == 0 && Kd % BK == 0) ? 256 : 128;
+// Family chosen for these dimensions (auto resolved).
+static int resolve_family(const GemmArgs& a) {
+  if (a.family != MXM_TILE_AUTO) return a.family;
+  return a.Ncols % 256 == 0 ? MXM_TILE_256x256 : MXM_TILE_128x128;
 }
 
 void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s) {
   if (a.max_mtiles <= 0) return;
-  if (mxm_mfma_tile_rows(a.Ncols, a.Kd, a.tile128) == 256)
-    launch_family<256, 256, 2, 4>(a, s);
-  else
-    launch_family<128, 128, 2, 2>(a, s);
+  switch (resolve_family(a)) {
+    case MXM_TILE_256x128:
+      launch_family<256, 128, 2, 2, 2, 3, 32>(a, s);
+      break;
+    case MXM_TILE_128x128:
+      launch_family<128, 128, 2, 2, 2, 2, 64>(a, s);
+      break;
+    default:
+      launch_family<256, 256, 2, 4, 2, 2, 64>(a, s);
+      break;
+  }
 }

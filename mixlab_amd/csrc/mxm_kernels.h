@@ -73,7 +73,7 @@ struct GemmArgs {
   int expert_type, activation;
   float slope;
   bool y_bf16;            // SIMT down: round y to bf16
-  bool tile128;           // MFMA: force the 128x128 tile family
+  int family;             // MFMA tile family (MXM_TILE_*), MXM_TILE_AUTO picks
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
@@ -81,9 +81,10 @@ void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s);
 // MFMA family: bf16 weights stored transposed ([out, in]); GLU gate/up rows
 // interleaved in groups of 32; H and Y are bf16.
 void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s);
-int mxm_mfma_bm();  // row-tile height of the 128-tile MFMA kernel
-// Row-tile height the MFMA launcher uses for a GEMM with these dimensions.
-int mxm_mfma_tile_rows(int Ncols, int Kd, bool tile128);
+enum { MXM_TILE_AUTO = 0, MXM_TILE_128x128 = 1, MXM_TILE_256x128 = 2, MXM_TILE_256x256 = 3 };
+// Row-tile height the MFMA launcher uses for a GEMM with these dimensions
+// (0: the family does not tile them).
+int mxm_mfma_tile_rows(int Ncols, int Kd, int family);
 int mxm_simt_bm();
 
 struct CombineArgs {

@@ -93,7 +93,8 @@ EXPERTS = [
 
 
 @pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
-@pytest.mark.parametrize("flow", ["fp32", "bf16_mfma", "bf16_mfma128", "bf16_simt"])
+@pytest.mark.parametrize("flow", ["fp32", "bf16_mfma", "bf16_mfma128", "bf16_mfma256x128",
+                                  "bf16_simt"])
 def test_expert_types(gpu_lib, name, etype, act, slope, flow):
     bf16 = flow != "fp32"
     x, wr, experts = random_case(7 + etype * 4 + act, 320, 256, 8, 256, expert_type=etype)
@@ -101,13 +102,15 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
         x, wr = round_bf16(x), round_bf16(wr)
         experts = [[round_bf16(m) for m in ws] for ws in experts]
     flags = {"bf16_simt": _lib.MXM_FLAG_FORCE_SIMT,
-             "bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128}.get(flow, 0)
+             "bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128,
+             "bf16_mfma256x128": _lib.MXM_FLAG_MFMA_TILE256x128}.get(flow, 0)
     delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=320, K=2, expert_type=etype,
                                              activation=act, slope=slope, bf16=bf16, flags=flags)
     want = run_oracle(x, wr, experts, K=2, expert_type=etype, activation=act, slope=slope,
                       bf16=bf16)
     assert info["mfma"] == flow.startswith("bf16_mfma")
-    assert info["gemm_bm"] == {"bf16_mfma": 256, "bf16_mfma128": 128}.get(flow, 64)
+    assert info["gemm_bm"] == {"bf16_mfma": 256, "bf16_mfma128": 128,
+                               "bf16_mfma256x128": 256}.get(flow, 64)
     assert_routing_equal(routing, want)
     if flow.startswith("bf16_mfma"):
         err = rel_l2(delta, want["delta"])
