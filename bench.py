@@ -3,9 +3,10 @@
 
 A step is one forward of the MoE feed-forward op (router, dispatch, grouped
 expert FFN, combine) over the whole batch, with inputs and weights resident
-in HBM.  Default workload: d_model 2048, 64 experts, top-8, gated expert
-hidden 1024, 65,536 tokens, bf16 (the configuration the headline metric is
-quoted on).  Prints one JSON line.
+in HBM.  The headline workload is C4: d_model 2048, 64 experts, top-8, gated
+expert hidden 1024, 65,536 tokens, bf16.  The same run also measures C5, the
+decode shape with int8 expert weights (64 tokens; HBM-bound), and reports it
+under "decode_int8".  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
 """
@@ -30,7 +31,7 @@ def log(msg: str) -> None:
 
 def stage_bytes(cfg) -> dict:
     """Algorithmic HBM bytes per launch of the memory-bound stages."""
-    N, D, E, K, F = cfg.N, cfg.D, cfg.E, cfg.K, cfg.F
+    N, D, E, K = cfg.N, cfg.D, cfg.E, cfg.K
     xb = 2 if cfg.dtype == "bf16" else 4
     NK = N * K
     tiles = (N + 63) // 64
@@ -42,6 +43,15 @@ def stage_bytes(cfg) -> dict:
         # K rows of y per token, gates + idx + pos, delta written fp32
         "combine": NK * D * (2 if cfg.dtype == "bf16" else 4) + NK * 12 + N * D * 4,
     }
+
+
+def int8_weight_bytes(cfg, counts) -> dict:
+    """Expert weight bytes the int8 kernels read: only experts with rows."""
+    routed = int(np.count_nonzero(counts))
+    D, F = cfg.D, cfg.F
+    up = routed * ((2 if cfg.wpe == 3 else 1) * D * F + (2 if cfg.wpe == 3 else 1) * F * 4)
+    down = routed * (F * D + D * 4)
+    return {"routed_experts": routed, "gemm_up": up, "gemm_down": down}
 
 
 def cpu_baseline(w, cfg, target_s: float) -> dict:
@@ -80,6 +90,58 @@ def cpu_baseline(w, cfg, target_s: float) -> dict:
                        f"runs of {med:.2f} s after warm-up")}
 
 
+def run_config(cfg, steps: int, warmup: int, flags: int = 0):
+    """Upload a generated workload, run warm-up + timed forwards.  Returns
+    (workload, result dict)."""
+    from mixlab_amd import _lib
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import make_workload
+
+    t0 = time.time()
+    w = make_workload(cfg)
+    log(f"workload {cfg.name} generated in {time.time() - t0:.1f}s ({cfg.note})")
+    if cfg.int8_weights:
+        flags |= _lib.MXM_FLAG_INT8_WEIGHTS
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype, flags=flags)
+    op.set_input(1, w.router_upload())
+    idx = 2
+    for e in range(cfg.E):
+        for j in range(cfg.wpe):
+            if cfg.int8_weights:
+                op.set_input_q8(idx, *w.q8[e][j])
+            else:
+                op.set_input(idx, w.matrix_upload(e, j))
+            idx += 1
+    xdev = _lib.DeviceBuffer.from_array(w.x_upload())
+    delta = _lib.DeviceBuffer(cfg.N * cfg.D * 4)
+    aux = _lib.DeviceBuffer(4)
+    ent = _lib.DeviceBuffer(4)
+    xcode = _lib.MXM_DTYPE_BF16 if cfg.dtype == "bf16" else _lib.MXM_DTYPE_F32
+    log(f"{cfg.name} weights uploaded; executor {op.info()}")
+
+    def step():
+        op.forward(xdev.value, xcode, cfg.N, delta.value, aux.value, ent.value)
+
+    for _ in range(warmup):
+        step()
+    op.synchronize()
+    op.set_profiling(True)
+    op.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    op.synchronize()
+    elapsed = time.perf_counter() - t0
+    stages = op.stage_times()
+    op.set_profiling(False)
+    counts = op.routing()["counts"]
+    op.close()
+    ms = elapsed * 1e3 / steps
+    log(f"{cfg.name}: {steps} steps, {ms:.4f} ms/step; stages {stages}")
+    return w, {"ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3), "stages": stages,
+               "counts": counts}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,6 +151,7 @@ def main() -> int:
     ap.add_argument("--flags", type=int, default=0, help="mxm_moe_create flags (include/mixmoe.h)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -99,50 +162,12 @@ def main() -> int:
         return 2
 
     from mixlab_amd import _lib
-    from mixlab_amd.op import MoEFeedForward
-    from mixlab_amd.workloads import CONFIGS, make_workload
+    from mixlab_amd.workloads import CONFIGS
 
     cfg = CONFIGS[args.config]
     log(f"device: {_lib.device_name()}")
-    t0 = time.time()
-    w = make_workload(cfg)
-    log(f"workload {cfg.name} generated in {time.time() - t0:.1f}s ({cfg.note})")
-
-    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype,
-                        flags=args.flags)
-    op.set_input(1, w.router_upload())
-    idx = 2
-    for e in range(cfg.E):
-        for j in range(cfg.wpe):
-            op.set_input(idx, w.matrix_upload(e, j))
-            idx += 1
-    xdev = _lib.DeviceBuffer.from_array(w.x_upload())
-    delta = _lib.DeviceBuffer(cfg.N * cfg.D * 4)
-    aux = _lib.DeviceBuffer(4)
-    ent = _lib.DeviceBuffer(4)
-    xcode = _lib.MXM_DTYPE_BF16 if cfg.dtype == "bf16" else _lib.MXM_DTYPE_F32
-    log(f"weights uploaded; executor {op.info()}")
-
-    def step():
-        op.forward(xdev.value, xcode, cfg.N, delta.value, aux.value, ent.value)
-
-    for _ in range(args.warmup):
-        step()
-    op.synchronize()
-    log(f"warmup {args.warmup} done")
-
-    op.set_profiling(True)
-    op.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    op.synchronize()
-    elapsed = time.perf_counter() - t0
-    stages = op.stage_times()
-    op.set_profiling(False)
-    ms_per_step = elapsed * 1e3 / args.steps
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; stages {stages}")
-
+    w, r = run_config(cfg, args.steps, args.warmup, args.flags)
+    stages = r["stages"]
     fl = cfg.flops()
     up_tflops = fl["up"] / (stages["gemm_up"] * 1e-3) / 1e12
     down_tflops = fl["down"] / (stages["gemm_down"] * 1e-3) / 1e12
@@ -156,15 +181,37 @@ def main() -> int:
         log("timing the CPU baseline")
         cpu = cpu_baseline(w, cfg, args.cpu_seconds)
         log(f"cpu baseline {cpu}")
+    del w
+
+    decode = None
+    if not args.no_decode:
+        c5 = CONFIGS["C5"]
+        _, d = run_config(c5, max(args.steps, 50), max(args.warmup, 10))
+        ds = d["stages"]
+        wb = int8_weight_bytes(c5, d["counts"])
+        xb = c5.N * c5.D * 2
+        total = wb["gemm_up"] + wb["gemm_down"] + sum(stage_bytes(c5).values()) + xb
+        up_gbs = (wb["gemm_up"] + xb) / (ds["gemm_up"] * 1e-3) / 1e9
+        decode = {
+            "workload": "C5", "tokens": c5.N, "tokens_per_s": d["tokens_per_s"],
+            "ms_per_step": d["ms_per_step"],
+            "routed_experts": wb["routed_experts"],
+            "hbm_gbs_forward": total / (d["ms_per_step"] * 1e-3) / 1e9,
+            "roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
+                         "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": up_gbs / PEAK_HBM_GBS, "traffic": None},
+            "gemm_down_gbs": (wb["gemm_down"]) / (ds["gemm_down"] * 1e-3) / 1e9,
+            "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
+        }
 
     line = {
         "metric": METRIC,
-        "value": cfg.N / (ms_per_step * 1e-3),
+        "value": r["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -181,10 +228,10 @@ def main() -> int:
                          "up_tflops": up_tflops, "down_tflops": down_tflops},
         "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
         "hbm_gbs": hbm,
+        "decode_int8": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-    op.close()
     return 0
 
 

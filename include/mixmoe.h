@@ -55,6 +55,8 @@ extern "C" {
 #define MXM_FLAG_MFMA_TILE256x128 8   /* 256 x 128 x 32 tiles, 4 waves, 3 LDS stages */
 #define MXM_FLAG_MFMA_TILE256x256 12  /* 256 x 256 x 64 tiles, 8 waves, 2 LDS stages */
 #define MXM_FLAG_MFMA_TILE_MASK 12
+#define MXM_FLAG_INT8_WEIGHTS 16 /* expert weights are int8 + per-output-channel scales
+                                    (mxm_moe_set_input_q8); bf16 compute */
 
 /* Stages timed by mxm_moe_stage_times, in launch order. */
 #define MXM_STAGE_ROUTER 0
@@ -113,6 +115,16 @@ int mxm_moe_destroy(int64_t op);
 int mxm_moe_set_input(int64_t op, int input_index, int dtype, const int64_t* shape, int ndim,
                       const void* data, int on_device);
 
+/* Bind expert weight input `input_index` (2 + e*wpe + j, as for
+ * mxm_moe_set_input) as symmetric int8: q [in, out] in x.W layout and fp32
+ * scales [out], i.e. W = q * scales[None, :] (per output channel).  Only for
+ * ops created with MXM_FLAG_INT8_WEIGHTS.  This has no counterpart in the
+ * reference, whose bridge takes fp32 weights only (gpu/mlx_bridge.cpp:210-217);
+ * it serves decode-shaped serving, where the expert weights are the traffic.
+ * D and ffn must be multiples of 64 and at most 2048. */
+int mxm_moe_set_input_q8(int64_t op, int input_index, const int8_t* q, const float* scales,
+                         const int64_t* shape, int ndim, int on_device);
+
 /* Run the op on x [rows = B*T, D] (dtype MXM_DTYPE_BF16 or MXM_DTYPE_F32;
  * fp32 x is rounded to bf16 first under bf16 compute), writing delta
  * [rows, D] fp32, aux [1] fp32 and entropy [1] fp32.  All pointers are
@@ -151,7 +163,8 @@ int mxm_moe_probs(int64_t op, float* probs);
 int mxm_moe_set_profiling(int64_t op, int enable);
 int mxm_moe_stage_times(int64_t op, float* ms, int n);
 
-/* Executor facts: info[0] = 1 if the MFMA expert kernels are used, info[1] =
+/* Executor facts: info[0] = expert kernel family (0 SIMT, 1 bf16 MFMA, 2 int8
+ * weights), info[1] =
  * workspace bytes, info[2] = row-tile height of the grouped GEMM, info[3] =
  * number of router tiles.  Returns the number of entries written. */
 int mxm_moe_info(int64_t op, int64_t* info, int n);

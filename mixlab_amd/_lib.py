@@ -23,6 +23,7 @@ MXM_FLAG_DEBUG_PROBS = 2
 MXM_FLAG_MFMA_TILE128 = 4
 MXM_FLAG_MFMA_TILE256x128 = 8
 MXM_FLAG_MFMA_TILE256x256 = 12
+MXM_FLAG_INT8_WEIGHTS = 16
 MXM_NUM_STAGES = 6
 STAGE_NAMES = ("router", "scan", "scatter", "gemm_up", "gemm_down", "combine")
 
@@ -46,6 +47,8 @@ SIGNATURES = {
     "mxm_moe_destroy": (ctypes.c_int, [ctypes.c_int64]),
     "mxm_moe_set_input": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int, ctypes.c_int, _I64P,
                                          ctypes.c_int, _VP, ctypes.c_int]),
+    "mxm_moe_set_input_q8": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int, _VP, _VP, _I64P,
+                                            ctypes.c_int, ctypes.c_int]),
     "mxm_moe_forward": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64, _VP,
                                        _VP, _VP]),
     "mxm_moe_forward_host": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64,

@@ -78,7 +78,7 @@ struct MoeOp {
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
   float slope = 0.0f;
   int N = 0, wpe = 0, n_inputs = 0;
-  bool bf16 = false, mfma = false, debug_probs = false;
+  bool bf16 = false, mfma = false, debug_probs = false, q8 = false;
   int family = MXM_TILE_AUTO;
   hipStream_t stream = nullptr;
 
@@ -86,13 +86,16 @@ struct MoeOp {
   // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
   // bf16 [E][2F or F][D] (GLU interleaved), w2 = bf16 [E][D][F].
   DevBuf router, w1, w1b, w2;
+  // int8 family: q1 = gate (GLU) or up (MLP), q1b = up (GLU), q2 = down, in
+  // the 1 KB block layout; s1, s1b, s2 = fp32 per-output-channel scales.
+  DevBuf q1, q1b, q2, s1, s1b, s2;
   std::vector<char> have;
 
   // workspace, sized for N at the first forward
   bool ws_ready = false;
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
-      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs;
+      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits;
   size_t ws_bytes = 0;
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
@@ -142,7 +145,9 @@ void alloc_workspace(MoeOp& o) {
   const size_t N = (size_t)o.N, K = (size_t)o.K, E = (size_t)o.E, NK = N * K;
   o.ntiles = (int)((N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
   const bool glu = o.etype != MXM_EXPERT_MLP;
-  if (o.mfma) {
+  if (o.q8) {
+    o.bm1 = o.bm2 = 256;  // tile schedules are not used by the int8 kernels
+  } else if (o.mfma) {
     o.bm1 = mxm_mfma_tile_rows(glu ? 2 * o.F : o.F, o.D, o.family);
     o.bm2 = mxm_mfma_tile_rows(o.D, o.F, o.family);
   } else {
@@ -172,12 +177,22 @@ void alloc_workspace(MoeOp& o) {
   A(o.mstart2, (E + 1) * 4);
   A(o.aux, 4);
   A(o.ent, 4);
-  const size_t esz = o.mfma ? 2 : 4;
+  const size_t esz = (o.mfma || o.q8) ? 2 : 4;
   A(o.H, NK * (size_t)o.F * esz);
   A(o.Y, NK * (size_t)o.D * esz);
   if (o.debug_probs) A(o.probs, N * E * 4);
+  if (N <= MXM_SMALL_BATCH) A(o.logits, N * E * 4);
   o.ws_bytes = total;
   o.ws_ready = true;
+}
+
+// Refuse to launch a GEMM whose operands are not all allocated (a kernel
+// would otherwise read through a null pointer).
+void require_operands(const GemmArgs& g, bool second_matrix, bool scaled) {
+  if (!g.a || !g.b0 || !g.out || !g.offsets || !g.mstart || (second_matrix && !g.b1) ||
+      (scaled && (!g.scale0 || (second_matrix && !g.scale1))) ||
+      (g.mode != MXM_GEMM_DOWN && !g.perm))
+    fail("OP_MOE_FEED_FORWARD internal error: expert GEMM operand not allocated (mode %d)", g.mode);
 }
 
 void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent) {
@@ -222,6 +237,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   ra.tile_psum = o.tile_psum.as<float>();
   ra.tile_ent = o.tile_ent.as<float>();
   ra.probs_out = o.debug_probs ? o.probs.as<float>() : nullptr;
+  ra.logits_scratch = o.logits.as<float>();
   mxm_launch_router(ra, o.bf16, st);
   HIPCK(hipGetLastError());
 
@@ -278,10 +294,20 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g1.expert_type = o.etype;
   g1.activation = o.act;
   g1.slope = o.slope;
-  if (o.mfma)
+  if (o.q8) {
+    g1.b0 = o.q1.p;
+    g1.b1 = o.q1b.p;
+    g1.scale0 = o.s1.as<float>();
+    g1.scale1 = o.s1b.as<float>();
+    require_operands(g1, glu, true);
+    mxm_launch_gemm_q8(g1, st);
+  } else if (o.mfma) {
+    require_operands(g1, false, false);
     mxm_launch_gemm_mfma(g1, st);
-  else
+  } else {
+    require_operands(g1, glu, false);
     mxm_launch_gemm_simt(g1, o.bf16, st);
+  }
   HIPCK(hipGetLastError());
 
   mark(4);
@@ -301,10 +327,18 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g2.activation = o.act;
   g2.slope = o.slope;
   g2.y_bf16 = o.bf16 && hidden_is_bf16(o.etype, o.act);
-  if (o.mfma)
+  if (o.q8) {
+    g2.b0 = o.q2.p;
+    g2.scale0 = o.s2.as<float>();
+    require_operands(g2, false, true);
+    mxm_launch_gemm_q8(g2, st);
+  } else if (o.mfma) {
+    require_operands(g2, false, false);
     mxm_launch_gemm_mfma(g2, st);
-  else
+  } else {
+    require_operands(g2, false, false);
     mxm_launch_gemm_simt(g2, o.bf16, st);
+  }
   HIPCK(hipGetLastError());
 
   mark(5);
@@ -317,7 +351,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   ca.D = o.D;
   ca.K = o.K;
   ca.delta = delta;
-  mxm_launch_combine(ca, o.mfma, st);
+  mxm_launch_combine(ca, o.mfma || o.q8, st);
   HIPCK(hipGetLastError());
   mark(6);
 }
@@ -326,6 +360,8 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
                 int on_device) {
   if (idx < 1 || idx >= o.n_inputs)
     fail("OP_MOE_FEED_FORWARD input index %d out of range [1,%d)", idx, o.n_inputs);
+  if (o.q8 && idx != 1)
+    fail("OP_MOE_FEED_FORWARD expert weights of an int8 op are bound with mxm_moe_set_input_q8");
   if (dtype != MXM_DTYPE_F32 && dtype != MXM_DTYPE_BF16)
     fail("OP_MOE_FEED_FORWARD weight dtype %d unsupported (want fp32 or bf16)", dtype);
   if (!data) fail("OP_MOE_FEED_FORWARD input w%d has no data", idx - 1);
@@ -392,6 +428,38 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
       mxm_launch_to_f32(src, dtype, dst, (int64_t)n, st);
     }
   }
+  HIPCK(hipGetLastError());
+  HIPCK(hipStreamSynchronize(st));
+  o.have[idx] = 1;
+}
+
+void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, const int64_t* shape,
+                   int ndim, int on_device) {
+  if (!o.q8) fail("OP_MOE_FEED_FORWARD op was not created with MXM_FLAG_INT8_WEIGHTS");
+  if (idx < 2 || idx >= o.n_inputs)
+    fail("OP_MOE_FEED_FORWARD int8 input index %d out of range [2,%d)", idx, o.n_inputs);
+  if (!q || !scales) fail("OP_MOE_FEED_FORWARD int8 input w%d has no data", idx - 1);
+  const int e = (idx - 2) / o.wpe, j = (idx - 2) % o.wpe;
+  const bool down = (j == o.wpe - 1);
+  const int rows = down ? o.F : o.D, cols = down ? o.D : o.F;
+  if (ndim != 2 || shape[0] != rows || shape[1] != cols) {
+    if (o.wpe == 3) fail("OP_MOE_FEED_FORWARD expert GLU weights have invalid shapes");
+    fail("OP_MOE_FEED_FORWARD expert MLP weights have invalid shapes");
+  }
+  const size_t n = (size_t)rows * cols;
+  hipStream_t st = o.stream;
+  DevBuf sq;
+  const int8_t* src = q;
+  if (!on_device) {
+    sq.alloc(n);
+    HIPCK(hipMemcpyAsync(sq.p, q, n, hipMemcpyHostToDevice, st));
+    src = sq.as<int8_t>();
+  }
+  DevBuf* qdst = down ? &o.q2 : (o.wpe == 3 && j == 1) ? &o.q1b : &o.q1;
+  DevBuf* sdst = down ? &o.s2 : (o.wpe == 3 && j == 1) ? &o.s1b : &o.s1;
+  mxm_launch_shuffle_q8(src, rows, cols, qdst->as<uint8_t>() + (size_t)e * n, st);
+  HIPCK(hipMemcpyAsync(sdst->as<float>() + (size_t)e * cols, scales, (size_t)cols * 4,
+                       on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
   HIPCK(hipGetLastError());
   HIPCK(hipStreamSynchronize(st));
   o.have[idx] = 1;
@@ -511,12 +579,27 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
                 mxm_mfma_tile_rows(o->D, o->F, f) > 0;
     }
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
+    o->q8 = (flags & MXM_FLAG_INT8_WEIGHTS) != 0;
+    if (o->q8) {
+      if (!o->bf16) fail("OP_MOE_FEED_FORWARD int8 weights need bf16 compute");
+      if (o->D % 64 || o->F % 64 || o->D > mxm_q8_max_kd() || o->F > mxm_q8_max_kd())
+        fail("OP_MOE_FEED_FORWARD int8 weights need D and ffn multiples of 64 and at most %d",
+             mxm_q8_max_kd());
+      o->mfma = false;
+    }
     o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
-    if (o->mfma) {
+    if (o->q8) {
+      o->q1.alloc(EE * DF);
+      if (o->wpe == 3) o->q1b.alloc(EE * DF);
+      o->q2.alloc(EE * DF);
+      o->s1.alloc(EE * o->F * 4);
+      if (o->wpe == 3) o->s1b.alloc(EE * o->F * 4);
+      o->s2.alloc(EE * o->D * 4);
+    } else if (o->mfma) {
       o->w1.alloc(EE * DF * 2 * (o->wpe == 3 ? 2 : 1));
       o->w2.alloc(EE * DF * 2);
     } else {
@@ -555,6 +638,16 @@ int mxm_moe_set_input(int64_t h, int input_index, int dtype, const int64_t* shap
   return fenced([&] {
     if (!shape && ndim > 0) fail("OP_MOE_FEED_FORWARD shape is NULL");
     set_weight(*op, input_index, dtype, shape, ndim, data, on_device);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_set_input_q8(int64_t h, int input_index, const int8_t* q, const float* scales,
+                         const int64_t* shape, int ndim, int on_device) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!shape && ndim > 0) fail("OP_MOE_FEED_FORWARD shape is NULL");
+    set_weight_q8(*op, input_index, q, scales, shape, ndim, on_device);
     return MXM_OK;
   });
 }
@@ -665,7 +758,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t vals[4] = {op->mfma ? 1 : 0, (int64_t)op->ws_bytes, (int64_t)op->bm1,
+  const int64_t vals[4] = {op->q8 ? 2 : op->mfma ? 1 : 0, (int64_t)op->ws_bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM)};
   int w = 0;
   for (; w < n && w < 4; ++w) info[w] = vals[w];

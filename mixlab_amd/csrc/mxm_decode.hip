@@ -1,0 +1,243 @@
+// Grouped expert FFN for int8 weights (symmetric, fp32 scale per output
+// channel), shaped for decode: few rows per expert, so the kernel is a
+// weight stream and its bound is HBM bandwidth.
+//
+// Weight layout (written at upload by mxm_launch_shuffle_q8): a matrix
+// W[Kd][C] (x.W layout) is cut into blocks of 64 k x 16 output columns; block
+// (cb, kb) occupies 1 KB at ((cb * Kd/64) + kb) * 1024 and holds, at bytes
+// 16*l .. 16*l+15, the 16 values W[64kb + 16*(l/16) + i][16cb + l%16] + 128
+// (offset binary, i.e. the int8 byte with its top bit flipped), i = 0..15.
+// Lane l of a wave therefore reads one contiguous 16-byte piece, a wave-load
+// is one coalesced 1 KB read, and the blocks of one column block are
+// contiguous (Kd/64 KB).
+//
+// MFMA: v_mfma_f32_16x16x32_bf16.  Within a 64-k block, lane group g = l/16
+// owns k = 16g .. 16g+15; the first 8 feed one MFMA, the last 8 a second.
+// The A operand (16 of the expert's rows, bf16) uses the same k assignment,
+// so the sum over k is the plain dot product.  The offset-binary byte u is
+// an integer in [0, 255], which bf16 holds exactly; the +128 offset is
+// removed after the loop with the rows' sums (an MFMA against ones).
+//
+// Work split: a workgroup = NW waves = NW consecutive column blocks of one
+// expert.  The workgroup stages 16 of the expert's rows (all Kd) in LDS; each
+// wave then streams its column block's weights over the whole of Kd through
+// a ring of P register slots (P block-loads per matrix in flight per wave),
+// so there is no split-K reduction and no barrier inside the stream.  More
+// than 16 rows take further passes.  Experts with no rows return at once, so
+// their weights are never read.
+#include "mxm_kernels.h"
+
+#ifndef MXM_Q8_DEPTH_GLU
+#define MXM_Q8_DEPTH_GLU 6
+#endif
+#ifndef MXM_Q8_DEPTH_ONE
+#define MXM_Q8_DEPTH_ONE 8
+#endif
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int NW = 8;          // waves (column blocks) per workgroup
+constexpr int MAX_KD = 2048;   // A staging: 16 rows x Kd bf16 in LDS (64 KB)
+
+// Eight offset-binary bytes (two dwords) -> eight bf16 of their value, exact.
+__device__ __forceinline__ bf16x8_t u8x8_to_bf16(unsigned lo, unsigned hi) {
+  bf16x8_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[i] = (__bf16)(float)((lo >> (8 * i)) & 0xffu);
+    r[4 + i] = (__bf16)(float)((hi >> (8 * i)) & 0xffu);
+  }
+  return r;
+}
+
+__device__ __forceinline__ int clamp_kb(int kb, int kblocks) {
+  return kb < kblocks ? kb : kblocks - 1;
+}
+
+// P: weight blocks in flight per matrix per wave.
+template <int EPI, int P>
+__global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
+  constexpr int MODE = Epi<EPI>::MODE;
+  constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
+  // A rows of the current pass: [kb][half][lane] 16-byte pieces; lane
+  // 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
+  __shared__ u32x4_t ash[MAX_KD / 64 * 2 * 64];
+
+  const int e = blockIdx.x / groups_per_expert;
+  const int grp = blockIdx.x % groups_per_expert;
+  const int row_begin = a.offsets[e];
+  const int count = a.offsets[e + 1] - row_begin;
+  if (count <= 0) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int Kd = a.Kd, NC = a.Ncols;  // NC: output columns per matrix
+  const int kblocks = Kd / 64;
+  const int pieces = Kd / 8;          // 16-byte pieces per row
+  const int cb = grp * NW + wave;
+  const bool active = cb < NC / 16;   // wave-uniform
+  const int g = lane >> 4, m = lane & 15;
+  const int c = cb * 16 + m;
+
+  const uint8_t* W[NMAT];
+  float sc[NMAT];
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt) {
+    const void* base = (mt == 0) ? a.b0 : a.b1;
+    W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd +
+            (size_t)(active ? cb : 0) * kblocks * 1024 + 16 * lane;
+    sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
+  }
+  const uint16_t* X = static_cast<const uint16_t*>(a.a);
+  bf16x8_t ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
+
+  for (int rc = 0; rc < count; rc += 16) {
+    __syncthreads();  // the previous pass has finished reading ash
+    for (int i = tid; i < 16 * pieces; i += NW * 64) {
+      const int r = i / pieces, c8 = i - r * pieces;
+      u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+      if (rc + r < count) {
+        const int p = row_begin + rc + r;
+        const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
+        v = *reinterpret_cast<const u32x4_t*>(X + (size_t)src * Kd + 8 * c8);
+      }
+      ash[((c8 >> 3) * 2 + (c8 & 1)) * 64 + ((c8 >> 1) & 3) * 16 + r] = v;
+    }
+    __syncthreads();
+    if (!active) continue;
+
+    u32x4_t wb[P][NMAT];
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)clamp_kb(s, kblocks) * 1024);
+
+    f32x4_t acc[NMAT], rs = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#define MXM_Q8_STEP(s, kbi)                                                              \
+  {                                                                                      \
+    const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, ash[((kbi) * 2 + 0) * 64 + lane]);  \
+    const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, ash[((kbi) * 2 + 1) * 64 + lane]);  \
+    rs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, rs, 0, 0, 0);                 \
+    rs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, rs, 0, 0, 0);                 \
+    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                \
+      const bf16x8_t b0 = u8x8_to_bf16(wb[s][mt].x, wb[s][mt].y);                        \
+      const bf16x8_t b1 = u8x8_to_bf16(wb[s][mt].z, wb[s][mt].w);                        \
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[mt], 0, 0, 0);       \
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[mt], 0, 0, 0);       \
+    }                                                                                    \
+  }
+
+    int kb = 0;
+    for (; kb + P < kblocks; kb += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        MXM_Q8_STEP(s, kb + s);
+        const int nk = clamp_kb(kb + P + s, kblocks);
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt)
+          wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)nk * 1024);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (kb + s < kblocks) MXM_Q8_STEP(s, kb + s);
+#undef MXM_Q8_STEP
+
+    // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rc + 4 * g + i;
+      if (r >= count) continue;
+      float v[NMAT];
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) v[mt] = (acc[mt][i] - 128.0f * rs[i]) * sc[mt];
+      float out;
+      if (MODE == MXM_GEMM_GLU) {
+        out = mxm_hidden<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf(v[0]),
+                               mxm_rbf(v[NMAT - 1]));
+      } else if (MODE == MXM_GEMM_MLP) {
+        out = mxm_hidden<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf(v[0]));
+      } else {
+        out = v[0];
+      }
+      static_cast<uint16_t*>(a.out)[(size_t)(row_begin + r) * NC + c] = mxm_f2bf(out);
+    }
+  }
+}
+
+template <int EPI, int P>
+void launch_q8(const GemmArgs& a, hipStream_t s) {
+  const int ncb = a.Ncols / 16;
+  const int gpe = (ncb + NW - 1) / NW;
+  hipLaunchKernelGGL((gemm_q8_kernel<EPI, P>), dim3(a.E * gpe), dim3(NW * 64), 0, s, a, gpe);
+}
+
+template <int EPI>
+void launch_epi(const GemmArgs& a, hipStream_t s) {
+  constexpr bool two = Epi<EPI>::MODE == MXM_GEMM_GLU;
+  launch_q8<EPI, two ? MXM_Q8_DEPTH_GLU : MXM_Q8_DEPTH_ONE>(a, s);
+}
+
+// Reorder one int8 matrix src [Kd][C] into the 1 KB block layout.
+__global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
+                                  uint8_t* __restrict__ dst) {
+  const size_t total = (size_t)Kd * C;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+       o += (size_t)gridDim.x * blockDim.x) {
+    const size_t blk = o >> 10;
+    const int within = (int)(o & 1023);
+    const int l = within >> 4, i = within & 15;
+    const int kblocks = Kd / 64;
+    const int cb = (int)(blk / kblocks), kb = (int)(blk % kblocks);
+    const int k = 64 * kb + 16 * (l >> 4) + i;
+    const int c = 16 * cb + (l & 15);
+    dst[o] = (uint8_t)((uint8_t)src[(size_t)k * C + c] ^ 0x80u);
+  }
+}
+
+}  // namespace
+
+int mxm_q8_max_kd() { return MAX_KD; }
+
+void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
+  if (a.mode == MXM_GEMM_DOWN) {
+    launch_epi<EPI_DOWN>(a, s);
+    return;
+  }
+  switch (mxm_epi_kind(a.expert_type, a.activation)) {
+    case EPI_GEGLU:
+      launch_epi<EPI_GEGLU>(a, s);
+      break;
+    case EPI_MLP_SILU:
+      launch_epi<EPI_MLP_SILU>(a, s);
+      break;
+    case EPI_MLP_GELU:
+      launch_epi<EPI_MLP_GELU>(a, s);
+      break;
+    case EPI_MLP_RELU:
+      launch_epi<EPI_MLP_RELU>(a, s);
+      break;
+    case EPI_MLP_LEAKY:
+      launch_epi<EPI_MLP_LEAKY>(a, s);
+      break;
+    default:
+      launch_epi<EPI_SWIGLU>(a, s);
+      break;
+  }
+}
+
+void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s) {
+  const size_t total = (size_t)Kd * C;
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 65536) blocks = 65536;
+  if (blocks > 0) hipLaunchKernelGGL(shuffle_q8_kernel, dim3(blocks), dim3(256), 0, s, src, Kd, C, dst);
+}

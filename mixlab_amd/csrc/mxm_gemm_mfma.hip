@@ -105,25 +105,6 @@ struct Tile {
   static_assert(A_CH % NT == 0 && B_CH % NT == 0, "whole chunks per thread");
 };
 
-// Epilogue kinds: the hidden activation (expert type x activation) of the up
-// projections, or the plain bf16 store of the down projection.
-enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN };
-
-template <int EPI>
-struct Epi {
-  static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
-                              : EPI == EPI_DOWN ? MXM_GEMM_DOWN
-                                                : MXM_GEMM_MLP;
-  static constexpr int ETYPE = EPI == EPI_SWIGLU ? MXM_EXPERT_SWIGLU
-                               : EPI == EPI_GEGLU ? MXM_EXPERT_GEGLU
-                                                  : MXM_EXPERT_MLP;
-  static constexpr int ACT = EPI == EPI_MLP_GELU    ? MXM_ACT_GELU
-                             : EPI == EPI_MLP_RELU  ? MXM_ACT_RELU
-                             : EPI == EPI_MLP_LEAKY ? MXM_ACT_LEAKY_RELU_SQ
-                             : EPI == EPI_GEGLU     ? MXM_ACT_GELU
-                                                    : MXM_ACT_SILU;
-};
-
 template <class TL, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(GemmArgs a,
                                                                             int ngroups) {
@@ -346,26 +327,27 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
   const int blocks = ((ngroups + 7) / 8) * 8 * per_group;
   if (a.mode == MXM_GEMM_DOWN) {
     launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
-  } else if (a.mode == MXM_GEMM_GLU) {
-    if (a.expert_type == MXM_EXPERT_GEGLU)
+    return;
+  }
+  switch (mxm_epi_kind(a.expert_type, a.activation)) {
+    case EPI_GEGLU:
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_GEGLU>(a, s, blocks, ngroups);
-    else
+      break;
+    case EPI_MLP_SILU:
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_SILU>(a, s, blocks, ngroups);
+      break;
+    case EPI_MLP_GELU:
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_GELU>(a, s, blocks, ngroups);
+      break;
+    case EPI_MLP_RELU:
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_RELU>(a, s, blocks, ngroups);
+      break;
+    case EPI_MLP_LEAKY:
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
+      break;
+    default:
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SWIGLU>(a, s, blocks, ngroups);
-  } else {
-    switch (a.activation) {
-      case MXM_ACT_GELU:
-        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_GELU>(a, s, blocks, ngroups);
-        break;
-      case MXM_ACT_RELU:
-        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_RELU>(a, s, blocks, ngroups);
-        break;
-      case MXM_ACT_LEAKY_RELU_SQ:
-        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
-        break;
-      default:
-        launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_SILU>(a, s, blocks, ngroups);
-        break;
-    }
+      break;
   }
 }
 

@@ -13,6 +13,41 @@
 // Largest expert count the router supports (4 experts per lane).
 #define MXM_MAX_EXPERTS 256
 
+// Value of v held by lane (lane ^ s) of the wave, s in {1, 2, 4, 8, 16, 32}
+// (a compile-time constant after unrolling).  Cross-lane moves on the VALU:
+// DPP quad permutes (1, 2), row shifts under bank masks (4), a row rotate
+// (8), and gfx950's permlane16/permlane32 swaps (16, 32) -- no LDS round
+// trip, unlike ds_bpermute.  Every lane of the wave must be active.
+__device__ __forceinline__ uint32_t mxm_xor_lane(uint32_t v, int s) {
+  const int lane = threadIdx.x & 63;
+  switch (s) {
+    case 1:
+      return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    case 2:
+      return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    case 4: {
+      const uint32_t r = __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xf, 0x5, false);  // row_shl:4
+      return __builtin_amdgcn_update_dpp(r, v, 0x114, 0xf, 0xa, false);              // row_shr:4
+    }
+    case 8:
+      return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
+  }
+}
+__device__ __forceinline__ float mxm_xor_lane_f(float v, int s) {
+  return __builtin_bit_cast(float, mxm_xor_lane(__builtin_bit_cast(uint32_t, v), s));
+}
+__device__ __forceinline__ int mxm_xor_lane_i(int v, int s) {
+  return (int)mxm_xor_lane((uint32_t)v, s);
+}
+
 struct RouterArgs {
   const void* x;   // [N, D], bf16 bits or fp32
   const void* wr;  // [D, E], same dtype
@@ -24,7 +59,10 @@ struct RouterArgs {
   float* tile_psum;      // [E, ntiles] sum of probabilities over the tile
   float* tile_ent;       // [ntiles] sum over the tile of sum_e p log max(p, 1e-12)
   float* probs_out;      // optional [N, E]
+  float* logits_scratch; // [N, E]: when set, logits come from the small-batch kernel
 };
+// Batches up to this many tokens take the small-batch logits kernel.
+#define MXM_SMALL_BATCH 1024
 void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s);
 
 struct ScanArgs {
@@ -87,6 +125,41 @@ enum { MXM_TILE_AUTO = 0, MXM_TILE_128x128 = 1, MXM_TILE_256x128 = 2, MXM_TILE_2
 int mxm_mfma_tile_rows(int Ncols, int Kd, int family);
 int mxm_simt_bm();
 
+// Epilogue kinds: the hidden activation (expert type x activation) of the up
+// projections, or the plain bf16 store of the down projection.
+enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN };
+
+template <int EPI>
+struct Epi {
+  static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
+                              : EPI == EPI_DOWN ? MXM_GEMM_DOWN
+                                                : MXM_GEMM_MLP;
+  static constexpr int ETYPE = EPI == EPI_SWIGLU ? MXM_EXPERT_SWIGLU
+                               : EPI == EPI_GEGLU ? MXM_EXPERT_GEGLU
+                                                  : MXM_EXPERT_MLP;
+  static constexpr int ACT = EPI == EPI_MLP_GELU    ? MXM_ACT_GELU
+                             : EPI == EPI_MLP_RELU  ? MXM_ACT_RELU
+                             : EPI == EPI_MLP_LEAKY ? MXM_ACT_LEAKY_RELU_SQ
+                             : EPI == EPI_GEGLU     ? MXM_ACT_GELU
+                                                    : MXM_ACT_SILU;
+};
+
+// Epilogue kind of the up-projection GEMM for an (expert type, activation).
+inline int mxm_epi_kind(int expert_type, int activation) {
+  if (expert_type == MXM_EXPERT_SWIGLU) return EPI_SWIGLU;
+  if (expert_type == MXM_EXPERT_GEGLU) return EPI_GEGLU;
+  switch (activation) {
+    case MXM_ACT_GELU:
+      return EPI_MLP_GELU;
+    case MXM_ACT_RELU:
+      return EPI_MLP_RELU;
+    case MXM_ACT_LEAKY_RELU_SQ:
+      return EPI_MLP_LEAKY;
+    default:
+      return EPI_MLP_SILU;
+  }
+}
+
 struct CombineArgs {
   const void* y;          // [N*K, D], fp32 or bf16
   const int32_t* top_idx; // [N, K]
@@ -105,3 +178,11 @@ void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n
 // interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up.
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
                                uint16_t* dst, hipStream_t s);
+
+// int8-weight family (decode shapes): weights in the 1 KB block layout of
+// mxm_launch_shuffle_q8, fp32 scale per output channel (scale0/scale1),
+// H and Y bf16.  Reduction length Kd must be a multiple of 64 and at most
+// mxm_q8_max_kd(); output columns a multiple of 16.
+void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s);
+void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s);
+int mxm_q8_max_kd();

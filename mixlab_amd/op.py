@@ -76,6 +76,16 @@ class MoEFeedForward:
                                              a.ndim, ctypes.c_void_p(a.ctypes.data), 0)
         _lib.check(rc, f"mxm_moe_set_input({input_index})")
 
+    def set_input_q8(self, input_index: int, q: np.ndarray, scales: np.ndarray) -> None:
+        """Bind an expert matrix as int8 q [in, out] with fp32 per-output-channel
+        scales [out] (W = q * scales); the op must use MXM_FLAG_INT8_WEIGHTS."""
+        q = np.ascontiguousarray(q, dtype=np.int8)
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        shp = (ctypes.c_int64 * 2)(*q.shape)
+        rc = self._lib.mxm_moe_set_input_q8(self.handle, input_index, ctypes.c_void_p(q.ctypes.data),
+                                            ctypes.c_void_p(sc.ctypes.data), shp, 2, 0)
+        _lib.check(rc, f"mxm_moe_set_input_q8({input_index})")
+
     def set_weights(self, router_w, expert_weights) -> None:
         """router_w [D, E]; expert_weights: per expert (w_gate, w_up, w_down) or (w_up, w_down)."""
         self.set_input(1, router_w)
@@ -148,8 +158,8 @@ class MoEFeedForward:
     def info(self) -> dict:
         arr = (ctypes.c_int64 * 4)()
         self._lib.mxm_moe_info(self.handle, arr, 4)
-        return dict(mfma=bool(arr[0]), workspace_bytes=int(arr[1]), gemm_bm=int(arr[2]),
-                    router_tiles=int(arr[3]))
+        return dict(mfma=arr[0] == 1, int8=arr[0] == 2, workspace_bytes=int(arr[1]),
+                    gemm_bm=int(arr[2]), router_tiles=int(arr[3]))
 
     def close(self) -> None:
         if getattr(self, "handle", 0):

@@ -73,17 +73,24 @@ def random_case(seed, N, D, E, F, expert_type=0, wscale=0.02):
 
 
 def run_gpu_workload(w, flags=0):
-    """Forward of a generated Workload, uploading its stored bits directly."""
+    """Forward of a generated Workload, uploading its stored bits directly
+    (int8 configurations upload q and the per-output-channel scales)."""
     from mixlab_amd.op import MoEFeedForward
 
     cfg = w.cfg
+    if cfg.int8_weights:
+        flags |= _lib.MXM_FLAG_INT8_WEIGHTS
     with MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype,
                         flags=flags) as op:
         op.set_input(1, w.router_upload())
         idx = 2
         for e in range(cfg.E):
             for j in range(cfg.wpe):
-                op.set_input(idx, w.matrix_upload(e, j))
+                if cfg.int8_weights:
+                    q, sc = w.q8[e][j]
+                    op.set_input_q8(idx, q, sc)
+                else:
+                    op.set_input(idx, w.matrix_upload(e, j))
                 idx += 1
         delta, aux, ent = op.forward_host(w.x_upload())
         routing = op.routing()

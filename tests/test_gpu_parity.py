@@ -200,3 +200,53 @@ def test_c3_zipf_full(gpu_lib):
 
 def test_c4_full(gpu_lib):
     _check_large("C4")
+
+
+def test_c5_int8_decode(gpu_lib):
+    """int8 weights with fp32 per-output-channel scales; the restatement is fed
+    the dequantised weights bf16(q * s), as the benchmark plan prescribes."""
+    cfg = CONFIGS["C5"]
+    w = make_workload(cfg)
+    delta, aux, ent, routing, info = run_gpu_workload(w)
+    want = run_oracle_workload(w)
+    assert info["int8"]
+    assert_routing_equal(routing, want)
+    err = rel_l2(delta, want["delta"])
+    print(f"C5 int8 delta rel L2 = {err:.3e}; max count = {routing['counts'].max()}")
+    assert err <= BF16_TOL
+
+
+@pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
+def test_int8_expert_types(gpu_lib, name, etype, act, slope):
+    """All expert kinds through the int8 kernels, with experts far above 16
+    rows (several row passes) and some with none."""
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import bf16_bits, quantize_int8
+
+    rng = np.random.default_rng(100 + etype * 4 + act)
+    N, D, E, K, F = 300, 256, 6, 2, 192
+    wpe = 2 if etype == 2 else 3
+    x = round_bf16(rng.standard_normal((N, D), dtype=np.float32))
+    wr = round_bf16(rng.standard_normal((D, E), dtype=np.float32) * np.float32(0.08))
+    # expert 5 is never chosen: a constant feature with a large negative weight
+    x[:, 0] = 4.0
+    wr[:, 5] = 0.0
+    wr[0, 5] = -8.0
+    q8 = [[quantize_int8(rng.standard_normal(((F, D) if j == wpe - 1 else (D, F)),
+                                             dtype=np.float32) * np.float32(0.02))
+           for j in range(wpe)] for _ in range(E)]
+    deq = [[round_bf16(q.astype(np.float32) * s[None, :]) for q, s in ws] for ws in q8]
+    ip = [1, N, D, E, K, etype, F, act]
+    with MoEFeedForward(ip, [slope], compute_dtype="bf16", flags=_lib.MXM_FLAG_INT8_WEIGHTS) as op:
+        op.set_input(1, bf16_bits(wr))
+        for e in range(E):
+            for j in range(wpe):
+                op.set_input_q8(2 + e * wpe + j, *q8[e][j])
+        delta, aux, ent = op.forward_host(bf16_bits(x))
+        routing = op.routing()
+    want = run_oracle(x, wr, deq, K=K, expert_type=etype, activation=act, slope=slope, bf16=True)
+    assert_routing_equal(routing, want)
+    assert routing["counts"][5] == 0 and routing["counts"].max() > 48
+    err = rel_l2(delta, want["delta"])
+    print(f"int8 {name} rel L2 = {err:.3e}")
+    assert err <= BF16_TOL
