@@ -54,6 +54,19 @@ def int8_weight_bytes(cfg, counts) -> dict:
     return {"routed_experts": routed, "gemm_up": up, "gemm_down": down}
 
 
+def measured_traffic(workload: str, stage: str, flags: int):
+    """HBM bytes per launch of a stage's kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/roofline_traffic.json); None
+    when absent or when non-default flags select another kernel."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "roofline_traffic.json")
+    if flags or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get(workload, {}).get(stage)
+    return None if entry is None else int(entry["fetch_bytes"] + entry["write_bytes"])
+
+
 def cpu_baseline(w, cfg, target_s: float) -> dict:
     """Time the dense fp32 BLAS restatement of the reference algorithm on a
     bounded prefix of the same tokens (oracle/dense_blas.py)."""
@@ -142,6 +155,21 @@ def run_config(cfg, steps: int, warmup: int, flags: int = 0):
                "counts": counts}
 
 
+def copy_calibration(mib: int, reps: int = 5) -> int:
+    """Copies of a known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this
+    run gives the counter-to-bytes factors used for roofline.traffic."""
+    from mixlab_amd import _lib
+
+    n = mib << 20
+    src, dst = _lib.DeviceBuffer(n), _lib.DeviceBuffer(n)
+    lib = _lib.init()
+    for _ in range(reps):
+        _lib.check(lib.mxm_memcpy_d2d(dst.ptr, src.ptr, n), "mxm_memcpy_d2d")
+    _lib.check(lib.mxm_device_synchronize(), "sync")
+    print(json.dumps({"copy_bytes": n, "reps": reps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,7 +180,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -199,7 +232,8 @@ def main() -> int:
             "hbm_gbs_forward": total / (d["ms_per_step"] * 1e-3) / 1e9,
             "roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
                          "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": up_gbs / PEAK_HBM_GBS, "traffic": None},
+                         "frac": up_gbs / PEAK_HBM_GBS,
+                         "traffic": measured_traffic("C5", "gemm_up", 0)},
             "gemm_down_gbs": (wb["gemm_down"]) / (ds["gemm_down"] * 1e-3) / 1e9,
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
@@ -223,7 +257,8 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "gemm_up (gate+up grouped GEMM, GLU epilogue)",
                      "achieved": up_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": up_tflops / PEAK_BF16_TFLOPS, "traffic": None},
+                     "frac": up_tflops / PEAK_BF16_TFLOPS,
+                     "traffic": measured_traffic(cfg.name, "gemm_up", args.flags)},
         "grouped_gemm": {"ms": gg_ms, "tflops": gg_tflops, "frac": gg_tflops / PEAK_BF16_TFLOPS,
                          "up_tflops": up_tflops, "down_tflops": down_tflops},
         "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
