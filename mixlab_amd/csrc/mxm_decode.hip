@@ -162,14 +162,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       for (int mt = 0; mt < NMAT; ++mt) v[mt] = (acc[mt][i] - 128.0f * rs[i]) * sc[mt];
       float out;
       if (MODE == MXM_GEMM_GLU) {
-        out = mxm_hidden<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf(v[0]),
-                               mxm_rbf(v[NMAT - 1]));
+        out = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(v[0]),
+                               mxm_rbf_fast(v[NMAT - 1]));
       } else if (MODE == MXM_GEMM_MLP) {
-        out = mxm_hidden<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf(v[0]));
+        out = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf_fast(v[0]));
       } else {
         out = v[0];
       }
-      static_cast<uint16_t*>(a.out)[(size_t)(row_begin + r) * NC + c] = mxm_f2bf(out);
+      static_cast<uint16_t*>(a.out)[(size_t)(row_begin + r) * NC + c] = mxm_f2bf_fast(out);
     }
   }
 }

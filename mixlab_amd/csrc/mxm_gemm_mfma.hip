@@ -5,16 +5,24 @@
 // x through `perm` (each row is D contiguous bf16), for the down projection
 // they are the contiguous rows of H.  B is the expert's weight stored
 // transposed ([out, in], k contiguous) so both operands stream k-contiguous
-// 16-byte chunks.  Tiles are staged through LDS, double-buffered with
-// register prefetch, with the 16-byte chunk index XOR-swizzled by (row & 7)
-// so the 8-lane phases of ds_read_b128 hit distinct banks.
+// 16-byte chunks.
 //
-// Two tile families share one template: 256 x 256 (8 waves as 2 x 4, each
-// wave 128 x 64 = 4 x 2 MFMA tiles) where the dimensions allow, else
-// 128 x 128 (4 waves as 2 x 2, each 64 x 64).  The GLU weight rows are
-// interleaved in groups of 32 (gate cols f..f+31, then up cols f..f+31), so a
-// wave's two column MFMA tiles hold gate and up for the same 32 hidden units
-// and the activation is applied straight from the accumulators.
+// Operand tiles move global -> LDS with global_load_lds_dwordx4 (no VGPR
+// round trip) into a ring of NS stages of BK k each; each lane's 16-byte
+// chunk lands at a swizzled position so the 16-lane phases of ds_read_b128
+// hit distinct banks.  Waves wait for their own loads with explicit vmcnt
+// counts and meet at s_barrier; the loads of the next stage are spread over
+// the first k steps of the current one so the vector memory path fills in
+// the background.  With three or more stages the barrier of stage kt+1 is
+// taken before the last k step of stage kt, so it overlaps MFMA work.
+//
+// Tile families (flags select; the default is 256 x 256 where the columns
+// allow): 256 x 256 x 64 (8 waves as 2 x 4, each 128 x 64 = 4 x 2 MFMA tiles,
+// 2 stages), 256 x 128 x 32 (4 waves, 3 stages, 2 workgroups per CU) and
+// 128 x 128 x 64 (4 waves, 2 stages).  The GLU weight rows are interleaved in
+// groups of 32 (gate cols f..f+31, then up cols f..f+31), so a wave's two
+// column MFMA tiles hold gate and up for the same 32 hidden units and the
+// activation is applied straight from the accumulators.
 //
 // Ragged experts: the scan kernel writes `mstart`, the prefix over experts of
 // ceil(count/BM) row tiles, so tile -> (expert, rows) is resolved on device
@@ -24,8 +32,9 @@
 // grouped GM at a time with the column tiles of a group adjacent, and group g
 // is placed on XCD g % 8, so each XCD's L2 sees a GM x (N/BN) block of tiles
 // sharing A rows and B columns, and the empty tail tiles are spread over all
-// XCDs.  The epilogue stages each wave's bf16 tile through LDS
-// (chunk-swizzled) and writes 16-byte row segments.
+// XCDs.  The epilogue applies the activation (hardware exp2 / rcp and bf16
+// conversion), stages each wave's bf16 tile through LDS (chunk-swizzled) and
+// writes 16-byte row segments.
 #include "mxm_kernels.h"
 
 namespace {
@@ -36,7 +45,14 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // scalar replacement of the prefetch registers).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int GM = 4;             // row tiles per scheduling group
+#ifndef MXM_DMA_STEPS
+#define MXM_DMA_STEPS 2
+#endif
+
+#ifndef MXM_GM
+#define MXM_GM 4
+#endif
+constexpr int GM = MXM_GM;        // row tiles per scheduling group
 
 // Physical 16-byte chunk of logical chunk kc in tile row `row` (CH chunks per
 // row).  ds_read_b128 is serviced 16 lanes (16 consecutive rows, one chunk)
@@ -170,31 +186,36 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kd + lkc * 8;
   const size_t bstep = (size_t)(NW * RPW) * Kd;
 
-#define MXM_DMA(STAGE, K0)                                                                    \
+// Direct-to-LDS loads Q0 .. Q1-1 of one stage (load q < QA fills A rows,
+// the rest B rows).
+#define MXM_DMA_PART(STAGE, K0, Q0, Q1)                                                       \
   do {                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < QA; ++i) {                                         \
-      const uint16_t* g_ = A + aoff[i] + (K0);                                                \
-      dma16(g_, STAGE + (wave + NW * i) * 64);                                                \
-    }                                                                                         \
-    _Pragma("unroll") for (int i = 0; i < QB; ++i) {                                         \
-      const uint16_t* g_ = bsrc + i * bstep + (K0);                                           \
-      dma16(g_, STAGE + A_CH + (wave + NW * i) * 64);                                         \
+    _Pragma("unroll") for (int q_ = (Q0); q_ < (Q1); ++q_) {                                  \
+      if (q_ < QA) {                                                                          \
+        dma16(A + aoff[q_] + (K0), STAGE + (wave + NW * q_) * 64);                            \
+      } else {                                                                                \
+        dma16(bsrc + (q_ - QA) * bstep + (K0), STAGE + A_CH + (wave + NW * (q_ - QA)) * 64); \
+      }                                                                                       \
     }                                                                                         \
   } while (0)
+#define MXM_DMA(STAGE, K0) MXM_DMA_PART(STAGE, K0, 0, LDPS)
   // Stage barrier: this thread's loads of the current stage have landed (at
   // most AHEAD later stages still in flight), then the workgroup barrier --
   // the stage is complete for every wave and the stage consumed in the
   // previous step is free.
 #define MXM_STAGE_BARRIER(AHEAD)              \
   do {                                        \
-    if ((AHEAD) >= 2)                         \
+    if ((AHEAD) >= 3)                         \
+      stage_barrier<3 * LDPS>();              \
+    else if ((AHEAD) == 2)                    \
       stage_barrier<2 * LDPS>();              \
     else if ((AHEAD) == 1)                    \
       stage_barrier<LDPS>();                  \
     else                                      \
       stage_barrier<0>();                     \
   } while (0)
-  static_assert(NS >= 2 && NS <= 4, "stage barrier counts cover up to two stages ahead");
+  static_assert(NS >= 2 && NS <= 5, "stage barrier counts cover up to three stages ahead");
+  static_assert(3 * LDPS <= 63, "vmcnt holds at most 63 outstanding loads");
 
   f32x16_t acc[TM][TN];
 #pragma unroll
@@ -214,14 +235,17 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   do {                                                                                        \
     const int kc_ = (KS) * 2 + (lane >> 5);                                                   \
     _Pragma("unroll") for (int i = 0; i < TM; ++i) af[P][i] =                                 \
-        __builtin_bit_cast(bf16x8_t, STAGE[swz<CH>(arow + i * 32, kc_)]);                         \
+        __builtin_bit_cast(bf16x8_t, (STAGE)[swz<CH>(arow + i * 32, kc_)]);                       \
     _Pragma("unroll") for (int j = 0; j < TN; ++j) bfm[P][j] =                                \
-        __builtin_bit_cast(bf16x8_t, STAGE[A_CH + swz<CH>(brow + j * 32, kc_)]);                  \
+        __builtin_bit_cast(bf16x8_t, (STAGE)[A_CH + swz<CH>(brow + j * 32, kc_)]);                \
   } while (0)
 // Per 16-wide k step: the fragment reads of the next step are interleaved
 // one by one between the MFMAs of this step (sched_group_barrier pins the
-// order: 1 MFMA, 1 LDS read, ...), so LDS latency hides behind MFMAs.
-#define MXM_COMPUTE(STAGE)                                                                    \
+// order: 1 MFMA, 1 LDS read, ...), so LDS latency hides behind MFMAs.  After
+// each step, a share of the direct-to-LDS loads of stage DSTAGE (k offset
+// DK0) is issued, so the vector memory path fills in the background instead
+// of stalling every wave right after the stage barrier.
+#define MXM_COMPUTE(STAGE, DO_DMA, DSTAGE, DK0)                                               \
   do {                                                                                        \
     MXM_FRAGS(STAGE, 0, 0);                                                                   \
     _Pragma("unroll") for (int ks = 0; ks < BK / 16; ++ks) {                                  \
@@ -236,26 +260,76 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
           if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 \
         }                                                                                     \
       }                                                                                       \
+      if (DO_DMA && ks < DSTEPS)                                                              \
+        MXM_DMA_PART(DSTAGE, DK0, ks * LDPS / DSTEPS, (ks + 1) * LDPS / DSTEPS);              \
     }                                                                                         \
   } while (0)
 
+// One 16-wide k step on fragment set P; if DOFRAG, the fragments of k step
+// FKS of stage FSTAGE are read into set P^1 in between the MFMAs.
+#define MXM_KSTEP(P, FSTAGE, FKS, DOFRAG)                                                     \
+  do {                                                                                        \
+    if (DOFRAG) MXM_FRAGS(FSTAGE, (P) ^ 1, FKS);                                              \
+    _Pragma("unroll") for (int i = 0; i < TM; ++i)                                            \
+        _Pragma("unroll") for (int j = 0; j < TN; ++j) acc[i][j] =                            \
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[P][i], bfm[P][j], acc[i][j], 0, 0, 0); \
+    if (DOFRAG) {                                                                             \
+      _Pragma("unroll") for (int q = 0; q < TM * TN; ++q) {                                   \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    \
+        if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                   \
+      }                                                                                       \
+    }                                                                                         \
+  } while (0)
+
+  // k steps over which the next stage's loads are spread
+  constexpr int DSTEPS = (MXM_DMA_STEPS > 0 && MXM_DMA_STEPS < BK / 16) ? MXM_DMA_STEPS : BK / 16;
+  constexpr int KS = BK / 16;
   const int nk = Kd / BK;
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < nk) MXM_DMA(lds + st * BUF, st * BK);
-  for (int kt = 0; kt < nk; ++kt) {
-    // stage kt is complete, the stage consumed at kt-1 is free and receives
-    // stage kt+NS-1, then the MFMAs of stage kt
-    MXM_STAGE_BARRIER(min(NS - 2, nk - 1 - kt));
-    if (kt + NS - 1 < nk) MXM_DMA(lds + ((kt + NS - 1) % NS) * BUF, (kt + NS - 1) * BK);
-    const u32x4_t* cur = lds + (kt % NS) * BUF;
-    MXM_COMPUTE(cur);
+  if constexpr (NS >= 3) {
+    // Deep ring: the barrier of stage kt+1 is taken before the last k step
+    // of stage kt, while that step's fragments are already in registers and
+    // the MFMAs issued just before it are still executing, so the barrier
+    // and the first fragment reads of the next stage overlap MFMA work.  At
+    // that barrier stage kt+1 has landed and stage kt-1 is free; it receives
+    // stage kt+NS-1.
+    static_assert(KS % 2 == 0, "fragment set parity repeats every stage");
+    MXM_STAGE_BARRIER(min(NS - 2, nk - 1));
+    MXM_FRAGS(lds, 0, 0);
+    // (the last stage is peeled so the accumulators flow through one path)
+    for (int kt = 0; kt < nk - 1; ++kt) {
+      const u32x4_t* cur = lds + (kt % NS) * BUF;
+#pragma unroll
+      for (int ks = 0; ks < KS - 1; ++ks) MXM_KSTEP(ks & 1, cur, ks + 1, true);
+      MXM_STAGE_BARRIER(min(NS - 3, nk - 2 - kt));
+      if (kt + NS - 1 < nk) MXM_DMA(lds + ((kt + NS - 1) % NS) * BUF, (kt + NS - 1) * BK);
+      MXM_KSTEP((KS - 1) & 1, lds + ((kt + 1) % NS) * BUF, 0, true);
+    }
+    {
+      const u32x4_t* cur = lds + ((nk - 1) % NS) * BUF;
+#pragma unroll
+      for (int ks = 0; ks < KS - 1; ++ks) MXM_KSTEP(ks & 1, cur, ks + 1, true);
+      MXM_KSTEP((KS - 1) & 1, cur, 0, false);
+    }
+  } else {
+    for (int kt = 0; kt < nk; ++kt) {
+      // stage kt is complete and the stage consumed at kt-1 is free; it
+      // receives stage kt+NS-1 while the MFMAs of stage kt run
+      MXM_STAGE_BARRIER(min(NS - 2, nk - 1 - kt));
+      const u32x4_t* cur = lds + (kt % NS) * BUF;
+      const bool more = kt + NS - 1 < nk;
+      MXM_COMPUTE(cur, more, lds + ((kt + NS - 1) % NS) * BUF, (kt + NS - 1) * BK);
+    }
   }
   MXM_STAGE_BARRIER(0);  // every wave is done reading before the staging reuse
 #undef MXM_DMA
+#undef MXM_DMA_PART
 #undef MXM_STAGE_BARRIER
 #undef MXM_FRAGS
 #undef MXM_COMPUTE
+#undef MXM_KSTEP
 
   // ---- epilogue: activation, bf16, per-wave LDS staging, 16-byte stores ----
   // 32x32 accumulator layout: register r of lane l holds
@@ -276,20 +350,20 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       if (MODE == MXM_GEMM_GLU) {
 #pragma unroll
         for (int pj = 0; pj < TN / 2; ++pj) {
-          const float gg = mxm_rbf(acc[i][2 * pj][r]);
-          const float u = mxm_rbf(acc[i][2 * pj + 1][r]);
-          const float h = mxm_hidden<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
+          const float gg = mxm_rbf_fast(acc[i][2 * pj][r]);
+          const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r]);
+          const float h = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
           const int c = pj * 32 + col;
-          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf(h);
+          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf_fast(h);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           float v = acc[i][j][r];
           if (MODE == MXM_GEMM_MLP)
-            v = mxm_hidden<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf(v));
+            v = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf_fast(v));
           const int c = j * 32 + col;
-          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf(v);
+          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf_fast(v);
         }
       }
     }

@@ -28,10 +28,11 @@ MXM_HD float mxm_u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 // bf16 <-> fp32 (bf16 kept as its 16-bit pattern).
 MXM_HD float mxm_bf2f(uint16_t h) { return mxm_u2f(((uint32_t)h) << 16); }
 MXM_HD uint16_t mxm_f2bf(float f) {
-  uint32_t u = mxm_f2u(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = mxm_f2u(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet_nan = (u >> 16) | 0x0040u;
+  // a select, not a branch: this sits in every epilogue
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? quiet_nan : rounded);
 }
 // Round an fp32 value to the nearest bf16 and widen it back.
 MXM_HD float mxm_rbf(float f) { return mxm_bf2f(mxm_f2bf(f)); }
@@ -42,11 +43,11 @@ MXM_HD float mxm_ftz(float f) {
 }
 
 MXM_HD float mxm_exp(float x) {
-  if (!(x == x)) return x;
-  if (x > 88.0f) return __builtin_inff();
-  if (x < -86.5f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.4426950408889634f);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  // The range cases are selected at the end rather than branched on; inside
+  // [-86.5, 88] the operations are exactly those of the polynomial path.
+  const float xc = (x > 88.0f) ? 88.0f : ((x < -86.5f || !(x == x)) ? -86.5f : x);
+  const float n = __builtin_rintf(xc * 1.4426950408889634f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
   r = __builtin_fmaf(-n, 1.4286068203094172e-06f, r);
   float p = 1.9841269841269841e-04f;                 // 1/5040
   p = __builtin_fmaf(p, r, 1.3888888888888889e-03f);  // 1/720
@@ -57,7 +58,8 @@ MXM_HD float mxm_exp(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   const uint32_t bits = (uint32_t)((int)n + 127) << 23;
-  return p * mxm_u2f(bits);
+  const float y = p * mxm_u2f(bits);
+  return !(x == x) ? x : (x > 88.0f ? __builtin_inff() : (x < -86.5f ? 0.0f : y));
 }
 
 MXM_HD float mxm_sigmoid(float x) { return 1.0f / (1.0f + mxm_exp(-x)); }
@@ -121,6 +123,49 @@ MXM_HD float mxm_hidden(int expert_type, int activation, float slope, float g, f
       return R(u * R(mxm_sigmoid(u)));
     case MXM_ACT_GELU:
       return mxm_gelu_tanh_sq(u, R(u * u));
+    case MXM_ACT_RELU:
+      return u > 0.0f ? u : 0.0f;
+    default: {
+      const float y = u > 0.0f ? u : u * slope;
+      return y * y;
+    }
+  }
+}
+
+// The same activations for the MFMA and int8 epilogues, whose products are
+// compared with the CPU restatement within a tolerance (their accumulation
+// order differs anyway): exp on the hardware exp2 and the reciprocal on
+// v_rcp_f32 (each within about 1 ulp) instead of the exactly specified
+// sequences above, and bf16 rounding by the hardware conversion.  The bf16
+// roundings of the dtype flow are kept.
+// Hardware round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ float mxm_rbf_fast(float f) { return (float)(__bf16)f; }
+__device__ __forceinline__ uint16_t mxm_f2bf_fast(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ float mxm_exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float mxm_sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + mxm_exp_fast(-x));
+}
+__device__ __forceinline__ float mxm_gelu_tanh_sq_fast(float v, float sq) {
+  const float d = 0.7978845608f * (v + (0.044715f * v) * sq);
+  const float t = mxm_exp_fast(-2.0f * __builtin_fabsf(d));
+  const float th = __builtin_copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), d);
+  return (0.5f * v) * (1.0f + th);
+}
+template <bool BF16>
+__device__ __forceinline__ float mxm_hidden_fast(int expert_type, int activation, float slope,
+                                                 float g, float u) {
+  auto R = [](float v) { return BF16 ? mxm_rbf_fast(v) : v; };
+  if (expert_type == MXM_EXPERT_SWIGLU) return R(R(mxm_sigmoid_fast(g)) * u);
+  if (expert_type == MXM_EXPERT_GEGLU) return mxm_gelu_tanh_sq_fast(g, R(g * g)) * u;
+  switch (activation) {
+    case MXM_ACT_SILU:
+      return R(u * R(mxm_sigmoid_fast(u)));
+    case MXM_ACT_GELU:
+      return mxm_gelu_tanh_sq_fast(u, R(u * u));
     case MXM_ACT_RELU:
       return u > 0.0f ? u : 0.0f;
     default: {
