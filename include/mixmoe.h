@@ -140,6 +140,29 @@ int mxm_moe_forward(int64_t op, const void* x, int x_dtype, int64_t rows, float*
 int mxm_moe_forward_host(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
                          float* aux, float* entropy);
 
+/* The whole MoE block of arch/moe.go:152-213 (emitMoEIR + emitMoEDeltaIR):
+ *   xn     = RMSNorm(x, norm_scale, eps)        gpu/ir.cpp:4949-4960 (OP_RMSNORM)
+ *   (delta, aux_raw, entropy) = op 74 on xn     gpu/ir.cpp:1073-1164
+ *   delta *= moe_scale   (when moe_scale != NULL; block scales, arch/moe.go:199-204)
+ *   x_out  = x + delta                          (the residual Add, arch/moe.go:164)
+ *   aux    = aux_weight * aux_raw               (ScalarMul, arch/moe.go:197)
+ * x [rows, D] is bf16 bits or fp32 (x_dtype); norm_scale and moe_scale [D]
+ * have scale_dtype (fp32 or bf16 bits); x_out [rows, D], aux and entropy are
+ * fp32.  xn is computed in the op's compute dtype.  The emitter uses
+ * eps = 1e-5 and aux_weight = the block's effective load_balance_loss_weight.
+ * Dropout (training only) is not applied.  Replaces the four IR ops the
+ * emitter produces for one block (RMSNorm, op 74, ScalarMul, Add); device
+ * pointers, asynchronous on the op's stream. */
+int mxm_moe_block_forward(int64_t op, const void* x, int x_dtype, int64_t rows,
+                          const void* norm_scale, const void* moe_scale, int scale_dtype, float eps,
+                          float aux_weight, float* x_out, float* aux, float* entropy);
+
+/* Same with host buffers; synchronous. */
+int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t rows,
+                               const void* norm_scale, const void* moe_scale, int scale_dtype,
+                               float eps, float aux_weight, float* x_out, float* aux,
+                               float* entropy);
+
 /* Wait for all work queued on the op's stream. */
 int mxm_moe_synchronize(int64_t op);
 

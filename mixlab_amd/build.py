@@ -25,6 +25,7 @@ SOURCES = [
     "mxm_gemm_mfma.hip",
     "mxm_decode.hip",
     "mxm_prep.hip",
+    "mxm_block.hip",
     "mxm_abi.hip",
 ]
 ARCH = os.environ.get("MIXMOE_OFFLOAD_ARCH", "gfx950")

@@ -96,6 +96,7 @@ struct MoeOp {
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
       tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits;
+  DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
   size_t ws_bytes = 0;
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
@@ -195,7 +196,19 @@ void require_operands(const GemmArgs& g, bool second_matrix, bool scaled) {
     fail("OP_MOE_FEED_FORWARD internal error: expert GEMM operand not allocated (mode %d)", g.mode);
 }
 
-void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent) {
+// Block-level extras of a forward (arch/moe.go:152-213): the rows before
+// the norm (the residual), the optional moe_scale, and the aux weight.
+struct BlockIO {
+  const void* x;
+  bool x_bf16;
+  const void* moe_scale;
+  bool scale_bf16;
+  float aux_weight;
+  float* aux_scaled;
+};
+
+void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent,
+                 const BlockIO* blk = nullptr) {
   for (int i = 1; i < o.n_inputs; ++i)
     if (!o.have[i]) fail("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
   if (!o.ws_ready) alloc_workspace(o);
@@ -259,6 +272,8 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   sa.mstart2 = o.mstart2.as<int32_t>();
   sa.aux = aux_p;
   sa.entropy = ent_p;
+  sa.aux_weight = blk ? blk->aux_weight : 1.0f;
+  sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
   mxm_launch_scan(sa, o.bf16, st);
   HIPCK(hipGetLastError());
 
@@ -351,6 +366,12 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   ca.D = o.D;
   ca.K = o.K;
   ca.delta = delta;
+  if (blk) {
+    ca.resid = blk->x;
+    ca.resid_bf16 = blk->x_bf16;
+    ca.rscale = blk->moe_scale;
+    ca.rscale_bf16 = blk->scale_bf16;
+  }
   mxm_launch_combine(ca, o.mfma || o.q8, st);
   HIPCK(hipGetLastError());
   mark(6);
@@ -680,6 +701,90 @@ int mxm_moe_forward_host(int64_t h, const void* x, int x_dtype, int64_t rows, fl
     if (aux) HIPCK(hipMemcpyAsync(aux, op->aux.p, 4, hipMemcpyDeviceToHost, op->stream));
     if (entropy) HIPCK(hipMemcpyAsync(entropy, op->ent.p, 4, hipMemcpyDeviceToHost, op->stream));
     HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+// Fused block forward (arch/moe.go:152-166, emitMoEDeltaIR :173-213):
+// xn = RMSNorm(x, norm_scale, eps) (gpu/ir.cpp:4949-4960) in the compute
+// dtype, op 74 on xn, delta *= moe_scale (if any), x_out = x + delta in fp32,
+// aux_out = aux_weight * aux_raw.  All pointers are device memory.
+void run_block(MoeOp& o, const void* x, int x_dtype, const void* norm_scale, const void* moe_scale,
+               int scale_dtype, float eps, float aux_weight, float* x_out, float* aux, float* ent) {
+  if (x_dtype != MXM_DTYPE_BF16 && x_dtype != MXM_DTYPE_F32)
+    fail("OP_MOE_FEED_FORWARD unsupported x dtype %d for the block", x_dtype);
+  if (scale_dtype != MXM_DTYPE_BF16 && scale_dtype != MXM_DTYPE_F32)
+    fail("OP_RMSNORM scale dtype %d unsupported (want fp32 or bf16)", scale_dtype);
+  if (!norm_scale) fail("OP_RMSNORM requires a scale input");
+  if (!o.ws_ready) alloc_workspace(o);
+  const size_t esz = o.bf16 ? 2 : 4;
+  if (!o.xn.p) o.xn.alloc((size_t)o.N * o.D * esz);
+  RmsNormArgs na{};
+  na.x = x;
+  na.x_bf16 = x_dtype == MXM_DTYPE_BF16;
+  na.scale = norm_scale;
+  na.scale_bf16 = scale_dtype == MXM_DTYPE_BF16;
+  na.N = o.N;
+  na.D = o.D;
+  na.eps = eps;
+  na.inv_d = (float)(1.0 / (double)o.D);
+  na.out = o.xn.p;
+  na.out_bf16 = o.bf16;
+  mxm_launch_rmsnorm(na, o.stream);
+  HIPCK(hipGetLastError());
+  BlockIO b{};
+  b.x = x;
+  b.x_bf16 = na.x_bf16;
+  b.moe_scale = moe_scale;
+  b.scale_bf16 = na.scale_bf16;
+  b.aux_weight = aux_weight;
+  b.aux_scaled = aux;
+  run_forward(o, o.xn.p, o.bf16 ? MXM_DTYPE_BF16 : MXM_DTYPE_F32, x_out, nullptr, ent, &b);
+}
+
+int mxm_moe_block_forward(int64_t h, const void* x, int x_dtype, int64_t rows,
+                          const void* norm_scale, const void* moe_scale, int scale_dtype, float eps,
+                          float aux_weight, float* x_out, float* aux, float* entropy) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !x_out) fail("OP_MOE_FEED_FORWARD x and x_out must be non-NULL");
+    run_block(*op, x, x_dtype, norm_scale, moe_scale, scale_dtype, eps, aux_weight, x_out, aux,
+              entropy);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t rows,
+                               const void* norm_scale, const void* moe_scale, int scale_dtype,
+                               float eps, float aux_weight, float* x_out, float* aux,
+                               float* entropy) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !x_out) fail("OP_MOE_FEED_FORWARD x and x_out must be non-NULL");
+    if (!norm_scale) fail("OP_RMSNORM requires a scale input");
+    const size_t xe = (x_dtype == MXM_DTYPE_BF16) ? 2 : 4;
+    const size_t se = (scale_dtype == MXM_DTYPE_BF16) ? 2 : 4;
+    const size_t D = (size_t)op->D;
+    DevBuf dx, dout, dres;
+    dx.alloc((size_t)op->N * D * xe);
+    dout.alloc((size_t)op->N * D * 4);
+    dres.alloc(8);
+    if (!op->blk_scales.p) op->blk_scales.alloc(2 * D * 4);
+    char* sc = op->blk_scales.as<char>();
+    HIPCK(hipMemcpyAsync(dx.p, x, dx.bytes, hipMemcpyHostToDevice, op->stream));
+    HIPCK(hipMemcpyAsync(sc, norm_scale, D * se, hipMemcpyHostToDevice, op->stream));
+    if (moe_scale)
+      HIPCK(hipMemcpyAsync(sc + D * 4, moe_scale, D * se, hipMemcpyHostToDevice, op->stream));
+    run_block(*op, dx.p, x_dtype, sc, moe_scale ? sc + D * 4 : nullptr, scale_dtype, eps,
+              aux_weight, dout.as<float>(), dres.as<float>(), dres.as<float>() + 1);
+    HIPCK(hipMemcpyAsync(x_out, dout.p, (size_t)op->N * D * 4, hipMemcpyDeviceToHost, op->stream));
+    float res[2];
+    HIPCK(hipMemcpyAsync(res, dres.p, 8, hipMemcpyDeviceToHost, op->stream));
+    HIPCK(hipStreamSynchronize(op->stream));
+    if (aux) *aux = res[0];
+    if (entropy) *entropy = res[1];
     return MXM_OK;
   });
 }

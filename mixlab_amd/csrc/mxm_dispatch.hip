@@ -92,7 +92,9 @@ __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
     a.offsets[a.E] = o;
     a.mstart1[a.E] = m1;
     a.mstart2[a.E] = m2;
-    a.aux[0] = aux * (float)a.E;
+    const float raw = aux * (float)a.E;
+    a.aux[0] = raw;
+    if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
   }
   __syncthreads();
 
@@ -193,6 +195,22 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
       const float g = sg[k];
 #pragma unroll
       for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], g));
+    }
+    if (a.resid) {
+      // block level: x + delta (* moe_scale), fp32
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        const size_t i = (size_t)n * a.D + d + q;
+        const float xr = a.resid_bf16 ? mxm_bf2f(static_cast<const uint16_t*>(a.resid)[i])
+                                      : static_cast<const float*>(a.resid)[i];
+        float v = acc[q];
+        if (a.rscale) {
+          const float sc = a.rscale_bf16 ? mxm_bf2f(static_cast<const uint16_t*>(a.rscale)[d + q])
+                                         : static_cast<const float*>(a.rscale)[d + q];
+          v = __fmul_rn(v, sc);
+        }
+        acc[q] = __fadd_rn(xr, v);
+      }
     }
     float* dst = a.delta + (size_t)n * a.D + d;
     if constexpr (VEC == 4 || VEC == 8) {

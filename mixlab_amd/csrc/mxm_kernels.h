@@ -78,6 +78,8 @@ struct ScanArgs {
   int32_t* mstart2;     // [E + 1] prefix of ceil(counts / bm2)
   float* aux;           // [1]
   float* entropy;       // [1]
+  float aux_weight;     // block level: aux_scaled = aux * aux_weight
+  float* aux_scaled;    // [1] or null
 };
 void mxm_launch_scan(const ScanArgs& a, bool bf16, hipStream_t s);
 
@@ -167,8 +169,32 @@ struct CombineArgs {
   const int32_t* slot_pos;
   int N, D, K;
   float* delta;           // [N, D]
+  // Block level (null resid: plain op output): delta[n, d] = resid[n, d] +
+  // combined * rscale[d] (or + combined when rscale is null), in fp32.
+  const void* resid;      // [N, D], bf16 bits or fp32 (resid_bf16)
+  bool resid_bf16;
+  const void* rscale;     // [D], bf16 bits or fp32 (rscale_bf16)
+  bool rscale_bf16;
 };
 void mxm_launch_combine(const CombineArgs& a, bool y_bf16, hipStream_t s);
+
+// RMSNorm of gpu/ir.cpp:4949-4960 with a fixed summation order: one wave
+// per row; lane l sums x[d]^2 (product rounded, then added) over
+// d = 256*i + 4*l + j in (i, j) order, the 64 partial sums meet in an xor
+// butterfly (distances 32, 16, ..., 1); ms = sum * inv_d; r = 1 / sqrt(ms +
+// eps) (both correctly rounded); y = (x * r) * scale, rounded to the output
+// dtype.
+struct RmsNormArgs {
+  const void* x;          // [N, D]
+  bool x_bf16;
+  const void* scale;      // [D]
+  bool scale_bf16;
+  int N, D;
+  float eps, inv_d;       // inv_d = (float)(1.0 / D)
+  void* out;              // [N, D]
+  bool out_bf16;
+};
+void mxm_launch_rmsnorm(const RmsNormArgs& a, hipStream_t s);
 
 // Weight preparation (run once at upload).
 void mxm_launch_to_f32(const void* src, int src_dtype, float* dst, int64_t n, hipStream_t s);

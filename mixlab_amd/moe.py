@@ -14,6 +14,8 @@ import math
 from dataclasses import dataclass, field
 from typing import Any, Optional
 
+import numpy as np
+
 # arch/ir.go:10-67 (op codes are a stable ABI shared with gpu/ir.h)
 OP_ADD = 3
 OP_MUL = 4
@@ -347,3 +349,59 @@ def op_flops(int_params) -> int:
     N = B * T
     per = (6 if etype != MOE_EXPERT_MLP else 4) * N * D * F
     return 2 * N * D * E + K * per
+
+
+# ---- aux / entropy aggregation into the loss (arch/loss_emit.go:244-303) ----
+
+def collect_moe_auxiliary_outputs(prog: Program) -> tuple[list, list]:
+    """arch/loss_emit.go:244-258: per-block outputs suffixed _moe_aux_loss /
+    _moe_router_entropy, in program order."""
+    aux, ent = [], []
+    for op in prog.ops:
+        for out in op.outputs:
+            if out.endswith("_moe_aux_loss") and out != "moe_aux_loss":
+                aux.append(out)
+            elif out.endswith("_moe_router_entropy") and out != "moe_router_entropy":
+                ent.append(out)
+    return aux, ent
+
+
+def emit_moe_auxiliary_aggregates_ir(prog: Program, task_loss_has_eval_loss: bool) -> bool:
+    """arch/loss_emit.go:260-303: moe_aux_loss = sum of the blocks' aux
+    losses (left to right), moe_router_entropy = their mean (sum times
+    1/count), loss = task_loss + moe_aux_loss."""
+    aux, ent = collect_moe_auxiliary_outputs(prog)
+    if not aux:
+        return False
+    if not task_loss_has_eval_loss:
+        prog.scalar_mul("loss", 1.0, "eval_loss")
+    prog.scalar_mul("loss", 1.0, "task_loss")
+    acc = aux[0]
+    for i in range(1, len(aux)):
+        nxt = f"moe_aux_accum_{i}"
+        prog.add(acc, aux[i], nxt)
+        acc = nxt
+    prog.scalar_mul(acc, 1.0, "moe_aux_loss")
+    if ent:
+        acc = ent[0]
+        for i in range(1, len(ent)):
+            nxt = f"moe_entropy_accum_{i}"
+            prog.add(acc, ent[i], nxt)
+            acc = nxt
+        prog.scalar_mul(acc, float(np.float32(1.0) / np.float32(len(ent))), "moe_router_entropy")
+    prog.add("task_loss", "moe_aux_loss", "loss")
+    return True
+
+
+def evaluate_scalar_ops(prog: Program, values: dict, start: int = 0) -> dict:
+    """Evaluate the scalar Add / ScalarMul ops of prog (from op index start)
+    in fp32, as the interpreter does for [1]-shaped tensors; values maps
+    names to floats and is extended in place."""
+    for op in prog.ops[start:]:
+        if op.code == OP_ADD:
+            a, b = (np.float32(values[n]) for n in op.inputs)
+            values[op.outputs[0]] = float(a + b)
+        elif op.code == OP_SCALAR_MUL:
+            values[op.outputs[0]] = float(np.float32(values[op.inputs[0]])
+                                          * np.float32(op.float_params[0]))
+    return values

@@ -14,7 +14,9 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _lib
-from .moe import MOE_EXPERT_MLP, OP_MOE_FEED_FORWARD, Op
+from .moe import (DEFAULT_FFN_MULTIPLIER, MOE_EXPERT_MLP, OP_MOE_FEED_FORWARD, OP_RMSNORM, BlockSpec,
+                  Op, Program, effective_moe_load_balance_loss_weight, emit_moe_ir,
+                  moe_weight_shapes)
 
 _DTYPES = {"fp32": _lib.MXM_DTYPE_F32, "float32": _lib.MXM_DTYPE_F32,
            "bf16": _lib.MXM_DTYPE_BF16, "bfloat16": _lib.MXM_DTYPE_BF16}
@@ -119,6 +121,37 @@ class MoEFeedForward:
                                        ctypes.c_void_p(ent_ptr) if ent_ptr else None)
         _lib.check(rc, "mxm_moe_forward")
 
+    def block_forward_host(self, x: np.ndarray, norm_scale: np.ndarray,
+                           moe_scale: Optional[np.ndarray] = None, eps: float = 1e-5,
+                           aux_weight: float = 0.01):
+        """The MoE block of arch/moe.go:152-213 on host arrays: RMSNorm, op 74,
+        optional moe_scale, residual add.  x [B*T, D] fp32 or bf16 bits; the
+        scales [D] fp32 or bf16 bits (both the same dtype).  Returns
+        (x_out [B*T, D] fp32, aux = aux_weight * aux_raw, entropy)."""
+        x = np.ascontiguousarray(x)
+        ns = np.ascontiguousarray(norm_scale)
+        ms = None if moe_scale is None else np.ascontiguousarray(moe_scale, dtype=ns.dtype)
+        out = np.empty((x.shape[0], self.D), np.float32)
+        aux = np.zeros(1, np.float32)
+        ent = np.zeros(1, np.float32)
+        vp = lambda a: None if a is None else ctypes.c_void_p(a.ctypes.data)  # noqa: E731
+        rc = self._lib.mxm_moe_block_forward_host(
+            self.handle, vp(x), _np_dtype_code(x), x.shape[0], vp(ns), vp(ms), _np_dtype_code(ns),
+            float(eps), float(aux_weight), vp(out), vp(aux), vp(ent))
+        _lib.check(rc, "mxm_moe_block_forward_host")
+        return out, float(aux[0]), float(ent[0])
+
+    def block_forward(self, x_ptr: int, x_dtype: int, rows: int, norm_scale_ptr: int,
+                      moe_scale_ptr: int, scale_dtype: int, eps: float, aux_weight: float,
+                      out_ptr: int, aux_ptr: int = 0, ent_ptr: int = 0) -> None:
+        """Asynchronous block forward on device pointers (ints; moe_scale_ptr 0 = none)."""
+        vp = lambda p: ctypes.c_void_p(p) if p else None  # noqa: E731
+        rc = self._lib.mxm_moe_block_forward(self.handle, vp(x_ptr), x_dtype, rows,
+                                             vp(norm_scale_ptr), vp(moe_scale_ptr), scale_dtype,
+                                             float(eps), float(aux_weight), vp(out_ptr),
+                                             vp(aux_ptr), vp(ent_ptr))
+        _lib.check(rc, "mxm_moe_block_forward")
+
     def synchronize(self) -> None:
         _lib.check(self._lib.mxm_moe_synchronize(self.handle), "mxm_moe_synchronize")
 
@@ -171,6 +204,73 @@ class MoEFeedForward:
             self.close()
         except Exception:
             pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class MoEBlock:
+    """One MoE block as the emitter builds it (arch/moe.go:152-213): RMSNorm,
+    op 74, aux weight, optional moe_scale, residual add -- run as one fused
+    call (mxm_moe_block_forward).  Weights follow the block's metas
+    (arch/moe.go:112-150): moe_norm_scale, router_w, per-expert matrices,
+    then moe_scale when block_scales is on."""
+
+    def __init__(self, spec: BlockSpec, B: int, T: int, D: int,
+                 mlp_mult: float = DEFAULT_FFN_MULTIPLIER, block_scales: bool = False,
+                 compute_dtype: str = "fp32", flags: int = 0):
+        prog = Program()
+        emit_moe_ir(prog, spec, "x", 0, D, T, B, 0, mlp_mult, block_scales)
+        norm = next(op for op in prog.ops if op.code == OP_RMSNORM)
+        ff = next(op for op in prog.ops if op.code == OP_MOE_FEED_FORWARD)
+        self.program = prog
+        self.eps = float(norm.float_params[0])
+        self.aux_weight = float(effective_moe_load_balance_loss_weight(spec))
+        self.metas = moe_weight_shapes(spec, D, mlp_mult, block_scales)
+        self.block_scales = block_scales
+        self.bf16 = compute_dtype in ("bf16", "bfloat16")
+        self.op = MoEFeedForward.from_op(ff, compute_dtype=compute_dtype, flags=flags)
+        self.norm_scale = None
+        self.moe_scale = None
+
+    def _conv(self, a):
+        from .workloads import bf16_bits
+        return bf16_bits(a) if self.bf16 else np.ascontiguousarray(a, dtype=np.float32)
+
+    def set_weights(self, weights) -> None:
+        """fp32 arrays in meta order (as the checkpoint holds them); under
+        bf16 compute they are cast to bf16 (gpu/ir_trainer.cpp:1395-1412)."""
+        if len(weights) != len(self.metas):
+            raise ValueError(f"moe block takes {len(self.metas)} weights, got {len(weights)}")
+        for m, w in zip(self.metas, weights):
+            if list(np.shape(w)) != list(m.shape):
+                raise ValueError(f"{m.name}: shape {list(np.shape(w))}, want {m.shape}")
+        self.norm_scale = self._conv(weights[0])
+        self.op.set_input(1, self._conv(weights[1]))
+        n_exp = len(self.metas) - 2 - (1 if self.block_scales else 0)
+        for i in range(n_exp):
+            self.op.set_input(2 + i, self._conv(weights[2 + i]))
+        self.moe_scale = self._conv(weights[-1]) if self.block_scales else None
+
+    def load(self, path: str, first_index: int = 0) -> None:
+        """Bind the block's weights from a native checkpoint (tensors
+        w{first_index + i}_{meta name}, train/import.go:71-89)."""
+        from .weights import load_weights
+        self.set_weights(load_weights(path, self.metas, first_index))
+
+    def forward_host(self, x: np.ndarray):
+        """x [B*T, D] (fp32, or bf16 bits) -> (x + delta [B*T, D] fp32,
+        aux = load-balance weight * aux_raw, router entropy)."""
+        if self.norm_scale is None:
+            raise ValueError("moe block weights are not set")
+        return self.op.block_forward_host(x, self.norm_scale, self.moe_scale, self.eps,
+                                          self.aux_weight)
+
+    def close(self) -> None:
+        self.op.close()
 
     def __enter__(self):
         return self

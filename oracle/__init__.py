@@ -61,6 +61,8 @@ def _load():
         lib.oracle_round_bf16.argtypes = [ctypes.c_float]
         lib.oracle_exp_array.argtypes = [f32p, f32p, ctypes.c_int64]
         lib.oracle_round_bf16_array.argtypes = [f32p, f32p, ctypes.c_int64]
+        lib.oracle_rmsnorm.argtypes = [ctypes.c_int, ctypes.c_int, f32p, f32p, ctypes.c_float,
+                                       ctypes.c_int, f32p]
         lib.oracle_hidden_array.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, f32p, f32p, f32p,
             ctypes.c_int64,
@@ -166,6 +168,39 @@ def moe_forward(x, router_w, expert_weights, *, top_k: int, expert_type: int = 0
     return dict(delta=delta, aux=float(aux[0]), entropy=float(ent[0]), top_idx=top_idx,
                 gates=gates, probs=probs, logits=logits, counts=counts, offsets=offsets,
                 perm=perm)
+
+
+def rmsnorm(x, scale, eps: float = 1e-5, out_bf16: bool = False) -> np.ndarray:
+    """RMSNorm of gpu/ir.cpp:4949-4960 in the fixed summation order of
+    oracle_rmsnorm.  x [N, D] and scale [D] hold the input values (bf16
+    inputs as their exact fp32 values); the result is fp32, rounded to bf16
+    values when out_bf16."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    N, D = x.shape
+    out = np.empty_like(x)
+    _load().oracle_rmsnorm(N, D, _p(x), _p(scale), eps, int(out_bf16), _p(out))
+    return out
+
+
+def block_forward(x, norm_scale, router_w, expert_weights, *, top_k: int,
+                  moe_scale=None, eps: float = 1e-5, aux_weight: float = 0.01,
+                  bf16: bool = False, **kw) -> dict:
+    """The MoE block of arch/moe.go:152-213: xn = RMSNorm(x), op 74 on xn
+    (moe_forward), delta *= moe_scale, x_out = x + delta (fp32), aux scaled by
+    aux_weight.  x, norm_scale and moe_scale hold the input values (round
+    them to bf16 first for the bf16 flow)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    xn = rmsnorm(x, norm_scale, eps, out_bf16=bf16)
+    res = moe_forward(xn, router_w, expert_weights, top_k=top_k, bf16=bf16, **kw)
+    delta = res["delta"]
+    if moe_scale is not None:
+        delta = delta * np.asarray(moe_scale, dtype=np.float32)[None, :]
+    res["xn"] = xn
+    res["aux_raw"] = res["aux"]
+    res["aux"] = float(np.float32(res["aux"]) * np.float32(aux_weight))
+    res["x_out"] = (x + delta).astype(np.float32)
+    return res
 
 
 def num_threads() -> int:

@@ -378,3 +378,44 @@ void oracle_hidden_array(int bf16, int etype, int act, float slope, const float*
                          const float* u, float* h, int64_t n) {
   for (int64_t i = 0; i < n; ++i) h[i] = oracle_hidden(bf16, etype, act, slope, g[i], u[i]);
 }
+
+/*
+ * RMSNorm in front of op 74 (block level, arch/moe.go:152-166), following
+ * gpu/ir.cpp:4949-4960: y = astype(x_f32 * (1 / sqrt(mean(x^2) + eps)) *
+ * scale, x.dtype).  MLX's reduction order is not specified; this build fixes
+ * it (and the device kernel follows it): 64 partial sums, partial l holding
+ * x[d]^2 (product rounded, then added) for d = 256*i + 4*l + j in (i, j)
+ * order; the partials meet in an xor butterfly over distances 32..1; the
+ * mean is sum * (float)(1/D).  sqrt and the division are correctly rounded.
+ * out_bf16 rounds y to bf16 (the bf16 flow), else y stays fp32.
+ */
+void oracle_rmsnorm(int N, int D, const float* x, const float* scale, float eps, int out_bf16,
+                    float* out) {
+  const float inv_d = (float)(1.0 / (double)D);
+  for (int n = 0; n < N; ++n) {
+    const float* xr = x + (size_t)n * D;
+    float lanes[64], tmp[64];
+    for (int l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (int d0 = 0; d0 < D; d0 += 256)
+        for (int j = 0; j < 4; ++j) {
+          const int d = d0 + 4 * l + j;
+          if (d < D) {
+            const float p = xr[d] * xr[d];
+            acc = acc + p;
+          }
+        }
+      lanes[l] = acc;
+    }
+    for (int s = 32; s >= 1; s >>= 1) {
+      for (int l = 0; l < 64; ++l) tmp[l] = lanes[l] + lanes[l ^ s];
+      memcpy(lanes, tmp, sizeof(lanes));
+    }
+    const float ms = lanes[0] * inv_d;
+    const float r = 1.0f / sqrtf(ms + eps);
+    for (int d = 0; d < D; ++d) {
+      const float y = (xr[d] * r) * scale[d];
+      out[(size_t)n * D + d] = out_bf16 ? oracle_round_bf16(y) : y;
+    }
+  }
+}

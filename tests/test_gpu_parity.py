@@ -250,3 +250,101 @@ def test_int8_expert_types(gpu_lib, name, etype, act, slope):
     err = rel_l2(delta, want["delta"])
     print(f"int8 {name} rel L2 = {err:.3e}")
     assert err <= BF16_TOL
+
+
+def _block_case(seed, N, D, E, F, bf16, x_fp32_in_bf16_flow=False):
+    rng = np.random.default_rng(seed)
+    x, wr, experts = random_case(seed, N, D, E, F)
+    x = x * np.float32(2.5)
+    ns = (np.float32(1.0) + rng.standard_normal(D, dtype=np.float32) * np.float32(0.2))
+    ms = rng.standard_normal(D, dtype=np.float32)
+    if bf16:
+        wr = round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+        ns, ms = round_bf16(ns), round_bf16(ms)
+        if not x_fp32_in_bf16_flow:
+            x = round_bf16(x)
+    return x, wr, experts, ns, ms
+
+
+@pytest.mark.parametrize("flow,D,xin", [("fp32", 256, "fp32"), ("fp32", 320, "fp32"),
+                                        ("bf16", 256, "bf16"), ("bf16", 256, "fp32")])
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_block_forward(gpu_lib, flow, D, xin, with_scale):
+    """arch/moe.go:152-213 fused: RMSNorm (gpu/ir.cpp:4949-4960), op 74,
+    moe_scale, residual add, aux weight.  The normalised rows feed the router,
+    so routing is bit-exact only if the norm is; fp32 runs (SIMT experts) are
+    bit-exact end to end."""
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import bf16_bits
+
+    bf16 = flow == "bf16"
+    B, T, E, K, F = 2, 160, 8, 2, 256
+    x, wr, experts, ns, ms = _block_case(21, B * T, D, E, F, bf16, x_fp32_in_bf16_flow=xin == "fp32")
+    ms = ms if with_scale else None
+    conv = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
+    xconv = bf16_bits if xin == "bf16" else (lambda a: np.ascontiguousarray(a, np.float32))
+    with MoEFeedForward([B, T, D, E, K, 0, F, 0], [0.0],
+                        compute_dtype="bf16" if bf16 else "fp32") as op:
+        op.set_weights(conv(wr), [[conv(w) for w in ws] for ws in experts])
+        out, aux, ent = op.block_forward_host(xconv(x), conv(ns), None if ms is None else conv(ms),
+                                              eps=1e-5, aux_weight=0.03)
+        routing = op.routing()
+        info = op.info()
+    import oracle
+    want = oracle.block_forward(x, ns, wr, experts, top_k=K, moe_scale=ms, eps=1e-5,
+                                aux_weight=0.03, bf16=bf16)
+    assert_routing_equal(routing, want)
+    if bf16:
+        assert info["mfma"]
+        assert rel_l2(out - x, want["x_out"] - x) <= BF16_TOL
+        assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+    else:
+        assert same_bits(out, want["x_out"])
+        assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
+    assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"])
+
+
+@pytest.mark.parametrize("flow", ["fp32", "bf16"])
+def test_moe_block_from_checkpoint(gpu_lib, tmp_path, flow):
+    """A block config -> emitter -> native checkpoint -> fused block forward,
+    against the restatement fed the same weights."""
+    from mixlab_amd import moe
+    from mixlab_amd.op import MoEBlock
+    from mixlab_amd.weights import export_safetensors
+
+    spec = moe.BlockSpec.from_json('{"type":"moe","num_experts":6,"top_k":2,'
+                                   '"load_balance_loss_weight":0.02}')
+    B, T, D = 2, 96, 128
+    bf16 = flow == "bf16"
+    with MoEBlock(spec, B, T, D, mlp_mult=2.0, block_scales=True,
+                  compute_dtype="bf16" if bf16 else "fp32") as blk:
+        rng = np.random.default_rng(31)
+        ws = []
+        for m in blk.metas:
+            a = rng.standard_normal(m.shape, dtype=np.float32) * np.float32(0.05)
+            if m.name in ("moe_norm_scale", "moe_scale"):
+                a = a + np.float32(1.0)
+            ws.append(a)
+        path = str(tmp_path / "m.safetensors")
+        export_safetensors(path, blk.metas, ws, first_index=7)
+        blk.load(path, first_index=7)
+        x = rng.standard_normal((B * T, D), dtype=np.float32)
+        if bf16:
+            x = round_bf16(x)
+            from mixlab_amd.workloads import bf16_bits
+            out, aux, ent = blk.forward_host(bf16_bits(x))
+        else:
+            out, aux, ent = blk.forward_host(x)
+        routing = blk.op.routing()
+    import oracle
+    r = round_bf16 if bf16 else (lambda a: a)
+    experts = [[r(w) for w in ws[2 + 3 * e:5 + 3 * e]] for e in range(6)]
+    want = oracle.block_forward(x, r(ws[0]), r(ws[1]), experts, top_k=2, moe_scale=r(ws[-1]),
+                                eps=1e-5, aux_weight=0.02, bf16=bf16)
+    assert_routing_equal(routing, want)
+    if bf16:
+        assert rel_l2(out - x, want["x_out"] - x) <= BF16_TOL
+    else:
+        assert same_bits(out, want["x_out"])
+    assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])

@@ -288,3 +288,68 @@ def test_dense_blas_baseline_matches_oracle():
     delta, aux, ent = dense_forward(x, wr, lambda e, j: ex[e][j], 6, 2, 0, 0, 0.0)
     assert _rel(delta, want["delta"].astype(np.float64)) <= 1e-5
     assert abs(aux - want["aux"]) <= 1e-5 and abs(ent - want["entropy"]) <= 1e-5
+
+
+# ---- block level: RMSNorm (gpu/ir.cpp:4949-4960) and the residual block ----
+
+def _rms64(x, scale, eps):
+    x64 = x.astype(np.float64)
+    return x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + eps) * scale.astype(np.float64)
+
+
+@pytest.mark.parametrize("D", [3, 64, 300, 2048])
+def test_rmsnorm_matches_float64(D):
+    rng = np.random.default_rng(10 + D)
+    x = rng.standard_normal((17, D), dtype=np.float32) * np.float32(3.0)
+    scale = (np.float32(1.0) + rng.standard_normal(D, dtype=np.float32) * np.float32(0.1))
+    got = oracle.rmsnorm(x, scale, 1e-5)
+    want = _rms64(x, scale, 1e-5)
+    assert float(np.max(np.abs(got - want) / (np.abs(want) + 1e-30))) <= 2e-6
+    # dropping eps, or averaging over D-1, is visible at this tolerance
+    xs = x * np.float32(1e-3)
+    got_small = oracle.rmsnorm(xs, scale, 1e-5)
+    assert float(np.max(np.abs(got_small - _rms64(xs, scale, 0.0)))) > 1e-3
+    if D > 3:
+        alt = xs.astype(np.float64) / np.sqrt((xs.astype(np.float64) ** 2).sum(1, keepdims=True)
+                                              / (D - 1) + 1e-5) * scale
+        assert float(np.max(np.abs(got_small - alt) / np.abs(alt))) > 1e-4
+
+
+def test_rmsnorm_invariances():
+    """Power-of-two scalings are exact through every step, so they commute
+    with the norm bit for bit (eps = 0 so it does not break the scaling)."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((9, 513), dtype=np.float32)
+    scale = rng.standard_normal(513, dtype=np.float32)
+    a = oracle.rmsnorm(x, scale, 0.0)
+    np.testing.assert_array_equal(oracle.rmsnorm(x * np.float32(8.0), scale, 0.0), a)
+    np.testing.assert_array_equal(oracle.rmsnorm(x, scale * np.float32(0.25), 0.0),
+                                  a * np.float32(0.25))
+    # a constant row normalises to sign * scale / sqrt(1 + eps / c^2)
+    c = np.full((1, 256), 3.0, np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(c, np.ones(256, np.float32), 0.0), 1.0, rtol=1e-7)
+    # bf16 output is the rounding of the fp32 output
+    np.testing.assert_array_equal(oracle.rmsnorm(x, scale, 1e-5, out_bf16=True),
+                                  oracle.round_bf16(oracle.rmsnorm(x, scale, 1e-5)))
+
+
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_block_forward_composition(with_scale):
+    """arch/moe.go:152-213: x + moe_scale * MoE(RMSNorm(x)), aux scaled by
+    the load-balance weight; against float64 evaluation of each step."""
+    rng = np.random.default_rng(12)
+    x, wr, ex = _rand_problem(rng, 48, 32, 6, 24)
+    ns = (np.float32(1.0) + rng.standard_normal(32, dtype=np.float32) * np.float32(0.1))
+    ms = rng.standard_normal(32, dtype=np.float32) if with_scale else None
+    got = oracle.block_forward(x, ns, wr, ex, top_k=2, moe_scale=ms, aux_weight=0.05)
+    xn64 = _rms64(x, ns, 1e-5)
+    np.testing.assert_allclose(got["xn"], xn64, rtol=2e-6, atol=1e-7)
+    want = np.zeros((48, 32))
+    for n in range(48):
+        for k in range(2):
+            e = got["top_idx"][n, k]
+            want[n] += got["gates"][n, k] * _ffn64(xn64[n:n + 1], ex[e])[0]
+    if with_scale:
+        want = want * ms
+    assert _rel(got["x_out"] - x, want) <= 2e-5
+    assert abs(got["aux"] - 0.05 * got["aux_raw"]) <= 1e-8
