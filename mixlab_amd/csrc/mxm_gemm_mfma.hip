@@ -50,7 +50,7 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 #endif
 
 #ifndef MXM_GM
-#define MXM_GM 4
+#define MXM_GM 6
 #endif
 constexpr int GM = MXM_GM;        // row tiles per scheduling group
 
