@@ -23,6 +23,7 @@ import numpy as np
 METRIC = "MoE layer tokens/sec at d=2048,64e top-8; grouped-GEMM % MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (AMD published)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (AMD published)
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 vector (AMD published)
 
 
 def log(msg: str) -> None:
@@ -170,6 +171,58 @@ def copy_calibration(mib: int, reps: int = 5) -> int:
     return 0
 
 
+def run_backward(cfg, steps: int, warmup: int) -> dict:
+    """Backward of op 74 (mxm_moe_backward: a forward with the routing kept,
+    then the gradients of x, the router and every routed expert) on a
+    configuration computed in fp32."""
+    from mixlab_amd import _lib
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import make_workload
+
+    w = make_workload(cfg)
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype="fp32")
+    op.set_input(1, np.ascontiguousarray(w.router_w, np.float32))
+    idx = 2
+    for e in range(cfg.E):
+        for j in range(cfg.wpe):
+            op.set_input(idx, np.ascontiguousarray(w.matrix(e, j), np.float32))
+            idx += 1
+    rng = np.random.default_rng(7)
+    xdev = _lib.DeviceBuffer.from_array(np.ascontiguousarray(w.x, np.float32))
+    dd = _lib.DeviceBuffer.from_array(rng.standard_normal((cfg.N, cfg.D), dtype=np.float32))
+    dx = _lib.DeviceBuffer(cfg.N * cfg.D * 4)
+    dwr = _lib.DeviceBuffer(cfg.D * cfg.E * 4)
+    dw = _lib.DeviceBuffer(cfg.E * cfg.wpe * cfg.D * cfg.F * 4)
+    lib = _lib.init()
+
+    def step():
+        _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, _lib.MXM_DTYPE_F32, cfg.N,
+                                        dd.value, 0.01, 0.0, dx.value, dwr.value, dw.value),
+                   "mxm_moe_backward")
+
+    for _ in range(warmup):
+        step()
+    op.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    op.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    op.close()
+    glu = cfg.expert_type != 2
+    nkdf = cfg.N * cfg.K * cfg.D * cfg.F
+    # forward (3 or 2 products) + recomputed projections + dH + dX + weight gradients
+    fl = 2 * nkdf * ((3 if glu else 2) + (2 if glu else 1) + 1 + (2 if glu else 1)
+                     + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"backward {cfg.name} fp32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+    return {"workload": f"{cfg.name} shape, fp32 compute", "tokens": cfg.N,
+            "ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3),
+            "roofline": {"bound": "valu", "kernel": "whole backward (SIMT fp32 products)",
+                         "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / PEAK_FP32_TFLOPS, "traffic": None}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,6 +233,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -238,6 +292,11 @@ def main() -> int:
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
 
+    backward = None
+    if not args.no_backward:
+        import dataclasses
+        backward = run_backward(dataclasses.replace(CONFIGS["C2"], dtype="fp32"), 5, 2)
+
     line = {
         "metric": METRIC,
         "value": r["tokens_per_s"],
@@ -264,6 +323,7 @@ def main() -> int:
         "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
         "hbm_gbs": hbm,
         "decode_int8": decode,
+        "backward_fp32": backward,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

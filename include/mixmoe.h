@@ -163,6 +163,23 @@ int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t r
                                float eps, float aux_weight, float* x_out, float* aux,
                                float* entropy);
 
+/* Backward of op 74 (the gradients MLX's autodiff takes through
+ * gpu/ir.cpp:1073-1164; the reference exercises them in
+ * gpu/moe_feed_forward_test.go:84-151), for ops with fp32 compute.  Given
+ * x [rows, D] fp32 and the upstream gradients d_delta [rows, D], d_aux and
+ * d_entropy (scalars), runs the forward on x (routing held fixed, as top-k
+ * indices carry no gradient) and writes dx [rows, D], d_router_w [D, E] and
+ * d_experts: the expert weight gradients in Op.Inputs order (per expert
+ * w_gate, w_up, w_down -- or w_up, w_down -- each in x.W layout, as
+ * mxm_moe_set_input takes them).  Device pointers, asynchronous. */
+int mxm_moe_backward(int64_t op, const void* x, int x_dtype, int64_t rows, const float* d_delta,
+                     float d_aux, float d_entropy, float* dx, float* d_router_w, float* d_experts);
+
+/* Same with host buffers; synchronous. */
+int mxm_moe_backward_host(int64_t op, const void* x, int x_dtype, int64_t rows,
+                          const float* d_delta, float d_aux, float d_entropy, float* dx,
+                          float* d_router_w, float* d_experts);
+
 /* Wait for all work queued on the op's stream. */
 int mxm_moe_synchronize(int64_t op);
 

@@ -59,6 +59,10 @@ SIGNATURES = {
     "mxm_moe_block_forward_host": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int,
                                                   ctypes.c_int64, _VP, _VP, ctypes.c_int,
                                                   ctypes.c_float, ctypes.c_float, _VP, _VP, _VP]),
+    "mxm_moe_backward": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64, _VP,
+                                        ctypes.c_float, ctypes.c_float, _VP, _VP, _VP]),
+    "mxm_moe_backward_host": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64,
+                                             _VP, ctypes.c_float, ctypes.c_float, _VP, _VP, _VP]),
     "mxm_moe_synchronize": (ctypes.c_int, [ctypes.c_int64]),
     "mxm_moe_routing": (ctypes.c_int, [ctypes.c_int64, _VP, _VP, _VP, _VP, _VP, ctypes.c_int]),
     "mxm_moe_probs": (ctypes.c_int, [ctypes.c_int64, _VP]),

@@ -26,6 +26,7 @@ SOURCES = [
     "mxm_decode.hip",
     "mxm_prep.hip",
     "mxm_block.hip",
+    "mxm_backward.hip",
     "mxm_abi.hip",
 ]
 ARCH = os.environ.get("MIXMOE_OFFLOAD_ARCH", "gfx950")

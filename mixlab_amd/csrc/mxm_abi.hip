@@ -97,6 +97,11 @@ struct MoeOp {
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
       tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
+  // backward (fp32 flow): recomputed intermediates, transposed weights
+  bool keep_probs = false, bw_ready = false;
+  DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
+      bw_dlogits, bw_dxr, bw_w1t, bw_w1bt, bw_w2t, bw_wrt, bw_one;
+  int32_t bw_one_host[4] = {0, 0, 0, 0};
   size_t ws_bytes = 0;
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
@@ -249,7 +254,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   ra.tile_counts = o.tile_counts.as<int32_t>();
   ra.tile_psum = o.tile_psum.as<float>();
   ra.tile_ent = o.tile_ent.as<float>();
-  ra.probs_out = o.debug_probs ? o.probs.as<float>() : nullptr;
+  ra.probs_out = (o.debug_probs || o.keep_probs) ? o.probs.as<float>() : nullptr;
   ra.logits_scratch = o.logits.as<float>();
   mxm_launch_router(ra, o.bf16, st);
   HIPCK(hipGetLastError());
@@ -785,6 +790,140 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
     HIPCK(hipStreamSynchronize(op->stream));
     if (aux) *aux = res[0];
     if (entropy) *entropy = res[1];
+    return MXM_OK;
+  });
+}
+
+// Backward of op 74 (fp32 flow): a forward on x (keeping the router
+// probabilities), then mxm_launch_backward.  d_experts receives the expert
+// weight gradients in Op.Inputs order (per expert gate, up, down -- or up,
+// down -- in x.W layout).
+void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
+                  float d_ent, float* dx, float* dwr, float* dw) {
+  if (o.bf16 || o.q8)
+    fail("OP_MOE_FEED_FORWARD backward is implemented for the fp32 compute dtype");
+  if (x_dtype != MXM_DTYPE_F32) fail("OP_MOE_FEED_FORWARD backward takes fp32 x");
+  if (!x || !d_delta || !dx || !dwr || !dw) fail("OP_MOE_FEED_FORWARD backward pointers must be non-NULL");
+  if (!o.ws_ready) alloc_workspace(o);
+  const size_t N = o.N, D = o.D, E = o.E, F = o.F, NK = (size_t)o.N * o.K;
+  if (!o.probs.p) o.probs.alloc(N * E * 4);
+  if (!o.bw_ready) {
+    o.bw_delta.alloc(N * D * 4);
+    o.bw_xp.alloc(NK * D * 4);
+    o.bw_dy.alloc(NK * D * 4);
+    o.bw_dxg.alloc(NK * D * 4);
+    o.bw_dxu.alloc(NK * D * 4);
+    o.bw_g.alloc(NK * F * 4);
+    o.bw_u.alloc(NK * F * 4);
+    o.bw_h.alloc(NK * F * 4);
+    o.bw_dh.alloc(NK * F * 4);
+    o.bw_dg.alloc(NK * F * 4);
+    o.bw_du.alloc(NK * F * 4);
+    o.bw_dgates.alloc(NK * 4);
+    o.bw_dlogits.alloc(N * E * 4);
+    o.bw_dxr.alloc(N * D * 4);
+    o.bw_w1t.alloc(E * D * F * 4);
+    o.bw_w1bt.alloc(E * D * F * 4);
+    o.bw_w2t.alloc(E * D * F * 4);
+    o.bw_wrt.alloc(D * E * 4);
+    o.bw_one.alloc(16);
+    o.bw_one_host[1] = o.N;
+    o.bw_one_host[3] = (o.N + 63) / 64;
+    HIPCK(hipMemcpyAsync(o.bw_one.p, o.bw_one_host, 16, hipMemcpyHostToDevice, o.stream));
+    o.bw_ready = true;
+  }
+  o.keep_probs = true;
+  run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr);
+  o.keep_probs = false;
+  BackwardArgs b{};
+  b.N = o.N;
+  b.D = o.D;
+  b.E = o.E;
+  b.K = o.K;
+  b.F = o.F;
+  b.etype = o.etype;
+  b.act = o.act;
+  b.wpe = o.wpe;
+  b.max_mtiles = o.max_mtiles2;
+  b.slope = o.slope;
+  b.x = static_cast<const float*>(x);
+  b.top_idx = o.top_idx.as<int32_t>();
+  b.gates = o.gates.as<float>();
+  b.slot_pos = o.slot_pos.as<int32_t>();
+  b.perm = o.perm.as<int32_t>();
+  b.counts = o.counts.as<int32_t>();
+  b.offsets = o.offsets.as<int32_t>();
+  b.mstart = o.mstart2.as<int32_t>();
+  b.probs = o.probs.as<float>();
+  b.Y = o.Y.as<float>();
+  b.wr = o.router.as<float>();
+  b.w1 = o.w1.as<float>();
+  b.w1b = o.w1b.as<float>();
+  b.w2 = o.w2.as<float>();
+  b.d_delta = d_delta;
+  b.d_aux = d_aux;
+  b.d_ent = d_ent;
+  b.xp = o.bw_xp.as<float>();
+  b.g = o.bw_g.as<float>();
+  b.u = o.bw_u.as<float>();
+  b.h = o.bw_h.as<float>();
+  b.dy = o.bw_dy.as<float>();
+  b.dh = o.bw_dh.as<float>();
+  b.dg = o.bw_dg.as<float>();
+  b.du = o.bw_du.as<float>();
+  b.dxg = o.bw_dxg.as<float>();
+  b.dxu = o.bw_dxu.as<float>();
+  b.dgates = o.bw_dgates.as<float>();
+  b.dlogits = o.bw_dlogits.as<float>();
+  b.dxr = o.bw_dxr.as<float>();
+  b.w1t = o.bw_w1t.as<float>();
+  b.w1bt = o.bw_w1bt.as<float>();
+  b.w2t = o.bw_w2t.as<float>();
+  b.wrt = o.bw_wrt.as<float>();
+  b.one = o.bw_one.as<int32_t>();
+  b.dx = dx;
+  b.dwr = dwr;
+  b.dw = dw;
+  mxm_launch_backward(b, o.stream);
+  HIPCK(hipGetLastError());
+}
+
+int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const float* d_delta,
+                     float d_aux, float d_entropy, float* dx, float* d_router_w, float* d_experts) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    run_backward(*op, x, x_dtype, d_delta, d_aux, d_entropy, dx, d_router_w, d_experts);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_backward_host(int64_t h, const void* x, int x_dtype, int64_t rows,
+                          const float* d_delta, float d_aux, float d_entropy, float* dx,
+                          float* d_router_w, float* d_experts) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !d_delta || !dx || !d_router_w || !d_experts)
+      fail("OP_MOE_FEED_FORWARD backward pointers must be non-NULL");
+    if (x_dtype != MXM_DTYPE_F32) fail("OP_MOE_FEED_FORWARD backward takes fp32 x");
+    const size_t ND = (size_t)op->N * op->D * 4;
+    const size_t nw = (size_t)op->E * op->wpe * op->D * op->F * 4;
+    DevBuf dx_, dd_, ddx_, dwr_, dw_;
+    dx_.alloc(ND);
+    dd_.alloc(ND);
+    ddx_.alloc(ND);
+    dwr_.alloc((size_t)op->D * op->E * 4);
+    dw_.alloc(nw);
+    HIPCK(hipMemcpyAsync(dx_.p, x, ND, hipMemcpyHostToDevice, op->stream));
+    HIPCK(hipMemcpyAsync(dd_.p, d_delta, ND, hipMemcpyHostToDevice, op->stream));
+    run_backward(*op, dx_.p, x_dtype, dd_.as<float>(), d_aux, d_entropy, ddx_.as<float>(),
+                 dwr_.as<float>(), dw_.as<float>());
+    HIPCK(hipMemcpyAsync(dx, ddx_.p, ND, hipMemcpyDeviceToHost, op->stream));
+    HIPCK(hipMemcpyAsync(d_router_w, dwr_.p, (size_t)op->D * op->E * 4, hipMemcpyDeviceToHost,
+                         op->stream));
+    HIPCK(hipMemcpyAsync(d_experts, dw_.p, nw, hipMemcpyDeviceToHost, op->stream));
+    HIPCK(hipStreamSynchronize(op->stream));
     return MXM_OK;
   });
 }

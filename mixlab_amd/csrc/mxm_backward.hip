@@ -1,0 +1,311 @@
+// Backward of the MoE feed-forward op (gpu/ir.cpp:1073-1164 differentiated
+// as MLX's autodiff does; the reference checks it with
+// gpu/moe_feed_forward_test.go:84-151), fp32 flow.
+//
+// With dD = dL/d(delta) and the routing of the forward held fixed:
+//   gate gradient   dg[n,k]  = <dD[n], y_k[n]>
+//   renorm          g_k = tp_k / max(S, 1e-12), S = sum_k tp_k:
+//                   dtp_k = sum_j tp_j (dg_k - dg_j) / S^2  (S > 1e-12; else dg_k / 1e-12)
+//   probabilities   dp[n,e] = sum_k [top_idx = e] dtp_k
+//                           + d_aux * E * counts[e] / (K N) / N
+//                           - d_ent / N * (log max(p, 1e-12) + [p > 1e-12])
+//   softmax         dlogits = p * (dp - <p, dp>)
+//   router          dWr = x^T dlogits,  dx += dlogits Wr^T
+//   experts (per routed slot, y = h W_down, h = act(g) * u or act(u)):
+//                   dY = gate * dD, dH = dY W_down^T, dW_down = H^T dY,
+//                   (dG, dU) from the activation's derivative,
+//                   dx += dG W_gate^T + dU W_up^T,
+//                   dW_gate = X^T dG, dW_up = X^T dU.
+// Expert products run on the SIMT grouped GEMM (the forward's kernel, rows
+// grouped by expert through the forward's offsets); the weight gradients
+// reduce over each expert's rows in ascending order (wgrad_kernel), so every
+// result is deterministic.
+#include "mxm_kernels.h"
+
+namespace {
+
+__global__ void gather_rows_kernel(const float* __restrict__ x, const int32_t* __restrict__ perm,
+                                   int D, float* __restrict__ out) {
+  const int s = blockIdx.x;
+  const float* src = x + (size_t)perm[s] * D;
+  float* dst = out + (size_t)s * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
+}
+
+// dst[b][c][r] = src[b][r][c]
+__global__ void transpose_f32_kernel(const float* __restrict__ src, int R, int C,
+                                     float* __restrict__ dst) {
+  __shared__ float t[32][33];
+  const size_t off = (size_t)blockIdx.z * R * C;
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int r = r0 + i, c = c0 + threadIdx.x;
+    t[i][threadIdx.x] = (r < R && c < C) ? src[off + (size_t)r * C + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int c = c0 + i, r = r0 + threadIdx.x;
+    if (r < R && c < C) dst[off + (size_t)c * R + r] = t[threadIdx.x][i];
+  }
+}
+
+// one wave per slot: dgates[n*K+k] = <dD[n], Y[slot_pos]>
+__global__ __launch_bounds__(256) void dgates_kernel(BackwardArgs a) {
+  const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (s >= a.N * a.K) return;
+  const int n = s / a.K;
+  const float* dd = a.d_delta + (size_t)n * a.D;
+  const float* y = a.Y + (size_t)a.slot_pos[s] * a.D;
+  float acc = 0.0f;
+  for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], y[d], acc);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc = acc + mxm_xor_lane_f(acc, m);
+  if (lane == 0) a.dgates[s] = acc;
+}
+
+// one thread per token: renorm, aux / entropy and softmax backward
+__global__ void router_bw_kernel(BackwardArgs a) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= a.N) return;
+  const int K = a.K, E = a.E;
+  const float* p = a.probs + (size_t)n * E;
+  const int32_t* sel = a.top_idx + (size_t)n * K;
+  const float* dg = a.dgates + (size_t)n * K;
+  float S = 0.0f;
+  for (int k = 0; k < K; ++k) S = S + p[sel[k]];
+  const float Sc = fmaxf(S, 1e-12f);
+  const bool renorm = S > 1e-12f;
+  // d(tp_k) = dg_k / S - sum_j dg_j tp_j / S^2 = sum_j tp_j (dg_k - dg_j) / S^2,
+  // the second form free of the cancellation of the first (exactly 0 at K = 1)
+  auto dtp_of = [&](int k) {
+    if (!renorm) return dg[k] / Sc;
+    float t = 0.0f;
+    for (int j = 0; j < K; ++j) t = t + p[sel[j]] * (dg[k] - dg[j]);
+    return t / (Sc * Sc);
+  };
+  const float inv_n = 1.0f / (float)a.N;
+  const float aux_c = a.d_aux * (float)E * inv_n / ((float)K * (float)a.N);
+  auto dp_of = [&](int e) {
+    const float pe = p[e];
+    float v = aux_c * (float)a.counts[e];
+    v = v - a.d_ent * inv_n * (logf(fmaxf(pe, 1e-12f)) + (pe > 1e-12f ? 1.0f : 0.0f));
+    for (int k = 0; k < K; ++k)
+      if (sel[k] == e) v = v + dtp_of(k);
+    return v;
+  };
+  float s = 0.0f;
+  for (int e = 0; e < E; ++e) s = s + p[e] * dp_of(e);
+  float* out = a.dlogits + (size_t)n * E;
+  for (int e = 0; e < E; ++e) out[e] = p[e] * (dp_of(e) - s);
+}
+
+// dY[slot_pos] = gate * dD[n]
+__global__ void dy_kernel(BackwardArgs a) {
+  const int s = blockIdx.x;
+  const int n = s / a.K;
+  const float g = a.gates[s];
+  const float* dd = a.d_delta + (size_t)n * a.D;
+  float* dst = a.dy + (size_t)a.slot_pos[s] * a.D;
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x) dst[d] = g * dd[d];
+}
+
+__device__ __forceinline__ float gelu_t(float v, float& deriv) {
+  const float c = 0.7978845608f, k = 0.044715f;
+  const float in = c * (v + k * v * v * v);
+  const float t = tanhf(in);
+  deriv = 0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * c * (1.0f + 3.0f * k * v * v);
+  return 0.5f * v * (1.0f + t);
+}
+
+// activation backward per element of [N*K, F]; recomputes H
+__global__ void act_bw_kernel(BackwardArgs a, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float dh = a.dh[i];
+    if (a.etype == MXM_EXPERT_MLP) {
+      const float u = a.u[i];
+      float h, d;
+      switch (a.act) {
+        case MXM_ACT_SILU: {
+          const float sg = 1.0f / (1.0f + expf(-u));
+          h = u * sg;
+          d = sg * (1.0f + u * (1.0f - sg));
+          break;
+        }
+        case MXM_ACT_GELU:
+          h = gelu_t(u, d);
+          break;
+        case MXM_ACT_RELU:
+          h = u > 0.0f ? u : 0.0f;
+          d = u > 0.0f ? 1.0f : 0.0f;
+          break;
+        default: {
+          const float y = u > 0.0f ? u : u * a.slope;
+          h = y * y;
+          d = 2.0f * y * (u > 0.0f ? 1.0f : a.slope);
+          break;
+        }
+      }
+      a.h[i] = h;
+      a.du[i] = dh * d;
+    } else {
+      const float g = a.g[i], u = a.u[i];
+      float act, d;
+      if (a.etype == MXM_EXPERT_SWIGLU) {
+        act = 1.0f / (1.0f + expf(-g));
+        d = act * (1.0f - act);
+      } else {
+        act = gelu_t(g, d);
+      }
+      a.h[i] = act * u;
+      a.dg[i] = dh * u * d;
+      a.du[i] = dh * act;
+    }
+  }
+}
+
+// Weight gradient: for each segment e (rows offsets[e] .. offsets[e+1]-1),
+// out[e][i][j] = sum_r A[r][i] * B[r][j], rows in ascending order.
+constexpr int WG_T = 64, WG_R = 16;
+__global__ __launch_bounds__(256) void wgrad_kernel(const float* __restrict__ A, int M,
+                                                    const float* __restrict__ B, int Nn,
+                                                    const int32_t* __restrict__ offsets,
+                                                    float* __restrict__ out, size_t out_stride) {
+  __shared__ float As[WG_R][WG_T + 4];
+  __shared__ float Bs[WG_R][WG_T + 4];
+  const int e = blockIdx.z;
+  const int i0 = blockIdx.y * WG_T, j0 = blockIdx.x * WG_T;
+  const int r0 = offsets[e], r1 = offsets[e + 1];
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int rb = r0; rb < r1; rb += WG_R) {
+    __syncthreads();
+    for (int q = tid; q < WG_R * WG_T; q += 256) {
+      const int rr = q / WG_T, c = q % WG_T;
+      const int r = rb + rr;
+      As[rr][c] = (r < r1 && i0 + c < M) ? A[(size_t)r * M + i0 + c] : 0.0f;
+      Bs[rr][c] = (r < r1 && j0 + c < Nn) ? B[(size_t)r * Nn + j0 + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < WG_R; ++rr) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[rr][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[rr][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+    }
+  }
+  float* o = out + (size_t)e * out_stride;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ii = i0 + ty * 4 + i;
+    if (ii >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int jj = j0 + tx * 4 + j;
+      if (jj < Nn) o[(size_t)ii * Nn + jj] = acc[i][j];
+    }
+  }
+}
+
+// dx[n] = dxr[n] + sum_k (dxg + dxu)[slot_pos(n, k)], k ascending
+__global__ void dx_kernel(BackwardArgs a) {
+  const int n = blockIdx.x;
+  const bool glu = a.etype != MXM_EXPERT_MLP;
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+    float acc = a.dxr[(size_t)n * a.D + d];
+    for (int k = 0; k < a.K; ++k) {
+      const size_t p = (size_t)a.slot_pos[(size_t)n * a.K + k] * a.D + d;
+      const float v = glu ? a.dxg[p] + a.dxu[p] : a.dxu[p];
+      acc = acc + v;
+    }
+    a.dx[(size_t)n * a.D + d] = acc;
+  }
+}
+
+void transpose_batch(const float* src, int batch, int R, int C, float* dst, hipStream_t s) {
+  if (batch <= 0 || R <= 0 || C <= 0) return;
+  hipLaunchKernelGGL(transpose_f32_kernel, dim3((C + 31) / 32, (R + 31) / 32, batch), dim3(32, 8),
+                     0, s, src, R, C, dst);
+}
+
+void grouped(const float* A, const float* B, float* out, int Kd, int NC, const int32_t* offsets,
+             const int32_t* mstart, int E, int max_mtiles, hipStream_t s) {
+  GemmArgs g{};
+  g.mode = MXM_GEMM_DOWN;
+  g.a = A;
+  g.b0 = B;
+  g.out = out;
+  g.offsets = offsets;
+  g.mstart = mstart;
+  g.E = E;
+  g.Kd = Kd;
+  g.Ncols = NC;
+  g.max_mtiles = max_mtiles;
+  g.y_bf16 = false;
+  mxm_launch_gemm_simt(g, false, s);
+}
+
+void wgrad(const float* A, int M, const float* B, int Nn, const int32_t* offsets, int E,
+           float* out, size_t out_stride, hipStream_t s) {
+  hipLaunchKernelGGL(wgrad_kernel, dim3((Nn + WG_T - 1) / WG_T, (M + WG_T - 1) / WG_T, E),
+                     dim3(256), 0, s, A, M, B, Nn, offsets, out, out_stride);
+}
+
+}  // namespace
+
+void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
+  const int N = a.N, D = a.D, E = a.E, K = a.K, F = a.F, NK = a.N * a.K;
+  const bool glu = a.etype != MXM_EXPERT_MLP;
+  const size_t DF = (size_t)D * F;
+  if (NK <= 0) return;
+  // gathered rows and the transposed weights
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(NK), dim3(256), 0, s, a.x, a.perm, D, a.xp);
+  transpose_batch(a.w2, E, F, D, a.w2t, s);   // [E][D][F]
+  transpose_batch(a.w1, E, D, F, a.w1t, s);   // [E][F][D]
+  if (glu) transpose_batch(a.w1b, E, D, F, a.w1bt, s);
+  transpose_batch(a.wr, 1, D, E, a.wrt, s);   // [E][D]
+  // projections of the forward (recomputed)
+  if (glu) {
+    grouped(a.xp, a.w1, a.g, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
+    grouped(a.xp, a.w1b, a.u, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
+  } else {
+    grouped(a.xp, a.w1, a.u, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
+  }
+  // gates and router
+  hipLaunchKernelGGL(dgates_kernel, dim3((NK + 3) / 4), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
+  // down projection
+  hipLaunchKernelGGL(dy_kernel, dim3(NK), dim3(256), 0, s, a);
+  grouped(a.dy, a.w2t, a.dh, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
+  const size_t total = (size_t)NK * F;
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(act_bw_kernel, dim3(blocks), dim3(256), 0, s, a, total);
+  // input gradient
+  if (glu) grouped(a.dg, a.w1t, a.dxg, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
+  grouped(a.du, glu ? a.w1bt : a.w1t, a.dxu, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
+  grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
+  hipLaunchKernelGGL(dx_kernel, dim3(N), dim3(256), 0, s, a);
+  // weight gradients (per expert blocks of a.dw in Op.Inputs order)
+  const size_t stride = (size_t)a.wpe * DF;
+  if (glu) {
+    wgrad(a.xp, D, a.dg, F, a.offsets, E, a.dw, stride, s);            // gate
+    wgrad(a.xp, D, a.du, F, a.offsets, E, a.dw + DF, stride, s);       // up
+    wgrad(a.h, F, a.dy, D, a.offsets, E, a.dw + 2 * DF, stride, s);    // down
+  } else {
+    wgrad(a.xp, D, a.du, F, a.offsets, E, a.dw, stride, s);            // up
+    wgrad(a.h, F, a.dy, D, a.offsets, E, a.dw + DF, stride, s);        // down
+  }
+  wgrad(a.x, D, a.dlogits, E, a.one, 1, a.dwr, 0, s);                  // router
+}

@@ -212,3 +212,39 @@ void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, in
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s);
 void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s);
 int mxm_q8_max_kd();
+
+// Backward of op 74 (fp32 flow).  Uses the routing, probabilities and Y of
+// a forward on the same x; every other intermediate is recomputed.  All
+// matrices are fp32 in the x.W layout of the forward's SIMT family.
+struct BackwardArgs {
+  int N, D, E, K, F, etype, act, wpe, max_mtiles;
+  float slope;
+  // forward state
+  const float* x;            // [N, D]
+  const int32_t* top_idx;    // [N, K]
+  const float* gates;        // [N, K]
+  const int32_t* slot_pos;   // [N*K]
+  const int32_t* perm;       // [N*K]
+  const int32_t* counts;     // [E]
+  const int32_t* offsets;    // [E + 1]
+  const int32_t* mstart;     // [E + 1] row tiles of 64
+  const float* probs;        // [N, E]
+  const float* Y;            // [N*K, D]
+  const float* wr;           // [D, E]
+  const float* w1;           // [E][D][F] gate (GLU) or up (MLP)
+  const float* w1b;          // [E][D][F] up (GLU)
+  const float* w2;           // [E][F][D] down
+  // upstream gradients
+  const float* d_delta;      // [N, D]
+  float d_aux, d_ent;
+  // scratch
+  float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
+  float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D]
+  float *w1t, *w1bt, *w2t, *wrt;                          // transposed weights
+  int32_t* one;                                           // [4]: offsets/mstart of one segment
+  // outputs
+  float* dx;                 // [N, D]
+  float* dwr;                // [D, E]
+  float* dw;                 // per expert, Op.Inputs order, x.W layout
+};
+void mxm_launch_backward(const BackwardArgs& a, hipStream_t s);

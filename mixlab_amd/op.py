@@ -152,6 +152,33 @@ class MoEFeedForward:
                                              vp(aux_ptr), vp(ent_ptr))
         _lib.check(rc, "mxm_moe_block_forward")
 
+    def backward_host(self, x: np.ndarray, d_delta: np.ndarray, d_aux: float = 0.0,
+                      d_entropy: float = 0.0):
+        """Gradients of op 74 (fp32 compute): returns (dx [B*T, D],
+        d_router_w [D, E], d_experts: per expert a list of the weight
+        gradients in Op.Inputs order, x.W layout)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        dd = np.ascontiguousarray(d_delta, dtype=np.float32)
+        wpe = 2 if self.expert_type == MOE_EXPERT_MLP else 3
+        dx = np.empty_like(x)
+        dwr = np.empty((self.D, self.E), np.float32)
+        dw = np.empty(self.E * wpe * self.D * self.F, np.float32)
+        vp = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
+        rc = self._lib.mxm_moe_backward_host(self.handle, vp(x), _lib.MXM_DTYPE_F32, x.shape[0],
+                                             vp(dd), float(d_aux), float(d_entropy), vp(dx),
+                                             vp(dwr), vp(dw))
+        _lib.check(rc, "mxm_moe_backward_host")
+        D, F = self.D, self.F
+        shapes = [(D, F), (D, F), (F, D)] if wpe == 3 else [(D, F), (F, D)]
+        experts, off = [], 0
+        for _ in range(self.E):
+            ws = []
+            for shp in shapes:
+                ws.append(dw[off:off + D * F].reshape(shp))
+                off += D * F
+            experts.append(ws)
+        return dx, dwr, experts
+
     def synchronize(self) -> None:
         _lib.check(self._lib.mxm_moe_synchronize(self.handle), "mxm_moe_synchronize")
 

@@ -348,3 +348,35 @@ def test_moe_block_from_checkpoint(gpu_lib, tmp_path, flow):
     else:
         assert same_bits(out, want["x_out"])
     assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+
+
+@pytest.mark.parametrize("etype,act,slope,K", [(0, 0, 0.0, 2), (1, 1, 0.0, 2), (2, 0, 0.0, 2),
+                                               (2, 1, 0.0, 3), (2, 2, 0.0, 2), (2, 3, 0.4, 2),
+                                               (0, 0, 0.0, 6), (0, 0, 0.0, 1)])
+def test_backward_fp32(gpu_lib, etype, act, slope, K):
+    """mxm_moe_backward against the float64 restatement (oracle/backward.py,
+    pinned by finite differences), routing held at the forward's."""
+    from mixlab_amd.op import MoEFeedForward
+    from oracle.backward import backward64
+
+    B, T, D, E, F = 2, 96, 64, 6, 96
+    x, wr, experts = random_case(61 + etype * 7 + act + K, B * T, D, E, F, expert_type=etype,
+                                 wscale=0.1)
+    rng = np.random.default_rng(62)
+    dD = rng.standard_normal((B * T, D), dtype=np.float32)
+    with MoEFeedForward([B, T, D, E, K, etype, F, act], [slope], compute_dtype="fp32") as op:
+        op.set_weights(wr, experts)
+        dx, dwr, dexp = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
+        routing = op.routing()
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope)
+    assert_routing_equal(routing, want)
+    rdx, rdwr, rdexp = backward64(x, wr, experts, want["top_idx"].astype(np.int64), dD, 0.3, -0.2,
+                                  etype, act, slope)
+    assert rel_l2(dx, rdx) <= 1e-4
+    assert rel_l2(dwr, rdwr) <= 1e-4
+    for e in range(E):
+        for m in range(len(experts[e])):
+            if np.any(rdexp[e][m]):
+                assert rel_l2(dexp[e][m], rdexp[e][m]) <= 1e-4, (e, m)
+            else:
+                assert not np.any(dexp[e][m]), (e, m)
