@@ -380,3 +380,24 @@ def test_backward_fp32(gpu_lib, etype, act, slope, K):
                 assert rel_l2(dexp[e][m], rdexp[e][m]) <= 1e-4, (e, m)
             else:
                 assert not np.any(dexp[e][m]), (e, m)
+
+
+@pytest.mark.parametrize("E", [65, 128, 200, 256])
+@pytest.mark.parametrize("N", [130, 1500])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_many_experts(gpu_lib, E, N, bf16):
+    """Expert counts past one lane per expert (2 and 4 per lane) on both
+    router paths: the small-batch logits kernel (N <= 1024) and the tiled one;
+    probabilities and routing bit-exact."""
+    D, F, K = 128, 128, 4
+    x, wr, experts = random_case(70 + E + N, N, D, E, F)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=bf16,
+                                             want_probs=True)
+    want = run_oracle(x, wr, experts, K=K, bf16=bf16)
+    assert same_bits(routing["probs"], want["probs"])
+    assert_routing_equal(routing, want)
+    assert rel_l2(delta, want["delta"]) <= (BF16_TOL if bf16 else FP32_TOL)
+    assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"])
