@@ -86,6 +86,10 @@ struct MoeOp {
   // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
   // bf16 [E][2F or F][D] (GLU interleaved), w2 = bf16 [E][D][F].
   DevBuf router, w1, w1b, w2;
+  // decode-sized batches: router_w in fp32, lane-interleaved (RouteSmallArgs::wr_t)
+  bool small_route = false;
+  int ldw = 0;
+  DevBuf router_t;
   // int8 family: q1 = gate (GLU) or up (MLP), q1b = up (GLU), q2 = down, in
   // the 1 KB block layout; s1, s1b, s2 = fp32 per-output-channel scales.
   DevBuf q1, q1b, q2, s1, s1b, s2;
@@ -95,7 +99,8 @@ struct MoeOp {
   bool ws_ready = false;
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
-      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits;
+      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits, tok_ent,
+      ticket;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
   // backward (fp32 flow): recomputed intermediates, transposed weights
   bool keep_probs = false, bw_ready = false;
@@ -187,7 +192,12 @@ void alloc_workspace(MoeOp& o) {
   A(o.H, NK * (size_t)o.F * esz);
   A(o.Y, NK * (size_t)o.D * esz);
   if (o.debug_probs) A(o.probs, N * E * 4);
-  if (N <= MXM_SMALL_BATCH) A(o.logits, N * E * 4);
+  if (o.small_route) {
+    A(o.logits, N * E * 4);  // probabilities when no caller copy is kept
+    A(o.tok_ent, N * 4);
+    A(o.ticket, 4);
+    HIPCK(hipMemsetAsync(o.ticket.p, 0, 4, o.stream));
+  }
   o.ws_bytes = total;
   o.ws_ready = true;
 }
@@ -241,59 +251,92 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   };
 
   mark(0);
-  RouterArgs ra{};
-  ra.x = xin;
-  ra.wr = o.router.p;
-  ra.N = o.N;
-  ra.D = o.D;
-  ra.E = o.E;
-  ra.K = o.K;
-  ra.top_idx = o.top_idx.as<int32_t>();
-  ra.gates = o.gates.as<float>();
-  ra.slot_rank = o.slot_rank.as<int32_t>();
-  ra.tile_counts = o.tile_counts.as<int32_t>();
-  ra.tile_psum = o.tile_psum.as<float>();
-  ra.tile_ent = o.tile_ent.as<float>();
-  ra.probs_out = (o.debug_probs || o.keep_probs) ? o.probs.as<float>() : nullptr;
-  ra.logits_scratch = o.logits.as<float>();
-  mxm_launch_router(ra, o.bf16, st);
-  HIPCK(hipGetLastError());
-
-  mark(1);
+  float* probs_keep = (o.debug_probs || o.keep_probs) ? o.probs.as<float>() : nullptr;
   ScanArgs sa{};
-  sa.tile_counts = ra.tile_counts;
-  sa.tile_psum = ra.tile_psum;
-  sa.tile_ent = ra.tile_ent;
-  sa.N = o.N;
-  sa.E = o.E;
-  sa.K = o.K;
-  sa.ntiles = o.ntiles;
-  sa.bm1 = o.bm1;
-  sa.bm2 = o.bm2;
   sa.counts = o.counts.as<int32_t>();
   sa.offsets = o.offsets.as<int32_t>();
-  sa.tile_base = o.tile_base.as<int32_t>();
   sa.mstart1 = o.mstart1.as<int32_t>();
   sa.mstart2 = o.mstart2.as<int32_t>();
-  sa.aux = aux_p;
-  sa.entropy = ent_p;
-  sa.aux_weight = blk ? blk->aux_weight : 1.0f;
-  sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
-  mxm_launch_scan(sa, o.bf16, st);
-  HIPCK(hipGetLastError());
-
-  mark(2);
   ScatterArgs sc{};
-  sc.top_idx = ra.top_idx;
-  sc.slot_rank = ra.slot_rank;
-  sc.tile_base = sa.tile_base;
-  sc.N = o.N;
-  sc.K = o.K;
-  sc.ntiles = o.ntiles;
   sc.perm = o.perm.as<int32_t>();
   sc.slot_pos = o.slot_pos.as<int32_t>();
-  mxm_launch_scatter(sc, st);
-  HIPCK(hipGetLastError());
+  if (o.small_route) {
+    // one launch: router, scan and scatter (stages 1 and 2 are empty)
+    RouteSmallArgs rs{};
+    rs.x = xin;
+    rs.wr_t = o.router_t.as<float>();
+    rs.ldw = o.ldw;
+    rs.N = o.N;
+    rs.D = o.D;
+    rs.E = o.E;
+    rs.K = o.K;
+    rs.bm1 = o.bm1;
+    rs.bm2 = o.bm2;
+    rs.top_idx = o.top_idx.as<int32_t>();
+    rs.gates = o.gates.as<float>();
+    rs.probs = probs_keep ? probs_keep : o.logits.as<float>();
+    rs.tok_ent = o.tok_ent.as<float>();
+    rs.counts = sa.counts;
+    rs.offsets = sa.offsets;
+    rs.mstart1 = sa.mstart1;
+    rs.mstart2 = sa.mstart2;
+    rs.perm = sc.perm;
+    rs.slot_pos = sc.slot_pos;
+    rs.aux = aux_p;
+    rs.entropy = ent_p;
+    rs.aux_weight = blk ? blk->aux_weight : 1.0f;
+    rs.aux_scaled = blk ? blk->aux_scaled : nullptr;
+    rs.ticket = o.ticket.as<int32_t>();
+    mxm_launch_route_small(rs, o.bf16, st);
+    HIPCK(hipGetLastError());
+    mark(1);
+    mark(2);
+  } else {
+    RouterArgs ra{};
+    ra.x = xin;
+    ra.wr = o.router.p;
+    ra.N = o.N;
+    ra.D = o.D;
+    ra.E = o.E;
+    ra.K = o.K;
+    ra.top_idx = o.top_idx.as<int32_t>();
+    ra.gates = o.gates.as<float>();
+    ra.slot_rank = o.slot_rank.as<int32_t>();
+    ra.tile_counts = o.tile_counts.as<int32_t>();
+    ra.tile_psum = o.tile_psum.as<float>();
+    ra.tile_ent = o.tile_ent.as<float>();
+    ra.probs_out = probs_keep;
+    mxm_launch_router(ra, o.bf16, st);
+    HIPCK(hipGetLastError());
+
+    mark(1);
+    sa.tile_counts = ra.tile_counts;
+    sa.tile_psum = ra.tile_psum;
+    sa.tile_ent = ra.tile_ent;
+    sa.N = o.N;
+    sa.E = o.E;
+    sa.K = o.K;
+    sa.ntiles = o.ntiles;
+    sa.bm1 = o.bm1;
+    sa.bm2 = o.bm2;
+    sa.tile_base = o.tile_base.as<int32_t>();
+    sa.aux = aux_p;
+    sa.entropy = ent_p;
+    sa.aux_weight = blk ? blk->aux_weight : 1.0f;
+    sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
+    mxm_launch_scan(sa, o.bf16, st);
+    HIPCK(hipGetLastError());
+
+    mark(2);
+    sc.top_idx = ra.top_idx;
+    sc.slot_rank = ra.slot_rank;
+    sc.tile_base = sa.tile_base;
+    sc.N = o.N;
+    sc.K = o.K;
+    sc.ntiles = o.ntiles;
+    mxm_launch_scatter(sc, st);
+    HIPCK(hipGetLastError());
+  }
 
   mark(3);
   const bool glu = o.etype != MXM_EXPERT_MLP;
@@ -364,8 +407,8 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   mark(5);
   CombineArgs ca{};
   ca.y = o.Y.p;
-  ca.top_idx = ra.top_idx;
-  ca.gates = ra.gates;
+  ca.top_idx = o.top_idx.as<int32_t>();
+  ca.gates = o.gates.as<float>();
   ca.slot_pos = sc.slot_pos;
   ca.N = o.N;
   ca.D = o.D;
@@ -424,6 +467,9 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
       mxm_launch_to_bf16(src, dtype, o.router.as<uint16_t>(), (int64_t)n, st);
     else
       mxm_launch_to_f32(src, dtype, o.router.as<float>(), (int64_t)n, st);
+    if (o.small_route)
+      mxm_launch_router_t(o.router.p, o.bf16 ? MXM_DTYPE_BF16 : MXM_DTYPE_F32, o.D, o.E, o.ldw,
+                          o.router_t.as<float>(), st);
   } else if (o.mfma) {
     const bool glu = o.wpe == 3;
     if (j == o.wpe - 1) {
@@ -618,6 +664,11 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
+    o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K);
+    if (o->small_route) {
+      o->ldw = (o->D + 3) / 4 * 4;
+      o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * 4);
+    }
     if (o->q8) {
       o->q1.alloc(EE * DF);
       if (o->wpe == 3) o->q1b.alloc(EE * DF);

@@ -59,11 +59,43 @@ struct RouterArgs {
   float* tile_psum;      // [E, ntiles] sum of probabilities over the tile
   float* tile_ent;       // [ntiles] sum over the tile of sum_e p log max(p, 1e-12)
   float* probs_out;      // optional [N, E]
-  float* logits_scratch; // [N, E]: when set, logits come from the small-batch kernel
 };
-// Batches up to this many tokens take the small-batch logits kernel.
-#define MXM_SMALL_BATCH 1024
 void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s);
+
+// Decode-sized batches (N <= MXM_SMALL_BATCH, N*K <= MXM_SMALL_SLOTS,
+// D <= MXM_SMALL_D) route in one launch: a workgroup per token computes its
+// logits, softmax, top-k and gates, and the last workgroup to finish (an
+// atomic ticket) computes counts, offsets, row-tile prefixes, the stable
+// permutation, aux and entropy -- the work of the router, scan and scatter
+// kernels of larger batches.
+#define MXM_SMALL_BATCH 1024
+#define MXM_SMALL_SLOTS 16384
+#define MXM_SMALL_D 16384
+struct RouteSmallArgs {
+  const void* x;       // [N, D], bf16 bits or fp32
+  const float* wr_t;   // fp32 [ceil(E/64)][ldw/4][64][4]: element (g, c, l, q) =
+                       // router_w[4c + q][64g + l], zero past D or E
+  int ldw;             // D rounded up to a multiple of 4
+  int N, D, E, K;
+  int bm1, bm2;        // row-tile heights of the two grouped GEMMs
+  int32_t* top_idx;    // [N, K]
+  float* gates;        // [N, K]
+  float* probs;        // [N, E] probabilities (the caller's copy, or scratch)
+  float* tok_ent;      // [N] per-token sum_e p log max(p, 1e-12)
+  int32_t* counts;     // [E]
+  int32_t* offsets;    // [E + 1]
+  int32_t* mstart1;    // [E + 1]
+  int32_t* mstart2;    // [E + 1]
+  int32_t* perm;       // [N*K]
+  int32_t* slot_pos;   // [N*K]
+  float* aux;          // [1]
+  float* entropy;      // [1]
+  float aux_weight;
+  float* aux_scaled;   // [1] or null
+  int32_t* ticket;     // [1], zero between calls (the last workgroup resets it)
+};
+bool mxm_route_small_fits(int N, int D, int E, int K);
+void mxm_launch_route_small(const RouteSmallArgs& a, bool bf16, hipStream_t s);
 
 struct ScanArgs {
   const int32_t* tile_counts;  // [E, ntiles]
@@ -204,6 +236,8 @@ void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n
 // interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up.
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
                                uint16_t* dst, hipStream_t s);
+void mxm_launch_router_t(const void* src, int src_dtype, int D, int E, int ldw, float* dst,
+                         hipStream_t s);
 
 // int8-weight family (decode shapes): weights in the 1 KB block layout of
 // mxm_launch_shuffle_q8, fp32 scale per output channel (scale0/scale1),

@@ -3,8 +3,7 @@
 // the aux / entropy outputs (gpu/ir.cpp:1150-1162).
 //
 // One workgroup owns a tile of MXM_ROUTER_TM consecutive tokens and all E
-// experts.  (Small batches compute the logits first with logits_small_kernel,
-// one wave per token, and the tile kernel starts at phase 2.)  Phase 1 is a register-tiled SIMT product: each output logit is
+// experts.  Phase 1 is a register-tiled SIMT product: each output logit is
 // accumulated in fp32 by fmaf over d = 0..D-1 in ascending order, which is
 // the order the CPU restatement uses, so logits are bit-identical.  Phase 2
 // gives each wavefront 16 tokens: one lane per expert (lane l holds experts
@@ -14,6 +13,11 @@
 // token bitmasks' popcounts (the tile histogram) and each slot's rank among
 // the tile's tokens routed to the same expert; the scan kernel turns these
 // into the stable permutation.
+//
+// Decode-sized batches take route_small_kernel instead (one launch for the
+// router, scan and scatter; see below).  Both kernels run the per-token
+// softmax / top-k / gate code of route_token, so their routing is the same
+// bit for bit.
 #include "mxm_kernels.h"
 
 namespace {
@@ -51,11 +55,99 @@ __device__ __forceinline__ void unpack16<uint16_t>(const uint4 raw, float* f) {
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return mxm_xor_lane_f(v, m); }
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return mxm_xor_lane_i(v, m); }
 
+// Softmax, stable top-k and renormalised gates of one token on one wave
+// (gpu/ir.cpp:1107-1111).  Lane l holds experts l + 64 j (j < NJ); v[j] is
+// that expert's logit (bf16-rounded in the bf16 flow), ignored past E.  On
+// return p[j] is the expert's probability (-1 past E), lane k % 64 holds
+// pick k's expert and gate in pick_e[k / 64] and pick_g[k / 64], and the
+// result is the token's sum_e p log max(p, 1e-12) (gpu/ir.cpp:1161), summed
+// lane-wise in j order and then by the xor butterfly.
+template <bool BF16, int NJ>
+__device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int E, int K,
+                                             float (&p)[NJ], int (&pick_e)[NJ],
+                                             float (&pick_g)[NJ]) {
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (lane + 64 * j < E) m = fmaxf(m, v[j]);
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
+  float ex[NJ];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = lane + 64 * j;
+    ex[j] = (e < E) ? mxm_exp(v[j] - m) : 0.0f;
+    sum = (j == 0) ? ex[j] : sum + ex[j];
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) sum = sum + shfl_xor_f(sum, s);
+  float ent_local = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = lane + 64 * j;
+    float q = mxm_ftz(ex[j] / sum);
+    if (BF16) q = mxm_rbf(q);
+    p[j] = (e < E) ? q : -1.0f;
+    if (e < E) {
+      const float term = q * logf(fmaxf(q, 1e-12f));
+      ent_local = (j == 0) ? term : ent_local + term;
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) ent_local = ent_local + shfl_xor_f(ent_local, s);
+
+  // top-k: K rounds of argmax under (p desc, e asc).  The argmax is
+  // wave-uniform, so every lane accumulates the same running sum of the
+  // picked probabilities (k order), and lane k%64 keeps pick k in slot k/64.
+  uint32_t taken = 0u;
+  float s_top = 0.0f;
+  float my_p[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    my_p[j] = 0.0f;
+    pick_e[j] = 0;
+  }
+  for (int k = 0; k < K; ++k) {
+    float bp = -2.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !((taken >> j) & 1u) && p[j] > bp) {
+        bp = p[j];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+      const float op = shfl_xor_f(bp, s);
+      const int oe = shfl_xor_i(be, s);
+      if (op > bp || (op == bp && oe < be)) {
+        bp = op;
+        be = oe;
+      }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    s_top = (k == 0) ? bp : s_top + bp;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (k == lane + 64 * j) {
+        my_p[j] = bp;
+        pick_e[j] = be;
+      }
+  }
+  if (BF16) s_top = mxm_rbf(s_top);
+  const float den = fmaxf(s_top, 1e-12f);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) pick_g[j] = my_p[j] / den;
+  return ent_local;
+}
+
 // EPT = experts per thread in phase 1 (E padded to 16*EPT).
-template <typename TX, bool BF16, int EPT, bool VEC, bool PRE>
-__global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
-    const TX* __restrict__ x, const TX* __restrict__ wr, const float* __restrict__ logits_in,
-    int N, int D, int E, int K,
+template <typename TX, bool BF16, int EPT, bool VEC>
+__global__ __launch_bounds__(NT) void router_kernel(
+    const TX* __restrict__ x, const TX* __restrict__ wr, int N, int D, int E, int K,
     int32_t* __restrict__ top_idx, float* __restrict__ gates, int32_t* __restrict__ slot_rank,
     int32_t* __restrict__ tile_counts, float* __restrict__ tile_psum, float* __restrict__ tile_ent,
     float* __restrict__ probs_out, int ntiles) {
@@ -67,7 +159,7 @@ __global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
   constexpr int SMEM_FLOATS = STAGE_FLOATS > LG_FLOATS ? STAGE_FLOATS : LG_FLOATS;
   __shared__ float smem[SMEM_FLOATS];
   __shared__ uint32_t mask[EP][2];
-  constexpr int THREADS = PRE ? 1024 : NT;
+  constexpr int THREADS = NT;
   constexpr int NWAVE = THREADS / 64;
   __shared__ float wave_psum[NWAVE][EP];
   __shared__ float wave_ent[NWAVE];
@@ -82,16 +174,6 @@ __global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
   for (int i = tid; i < EP * 2; i += THREADS) (&mask[0][0])[i] = 0u;
 
   // ---- phase 1: logits --------------------------------------------------
-  if (PRE) {
-    // logits computed by logits_small_kernel (same accumulation order)
-    for (int i = tid; i < TM * EP; i += THREADS) {
-      const int t = i / EP, e = i % EP;
-      const int n = n0 + t;
-      const float v = (n < N && e < E) ? logits_in[(size_t)n * E + e] : 0.0f;
-      lg[t * LG_STRIDE + e] = BF16 ? mxm_rbf(v) : v;
-    }
-    __syncthreads();
-  } else {
   const int ty = tid >> 4;  // tokens ty*4 .. ty*4+3
   const int tx = tid & 15;  // experts tx*EPT .. tx*EPT+EPT-1
   float acc[4][EPT];
@@ -158,8 +240,6 @@ __global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
     }
   __syncthreads();
 
-  }
-
   // ---- phase 2: softmax, top-k, gates -----------------------------------
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -173,94 +253,29 @@ __global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
     const int n = n0 + t;
     if (n >= N) break;
     float v[NJ];
-    float m = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int e = lane + 64 * j;
       v[j] = (e < E) ? lg[t * LG_STRIDE + e] : -__builtin_inff();
-      m = fmaxf(m, v[j]);
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
-    float ex[NJ];
-    float sum = 0.0f;
+    float p[NJ], pick_g[NJ];
+    int pick_e[NJ];
+    ent_acc = ent_acc + route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int e = lane + 64 * j;
-      ex[j] = (e < E) ? mxm_exp(v[j] - m) : 0.0f;
-      sum = (j == 0) ? ex[j] : sum + ex[j];
-    }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) sum = sum + shfl_xor_f(sum, s);
-    float p[NJ];
-    float ent_local = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int e = lane + 64 * j;
-      float q = mxm_ftz(ex[j] / sum);
-      if (BF16) q = mxm_rbf(q);
-      p[j] = (e < E) ? q : -1.0f;
       if (e < E) {
-        psum[j] = psum[j] + q;
-        const float term = q * logf(fmaxf(q, 1e-12f));
-        ent_local = (j == 0) ? term : ent_local + term;
-        if (probs_out) probs_out[(size_t)n * E + e] = q;
+        psum[j] = psum[j] + p[j];
+        if (probs_out) probs_out[(size_t)n * E + e] = p[j];
       }
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) ent_local = ent_local + shfl_xor_f(ent_local, s);
-    ent_acc = ent_acc + ent_local;
-
-    // top-k: K rounds of argmax under (p desc, e asc).  The argmax is
-    // wave-uniform, so every lane accumulates the same running sum of the
-    // picked probabilities (k order), and lane k%64 keeps pick k in slot k/64.
-    uint32_t taken = 0u;
-    float s_top = 0.0f;
-    float my_p[NJ];
-    int my_e[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      my_p[j] = 0.0f;
-      my_e[j] = 0;
-    }
-    for (int k = 0; k < K; ++k) {
-      float bp = -2.0f;
-      int be = 0x7fffffff;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && !((taken >> j) & 1u) && p[j] > bp) {
-          bp = p[j];
-          be = e;
-        }
-      }
-#pragma unroll
-      for (int s = 32; s >= 1; s >>= 1) {
-        const float op = shfl_xor_f(bp, s);
-        const int oe = shfl_xor_i(be, s);
-        if (op > bp || (op == bp && oe < be)) {
-          bp = op;
-          be = oe;
-        }
-      }
-      if ((be & 63) == lane) taken |= 1u << (be >> 6);
-      s_top = (k == 0) ? bp : s_top + bp;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        if (k == lane + 64 * j) {
-          my_p[j] = bp;
-          my_e[j] = be;
-        }
-    }
-    if (BF16) s_top = mxm_rbf(s_top);
-    const float den = fmaxf(s_top, 1e-12f);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int k = lane + 64 * j;
       if (k < K) {
-        top_idx[(size_t)n * K + k] = my_e[j];
-        gates[(size_t)n * K + k] = my_p[j] / den;
-        atomicOr(&mask[my_e[j]][t >> 5], 1u << (t & 31));
+        top_idx[(size_t)n * K + k] = pick_e[j];
+        gates[(size_t)n * K + k] = pick_g[j];
+        atomicOr(&mask[pick_e[j]][t >> 5], 1u << (t & 31));
       }
     }
   }
@@ -302,159 +317,334 @@ __global__ __launch_bounds__(PRE ? 1024 : NT) void router_kernel(
   }
 }
 
-// Logits for small batches, where the tiled kernel would run on a handful of
-// workgroups.  A workgroup takes four tokens, one per wave; lane l computes
-// experts l, l+64, ...  Each logit is fmaf-accumulated over d = 0..D-1 in
-// ascending order from 0, exactly as the tiled phase 1 does, so the bits are
-// the same.  The router weights pass through LDS in chunks of BK rows (fp32,
-// double-buffered: the next chunk's global loads are in flight while the
-// current one is consumed); the tokens' x values travel the same way.
-template <typename TX, int NJ, bool VEC>
-__global__ __launch_bounds__(256) void logits_small_kernel(const TX* __restrict__ x,
-                                                           const TX* __restrict__ wr, int N, int D,
-                                                           int E, float* __restrict__ out) {
-  constexpr int EP = 64 * NJ;
-  constexpr int BK = 128 / NJ;             // one 32 KB fp32 buffer per chunk
-  constexpr int VW = 16 / sizeof(TX);      // elements per 16-byte load
-  constexpr int CPR = EP / VW;             // vectors per weight row
-  constexpr int RPP = 256 / CPR;           // weight rows per loader pass
-  constexpr int WPASS = BK / RPP;
-  constexpr int XV = 4 * BK / VW;          // x vectors per chunk (4 tokens)
-  static_assert(XV <= 256, "x chunk fits one loader pass");
-  __shared__ __attribute__((aligned(16))) float ws[2][BK][EP];
-  __shared__ __attribute__((aligned(16))) float xs[2][4][BK];
+// Decode-sized batches: routing in one launch.  Workgroup n owns token n.
+// Its x row is staged in LDS as fp32; wave w < NJ computes the logits of
+// experts 64 w + lane by fmaf over d = 0..D-1 ascending from 0 -- the tiled
+// kernel's accumulation order, so the bits are the same.  The fp32 router
+// weights are stored lane-interleaved (each wave load is 1 KB contiguous,
+// 16 bytes = the next four d of the lane's expert) and stream through a ring
+// of RS_RD register blocks (RS_RD - 1 blocks in flight); x is broadcast from
+// LDS through a ring of RS_XR blocks.  Wave 0 then runs route_token and writes the token's
+// picks, gates, probabilities and entropy term.  Every workgroup then takes a
+// ticket (agent-scope fence, atomic add); the one that takes the last ticket
+// reads all tokens' results back and computes what the scan and scatter
+// kernels compute for larger batches: per-expert counts (LDS histogram),
+// offsets and row-tile prefixes (one wave's scan), aux and entropy, and the
+// stable permutation (per 64-token chunk, the rank of a slot among the
+// chunk's tokens on its expert from a 64-bit token mask, plus the running
+// count of earlier chunks).  It resets the ticket for the next call.  No
+// workgroup waits on another, so the kernel always drains.
+constexpr int RS_NT = 256;
+constexpr int RS_BD = 16;  // d per register block
+constexpr int RS_RD = 8;   // weight blocks in the register ring
+constexpr int RS_XR = 4;   // x blocks in the register ring
+static_assert(RS_RD % RS_XR == 0, "x slots repeat with the weight ring");
 
+__device__ __forceinline__ float rs_wave_sum(float v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v = v + shfl_xor_f(v, s);
+  return v;
+}
+
+template <typename TX, bool BF16, int NJ, bool VEC>
+__global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float rs_dyn[];  // x row, then the slots
+  __shared__ float lg[NJ * 64];
+  __shared__ int cnt[MXM_MAX_EXPERTS];
+  __shared__ int offs[MXM_MAX_EXPERTS];
+  __shared__ int runc[MXM_MAX_EXPERTS];
+  __shared__ float pmean[MXM_MAX_EXPERTS];
+  __shared__ uint32_t msk[MXM_MAX_EXPERTS][2];
+  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * 4;
-  const int nchunks = (D + BK - 1) / BK;
+  const int n = blockIdx.x;
+  const int N = a.N, D = a.D, E = a.E, K = a.K;
 
-  // Raw 16-byte pieces of the next chunk; they are converted (and the ones
-  // outside [D, E] zeroed) only when written to LDS, after the current
-  // chunk's arithmetic, so the loads stay in flight meanwhile.
-  uint4 wraw[WPASS];
-  uint4 xraw = make_uint4(0u, 0u, 0u, 0u);
-  uint32_t wok = 0u;  // bit p*VW + q: element q of piece p lies inside [D, E]
-  bool xok = false;
-  auto load = [&](int c) {
-    const int d0 = c * BK;
-    wok = 0u;
+  // ---- the token's x row -> LDS (fp32) ----------------------------------
+  const TX* xrow = static_cast<const TX*>(a.x) + (size_t)n * D;
+  float* xl = rs_dyn;
+  if (VEC) {
+    constexpr int PER = 16 / sizeof(TX);
+    for (int i = tid; i < D / PER; i += RS_NT) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xrow + i * PER);
+      float f[PER];
+      unpack16<TX>(raw, f);
 #pragma unroll
-    for (int p = 0; p < WPASS; ++p) {
-      const int d = d0 + p * RPP + tid / CPR, e = (tid % CPR) * VW;
-      if (VEC) {
-        const bool ok = d < D && e < E;
-        wraw[p] = *reinterpret_cast<const uint4*>(wr + (ok ? (size_t)d * E + e : 0));
-        wok |= ok ? (((1u << VW) - 1u) << (p * VW)) : 0u;
-      } else {
-        TX v[VW];
-#pragma unroll
-        for (int q = 0; q < VW; ++q) {
-          const bool ok = d < D && e + q < E;
-          v[q] = wr[ok ? (size_t)d * E + e + q : 0];
-          wok |= ok ? (1u << (p * VW + q)) : 0u;
-        }
-        wraw[p] = __builtin_bit_cast(uint4, v);
-      }
+      for (int q = 0; q < PER; q += 4)
+        *reinterpret_cast<float4*>(xl + i * PER + q) = make_float4(f[q], f[q + 1], f[q + 2], f[q + 3]);
     }
-    if (tid < XV) {
-      const int t = tid / (BK / VW), d = d0 + (tid % (BK / VW)) * VW;
-      const int n = n0 + t;
-      xok = n < N && d < D;
-      if (VEC) {
-        xraw = *reinterpret_cast<const uint4*>(x + (xok ? (size_t)n * D + d : 0));
-      } else {
-        TX v[VW];
-#pragma unroll
-        for (int q = 0; q < VW; ++q) v[q] = (xok && d + q < D) ? x[(size_t)n * D + d + q] : TX(0);
-        xraw = __builtin_bit_cast(uint4, v);
-      }
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < WPASS; ++p) {
-      float f[VW];
-      unpack16<TX>(wraw[p], f);
-      float* dst = &ws[buf][p * RPP + tid / CPR][(tid % CPR) * VW];
-#pragma unroll
-      for (int q = 0; q < VW; ++q) dst[q] = ((wok >> (p * VW + q)) & 1u) ? f[q] : 0.0f;
-    }
-    if (tid < XV) {
-      float f[VW];
-      unpack16<TX>(xraw, f);
-      float* dst = &xs[buf][tid / (BK / VW)][(tid % (BK / VW)) * VW];
-#pragma unroll
-      for (int q = 0; q < VW; ++q) dst[q] = xok ? f[q] : 0.0f;
-    }
-  };
-
-  float acc[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = 0.0f;
-  load(0);
-  store(0);
+  } else {
+    for (int d = tid; d < D; d += RS_NT) xl[d] = ld_as_f32<TX>(xrow + d);
+  }
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nchunks) load(c + 1);
-    // rows past D are zero in both buffers: fmaf(0, 0, acc) leaves acc's
-    // value unchanged
-    const float* xw = xs[buf][wave];
-#pragma unroll 8
-    for (int dd = 0; dd < BK; dd += 4) {
-      const float4 xv = *reinterpret_cast<const float4*>(xw + dd);
-      const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+
+  // ---- logits ---------------------------------------------------------------
+  if (wave < NJ) {
+    const int e = wave * 64 + lane;
+    // the lane's 16-byte piece of chunk c (d = 4c .. 4c+3) is wlane[256 c]
+    const float* wlane = a.wr_t + (size_t)wave * a.ldw * 64 + lane * 4;
+    float acc = 0.0f;
+    const int nblk = D / RS_BD;
+    float4 w[RS_RD][RS_BD / 4];
+    float4 xv[RS_XR][RS_BD / 4];  // x of the current and the next RS_XR - 1 blocks
+    auto ld = [&](float4 (&dst)[RS_BD / 4], int b) {
+      const float* src = wlane + (size_t)b * (RS_BD / 4) * 256;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < RS_BD / 4; ++q) dst[q] = *reinterpret_cast<const float4*>(src + q * 256);
+    };
+    auto ldx = [&](float4 (&dst)[RS_BD / 4], int b) {
+      const float4* src = reinterpret_cast<const float4*>(xl + b * RS_BD);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[j] = __builtin_fmaf(xa[q], ws[buf][dd + q][lane + 64 * j], acc[j]);
+      for (int q = 0; q < RS_BD / 4; ++q) dst[q] = src[q];
+    };
+    auto fma_blk = [&](const float4 (&wv)[RS_BD / 4], const float4 (&xb)[RS_BD / 4]) {
+#pragma unroll
+      for (int q = 0; q < RS_BD / 4; ++q) {
+        acc = __builtin_fmaf(xb[q].x, wv[q].x, acc);
+        acc = __builtin_fmaf(xb[q].y, wv[q].y, acc);
+        acc = __builtin_fmaf(xb[q].z, wv[q].z, acc);
+        acc = __builtin_fmaf(xb[q].w, wv[q].w, acc);
+      }
+    };
+    const int nround = nblk / RS_RD;
+    if (nround > 0) {
+#pragma unroll
+      for (int r = 0; r < RS_RD - 1; ++r) ld(w[r], r);
+#pragma unroll
+      for (int r = 0; r < RS_XR - 1; ++r) ldx(xv[r], r);
+      // step b refills the weight slot consumed at step b - 1 with block
+      // b + RS_RD - 1 and the x slot with block b + RS_XR - 1 (RS_RD is a
+      // multiple of RS_XR, so step r's x slot is r % RS_XR).  The scheduling
+      // barrier keeps the LDS reads ahead of the block's FMAs.
+      for (int it = 0; it + 1 < nround; ++it) {
+#pragma unroll
+        for (int r = 0; r < RS_RD; ++r) {
+          const int b = it * RS_RD + r;
+          ld(w[(r + RS_RD - 1) % RS_RD], b + RS_RD - 1);
+          ldx(xv[(r + RS_XR - 1) % RS_XR], b + RS_XR - 1);
+          __builtin_amdgcn_sched_barrier(0);
+          fma_blk(w[r], xv[r % RS_XR]);
+        }
+      }
+      // last full round: only its first step has a block of the full rounds
+      // left to fetch
+      const int bl = (nround - 1) * RS_RD;
+#pragma unroll
+      for (int r = 0; r < RS_RD; ++r) {
+        if (r == 0) ld(w[RS_RD - 1], bl + RS_RD - 1);
+        if (r + RS_XR - 1 < RS_RD) ldx(xv[(r + RS_XR - 1) % RS_XR], bl + r + RS_XR - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        fma_blk(w[r], xv[r % RS_XR]);
+      }
     }
-    if (c + 1 < nchunks) store(buf ^ 1);
+    for (int b = nround * RS_RD; b < nblk; ++b) {
+      float4 wv[RS_BD / 4], xb[RS_BD / 4];
+      ld(wv, b);
+      ldx(xb, b);
+      fma_blk(wv, xb);
+    }
+    for (int d = nblk * RS_BD; d < D; ++d)
+      acc = __builtin_fmaf(xl[d], wlane[(size_t)(d >> 2) * 256 + (d & 3)], acc);
+    lg[e] = BF16 ? mxm_rbf(acc) : acc;
+  }
+  __syncthreads();
+
+  // ---- softmax, top-k, gates ---------------------------------------------
+  if (wave == 0) {
+    float v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) v[j] = lg[lane + 64 * j];
+    float p[NJ], pick_g[NJ];
+    int pick_e[NJ];
+    const float ent = route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) a.probs[(size_t)n * E + e] = p[j];
+      if (e < K) {
+        a.top_idx[(size_t)n * K + e] = pick_e[j];
+        a.gates[(size_t)n * K + e] = pick_g[j];
+      }
+    }
+    if (lane == 0) a.tok_ent[n] = ent;
+  }
+
+  // ---- ticket: the last workgroup continues --------------------------------
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // ---- dispatch, aux, entropy (one workgroup) -----------------------------
+  const int NK = N * K;
+  int* sidx = reinterpret_cast<int*>(rs_dyn);  // the x row is no longer needed
+  for (int e = tid; e < E; e += RS_NT) {
+    cnt[e] = 0;
+    runc[e] = 0;
+  }
+  for (int s0 = 0; s0 < NK; s0 += RS_NT * 8) {
+    int v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int sl = s0 + q * RS_NT + tid;
+      v[q] = sl < NK ? a.top_idx[sl] : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int sl = s0 + q * RS_NT + tid;
+      if (sl < NK) sidx[sl] = v[q];
+    }
+  }
+  // per-expert probability sums over tokens in ascending order
+  if (tid < E) {
+    float ps = 0.0f;
+    for (int t0 = 0; t0 < N; t0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = (t0 + q < N) ? a.probs[(size_t)(t0 + q) * E + tid] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (t0 + q < N) ps = ps + v[q];
+    }
+    const float mean = ps / (float)N;
+    pmean[tid] = BF16 ? mxm_rbf(mean) : mean;
+  }
+  if (wave == RS_NT / 64 - 1) {
+    float es = 0.0f;
+    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
+    es = rs_wave_sum(es);
+    if (lane == 0) a.entropy[0] = -(es / (float)N);
+  }
+  __syncthreads();
+  for (int sl = tid; sl < NK; sl += RS_NT) atomicAdd(&cnt[sidx[sl]], 1);
+  __syncthreads();
+
+  if (wave == 0) {
+    // lane l takes experts 4l .. 4l+3 (E <= 256): exclusive prefixes of the
+    // counts and of the row tiles of both GEMM families
+    int c[4], t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * lane + q;
+      c[q] = e < E ? cnt[e] : 0;
+      t0 += c[q];
+      t1 += (c[q] + a.bm1 - 1) / a.bm1;
+      t2 += (c[q] + a.bm2 - 1) / a.bm2;
+    }
+    int i0 = t0, i1 = t1, i2 = t2;
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+      const int u0 = __shfl_up(i0, sh, 64), u1 = __shfl_up(i1, sh, 64), u2 = __shfl_up(i2, sh, 64);
+      if (lane >= sh) {
+        i0 += u0;
+        i1 += u1;
+        i2 += u2;
+      }
+    }
+    int o = i0 - t0, m1 = i1 - t1, m2 = i2 - t2;
+    float aux = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * lane + q;
+      if (e < E) {
+        offs[e] = o;
+        a.offsets[e] = o;
+        a.counts[e] = c[q];
+        a.mstart1[e] = m1;
+        a.mstart2[e] = m2;
+        o += c[q];
+        m1 += (c[q] + a.bm1 - 1) / a.bm1;
+        m2 += (c[q] + a.bm2 - 1) / a.bm2;
+        const float frac = ((float)c[q] / (float)K) / (float)N;
+        const float term = pmean[e] * frac;
+        aux = (q == 0) ? term : aux + term;
+      }
+    }
+    aux = rs_wave_sum(aux);
+    if (lane == 63) {
+      a.offsets[E] = i0;
+      a.mstart1[E] = i1;
+      a.mstart2[E] = i2;
+    }
+    if (lane == 0) {
+      const float raw = aux * (float)E;
+      a.aux[0] = raw;
+      if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
+    }
+  }
+  __syncthreads();
+
+  // stable permutation, 64 tokens at a time
+  for (int c0 = 0; c0 < N; c0 += 64) {
+    const int ct = min(64, N - c0);
+    for (int e = tid; e < E; e += RS_NT) {
+      msk[e][0] = 0u;
+      msk[e][1] = 0u;
+    }
+    __syncthreads();
+    for (int i = tid; i < ct * K; i += RS_NT) {
+      const int t = i / K;
+      atomicOr(&msk[sidx[c0 * K + i]][t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+    for (int i = tid; i < ct * K; i += RS_NT) {
+      const int t = i / K, sl = c0 * K + i;
+      const int e = sidx[sl];
+      const uint32_t lo = msk[e][0], hi = msk[e][1];
+      const int r = t < 32 ? __popc(lo & ((1u << t) - 1u))
+                           : __popc(lo) + __popc(hi & ((1u << (t - 32)) - 1u));
+      const int pos = offs[e] + runc[e] + r;
+      a.perm[pos] = c0 + t;
+      a.slot_pos[sl] = pos;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += RS_NT) runc[e] += __popc(msk[e][0]) + __popc(msk[e][1]);
     __syncthreads();
   }
-  const int n = n0 + wave;
-  if (n < N) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (lane + 64 * j < E) out[(size_t)n * E + lane + 64 * j] = acc[j];
-  }
+  if (tid == 0) __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename TX, bool BF16, int NJ>
+void launch_route_small_t(const RouteSmallArgs& a, hipStream_t s) {
+  constexpr int PER = 16 / (int)sizeof(TX);
+  const bool vec = a.D % PER == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+  size_t lds = (size_t)a.D * 4;
+  const size_t slots = (size_t)a.N * a.K * 4;
+  if (slots > lds) lds = slots;
+  lds = (lds + 15) / 16 * 16;
+  if (vec)
+    hipLaunchKernelGGL((route_small_kernel<TX, BF16, NJ, true>), dim3(a.N), dim3(RS_NT), lds, s, a);
+  else
+    hipLaunchKernelGGL((route_small_kernel<TX, BF16, NJ, false>), dim3(a.N), dim3(RS_NT), lds, s, a);
+}
+
+template <typename TX, bool BF16>
+void launch_route_small_dt(const RouteSmallArgs& a, hipStream_t s) {
+  if (a.E <= 64)
+    launch_route_small_t<TX, BF16, 1>(a, s);
+  else if (a.E <= 128)
+    launch_route_small_t<TX, BF16, 2>(a, s);
+  else if (a.E <= 192)
+    launch_route_small_t<TX, BF16, 3>(a, s);
+  else
+    launch_route_small_t<TX, BF16, 4>(a, s);
 }
 
 template <typename TX, bool BF16, int EPT>
 void launch_router_t(const RouterArgs& a, hipStream_t s) {
-  if (a.logits_scratch) {
-    constexpr int NJ = (16 * EPT + 63) / 64;
-    constexpr int VW = 16 / (int)sizeof(TX);
-    const bool vec = a.E % VW == 0 && a.D % VW == 0 &&
-                     (reinterpret_cast<uintptr_t>(a.x) % 16) == 0 &&
-                     (reinterpret_cast<uintptr_t>(a.wr) % 16) == 0;
-    if (vec)
-      hipLaunchKernelGGL((logits_small_kernel<TX, NJ, true>), dim3((a.N + 3) / 4), dim3(256), 0, s,
-                         static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
-                         a.logits_scratch);
-    else
-      hipLaunchKernelGGL((logits_small_kernel<TX, NJ, false>), dim3((a.N + 3) / 4), dim3(256), 0, s,
-                         static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
-                         a.logits_scratch);
-    const int ntiles = (a.N + TM - 1) / TM;
-    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false, true>), dim3(ntiles), dim3(1024), 0, s,
-                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr),
-                       a.logits_scratch, a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank,
-                       a.tile_counts, a.tile_psum, a.tile_ent, a.probs_out, ntiles);
-    return;
-  }
   const int ntiles = (a.N + TM - 1) / TM;
   const bool vec = (a.D % (16 / (int)sizeof(TX))) == 0 &&
                    (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   if (vec)
-    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true, false>), dim3(ntiles), dim3(NT), 0, s,
-                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), nullptr, a.N, a.D, a.E,
+    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true>), dim3(ntiles), dim3(NT), 0, s,
+                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
                        a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts, a.tile_psum,
                        a.tile_ent, a.probs_out, ntiles);
   else
-    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false, false>), dim3(ntiles), dim3(NT), 0, s,
-                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), nullptr, a.N, a.D, a.E,
+    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false>), dim3(ntiles), dim3(NT), 0, s,
+                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
                        a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts, a.tile_psum,
                        a.tile_ent, a.probs_out, ntiles);
 }
@@ -480,4 +670,16 @@ void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s) {
     launch_router_dt<uint16_t, true>(a, s);
   else
     launch_router_dt<float, false>(a, s);
+}
+
+bool mxm_route_small_fits(int N, int D, int E, int K) {
+  return N >= 1 && N <= MXM_SMALL_BATCH && (int64_t)N * K <= MXM_SMALL_SLOTS && D >= 1 &&
+         D <= MXM_SMALL_D && E >= 1 && E <= MXM_MAX_EXPERTS;
+}
+
+void mxm_launch_route_small(const RouteSmallArgs& a, bool bf16, hipStream_t s) {
+  if (bf16)
+    launch_route_small_dt<uint16_t, true>(a, s);
+  else
+    launch_route_small_dt<float, false>(a, s);
 }

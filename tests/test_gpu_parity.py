@@ -401,3 +401,51 @@ def test_many_experts(gpu_lib, E, N, bf16):
     assert_routing_equal(routing, want)
     assert rel_l2(delta, want["delta"]) <= (BF16_TOL if bf16 else FP32_TOL)
     assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"])
+
+
+@pytest.mark.parametrize("N,D,E,K,bf16", [
+    (1, 64, 8, 2, False),        # one token: one workgroup takes the only ticket
+    (1024, 128, 64, 16, True),   # N*K at the one-launch router's slot limit
+    (1024, 128, 64, 17, True),   # one slot row past it: the tiled router
+    (200, 100, 16, 4, True),     # bf16 rows not in 16-byte pieces; no full register round
+    (96, 300, 40, 3, False),     # full rounds, remainder blocks and a d tail
+    (77, 2051, 96, 5, True),     # odd D, two waves of router logits
+])
+def test_decode_router_shapes(gpu_lib, N, D, E, K, bf16):
+    """Decode-sized batches route in one launch (logits, softmax, top-k, then
+    counts, offsets, permutation, aux and entropy in the last workgroup);
+    routing bit-exact at its edges and on the tiled router just past them."""
+    F = 32
+    x, wr, experts = random_case(300 + N + D + E + K, N, D, E, F)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    delta, aux, ent, routing, _ = run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=bf16,
+                                          want_probs=True)
+    want = run_oracle(x, wr, experts, K=K, bf16=bf16)
+    assert same_bits(routing["probs"], want["probs"])
+    assert_routing_equal(routing, want)
+    assert rel_l2(delta, want["delta"]) <= (BF16_TOL if bf16 else FP32_TOL)
+    assert abs(aux - want["aux"]) <= (1e-2 if bf16 else 1e-5) * abs(want["aux"])
+    assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"])
+
+
+def test_decode_router_repeated_calls(gpu_lib):
+    """The one-launch router elects its dispatch workgroup with a ticket that
+    the elected workgroup resets: consecutive forwards on one executor each
+    route their own input."""
+    from mixlab_amd.op import MoEFeedForward
+
+    N, D, E, K, F = 64, 256, 64, 8, 64
+    _, wr, experts = random_case(91, N, D, E, F)
+    rng = np.random.default_rng(92)
+    with MoEFeedForward([1, N, D, E, K, 0, F, 0], [0.0], compute_dtype="fp32") as op:
+        op.set_weights(wr, experts)
+        for _ in range(3):
+            x = rng.standard_normal((N, D), dtype=np.float32)
+            delta, aux, ent = op.forward_host(x)
+            want = run_oracle(x, wr, experts, K=K)
+            assert_routing_equal(op.routing(), want)
+            assert same_bits(delta, want["delta"])
+            assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
+            assert abs(ent - want["entropy"]) <= 1e-5 * abs(want["entropy"])
