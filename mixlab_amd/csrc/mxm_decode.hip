@@ -4,12 +4,13 @@
 //
 // Weight layout (written at upload by mxm_launch_shuffle_q8): a matrix
 // W[Kd][C] (x.W layout) is cut into blocks of 64 k x 16 output columns; block
-// (cb, kb) occupies 1 KB at ((cb * Kd/64) + kb) * 1024 and holds, at bytes
+// (cb, kb) occupies 1 KB at ((kb * C/16) + cb) * 1024 and holds, at bytes
 // 16*l .. 16*l+15, the 16 values W[64kb + 16*(l/16) + i][16cb + l%16] + 128
 // (offset binary, i.e. the int8 byte with its top bit flipped), i = 0..15.
 // Lane l of a wave therefore reads one contiguous 16-byte piece, a wave-load
-// is one coalesced 1 KB read, and the blocks of one column block are
-// contiguous (Kd/64 KB).
+// is one coalesced 1 KB read, and the waves of a workgroup, which walk k in
+// step, read adjacent 1 KB blocks (a k block of all columns is C/16 KB
+// contiguous).
 //
 // MFMA: v_mfma_f32_16x16x32_bf16.  Within a 64-k block, lane group g = l/16
 // owns k = 16g .. 16g+15; the first 8 feed one MFMA, the last 8 a second.
@@ -19,10 +20,11 @@
 // removed after the loop with the rows' sums (an MFMA against ones).
 //
 // Work split: a workgroup = NW waves = NW consecutive column blocks of one
-// expert.  The workgroup stages 16 of the expert's rows (all Kd) in LDS; each
-// wave then streams its column block's weights over the whole of Kd through
-// a ring of P register slots (P block-loads per matrix in flight per wave),
-// so there is no split-K reduction and no barrier inside the stream.  More
+// expert.  Each wave requests the first P blocks of its weight stream, the
+// workgroup stages 16 of the expert's rows (all Kd) in LDS, and each wave
+// then streams its column block's weights over the whole of Kd through a
+// ring of P register slots (P block-loads per matrix in flight per wave), so
+// there is no split-K reduction and no barrier inside the stream.  More
 // than 16 rows take further passes.  Experts with no rows return at once, so
 // their weights are never read.
 #include "mxm_kernels.h"
@@ -76,6 +78,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int Kd = a.Kd, NC = a.Ncols;  // NC: output columns per matrix
   const int kblocks = Kd / 64;
+  const size_t kstride = (size_t)NC * 64;  // bytes between k blocks of one column block
   const int pieces = Kd / 8;          // 16-byte pieces per row
   const int cb = grp * NW + wave;
   const bool active = cb < NC / 16;   // wave-uniform
@@ -88,13 +91,25 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   for (int mt = 0; mt < NMAT; ++mt) {
     const void* base = (mt == 0) ? a.b0 : a.b1;
     W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd +
-            (size_t)(active ? cb : 0) * kblocks * 1024 + 16 * lane;
+            (size_t)(active ? cb : 0) * 1024 + 16 * lane;
     sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
   }
   const uint16_t* X = static_cast<const uint16_t*>(a.a);
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
+
+  u32x4_t wb[P][NMAT];
+  auto prologue = [&]() {
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)clamp_kb(s, kblocks) * kstride);
+  };
+  // the first blocks of the weight stream are requested before the rows are
+  // staged, so HBM is busy from the workgroup's start
+  if (active) prologue();
 
   for (int rc = 0; rc < count; rc += 16) {
     __syncthreads();  // the previous pass has finished reading ash
@@ -110,13 +125,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     }
     __syncthreads();
     if (!active) continue;
-
-    u32x4_t wb[P][NMAT];
-#pragma unroll
-    for (int s = 0; s < P; ++s)
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt)
-        wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)clamp_kb(s, kblocks) * 1024);
+    if (rc > 0) prologue();
 
     f32x4_t acc[NMAT], rs = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -144,7 +153,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         const int nk = clamp_kb(kb + P + s, kblocks);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt)
-          wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)nk * 1024);
+          wb[s][mt] = *reinterpret_cast<const u32x4_t*>(W[mt] + (size_t)nk * kstride);
       }
     }
 #pragma unroll
@@ -196,8 +205,8 @@ __global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
     const size_t blk = o >> 10;
     const int within = (int)(o & 1023);
     const int l = within >> 4, i = within & 15;
-    const int kblocks = Kd / 64;
-    const int cb = (int)(blk / kblocks), kb = (int)(blk % kblocks);
+    const int ncb = C / 16;
+    const int kb = (int)(blk / ncb), cb = (int)(blk % ncb);
     const int k = 64 * kb + 16 * (l >> 4) + i;
     const int c = 16 * cb + (l & 15);
     dst[o] = (uint8_t)((uint8_t)src[(size_t)k * C + c] ^ 0x80u);

@@ -480,11 +480,32 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   // ---- dispatch, aux, entropy (one workgroup) -----------------------------
   const int NK = N * K;
   int* sidx = reinterpret_cast<int*>(rs_dyn);  // the x row is no longer needed
+  // The first loads of all three inputs are issued together, so a decode
+  // batch (N <= 64, N*K <= 2048) reads them in one round trip: slots, the
+  // probabilities of the first 64 tokens, their entropy terms.
+  int sv[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int sl = q * RS_NT + tid;
+    sv[q] = sl < NK ? a.top_idx[sl] : 0;
+  }
+  const int t_first = min(N, 64);
+  float pv[64];
+#pragma unroll
+  for (int q = 0; q < 64; ++q)
+    pv[q] = (tid < E && q < t_first) ? a.probs[(size_t)q * E + tid] : 0.0f;
+  constexpr int ENT_WAVE = RS_NT / 64 - 1;
+  const float ev = (wave == ENT_WAVE && lane < N) ? a.tok_ent[lane] : 0.0f;
   for (int e = tid; e < E; e += RS_NT) {
     cnt[e] = 0;
     runc[e] = 0;
   }
-  for (int s0 = 0; s0 < NK; s0 += RS_NT * 8) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int sl = q * RS_NT + tid;
+    if (sl < NK) sidx[sl] = sv[q];
+  }
+  for (int s0 = RS_NT * 8; s0 < NK; s0 += RS_NT * 8) {
     int v[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -500,20 +521,23 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   // per-expert probability sums over tokens in ascending order
   if (tid < E) {
     float ps = 0.0f;
-    for (int t0 = 0; t0 < N; t0 += 16) {
-      float v[16];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) v[q] = (t0 + q < N) ? a.probs[(size_t)(t0 + q) * E + tid] : 0.0f;
+    for (int q = 0; q < 64; ++q)
+      if (q < t_first) ps = ps + pv[q];
+    for (int t0 = 64; t0 < N; t0 += 64) {
+      float v[64];
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
+      for (int q = 0; q < 64; ++q) v[q] = (t0 + q < N) ? a.probs[(size_t)(t0 + q) * E + tid] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 64; ++q)
         if (t0 + q < N) ps = ps + v[q];
     }
     const float mean = ps / (float)N;
     pmean[tid] = BF16 ? mxm_rbf(mean) : mean;
   }
-  if (wave == RS_NT / 64 - 1) {
-    float es = 0.0f;
-    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
+  if (wave == ENT_WAVE) {
+    float es = ev;
+    for (int t = lane + 64; t < N; t += 64) es = es + a.tok_ent[t];
     es = rs_wave_sum(es);
     if (lane == 0) a.entropy[0] = -(es / (float)N);
   }
