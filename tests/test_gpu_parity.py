@@ -387,7 +387,7 @@ def test_backward_fp32(gpu_lib, etype, act, slope, K):
 @pytest.mark.parametrize("bf16", [False, True])
 def test_many_experts(gpu_lib, E, N, bf16):
     """Expert counts past one lane per expert (2 and 4 per lane) on both
-    router paths: the small-batch logits kernel (N <= 1024) and the tiled one;
+    router paths: the one-launch decode router (N <= 1024) and the tiled one;
     probabilities and routing bit-exact."""
     D, F, K = 128, 128, 4
     x, wr, experts = random_case(70 + E + N, N, D, E, F)
