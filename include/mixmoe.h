@@ -165,8 +165,11 @@ int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t r
 
 /* Backward of op 74 (the gradients MLX's autodiff takes through
  * gpu/ir.cpp:1073-1164; the reference exercises them in
- * gpu/moe_feed_forward_test.go:84-151), for ops with fp32 compute.  Given
- * x [rows, D] fp32 and the upstream gradients d_delta [rows, D], d_aux and
+ * gpu/moe_feed_forward_test.go:84-151), computed in fp32.  Under bf16 compute
+ * it uses the bf16 flow's values (x and weights rounded to bf16, the
+ * forward's bf16 expert outputs); int8-weight ops have no backward.  Given
+ * x [rows, D] (fp32, or bf16 bits under bf16 compute) and the upstream
+ * gradients d_delta [rows, D] fp32, d_aux and
  * d_entropy (scalars), runs the forward on x (routing held fixed, as top-k
  * indices carry no gradient) and writes dx [rows, D], d_router_w [D, E] and
  * d_experts: the expert weight gradients in Op.Inputs order (per expert

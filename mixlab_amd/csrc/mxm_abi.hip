@@ -106,6 +106,10 @@ struct MoeOp {
   bool keep_probs = false, bw_ready = false;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
       bw_dlogits, bw_dxr, bw_w1t, bw_w1bt, bw_w2t, bw_wrt, bw_one;
+  // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
+  // and of the forward's expert outputs, for the fp32 backward kernels
+  bool bw_w32_ready = false;
+  DevBuf bw_w1_32, bw_w1b_32, bw_w2_32, bw_wr32, bw_x32, bw_y32, bw_mstart;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
   size_t ws_bytes = 0;
 
@@ -503,6 +507,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
   HIPCK(hipGetLastError());
   HIPCK(hipStreamSynchronize(st));
   o.have[idx] = 1;
+  o.bw_w32_ready = false;
 }
 
 void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, const int64_t* shape,
@@ -535,6 +540,7 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   HIPCK(hipGetLastError());
   HIPCK(hipStreamSynchronize(st));
   o.have[idx] = 1;
+  o.bw_w32_ready = false;
 }
 
 }  // namespace
@@ -845,15 +851,17 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
   });
 }
 
-// Backward of op 74 (fp32 flow): a forward on x (keeping the router
-// probabilities), then mxm_launch_backward.  d_experts receives the expert
+// Backward of op 74: a forward on x (keeping the router probabilities), then
+// mxm_launch_backward, whose kernels compute in fp32.  Under bf16 compute
+// they take the bf16 flow's values: x and the weights as rounded to bf16,
+// and the forward's bf16 expert outputs, converted to fp32.  d_experts receives the expert
 // weight gradients in Op.Inputs order (per expert gate, up, down -- or up,
 // down -- in x.W layout).
 void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
                   float d_ent, float* dx, float* dwr, float* dw) {
-  if (o.bf16 || o.q8)
-    fail("OP_MOE_FEED_FORWARD backward is implemented for the fp32 compute dtype");
-  if (x_dtype != MXM_DTYPE_F32) fail("OP_MOE_FEED_FORWARD backward takes fp32 x");
+  if (o.q8) fail("OP_MOE_FEED_FORWARD backward is not available for int8 expert weights");
+  if (x_dtype != MXM_DTYPE_F32 && !(o.bf16 && x_dtype == MXM_DTYPE_BF16))
+    fail("OP_MOE_FEED_FORWARD backward takes fp32 x (or bf16 x under bf16 compute)");
   if (!x || !d_delta || !dx || !dwr || !dw) fail("OP_MOE_FEED_FORWARD backward pointers must be non-NULL");
   if (!o.ws_ready) alloc_workspace(o);
   const size_t N = o.N, D = o.D, E = o.E, F = o.F, NK = (size_t)o.N * o.K;
@@ -883,9 +891,54 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     HIPCK(hipMemcpyAsync(o.bw_one.p, o.bw_one_host, 16, hipMemcpyHostToDevice, o.stream));
     o.bw_ready = true;
   }
+  const float *w1 = o.w1.as<float>(), *w1b = o.w1b.as<float>(), *w2 = o.w2.as<float>();
+  const float* wr = o.router.as<float>();
+  const float* x32 = static_cast<const float*>(x);
+  const float* y32 = o.Y.as<float>();
+  if (o.bf16) {
+    // The bf16 flow's values (x and weights rounded to bf16, the forward's
+    // bf16 expert outputs) go through the fp32 backward kernels.
+    if (!o.bw_w32_ready) {
+      const size_t DF = D * F;
+      if (!o.bw_wr32.p) o.bw_wr32.alloc(D * E * 4);
+      mxm_launch_to_f32(o.router.p, MXM_DTYPE_BF16, o.bw_wr32.as<float>(), (int64_t)(D * E),
+                        o.stream);
+      if (o.mfma) {
+        const bool glu = o.wpe == 3;
+        if (!o.bw_w1_32.p) o.bw_w1_32.alloc(E * DF * 4);
+        if (glu && !o.bw_w1b_32.p) o.bw_w1b_32.alloc(E * DF * 4);
+        if (!o.bw_w2_32.p) o.bw_w2_32.alloc(E * DF * 4);
+        const uint16_t* m1 = o.w1.as<uint16_t>();
+        mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, glu ? 0 : -1, o.bw_w1_32.as<float>(), o.stream);
+        if (glu) mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, 1, o.bw_w1b_32.as<float>(), o.stream);
+        mxm_launch_w2_to_xw(o.w2.as<uint16_t>(), o.E, o.D, o.F, o.bw_w2_32.as<float>(), o.stream);
+      }
+      HIPCK(hipGetLastError());
+      o.bw_w32_ready = true;
+    }
+    wr = o.bw_wr32.as<float>();
+    if (o.mfma) {
+      w1 = o.bw_w1_32.as<float>();
+      w1b = o.bw_w1b_32.as<float>();
+      w2 = o.bw_w2_32.as<float>();
+    }
+    if (!o.bw_x32.p) o.bw_x32.alloc(N * D * 4);
+    x32 = o.bw_x32.as<float>();
+  }
   o.keep_probs = true;
   run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr);
   o.keep_probs = false;
+  if (o.bf16) {
+    // x as the forward saw it (rounded to bf16 when given in fp32)
+    const void* xb = x_dtype == MXM_DTYPE_BF16 ? x : o.xcast.p;
+    mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
+    if (o.mfma) {
+      if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
+      mxm_launch_to_f32(o.Y.p, MXM_DTYPE_BF16, o.bw_y32.as<float>(), (int64_t)(NK * D), o.stream);
+      y32 = o.bw_y32.as<float>();
+    }
+    HIPCK(hipGetLastError());
+  }
   BackwardArgs b{};
   b.N = o.N;
   b.D = o.D;
@@ -895,22 +948,31 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.etype = o.etype;
   b.act = o.act;
   b.wpe = o.wpe;
+  // the backward's grouped products are SIMT kernels: their row tiles
   b.max_mtiles = o.max_mtiles2;
+  b.mstart = o.mstart2.as<int32_t>();
+  if (o.bm2 != mxm_simt_bm()) {
+    if (!o.bw_mstart.p) o.bw_mstart.alloc(((size_t)o.E + 1) * 4);
+    mxm_launch_tile_prefix(o.counts.as<int32_t>(), o.E, mxm_simt_bm(), o.bw_mstart.as<int32_t>(),
+                           o.stream);
+    HIPCK(hipGetLastError());
+    b.mstart = o.bw_mstart.as<int32_t>();
+    b.max_mtiles = (int)((NK + mxm_simt_bm() - 1) / mxm_simt_bm()) + o.E;
+  }
   b.slope = o.slope;
-  b.x = static_cast<const float*>(x);
+  b.x = x32;
   b.top_idx = o.top_idx.as<int32_t>();
   b.gates = o.gates.as<float>();
   b.slot_pos = o.slot_pos.as<int32_t>();
   b.perm = o.perm.as<int32_t>();
   b.counts = o.counts.as<int32_t>();
   b.offsets = o.offsets.as<int32_t>();
-  b.mstart = o.mstart2.as<int32_t>();
   b.probs = o.probs.as<float>();
-  b.Y = o.Y.as<float>();
-  b.wr = o.router.as<float>();
-  b.w1 = o.w1.as<float>();
-  b.w1b = o.w1b.as<float>();
-  b.w2 = o.w2.as<float>();
+  b.Y = y32;
+  b.wr = wr;
+  b.w1 = w1;
+  b.w1b = w1b;
+  b.w2 = w2;
   b.d_delta = d_delta;
   b.d_aux = d_aux;
   b.d_ent = d_ent;
@@ -957,16 +1019,18 @@ int mxm_moe_backward_host(int64_t h, const void* x, int x_dtype, int64_t rows,
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
     if (!x || !d_delta || !dx || !d_router_w || !d_experts)
       fail("OP_MOE_FEED_FORWARD backward pointers must be non-NULL");
-    if (x_dtype != MXM_DTYPE_F32) fail("OP_MOE_FEED_FORWARD backward takes fp32 x");
+    if (x_dtype != MXM_DTYPE_F32 && !(op->bf16 && x_dtype == MXM_DTYPE_BF16))
+      fail("OP_MOE_FEED_FORWARD backward takes fp32 x (or bf16 x under bf16 compute)");
     const size_t ND = (size_t)op->N * op->D * 4;
+    const size_t NDx = (size_t)op->N * op->D * (x_dtype == MXM_DTYPE_BF16 ? 2 : 4);
     const size_t nw = (size_t)op->E * op->wpe * op->D * op->F * 4;
     DevBuf dx_, dd_, ddx_, dwr_, dw_;
-    dx_.alloc(ND);
+    dx_.alloc(NDx);
     dd_.alloc(ND);
     ddx_.alloc(ND);
     dwr_.alloc((size_t)op->D * op->E * 4);
     dw_.alloc(nw);
-    HIPCK(hipMemcpyAsync(dx_.p, x, ND, hipMemcpyHostToDevice, op->stream));
+    HIPCK(hipMemcpyAsync(dx_.p, x, NDx, hipMemcpyHostToDevice, op->stream));
     HIPCK(hipMemcpyAsync(dd_.p, d_delta, ND, hipMemcpyHostToDevice, op->stream));
     run_backward(*op, dx_.p, x_dtype, dd_.as<float>(), d_aux, d_entropy, ddx_.as<float>(),
                  dwr_.as<float>(), dw_.as<float>());

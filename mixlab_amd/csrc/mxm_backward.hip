@@ -262,7 +262,23 @@ void wgrad(const float* A, int M, const float* B, int Nn, const int32_t* offsets
                      dim3(256), 0, s, A, M, B, Nn, offsets, out, out_stride);
 }
 
+// Row-tile prefix of a grouped GEMM family with tile height bm:
+// mstart[e] = sum over e' < e of ceil(counts[e'] / bm), e = 0..E.
+__global__ void tile_prefix_kernel(const int32_t* counts, int E, int bm, int32_t* mstart) {
+  if (threadIdx.x != 0) return;
+  int m = 0;
+  for (int e = 0; e < E; ++e) {
+    mstart[e] = m;
+    m += (counts[e] + bm - 1) / bm;
+  }
+  mstart[E] = m;
+}
+
 }  // namespace
+
+void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s) {
+  hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, counts, E, bm, mstart);
+}
 
 void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
   const int N = a.N, D = a.D, E = a.E, K = a.K, F = a.F, NK = a.N * a.K;

@@ -238,6 +238,10 @@ void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, in
                                uint16_t* dst, hipStream_t s);
 void mxm_launch_router_t(const void* src, int src_dtype, int D, int E, int ldw, float* dst,
                          hipStream_t s);
+// MFMA-family expert weights back to fp32 x.W layout (backward of bf16 ops).
+void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int slot, float* dst,
+                         hipStream_t s);
+void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, float* dst, hipStream_t s);
 
 // int8-weight family (decode shapes): weights in the 1 KB block layout of
 // mxm_launch_shuffle_q8, fp32 scale per output channel (scale0/scale1),
@@ -282,3 +286,5 @@ struct BackwardArgs {
   float* dw;                 // per expert, Op.Inputs order, x.W layout
 };
 void mxm_launch_backward(const BackwardArgs& a, hipStream_t s);
+// Row-tile prefix of counts for tile height bm (mstart[0..E]).
+void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);

@@ -94,3 +94,49 @@ void mxm_launch_router_t(const void* src, int src_dtype, int D, int E, int ldw, 
     hipLaunchKernelGGL(router_t_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, D, E,
                        ldw, dst);
 }
+
+namespace {
+
+// MFMA-family expert weights back to fp32 in x.W layout, for the backward of
+// bf16 ops.  w1 holds per expert [NC][D] bf16 (NC = 2F, gate and up rows
+// interleaved in groups of 32, or F for one matrix); slot picks the matrix
+// (0 gate, 1 up, -1 not interleaved).  dst[e][d][f] = w1[e][q(f)][d].
+__global__ void w1_to_xw_kernel(const uint16_t* w1, int E, int D, int F, int slot, float* dst) {
+  const int NC = slot < 0 ? F : 2 * F;
+  const int64_t n = (int64_t)E * D * F;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int f = (int)(i % F);
+    const int64_t ed = i / F;
+    const int d = (int)(ed % D), e = (int)(ed / D);
+    const int q = slot < 0 ? f : (f >> 5) * 64 + slot * 32 + (f & 31);
+    dst[i] = mxm_bf2f(w1[((size_t)e * NC + q) * D + d]);
+  }
+}
+
+// w2 [E][D][F] bf16 (the down projection, k = F contiguous) -> dst [E][F][D].
+__global__ void w2_to_xw_kernel(const uint16_t* w2, int E, int D, int F, float* dst) {
+  const int64_t n = (int64_t)E * D * F;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % D);
+    const int64_t ef = i / D;
+    const int f = (int)(ef % F), e = (int)(ef / F);
+    dst[i] = mxm_bf2f(w2[((size_t)e * D + d) * F + f]);
+  }
+}
+
+}  // namespace
+
+void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int slot, float* dst,
+                         hipStream_t s) {
+  const int64_t n = (int64_t)E * D * F;
+  if (n > 0)
+    hipLaunchKernelGGL(w1_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w1, E, D, F, slot, dst);
+}
+
+void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, float* dst, hipStream_t s) {
+  const int64_t n = (int64_t)E * D * F;
+  if (n > 0)
+    hipLaunchKernelGGL(w2_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w2, E, D, F, dst);
+}

@@ -154,9 +154,10 @@ class MoEFeedForward:
 
     def backward_host(self, x: np.ndarray, d_delta: np.ndarray, d_aux: float = 0.0,
                       d_entropy: float = 0.0):
-        """Gradients of op 74 (fp32 compute): returns (dx [B*T, D],
-        d_router_w [D, E], d_experts: per expert a list of the weight
-        gradients in Op.Inputs order, x.W layout)."""
+        """Gradients of op 74: returns (dx [B*T, D], d_router_w [D, E],
+        d_experts: per expert a list of the weight gradients in Op.Inputs
+        order, x.W layout).  x is fp32 (rounded to bf16 by the library under
+        bf16 compute); the gradients are computed in fp32."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         dd = np.ascontiguousarray(d_delta, dtype=np.float32)
         wpe = 2 if self.expert_type == MOE_EXPERT_MLP else 3

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from mixlab_amd import _lib
-from mixlab_amd.workloads import CONFIGS, make_workload, round_bf16
+from mixlab_amd.workloads import CONFIGS, bf16_bits, make_workload, round_bf16
 from tests.moe_testutil import (assert_routing_equal, random_case, rel_l2, run_gpu,
                                 run_gpu_workload, run_oracle, run_oracle_workload, same_bits)
 
@@ -449,3 +449,42 @@ def test_decode_router_repeated_calls(gpu_lib):
             assert same_bits(delta, want["delta"])
             assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
             assert abs(ent - want["entropy"]) <= 1e-5 * abs(want["entropy"])
+
+
+@pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0), (2, 1, 0.0), (2, 3, 0.4)])
+@pytest.mark.parametrize("flow", ["bf16_mfma", "bf16_simt"])
+def test_backward_bf16(gpu_lib, etype, act, slope, flow):
+    """mxm_moe_backward under bf16 compute: the fp32 backward kernels take
+    the bf16 flow's values (x and weights rounded to bf16, the forward's bf16
+    expert outputs); against the float64 restatement on the bf16-rounded
+    inputs with the bf16 routing, within the bf16 bar (2e-2 relative L2)."""
+    from mixlab_amd.op import MoEFeedForward
+    from oracle.backward import backward64
+
+    B, T, D, E, F, K = 2, 96, 256, 6, 256, 2
+    x, wr, experts = random_case(81 + etype * 7 + act, B * T, D, E, F, expert_type=etype,
+                                 wscale=0.1)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(w) for w in ws] for ws in experts]
+    rng = np.random.default_rng(82)
+    dD = rng.standard_normal((B * T, D), dtype=np.float32)
+    flags = _lib.MXM_FLAG_FORCE_SIMT if flow == "bf16_simt" else 0
+    with MoEFeedForward([B, T, D, E, K, etype, F, act], [slope], compute_dtype="bf16",
+                        flags=flags) as op:
+        op.set_weights(bf16_bits(wr), [[bf16_bits(w) for w in ws] for ws in experts])
+        dx, dwr, dexp = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
+        routing = op.routing()
+        assert op.info()["mfma"] == (flow == "bf16_mfma")
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
+                      bf16=True)
+    assert_routing_equal(routing, want)
+    rdx, rdwr, rdexp = backward64(x, wr, experts, want["top_idx"].astype(np.int64), dD, 0.3, -0.2,
+                                  etype, act, slope)
+    assert rel_l2(dx, rdx) <= BF16_TOL
+    assert rel_l2(dwr, rdwr) <= BF16_TOL
+    for e in range(E):
+        for m in range(len(experts[e])):
+            if np.any(rdexp[e][m]):
+                assert rel_l2(dexp[e][m], rdexp[e][m]) <= BF16_TOL, (e, m)
+            else:
+                assert not np.any(dexp[e][m]), (e, m)
