@@ -104,7 +104,7 @@ def cpu_baseline(w, cfg, target_s: float) -> dict:
                        f"runs of {med:.2f} s after warm-up")}
 
 
-def run_config(cfg, steps: int, warmup: int, flags: int = 0):
+def run_config(cfg, steps: int, warmup: int, flags: int = 0, stage_repeats: int = 1):
     """Upload a generated workload, run warm-up + timed forwards.  Returns
     (workload, result dict)."""
     from mixlab_amd import _lib
@@ -145,8 +145,9 @@ def run_config(cfg, steps: int, warmup: int, flags: int = 0):
     op.synchronize()
     elapsed = time.perf_counter() - t0
     # stage times from a second pass with HIP events between the stages (the
-    # events add gaps between kernels, so they stay out of the timed pass)
-    op.set_profiling(True)
+    # events add gaps between kernels, so they stay out of the timed pass);
+    # short stages are launched `stage_repeats` times between their events
+    op.set_profiling(True, stage_repeats)
     for _ in range(steps):
         step()
     op.synchronize()
@@ -277,7 +278,7 @@ def main() -> int:
     decode = None
     if not args.no_decode:
         c5 = CONFIGS["C5"]
-        _, d = run_config(c5, max(args.steps, 50), max(args.warmup, 10))
+        _, d = run_config(c5, max(args.steps, 50), max(args.warmup, 10), stage_repeats=10)
         ds = d["stages"]
         wb = int8_weight_bytes(c5, d["counts"])
         xb = c5.N * c5.D * 2

@@ -200,9 +200,13 @@ int mxm_moe_probs(int64_t op, float* probs);
 
 /* Per-stage HIP-event timing on the op's stream.  mxm_moe_set_profiling
  * (re)starts a recording: every later forward records events between its
- * kernels.  mxm_moe_stage_times waits for the recorded forwards and writes
- * the mean duration of each of the MXM_NUM_STAGES stages in milliseconds;
- * it returns the number of forwards averaged (> 0) or an error code. */
+ * kernels (enable = 0 stops it).  With enable = R > 1 each stage is launched
+ * R times between its events (the stages are idempotent, so outputs are
+ * unchanged), which times short kernels without the events' own gaps.
+ * mxm_moe_stage_times waits for the recorded forwards and writes the mean
+ * duration of one launch of each of the MXM_NUM_STAGES stages in
+ * milliseconds; it returns the number of forwards averaged (> 0) or an error
+ * code. */
 int mxm_moe_set_profiling(int64_t op, int enable);
 int mxm_moe_stage_times(int64_t op, float* ms, int n);
 

@@ -115,6 +115,7 @@ struct MoeOp {
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
   bool profiling = false;
+  int prof_reps = 1;  // launches of each stage between its events
   std::vector<std::array<hipEvent_t, MXM_NUM_STAGES + 1>> ev_sets;
   size_t ev_used = 0;
 
@@ -253,6 +254,10 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   auto mark = [&](int i) {
     if (evs) HIPCK(hipEventRecord(evs[i], st));
   };
+  // profiled forwards may launch each stage several times between its events
+  // (every stage is idempotent), so that short kernels are timed without the
+  // events' own gaps
+  const int reps = evs ? o.prof_reps : 1;
 
   mark(0);
   float* probs_keep = (o.debug_probs || o.keep_probs) ? o.probs.as<float>() : nullptr;
@@ -291,7 +296,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     rs.aux_weight = blk ? blk->aux_weight : 1.0f;
     rs.aux_scaled = blk ? blk->aux_scaled : nullptr;
     rs.ticket = o.ticket.as<int32_t>();
-    mxm_launch_route_small(rs, o.bf16, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_route_small(rs, o.bf16, st);
     HIPCK(hipGetLastError());
     mark(1);
     mark(2);
@@ -310,7 +315,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     ra.tile_psum = o.tile_psum.as<float>();
     ra.tile_ent = o.tile_ent.as<float>();
     ra.probs_out = probs_keep;
-    mxm_launch_router(ra, o.bf16, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_router(ra, o.bf16, st);
     HIPCK(hipGetLastError());
 
     mark(1);
@@ -328,7 +333,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     sa.entropy = ent_p;
     sa.aux_weight = blk ? blk->aux_weight : 1.0f;
     sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
-    mxm_launch_scan(sa, o.bf16, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_scan(sa, o.bf16, st);
     HIPCK(hipGetLastError());
 
     mark(2);
@@ -338,7 +343,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     sc.N = o.N;
     sc.K = o.K;
     sc.ntiles = o.ntiles;
-    mxm_launch_scatter(sc, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_scatter(sc, st);
     HIPCK(hipGetLastError());
   }
 
@@ -367,13 +372,13 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     g1.scale0 = o.s1.as<float>();
     g1.scale1 = o.s1b.as<float>();
     require_operands(g1, glu, true);
-    mxm_launch_gemm_q8(g1, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
   } else if (o.mfma) {
     require_operands(g1, false, false);
-    mxm_launch_gemm_mfma(g1, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
   } else {
     require_operands(g1, glu, false);
-    mxm_launch_gemm_simt(g1, o.bf16, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_simt(g1, o.bf16, st);
   }
   HIPCK(hipGetLastError());
 
@@ -398,13 +403,13 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     g2.b0 = o.q2.p;
     g2.scale0 = o.s2.as<float>();
     require_operands(g2, false, true);
-    mxm_launch_gemm_q8(g2, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g2, st);
   } else if (o.mfma) {
     require_operands(g2, false, false);
-    mxm_launch_gemm_mfma(g2, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g2, st);
   } else {
     require_operands(g2, false, false);
-    mxm_launch_gemm_simt(g2, o.bf16, st);
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_simt(g2, o.bf16, st);
   }
   HIPCK(hipGetLastError());
 
@@ -424,7 +429,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     ca.rscale = blk->moe_scale;
     ca.rscale_bf16 = blk->scale_bf16;
   }
-  mxm_launch_combine(ca, o.mfma || o.q8, st);
+  for (int rep = 0; rep < reps; ++rep) mxm_launch_combine(ca, o.mfma || o.q8, st);
   HIPCK(hipGetLastError());
   mark(6);
 }
@@ -1088,6 +1093,7 @@ int mxm_moe_set_profiling(int64_t h, int enable) {
   return fenced([&] {
     HIPCK(hipStreamSynchronize(op->stream));
     op->profiling = enable != 0;
+    op->prof_reps = enable > 1 ? enable : 1;
     op->ev_used = 0;
     return MXM_OK;
   });
@@ -1108,7 +1114,8 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
         ms[i] += t;
       }
     }
-    for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i) ms[i] /= (float)op->ev_used;
+    for (int i = 0; i < MXM_NUM_STAGES && i < n; ++i)
+      ms[i] /= (float)op->ev_used * (float)op->prof_reps;
     count = (int)op->ev_used;
     return MXM_OK;
   });

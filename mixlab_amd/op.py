@@ -203,8 +203,11 @@ class MoEFeedForward:
                    "mxm_moe_probs")
         return p
 
-    def set_profiling(self, enable: bool) -> None:
-        _lib.check(self._lib.mxm_moe_set_profiling(self.handle, int(enable)), "set_profiling")
+    def set_profiling(self, enable: bool, repeats: int = 1) -> None:
+        """Record per-stage events in later forwards; with repeats > 1 each
+        stage is launched that many times between its events."""
+        code = 0 if not enable else max(1, int(repeats))
+        _lib.check(self._lib.mxm_moe_set_profiling(self.handle, code), "set_profiling")
 
     def stage_times(self) -> dict:
         """Mean per-stage milliseconds over the forwards since set_profiling(True)."""

@@ -488,3 +488,31 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow):
                 assert rel_l2(dexp[e][m], rdexp[e][m]) <= BF16_TOL, (e, m)
             else:
                 assert not np.any(dexp[e][m]), (e, m)
+
+
+@pytest.mark.parametrize("T", [64, 1536])
+def test_stage_profiling_repeats(gpu_lib, T):
+    """Profiled forwards that launch each stage several times between its
+    events (mxm_moe_set_profiling with R > 1) leave the outputs unchanged:
+    every stage is idempotent, on the one-launch router (T=64) and on the
+    tiled router + scan + scatter (T=1536)."""
+    from mixlab_amd.op import MoEFeedForward
+
+    D, E, K, F = 256, 8, 2, 256
+    x, wr, experts = random_case(95 + T, T, D, E, F)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(w) for w in ws] for ws in experts]
+    with MoEFeedForward([1, T, D, E, K, 0, F, 0], [0.0], compute_dtype="bf16") as op:
+        op.set_weights(bf16_bits(wr), [[bf16_bits(w) for w in ws] for ws in experts])
+        d0, a0, e0 = op.forward_host(bf16_bits(x))
+        r0 = op.routing()
+        op.set_profiling(True, 5)
+        d1, a1, e1 = op.forward_host(bf16_bits(x))
+        st = op.stage_times()
+        op.set_profiling(False)
+        r1 = op.routing()
+    assert same_bits(d0, d1) and a0 == a1 and e0 == e1
+    for k in ("top_idx", "gates", "counts", "offsets", "perm"):
+        assert same_bits(r0[k], r1[k]), k
+    assert st["forwards"] == 1
+    assert all(st[k] >= 0.0 for k in st) and st["gemm_up"] > 0.0 and st["gemm_down"] > 0.0
