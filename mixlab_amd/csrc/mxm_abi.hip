@@ -366,6 +366,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g1.expert_type = o.etype;
   g1.activation = o.act;
   g1.slope = o.slope;
+  g1.rows_total = o.N * o.K;
   if (o.q8) {
     g1.b0 = o.q1.p;
     g1.b1 = o.q1b.p;
@@ -399,6 +400,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g2.activation = o.act;
   g2.slope = o.slope;
   g2.y_bf16 = o.bf16 && hidden_is_bf16(o.etype, o.act);
+  g2.rows_total = o.N * o.K;
   if (o.q8) {
     g2.b0 = o.q2.p;
     g2.scale0 = o.s2.as<float>();

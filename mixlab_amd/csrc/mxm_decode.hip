@@ -60,14 +60,16 @@ __device__ __forceinline__ int clamp_kb(int kb, int kblocks) {
   return kb < kblocks ? kb : kblocks - 1;
 }
 
-// P: weight blocks in flight per matrix per wave.
-template <int EPI, int P>
+// P: weight blocks in flight per matrix per wave.  RG: groups of 16 rows per
+// pass (each weight block, converted once, feeds RG MFMA row groups).
+template <int EPI, int P, int RG>
 __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
-  // A rows of the current pass: [kb][half][lane] 16-byte pieces; lane
-  // 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
-  __shared__ u32x4_t ash[MAX_KD / 64 * 2 * 64];
+  constexpr int ASZ = MAX_KD / 64 * 2 * 64;  // pieces of one row group
+  // A rows of the current pass, per row group: [kb][half][lane] 16-byte
+  // pieces; lane 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
+  __shared__ u32x4_t ash[RG * ASZ];
 
   const int e = blockIdx.x / groups_per_expert;
   const int grp = blockIdx.x % groups_per_expert;
@@ -111,9 +113,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   // staged, so HBM is busy from the workgroup's start
   if (active) prologue();
 
-  for (int rc = 0; rc < count; rc += 16) {
+  for (int rc = 0; rc < count; rc += 16 * RG) {
     __syncthreads();  // the previous pass has finished reading ash
-    for (int i = tid; i < 16 * pieces; i += NW * 64) {
+    for (int i = tid; i < 16 * RG * pieces; i += NW * 64) {
       const int r = i / pieces, c8 = i - r * pieces;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
       if (rc + r < count) {
@@ -121,28 +123,37 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
         v = *reinterpret_cast<const u32x4_t*>(X + (size_t)src * Kd + 8 * c8);
       }
-      ash[((c8 >> 3) * 2 + (c8 & 1)) * 64 + ((c8 >> 1) & 3) * 16 + r] = v;
+      ash[(r >> 4) * ASZ + ((c8 >> 3) * 2 + (c8 & 1)) * 64 + ((c8 >> 1) & 3) * 16 + (r & 15)] = v;
     }
     __syncthreads();
     if (!active) continue;
     if (rc > 0) prologue();
 
-    f32x4_t acc[NMAT], rs = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[RG][NMAT], rs[RG];
 #pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rg = 0; rg < RG; ++rg) {
+      rs[rg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) acc[rg][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
-#define MXM_Q8_STEP(s, kbi)                                                              \
-  {                                                                                      \
-    const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, ash[((kbi) * 2 + 0) * 64 + lane]);  \
-    const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, ash[((kbi) * 2 + 1) * 64 + lane]);  \
-    rs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, rs, 0, 0, 0);                 \
-    rs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, rs, 0, 0, 0);                 \
-    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                \
-      const bf16x8_t b0 = u8x8_to_bf16(wb[s][mt].x, wb[s][mt].y);                        \
-      const bf16x8_t b1 = u8x8_to_bf16(wb[s][mt].z, wb[s][mt].w);                        \
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[mt], 0, 0, 0);       \
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[mt], 0, 0, 0);       \
-    }                                                                                    \
+#define MXM_Q8_STEP(s, kbi)                                                                  \
+  {                                                                                          \
+    bf16x8_t a0[RG], a1[RG];                                                                 \
+    _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
+      a0[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);    \
+      a1[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);    \
+      rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], ones, rs[rg], 0, 0, 0);       \
+      rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], ones, rs[rg], 0, 0, 0);       \
+    }                                                                                        \
+    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
+      const bf16x8_t b0 = u8x8_to_bf16(wb[s][mt].x, wb[s][mt].y);                            \
+      const bf16x8_t b1 = u8x8_to_bf16(wb[s][mt].z, wb[s][mt].w);                            \
+      _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                    \
+        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt], 0, 0, 0); \
+        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt], 0, 0, 0); \
+      }                                                                                      \
+    }                                                                                        \
   }
 
     int kb = 0;
@@ -163,12 +174,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 
     // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
 #pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = rc + 4 * g + i;
+      const int r = rc + 16 * rg + 4 * g + i;
       if (r >= count) continue;
       float v[NMAT];
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) v[mt] = (acc[mt][i] - 128.0f * rs[i]) * sc[mt];
+      for (int mt = 0; mt < NMAT; ++mt) v[mt] = (acc[rg][mt][i] - 128.0f * rs[rg][i]) * sc[mt];
       float out;
       if (MODE == MXM_GEMM_GLU) {
         out = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(v[0]),
@@ -183,17 +196,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   }
 }
 
-template <int EPI, int P>
+template <int EPI, int P, int RG>
 void launch_q8(const GemmArgs& a, hipStream_t s) {
   const int ncb = a.Ncols / 16;
   const int gpe = (ncb + NW - 1) / NW;
-  hipLaunchKernelGGL((gemm_q8_kernel<EPI, P>), dim3(a.E * gpe), dim3(NW * 64), 0, s, a, gpe);
+  hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG>), dim3(a.E * gpe), dim3(NW * 64), 0, s, a, gpe);
 }
 
 template <int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s) {
   constexpr bool two = Epi<EPI>::MODE == MXM_GEMM_GLU;
-  launch_q8<EPI, two ? MXM_Q8_DEPTH_GLU : MXM_Q8_DEPTH_ONE>(a, s);
+  constexpr int P = two ? MXM_Q8_DEPTH_GLU : MXM_Q8_DEPTH_ONE;
+  // 32 rows per pass once an expert averages more than 12 rows (the weights
+  // of an expert with r rows are streamed ceil(r / rows per pass) times; one
+  // row group keeps the LDS at 64 KB, two workgroups per CU)
+  if (a.rows_total > 12 * a.E)
+    launch_q8<EPI, P, 2>(a, s);
+  else
+    launch_q8<EPI, P, 1>(a, s);
 }
 
 // Reorder one int8 matrix src [Kd][C] into the 1 KB block layout.

@@ -146,6 +146,7 @@ struct GemmArgs {
   float slope;
   bool y_bf16;            // SIMT down: round y to bf16
   int family;             // MFMA tile family (MXM_TILE_*), MXM_TILE_AUTO picks
+  int rows_total;         // N*K routed rows (int8 family: picks rows per pass)
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
