@@ -157,7 +157,7 @@ __global__ __launch_bounds__(NT) void router_kernel(
   constexpr int STAGE_FLOATS = BK * TM + BK * EP;
   constexpr int LG_FLOATS = TM * LG_STRIDE;
   constexpr int SMEM_FLOATS = STAGE_FLOATS > LG_FLOATS ? STAGE_FLOATS : LG_FLOATS;
-  __shared__ float smem[SMEM_FLOATS];
+  __shared__ __attribute__((aligned(16))) float smem[SMEM_FLOATS];
   __shared__ uint32_t mask[EP][2];
   constexpr int THREADS = NT;
   constexpr int NWAVE = THREADS / 64;
@@ -182,39 +182,8 @@ __global__ __launch_bounds__(NT) void router_kernel(
 #pragma unroll
     for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
 
-  for (int d0 = 0; d0 < D; d0 += BK) {
-    __syncthreads();
-    if (VEC) {
-      // 16-byte loads along d, token-fastest across lanes so the transposed
-      // LDS store is conflict-free.
-      constexpr int PER = 16 / sizeof(TX);
-      for (int i = tid; i < TM * (BK / PER); i += NT) {
-        const int t = i % TM, dc = i / TM;
-        const int n = n0 + t, d = d0 + dc * PER;
-        float f[PER];
-        if (n < N && d < D) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(x + (size_t)n * D + d);
-          unpack16<TX>(raw, f);
-        } else {
-#pragma unroll
-          for (int q = 0; q < PER; ++q) f[q] = 0.0f;
-        }
-#pragma unroll
-        for (int q = 0; q < PER; ++q) xs[(dc * PER + q) * TM + t] = f[q];
-      }
-    } else {
-      for (int i = tid; i < TM * BK; i += NT) {
-        const int t = i % TM, dd = i / TM;
-        const int n = n0 + t, d = d0 + dd;
-        xs[dd * TM + t] = (n < N && d < D) ? ld_as_f32<TX>(x + (size_t)n * D + d) : 0.0f;
-      }
-    }
-    for (int i = tid; i < BK * EP; i += NT) {
-      const int dd = i / EP, e = i % EP;
-      const int d = d0 + dd;
-      ws[i] = (d < D && e < E) ? ld_as_f32<TX>(wr + (size_t)d * E + e) : 0.0f;
-    }
-    __syncthreads();
+  // products of one BK chunk held in LDS
+  auto compute = [&]() {
 #pragma unroll 4
     for (int dd = 0; dd < BK; ++dd) {
       const float4 xv = *reinterpret_cast<const float4*>(&xs[dd * TM + ty * 4]);
@@ -228,6 +197,94 @@ __global__ __launch_bounds__(NT) void router_kernel(
         acc[2][j] = __builtin_fmaf(xv.z, wv[j], acc[2][j]);
         acc[3][j] = __builtin_fmaf(xv.w, wv[j], acc[3][j]);
       }
+    }
+  };
+  if constexpr (VEC) {
+    // 16-byte pieces of x (token-fastest across lanes, so the transposed LDS
+    // store is conflict-free) and of router_w rows.  The next chunk's pieces
+    // are loaded into registers while the current chunk's products run;
+    // pieces outside [N, D] x [D, E] are loaded from a valid address and
+    // zeroed when stored.
+    constexpr int PER = 16 / (int)sizeof(TX);
+    constexpr int XPC = TM * BK / PER;  // x pieces per chunk
+    constexpr int WPC = BK * EP / PER;  // router_w pieces per chunk
+    constexpr int XP = (XPC + NT - 1) / NT, WP = (WPC + NT - 1) / NT;
+    static_assert(WP <= 32 && XP <= 32, "validity masks are 32 bits");
+    uint4 xr[XP], wrr[WP];
+    uint32_t xok = 0u, wok = 0u;
+    auto load = [&](int d0) {
+      xok = 0u;
+      wok = 0u;
+#pragma unroll
+      for (int p = 0; p < XP; ++p) {
+        const int i = tid + p * NT;
+        const int t = i % TM, dc = i / TM;
+        const int n = n0 + t, d = d0 + dc * PER;
+        const bool ok = i < XPC && n < N && d < D;
+        xr[p] = *reinterpret_cast<const uint4*>(x + (ok ? (size_t)n * D + d : 0));
+        xok |= ok ? (1u << p) : 0u;
+      }
+#pragma unroll
+      for (int p = 0; p < WP; ++p) {
+        const int j = tid + p * NT;
+        const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
+        const int d = d0 + dd;
+        const bool ok = j < WPC && d < D && ec < E;
+        wrr[p] = *reinterpret_cast<const uint4*>(wr + (ok ? (size_t)d * E + ec : 0));
+        wok |= ok ? (1u << p) : 0u;
+      }
+    };
+    auto store = [&]() {
+#pragma unroll
+      for (int p = 0; p < XP; ++p) {
+        const int i = tid + p * NT;
+        if (i < XPC) {
+          const int t = i % TM, dc = i / TM;
+          float f[PER];
+          unpack16<TX>(xr[p], f);
+          const bool ok = (xok >> p) & 1u;
+#pragma unroll
+          for (int q = 0; q < PER; ++q) xs[(dc * PER + q) * TM + t] = ok ? f[q] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < WP; ++p) {
+        const int j = tid + p * NT;
+        if (j < WPC) {
+          const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
+          float f[PER];
+          unpack16<TX>(wrr[p], f);
+          const bool ok = (wok >> p) & 1u;
+#pragma unroll
+          for (int q = 0; q < PER; q += 4)
+            *reinterpret_cast<float4*>(&ws[dd * EP + ec + q]) =
+                ok ? make_float4(f[q], f[q + 1], f[q + 2], f[q + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    };
+    load(0);
+    for (int d0 = 0; d0 < D; d0 += BK) {
+      __syncthreads();  // the previous chunk's products are done with LDS
+      store();
+      __syncthreads();
+      if (d0 + BK < D) load(d0 + BK);
+      compute();
+    }
+  } else {
+    for (int d0 = 0; d0 < D; d0 += BK) {
+      __syncthreads();
+      for (int i = tid; i < TM * BK; i += NT) {
+        const int t = i % TM, dd = i / TM;
+        const int n = n0 + t, d = d0 + dd;
+        xs[dd * TM + t] = (n < N && d < D) ? ld_as_f32<TX>(x + (size_t)n * D + d) : 0.0f;
+      }
+      for (int i = tid; i < BK * EP; i += NT) {
+        const int dd = i / EP, e = i % EP;
+        const int d = d0 + dd;
+        ws[i] = (d < D && e < E) ? ld_as_f32<TX>(wr + (size_t)d * E + e) : 0.0f;
+      }
+      __syncthreads();
+      compute();
     }
   }
   __syncthreads();
@@ -659,8 +716,10 @@ void launch_route_small_dt(const RouteSmallArgs& a, hipStream_t s) {
 template <typename TX, bool BF16, int EPT>
 void launch_router_t(const RouterArgs& a, hipStream_t s) {
   const int ntiles = (a.N + TM - 1) / TM;
-  const bool vec = (a.D % (16 / (int)sizeof(TX))) == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+  constexpr int PER = 16 / (int)sizeof(TX);
+  const bool vec = a.D % PER == 0 && a.E % PER == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.x) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.wr) % 16) == 0;
   if (vec)
     hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true>), dim3(ntiles), dim3(NT), 0, s,
                        static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
