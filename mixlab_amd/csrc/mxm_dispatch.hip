@@ -47,13 +47,27 @@ __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
   const int T = a.ntiles;
 
   // pass 1: per-expert totals and probability sums (lane-strided sequential
-  // partial sums, then a fixed butterfly)
+  // partial sums, then a fixed butterfly); the loads of SB tiles per lane are
+  // issued together
+  constexpr int SB = 16;
   for (int e = wave; e < a.E; e += NW) {
     int c = 0;
     float ps = 0.0f;
-    for (int t = lane; t < T; t += 64) {
-      c += a.tile_counts[(size_t)e * T + t];
-      ps = ps + a.tile_psum[(size_t)e * T + t];
+    for (int t0 = lane; t0 < T; t0 += 64 * SB) {
+      int cv[SB];
+      float pv[SB];
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        const int t = t0 + 64 * b;
+        cv[b] = t < T ? a.tile_counts[(size_t)e * T + t] : 0;
+        pv[b] = t < T ? a.tile_psum[(size_t)e * T + t] : 0.0f;
+      }
+#pragma unroll
+      for (int b = 0; b < SB; ++b)
+        if (t0 + 64 * b < T) {
+          c += cv[b];
+          ps = ps + pv[b];
+        }
     }
     c = wave_sum_int(c);
     ps = wave_sum_fixed(ps);
@@ -65,7 +79,14 @@ __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
   }
   if (wave == NW - 1) {
     float s = 0.0f;
-    for (int t = lane; t < T; t += 64) s = s + a.tile_ent[t];
+    for (int t0 = lane; t0 < T; t0 += 64 * SB) {
+      float ev[SB];
+#pragma unroll
+      for (int b = 0; b < SB; ++b) ev[b] = t0 + 64 * b < T ? a.tile_ent[t0 + 64 * b] : 0.0f;
+#pragma unroll
+      for (int b = 0; b < SB; ++b)
+        if (t0 + 64 * b < T) s = s + ev[b];
+    }
     s = wave_sum_fixed(s);
     if (lane == 0) a.entropy[0] = -(s / (float)a.N);
   }
@@ -98,20 +119,30 @@ __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
   }
   __syncthreads();
 
-  // pass 2: exclusive scan over tiles, per expert
+  // pass 2: exclusive scan over tiles, per expert (SB chunks of 64 tiles
+  // loaded together, then scanned in order)
   for (int e = wave; e < a.E; e += NW) {
     int carry = offs[e];
-    for (int t0 = 0; t0 < T; t0 += 64) {
-      const int t = t0 + lane;
-      const int c = (t < T) ? a.tile_counts[(size_t)e * T + t] : 0;
-      int incl = c;
+    for (int c0 = 0; c0 < T; c0 += 64 * SB) {
+      int cv[SB];
 #pragma unroll
-      for (int s = 1; s < 64; s <<= 1) {
-        const int up = __shfl_up(incl, s, 64);
-        if (lane >= s) incl += up;
+      for (int b = 0; b < SB; ++b) {
+        const int t = c0 + 64 * b + lane;
+        cv[b] = t < T ? a.tile_counts[(size_t)e * T + t] : 0;
       }
-      if (t < T) a.tile_base[(size_t)e * T + t] = carry + incl - c;
-      carry += __shfl(incl, 63, 64);
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        const int t = c0 + 64 * b + lane;
+        if (c0 + 64 * b >= T) break;
+        int incl = cv[b];
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) {
+          const int up = __shfl_up(incl, s, 64);
+          if (lane >= s) incl += up;
+        }
+        if (t < T) a.tile_base[(size_t)e * T + t] = carry + incl - cv[b];
+        carry += __shfl(incl, 63, 64);
+      }
     }
   }
 }
