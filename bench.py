@@ -178,30 +178,37 @@ def copy_calibration(mib: int, reps: int = 5) -> int:
 
 def run_backward(cfg, steps: int, warmup: int) -> dict:
     """Backward of op 74 (mxm_moe_backward: a forward with the routing kept,
-    then the gradients of x, the router and every routed expert) on a
-    configuration computed in fp32."""
+    then the gradients of x, the router and every routed expert) on the
+    configuration's compute dtype.  fp32: products on the SIMT kernels; bf16
+    (MFMA weight family): products on MFMA and, for the weight gradients,
+    rocBLAS bf16 GEMMs with fp32 output."""
     from mixlab_amd import _lib
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import make_workload
 
+    bf16 = cfg.dtype == "bf16"
     w = make_workload(cfg)
-    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype="fp32")
-    op.set_input(1, np.ascontiguousarray(w.router_w, np.float32))
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype)
+    op.set_input(1, w.router_upload() if bf16 else np.ascontiguousarray(w.router_w, np.float32))
     idx = 2
     for e in range(cfg.E):
         for j in range(cfg.wpe):
-            op.set_input(idx, np.ascontiguousarray(w.matrix(e, j), np.float32))
+            op.set_input(idx, w.matrix_upload(e, j) if bf16
+                         else np.ascontiguousarray(w.matrix(e, j), np.float32))
             idx += 1
     rng = np.random.default_rng(7)
-    xdev = _lib.DeviceBuffer.from_array(np.ascontiguousarray(w.x, np.float32))
+    xdev = _lib.DeviceBuffer.from_array(w.x_upload() if bf16
+                                        else np.ascontiguousarray(w.x, np.float32))
+    xcode = _lib.MXM_DTYPE_BF16 if bf16 else _lib.MXM_DTYPE_F32
     dd = _lib.DeviceBuffer.from_array(rng.standard_normal((cfg.N, cfg.D), dtype=np.float32))
     dx = _lib.DeviceBuffer(cfg.N * cfg.D * 4)
     dwr = _lib.DeviceBuffer(cfg.D * cfg.E * 4)
     dw = _lib.DeviceBuffer(cfg.E * cfg.wpe * cfg.D * cfg.F * 4)
     lib = _lib.init()
+    mfma = op.info()["mfma"]
 
     def step():
-        _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, _lib.MXM_DTYPE_F32, cfg.N,
+        _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, xcode, cfg.N,
                                         dd.value, 0.01, 0.0, dx.value, dwr.value, dw.value),
                    "mxm_moe_backward")
 
@@ -220,12 +227,17 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     fl = 2 * nkdf * ((3 if glu else 2) + (2 if glu else 1) + 1 + (2 if glu else 1)
                      + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
     tf = fl / (ms * 1e-3) / 1e12
-    log(f"backward {cfg.name} fp32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
-    return {"workload": f"{cfg.name} shape, fp32 compute", "tokens": cfg.N,
-            "ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3),
-            "roofline": {"bound": "valu", "kernel": "whole backward (SIMT fp32 products)",
-                         "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": tf / PEAK_FP32_TFLOPS, "traffic": None}}
+    log(f"backward {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+    if bf16 and mfma:
+        roof = {"bound": "mfma", "kernel": "whole backward (MFMA grouped products, rocBLAS "
+                "weight gradients)", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": tf / PEAK_BF16_TFLOPS, "traffic": None}
+    else:
+        roof = {"bound": "valu", "kernel": "whole backward (SIMT fp32 products)",
+                "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": tf / PEAK_FP32_TFLOPS, "traffic": None}
+    return {"workload": f"{cfg.name} shape, {cfg.dtype} compute", "tokens": cfg.N,
+            "ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3), "roofline": roof}
 
 
 def main() -> int:
@@ -297,10 +309,11 @@ def main() -> int:
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
 
-    backward = None
+    backward = backward_bf16 = None
     if not args.no_backward:
         import dataclasses
         backward = run_backward(dataclasses.replace(CONFIGS["C2"], dtype="fp32"), 5, 2)
+        backward_bf16 = run_backward(CONFIGS["C2"], 10, 3)
 
     line = {
         "metric": METRIC,
@@ -329,6 +342,7 @@ def main() -> int:
         "hbm_gbs": hbm,
         "decode_int8": decode,
         "backward_fp32": backward,
+        "backward_bf16": backward_bf16,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -7,6 +7,7 @@
 // point (gpu/mlx_bridge.cpp:64-82) that turns failures into status codes and
 // a per-thread message.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <array>
 #include <cstdarg>
@@ -105,11 +106,17 @@ struct MoeOp {
   // backward (fp32 flow): recomputed intermediates, transposed weights
   bool keep_probs = false, bw_ready = false;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
-      bw_dlogits, bw_dxr, bw_w1t, bw_w1bt, bw_w2t, bw_wrt, bw_one;
+      bw_dlogits, bw_dxr, bw_w1t, bw_w1bt, bw_w2t, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
   // and of the forward's expert outputs, for the fp32 backward kernels
   bool bw_w32_ready = false;
   DevBuf bw_w1_32, bw_w1b_32, bw_w2_32, bw_wr32, bw_x32, bw_y32, bw_mstart;
+  // bf16 ops of the MFMA family: bf16 intermediates of the MFMA backward, the
+  // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
+  // handle for the weight gradients
+  bool bw_wbf_ready = false;
+  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_dw1cat, bw_ms, bw_w2o, bw_w1u;
+  rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
   size_t ws_bytes = 0;
 
@@ -127,6 +134,7 @@ struct MoeOp {
     for (auto& set : ev_sets)
       for (auto& e : set)
         if (e) (void)hipEventDestroy(e);
+    if (bw_blas) (void)rocblas_destroy_handle(bw_blas);
   }
 };
 
@@ -515,6 +523,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
   HIPCK(hipStreamSynchronize(st));
   o.have[idx] = 1;
   o.bw_w32_ready = false;
+  o.bw_wbf_ready = false;
 }
 
 void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, const int64_t* shape,
@@ -548,6 +557,7 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   HIPCK(hipStreamSynchronize(st));
   o.have[idx] = 1;
   o.bw_w32_ready = false;
+  o.bw_wbf_ready = false;
 }
 
 }  // namespace
@@ -859,11 +869,141 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
 }
 
 // Backward of op 74: a forward on x (keeping the router probabilities), then
-// mxm_launch_backward, whose kernels compute in fp32.  Under bf16 compute
-// they take the bf16 flow's values: x and the weights as rounded to bf16,
-// and the forward's bf16 expert outputs, converted to fp32.  d_experts receives the expert
-// weight gradients in Op.Inputs order (per expert gate, up, down -- or up,
-// down -- in x.W layout).
+// the gate / router gradients (mxm_launch_backward_router) and the experts'
+// products.  fp32 ops and bf16 ops whose shapes the MFMA family does not
+// tile run the experts' products on the fp32 SIMT kernels, the bf16 flow's
+// values (x and weights rounded to bf16, the forward's bf16 expert outputs)
+// converted to fp32.  bf16 ops of the MFMA family run them on MFMA
+// (run_backward_mfma).  d_experts receives the expert weight gradients in
+// Op.Inputs order (per expert gate, up, down -- or up, down -- in x.W layout).
+
+// Shapes of the MFMA backward's three grouped products: dH = dY W_down^T
+// (F columns, reduction D), the recomputed projections (NC, D) and
+// dX = dGU W1^T (D, NC), NC = 2F (GLU) or F.
+bool mfma_backward_fits(const MoeOp& o) {
+  const int NC = o.wpe == 3 ? 2 * o.F : o.F;
+  return o.mfma && mxm_mfma_tile_rows(o.F, o.D, o.family) > 0 &&
+         mxm_mfma_tile_rows(NC, o.D, o.family) > 0 && mxm_mfma_tile_rows(o.D, NC, o.family) > 0;
+}
+
+void check_blas(rocblas_status st, const char* what) {
+  if (st != rocblas_status_success)
+    fail("OP_MOE_FEED_FORWARD backward: %s failed (rocBLAS status %d)", what, (int)st);
+}
+
+// dst[rows][C] (row-major, fp32) = A^T B over `rows`, A [rows][M], B [rows][C]
+// bf16 row-major (rocBLAS is column-major: dst^T = B^T A).
+void gemm_at_b(rocblas_handle h, const uint16_t* A, int M, const uint16_t* B, int C, int rows,
+               float* dst) {
+  const float one = 1.0f, zero = 0.0f;
+  check_blas(rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, C, M, rows, &one,
+                             B, rocblas_datatype_bf16_r, C, A, rocblas_datatype_bf16_r, M, &zero, dst,
+                             rocblas_datatype_f32_r, C, dst, rocblas_datatype_f32_r, C,
+                             rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
+             "weight-gradient GEMM");
+}
+
+// The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
+// permuted order throughout (expert e owns rows offsets[e] ..).
+//   dH  = dY W_down^T          MFMA grouped GEMM, W_down kept as [F][D] bf16
+//   G|U = Xp W1                MFMA grouped GEMM with the forward's W1 (the
+//                              bf16 flow's projections, recomputed)
+//   dG|dU                      elementwise (act_bw_bf16)
+//   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
+//   dx  = dxr + sum_k dXe      (dx_bf16)
+//   dW1 = Xp^T dG|dU, dW_down = H^T dY   per expert, rocBLAS bf16 -> fp32
+void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* dx, float* dw) {
+  hipStream_t st = o.stream;
+  const bool glu = o.wpe == 3;
+  const int D = o.D, F = o.F, E = o.E, NC = glu ? 2 * F : F;
+  const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
+  if (!o.bw_dyb.p) {
+    o.bw_dyb.alloc(NK * D * 2);
+    o.bw_xpb.alloc(NK * D * 2);
+    o.bw_dhb.alloc(NK * F * 2);
+    o.bw_gub.alloc(NK * NC * 2);
+    o.bw_dgub.alloc(NK * NC * 2);
+    o.bw_dxeb.alloc(NK * D * 2);
+    if (glu) o.bw_dw1cat.alloc((size_t)E * D * NC * 4);
+    o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
+    o.bw_w2o.alloc((size_t)E * DF * 2);
+    o.bw_w1u.alloc((size_t)E * D * NC * 2);
+  }
+  if (!o.bw_wbf_ready) {
+    for (int e = 0; e < E; ++e) {
+      // W_down: forward [D][F] -> [F][D]; W1: forward [NC][D] -> [D][NC]
+      mxm_launch_transpose_bf16(o.w2.as<uint16_t>() + (size_t)e * DF, MXM_DTYPE_BF16, D, F, -1,
+                                o.bw_w2o.as<uint16_t>() + (size_t)e * DF, st);
+      mxm_launch_transpose_bf16(o.w1.as<uint16_t>() + (size_t)e * NC * D, MXM_DTYPE_BF16, NC, D, -1,
+                                o.bw_w1u.as<uint16_t>() + (size_t)e * D * NC, st);
+    }
+    HIPCK(hipGetLastError());
+    o.bw_wbf_ready = true;
+  }
+  uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *xpb = o.bw_xpb.as<uint16_t>(),
+           *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
+           *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>();
+  mxm_launch_to_bf16(b.dy, MXM_DTYPE_F32, dyb, (int64_t)(NK * D), st);
+  mxm_launch_gather_rows_bf16(static_cast<const uint16_t*>(xb), b.perm, (int)NK, D, xpb, st);
+  auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols) {
+    const int bm = mxm_mfma_tile_rows(Ncols, Kd, o.family);
+    int32_t* ms = o.bw_ms.as<int32_t>() + (size_t)which * (E + 1);
+    mxm_launch_tile_prefix(b.counts, E, bm, ms, st);
+    GemmArgs g{};
+    g.mode = MXM_GEMM_DOWN;
+    g.a = A;
+    g.b0 = W;
+    g.out = out;
+    g.offsets = b.offsets;
+    g.mstart = ms;
+    g.E = E;
+    g.Kd = Kd;
+    g.Ncols = Ncols;
+    g.max_mtiles = (int)((NK + bm - 1) / bm) + E;
+    g.family = o.family;
+    g.rows_total = (int)NK;
+    require_operands(g, false, false);
+    mxm_launch_gemm_mfma(g, st);
+    HIPCK(hipGetLastError());
+  };
+  product(0, dyb, o.bw_w2o.p, dhb, D, F);
+  product(1, xpb, o.w1.p, gub, D, NC);
+  mxm_launch_act_bw_bf16(gub, dhb, (int)NK, F, o.etype, o.act, o.slope, dgub, st);
+  product(2, dgub, o.bw_w1u.p, dxeb, NC, D);
+  mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
+  HIPCK(hipGetLastError());
+
+  // weight gradients: one rocBLAS GEMM per expert and matrix pair, sized by
+  // the expert's row count
+  std::vector<int32_t> cnt(E);
+  HIPCK(hipMemcpyAsync(cnt.data(), b.counts, (size_t)E * 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  if (!o.bw_blas) {
+    check_blas(rocblas_create_handle(&o.bw_blas), "rocblas_create_handle");
+  }
+  check_blas(rocblas_set_stream(o.bw_blas, st), "rocblas_set_stream");
+  const uint16_t* hb = o.H.as<uint16_t>();
+  float* w1g = glu ? o.bw_dw1cat.as<float>() : nullptr;
+  size_t off = 0;
+  for (int e = 0; e < E; ++e) {
+    const int rows = cnt[e];
+    float* dwe = dw + (size_t)e * stride;
+    if (rows <= 0) {
+      HIPCK(hipMemsetAsync(dwe, 0, stride * 4, st));
+      if (glu) HIPCK(hipMemsetAsync(w1g + (size_t)e * D * NC, 0, (size_t)D * NC * 4, st));
+      continue;
+    }
+    // gate|up (interleaved, GLU) or up (MLP): [D][NC] = Xp^T dGU
+    gemm_at_b(o.bw_blas, xpb + off * D, D, dgub + off * NC, NC, rows,
+              glu ? w1g + (size_t)e * D * NC : dwe);
+    // down: [F][D] = H^T dY
+    gemm_at_b(o.bw_blas, hb + off * F, F, dyb + off * D, D, rows, dwe + (glu ? 2 : 1) * DF);
+    off += (size_t)rows;
+  }
+  if (glu) mxm_launch_deinterleave(w1g, E, D, F, dw, stride, st);
+  HIPCK(hipGetLastError());
+}
+
 void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
                   float d_ent, float* dx, float* dwr, float* dw) {
   if (o.q8) fail("OP_MOE_FEED_FORWARD backward is not available for int8 expert weights");
@@ -872,30 +1012,34 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   if (!x || !d_delta || !dx || !dwr || !dw) fail("OP_MOE_FEED_FORWARD backward pointers must be non-NULL");
   if (!o.ws_ready) alloc_workspace(o);
   const size_t N = o.N, D = o.D, E = o.E, F = o.F, NK = (size_t)o.N * o.K;
+  const bool mfma_bw = mfma_backward_fits(o);
   if (!o.probs.p) o.probs.alloc(N * E * 4);
   if (!o.bw_ready) {
     o.bw_delta.alloc(N * D * 4);
-    o.bw_xp.alloc(NK * D * 4);
     o.bw_dy.alloc(NK * D * 4);
-    o.bw_dxg.alloc(NK * D * 4);
-    o.bw_dxu.alloc(NK * D * 4);
-    o.bw_g.alloc(NK * F * 4);
-    o.bw_u.alloc(NK * F * 4);
-    o.bw_h.alloc(NK * F * 4);
-    o.bw_dh.alloc(NK * F * 4);
-    o.bw_dg.alloc(NK * F * 4);
-    o.bw_du.alloc(NK * F * 4);
     o.bw_dgates.alloc(NK * 4);
     o.bw_dlogits.alloc(N * E * 4);
     o.bw_dxr.alloc(N * D * 4);
-    o.bw_w1t.alloc(E * D * F * 4);
-    o.bw_w1bt.alloc(E * D * F * 4);
-    o.bw_w2t.alloc(E * D * F * 4);
     o.bw_wrt.alloc(D * E * 4);
+    o.bw_wr_part.alloc((size_t)wgrad_router_chunks(o.N) * D * E * 4);
     o.bw_one.alloc(16);
     o.bw_one_host[1] = o.N;
     o.bw_one_host[3] = (o.N + 63) / 64;
     HIPCK(hipMemcpyAsync(o.bw_one.p, o.bw_one_host, 16, hipMemcpyHostToDevice, o.stream));
+    if (!mfma_bw) {
+      o.bw_xp.alloc(NK * D * 4);
+      o.bw_dxg.alloc(NK * D * 4);
+      o.bw_dxu.alloc(NK * D * 4);
+      o.bw_g.alloc(NK * F * 4);
+      o.bw_u.alloc(NK * F * 4);
+      o.bw_h.alloc(NK * F * 4);
+      o.bw_dh.alloc(NK * F * 4);
+      o.bw_dg.alloc(NK * F * 4);
+      o.bw_du.alloc(NK * F * 4);
+      o.bw_w1t.alloc(E * D * F * 4);
+      o.bw_w1bt.alloc(E * D * F * 4);
+      o.bw_w2t.alloc(E * D * F * 4);
+    }
     o.bw_ready = true;
   }
   const float *w1 = o.w1.as<float>(), *w1b = o.w1b.as<float>(), *w2 = o.w2.as<float>();
@@ -904,13 +1048,13 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   const float* y32 = o.Y.as<float>();
   if (o.bf16) {
     // The bf16 flow's values (x and weights rounded to bf16, the forward's
-    // bf16 expert outputs) go through the fp32 backward kernels.
+    // bf16 expert outputs) in fp32 for the fp32 kernels.
     if (!o.bw_w32_ready) {
       const size_t DF = D * F;
       if (!o.bw_wr32.p) o.bw_wr32.alloc(D * E * 4);
       mxm_launch_to_f32(o.router.p, MXM_DTYPE_BF16, o.bw_wr32.as<float>(), (int64_t)(D * E),
                         o.stream);
-      if (o.mfma) {
+      if (o.mfma && !mfma_bw) {
         const bool glu = o.wpe == 3;
         if (!o.bw_w1_32.p) o.bw_w1_32.alloc(E * DF * 4);
         if (glu && !o.bw_w1b_32.p) o.bw_w1b_32.alloc(E * DF * 4);
@@ -935,9 +1079,9 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   o.keep_probs = true;
   run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr);
   o.keep_probs = false;
+  // x as the forward saw it (rounded to bf16 when given in fp32)
+  const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.xcast.p;
   if (o.bf16) {
-    // x as the forward saw it (rounded to bf16 when given in fp32)
-    const void* xb = x_dtype == MXM_DTYPE_BF16 ? x : o.xcast.p;
     mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
     if (o.mfma) {
       if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
@@ -955,17 +1099,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.etype = o.etype;
   b.act = o.act;
   b.wpe = o.wpe;
-  // the backward's grouped products are SIMT kernels: their row tiles
-  b.max_mtiles = o.max_mtiles2;
-  b.mstart = o.mstart2.as<int32_t>();
-  if (o.bm2 != mxm_simt_bm()) {
-    if (!o.bw_mstart.p) o.bw_mstart.alloc(((size_t)o.E + 1) * 4);
-    mxm_launch_tile_prefix(o.counts.as<int32_t>(), o.E, mxm_simt_bm(), o.bw_mstart.as<int32_t>(),
-                           o.stream);
-    HIPCK(hipGetLastError());
-    b.mstart = o.bw_mstart.as<int32_t>();
-    b.max_mtiles = (int)((NK + mxm_simt_bm() - 1) / mxm_simt_bm()) + o.E;
-  }
   b.slope = o.slope;
   b.x = x32;
   b.top_idx = o.top_idx.as<int32_t>();
@@ -977,34 +1110,52 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.probs = o.probs.as<float>();
   b.Y = y32;
   b.wr = wr;
-  b.w1 = w1;
-  b.w1b = w1b;
-  b.w2 = w2;
   b.d_delta = d_delta;
   b.d_aux = d_aux;
   b.d_ent = d_ent;
+  b.dy = o.bw_dy.as<float>();
+  b.dgates = o.bw_dgates.as<float>();
+  b.dlogits = o.bw_dlogits.as<float>();
+  b.dxr = o.bw_dxr.as<float>();
+  b.wrt = o.bw_wrt.as<float>();
+  b.one = o.bw_one.as<int32_t>();
+  b.wr_part = o.bw_wr_part.as<float>();
+  b.dx = dx;
+  b.dwr = dwr;
+  b.dw = dw;
+  mxm_launch_backward_router(b, o.stream);
+  HIPCK(hipGetLastError());
+  if (mfma_bw) {
+    run_backward_mfma(o, xb, b, dx, dw);
+    return;
+  }
+  // the experts' products on the SIMT kernels, with their row tiles
+  b.max_mtiles = o.max_mtiles2;
+  b.mstart = o.mstart2.as<int32_t>();
+  if (o.bm2 != mxm_simt_bm()) {
+    if (!o.bw_mstart.p) o.bw_mstart.alloc(((size_t)o.E + 1) * 4);
+    mxm_launch_tile_prefix(o.counts.as<int32_t>(), o.E, mxm_simt_bm(), o.bw_mstart.as<int32_t>(),
+                           o.stream);
+    HIPCK(hipGetLastError());
+    b.mstart = o.bw_mstart.as<int32_t>();
+    b.max_mtiles = (int)((NK + mxm_simt_bm() - 1) / mxm_simt_bm()) + o.E;
+  }
+  b.w1 = w1;
+  b.w1b = w1b;
+  b.w2 = w2;
   b.xp = o.bw_xp.as<float>();
   b.g = o.bw_g.as<float>();
   b.u = o.bw_u.as<float>();
   b.h = o.bw_h.as<float>();
-  b.dy = o.bw_dy.as<float>();
   b.dh = o.bw_dh.as<float>();
   b.dg = o.bw_dg.as<float>();
   b.du = o.bw_du.as<float>();
   b.dxg = o.bw_dxg.as<float>();
   b.dxu = o.bw_dxu.as<float>();
-  b.dgates = o.bw_dgates.as<float>();
-  b.dlogits = o.bw_dlogits.as<float>();
-  b.dxr = o.bw_dxr.as<float>();
   b.w1t = o.bw_w1t.as<float>();
   b.w1bt = o.bw_w1bt.as<float>();
   b.w2t = o.bw_w2t.as<float>();
-  b.wrt = o.bw_wrt.as<float>();
-  b.one = o.bw_one.as<int32_t>();
-  b.dx = dx;
-  b.dwr = dwr;
-  b.dw = dw;
-  mxm_launch_backward(b, o.stream);
+  mxm_launch_backward_experts(b, o.stream);
   HIPCK(hipGetLastError());
 }
 

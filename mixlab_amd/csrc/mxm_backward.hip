@@ -218,6 +218,69 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const float* __restrict__ A,
   }
 }
 
+// Row-split weight gradient of one segment: part[c][i][j] = sum over rows
+// r in chunk c (rows c*rc .. c*rc+rc-1, ascending) of A[r][i] * B[r][j].
+__global__ __launch_bounds__(256) void wgrad_part_kernel(const float* __restrict__ A, int M,
+                                                         const float* __restrict__ B, int Nn,
+                                                         int rows, int rc,
+                                                         float* __restrict__ part) {
+  __shared__ float As[WG_R][WG_T + 4];
+  __shared__ float Bs[WG_R][WG_T + 4];
+  const int c = blockIdx.z;
+  const int i0 = blockIdx.y * WG_T, j0 = blockIdx.x * WG_T;
+  const int r0 = c * rc, r1 = min(rows, r0 + rc);
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int rb = r0; rb < r1; rb += WG_R) {
+    __syncthreads();
+    for (int q = tid; q < WG_R * WG_T; q += 256) {
+      const int rr = q / WG_T, cc = q % WG_T;
+      const int r = rb + rr;
+      As[rr][cc] = (r < r1 && i0 + cc < M) ? A[(size_t)r * M + i0 + cc] : 0.0f;
+      Bs[rr][cc] = (r < r1 && j0 + cc < Nn) ? B[(size_t)r * Nn + j0 + cc] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < WG_R; ++rr) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[rr][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[rr][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+    }
+  }
+  float* o = part + (size_t)c * M * Nn;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ii = i0 + ty * 4 + i;
+    if (ii >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int jj = j0 + tx * 4 + j;
+      if (jj < Nn) o[(size_t)ii * Nn + jj] = acc[i][j];
+    }
+  }
+}
+
+// out[q] = sum over chunks c ascending of part[c][q]
+__global__ void wgrad_sum_kernel(const float* __restrict__ part, int nchunks, size_t n,
+                                 float* __restrict__ out) {
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n;
+       q += (size_t)gridDim.x * blockDim.x) {
+    float acc = part[q];
+    for (int c = 1; c < nchunks; ++c) acc = acc + part[(size_t)c * n + q];
+    out[q] = acc;
+  }
+}
+
 // dx[n] = dxr[n] + sum_k (dxg + dxu)[slot_pos(n, k)], k ascending
 __global__ void dx_kernel(BackwardArgs a) {
   const int n = blockIdx.x;
@@ -262,6 +325,111 @@ void wgrad(const float* A, int M, const float* B, int Nn, const int32_t* offsets
                      dim3(256), 0, s, A, M, B, Nn, offsets, out, out_stride);
 }
 
+// ---- bf16 flow on the MFMA family --------------------------------------------
+
+// out[s] = x[perm[s]] (bf16 rows, permuted order)
+__global__ void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
+                                        const int32_t* __restrict__ perm, int D,
+                                        uint16_t* __restrict__ out) {
+  const int s = blockIdx.x;
+  const uint16_t* src = x + (size_t)perm[s] * D;
+  uint16_t* dst = out + (size_t)s * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
+}
+
+// Activation backward on the recomputed bf16 projections gu [N*K, NC] (GLU:
+// NC = 2F, gate and up columns interleaved in groups of 32 as the MFMA
+// family's W1 rows; MLP: NC = F, up only) and dH [N*K, F]: writes dG and dU
+// into dgu at the columns of g and u, rounded to bf16.
+__global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dh,
+                                   int F, int etype, int act, float slope, size_t total,
+                                   uint16_t* __restrict__ dgu) {
+  const bool glu = etype != MXM_EXPERT_MLP;
+  const int NC = glu ? 2 * F : F;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / F;
+    const int f = (int)(i % F);
+    const float d_h = mxm_bf2f(dh[i]);
+    if (glu) {
+      const size_t cg = r * NC + (f >> 5) * 64 + (f & 31), cu = cg + 32;
+      const float g = mxm_bf2f(gu[cg]), u = mxm_bf2f(gu[cu]);
+      float a, d;
+      if (etype == MXM_EXPERT_SWIGLU) {
+        a = 1.0f / (1.0f + expf(-g));
+        d = a * (1.0f - a);
+      } else {
+        a = gelu_t(g, d);
+      }
+      dgu[cg] = mxm_f2bf(d_h * u * d);
+      dgu[cu] = mxm_f2bf(d_h * a);
+    } else {
+      const float u = mxm_bf2f(gu[i]);
+      float d;
+      switch (act) {
+        case MXM_ACT_SILU: {
+          const float sg = 1.0f / (1.0f + expf(-u));
+          d = sg * (1.0f + u * (1.0f - sg));
+          break;
+        }
+        case MXM_ACT_GELU:
+          (void)gelu_t(u, d);
+          break;
+        case MXM_ACT_RELU:
+          d = u > 0.0f ? 1.0f : 0.0f;
+          break;
+        default: {
+          const float y = u > 0.0f ? u : u * slope;
+          d = 2.0f * y * (u > 0.0f ? 1.0f : slope);
+          break;
+        }
+      }
+      dgu[i] = mxm_f2bf(d_h * d);
+    }
+  }
+}
+
+// dx[n] = dxr[n] + sum_k dxe[slot_pos(n, k)] (bf16 rows), k ascending
+__global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __restrict__ dxe,
+                               const int32_t* __restrict__ slot_pos, int D, int K,
+                               float* __restrict__ dx) {
+  const int n = blockIdx.x;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float acc = dxr[(size_t)n * D + d];
+    for (int k = 0; k < K; ++k)
+      acc = acc + mxm_bf2f(dxe[(size_t)slot_pos[(size_t)n * K + k] * D + d]);
+    dx[(size_t)n * D + d] = acc;
+  }
+}
+
+// The GLU pair's weight gradient from the interleaved product src [E][D][2F]
+// (column c: gate (c/32 even) or up of hidden unit (c/64)*32 + c%32) into
+// the gate and up blocks of each expert's gradients (stride floats apart).
+__global__ void deinterleave_kernel(const float* __restrict__ src, int E, int D, int F,
+                                    float* __restrict__ dw, size_t stride) {
+  const size_t total = (size_t)E * D * 2 * F;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % (2 * F));
+    const size_t ed = i / (2 * F);
+    const int d = (int)(ed % D), e = (int)(ed / D);
+    const int m = (c >> 5) & 1, f = (c >> 6) * 32 + (c & 31);
+    dw[(size_t)e * stride + (size_t)m * D * F + (size_t)d * F + f] = src[i];
+  }
+}
+
+int grid_of(size_t n) {
+  size_t b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  return (int)(b < 1 ? 1 : b);
+}
+
+// Row chunks of the router's weight gradient: at most 64, of at least 256 rows.
+int wgrad_router_chunks_impl(int N) {
+  int c = (N + 255) / 256;
+  return c < 1 ? 1 : (c > 64 ? 64 : c);
+}
+
 // Row-tile prefix of a grouped GEMM family with tile height bm:
 // mstart[e] = sum over e' < e of ceil(counts[e'] / bm), e = 0..E.
 __global__ void tile_prefix_kernel(const int32_t* counts, int E, int bm, int32_t* mstart) {
@@ -276,12 +444,64 @@ __global__ void tile_prefix_kernel(const int32_t* counts, int E, int bm, int32_t
 
 }  // namespace
 
+int wgrad_router_chunks(int N) { return wgrad_router_chunks_impl(N); }
+
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s) {
   hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, counts, E, bm, mstart);
 }
 
-void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
-  const int N = a.N, D = a.D, E = a.E, K = a.K, F = a.F, NK = a.N * a.K;
+void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
+                                 uint16_t* out, hipStream_t s) {
+  if (rows > 0) hipLaunchKernelGGL(gather_rows_bf16_kernel, dim3(rows), dim3(256), 0, s, x, perm, D, out);
+}
+
+void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
+                            int act, float slope, uint16_t* dgu, hipStream_t s) {
+  const size_t total = (size_t)rows * F;
+  if (total > 0)
+    hipLaunchKernelGGL(act_bw_bf16_kernel, dim3(grid_of(total)), dim3(256), 0, s, gu, dh, F, etype,
+                       act, slope, total, dgu);
+}
+
+void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
+                        int D, int K, float* dx, hipStream_t s) {
+  if (N > 0) hipLaunchKernelGGL(dx_bf16_kernel, dim3(N), dim3(256), 0, s, dxr, dxe, slot_pos, D, K, dx);
+}
+
+void mxm_launch_deinterleave(const float* src, int E, int D, int F, float* dw, size_t stride,
+                             hipStream_t s) {
+  const size_t total = (size_t)E * D * 2 * F;
+  if (total > 0)
+    hipLaunchKernelGGL(deinterleave_kernel, dim3(grid_of(total)), dim3(256), 0, s, src, E, D, F, dw,
+                       stride);
+}
+
+// Gate, renorm, aux / entropy and softmax gradients, the router's products
+// (dx's router term dxr, d router_w) and dY = gate * dD.
+void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
+  const int N = a.N, D = a.D, E = a.E, K = a.K, NK = a.N * a.K;
+  if (NK <= 0) return;
+  transpose_batch(a.wr, 1, D, E, a.wrt, s);  // [E][D]
+  hipLaunchKernelGGL(dgates_kernel, dim3((NK + 3) / 4), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
+  hipLaunchKernelGGL(dy_kernel, dim3(NK), dim3(256), 0, s, a);
+  grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
+  // router: d router_w = x^T dlogits over all N rows -- a D x E output, so
+  // the rows are split in chunks (fixed chunk order, rows ascending within a
+  // chunk) to spread the reduction over the GPU
+  const int nch = wgrad_router_chunks(N);
+  const int rc = (N + nch - 1) / nch;
+  hipLaunchKernelGGL(wgrad_part_kernel, dim3((E + WG_T - 1) / WG_T, (D + WG_T - 1) / WG_T, nch),
+                     dim3(256), 0, s, a.x, D, a.dlogits, E, N, rc, a.wr_part);
+  const size_t n = (size_t)D * E;
+  hipLaunchKernelGGL(wgrad_sum_kernel, dim3(grid_of(n)), dim3(256), 0, s, a.wr_part, nch, n, a.dwr);
+  (void)K;
+}
+
+// The experts' products on the fp32 SIMT kernels: recomputed projections,
+// activation backward, dx (with the router term) and the weight gradients.
+void mxm_launch_backward_experts(const BackwardArgs& a, hipStream_t s) {
+  const int N = a.N, D = a.D, E = a.E, F = a.F, NK = a.N * a.K;
   const bool glu = a.etype != MXM_EXPERT_MLP;
   const size_t DF = (size_t)D * F;
   if (NK <= 0) return;
@@ -290,7 +510,6 @@ void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
   transpose_batch(a.w2, E, F, D, a.w2t, s);   // [E][D][F]
   transpose_batch(a.w1, E, D, F, a.w1t, s);   // [E][F][D]
   if (glu) transpose_batch(a.w1b, E, D, F, a.w1bt, s);
-  transpose_batch(a.wr, 1, D, E, a.wrt, s);   // [E][D]
   // projections of the forward (recomputed)
   if (glu) {
     grouped(a.xp, a.w1, a.g, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
@@ -298,11 +517,7 @@ void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
   } else {
     grouped(a.xp, a.w1, a.u, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
   }
-  // gates and router
-  hipLaunchKernelGGL(dgates_kernel, dim3((NK + 3) / 4), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
   // down projection
-  hipLaunchKernelGGL(dy_kernel, dim3(NK), dim3(256), 0, s, a);
   grouped(a.dy, a.w2t, a.dh, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
   const size_t total = (size_t)NK * F;
   int blocks = (int)((total + 255) / 256);
@@ -311,7 +526,6 @@ void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
   // input gradient
   if (glu) grouped(a.dg, a.w1t, a.dxg, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
   grouped(a.du, glu ? a.w1bt : a.w1t, a.dxu, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
-  grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
   hipLaunchKernelGGL(dx_kernel, dim3(N), dim3(256), 0, s, a);
   // weight gradients (per expert blocks of a.dw in Op.Inputs order)
   const size_t stride = (size_t)a.wpe * DF;
@@ -323,5 +537,9 @@ void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
     wgrad(a.xp, D, a.du, F, a.offsets, E, a.dw, stride, s);            // up
     wgrad(a.h, F, a.dy, D, a.offsets, E, a.dw + DF, stride, s);        // down
   }
-  wgrad(a.x, D, a.dlogits, E, a.one, 1, a.dwr, 0, s);                  // router
+}
+
+void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
+  mxm_launch_backward_router(a, s);
+  mxm_launch_backward_experts(a, s);
 }

@@ -132,16 +132,17 @@ __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
       }
 #pragma unroll
       for (int b = 0; b < SB; ++b) {
-        const int t = c0 + 64 * b + lane;
-        if (c0 + 64 * b >= T) break;
-        int incl = cv[b];
+        if (c0 + 64 * b < T) {  // wave-uniform
+          const int t = c0 + 64 * b + lane;
+          int incl = cv[b];
 #pragma unroll
-        for (int s = 1; s < 64; s <<= 1) {
-          const int up = __shfl_up(incl, s, 64);
-          if (lane >= s) incl += up;
+          for (int s = 1; s < 64; s <<= 1) {
+            const int up = __shfl_up(incl, s, 64);
+            if (lane >= s) incl += up;
+          }
+          if (t < T) a.tile_base[(size_t)e * T + t] = carry + incl - cv[b];
+          carry += __shfl(incl, 63, 64);
         }
-        if (t < T) a.tile_base[(size_t)e * T + t] = carry + incl - cv[b];
-        carry += __shfl(incl, 63, 64);
       }
     }
   }

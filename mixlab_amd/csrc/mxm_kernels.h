@@ -281,11 +281,31 @@ struct BackwardArgs {
   float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D]
   float *w1t, *w1bt, *w2t, *wrt;                          // transposed weights
   int32_t* one;                                           // [4]: offsets/mstart of one segment
+  float* wr_part;            // [wgrad_router_chunks(N)][D][E]: row-chunk partials of d router_w
   // outputs
   float* dx;                 // [N, D]
   float* dwr;                // [D, E]
   float* dw;                 // per expert, Op.Inputs order, x.W layout
 };
 void mxm_launch_backward(const BackwardArgs& a, hipStream_t s);
+// Row chunks of d router_w's reduction (BackwardArgs::wr_part holds one D x E
+// partial per chunk).
+int wgrad_router_chunks(int N);
+// Its two halves: gate/router gradients, dY, dx's router term and d router_w;
+// then the experts' products on the fp32 SIMT kernels.
+void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s);
+void mxm_launch_backward_experts(const BackwardArgs& a, hipStream_t s);
+// bf16 flow on the MFMA family (products by the MFMA grouped GEMM and, for
+// the weight gradients, rocBLAS): gathered bf16 rows, activation backward on
+// the recomputed bf16 projections, dx from bf16 expert input gradients, and
+// the GLU pair's gradient de-interleaved into Op.Inputs order.
+void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
+                                 uint16_t* out, hipStream_t s);
+void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
+                            int act, float slope, uint16_t* dgu, hipStream_t s);
+void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
+                        int D, int K, float* dx, hipStream_t s);
+void mxm_launch_deinterleave(const float* src, int E, int D, int F, float* dw, size_t stride,
+                             hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);
