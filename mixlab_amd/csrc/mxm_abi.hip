@@ -879,10 +879,11 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
 
 // Shapes of the MFMA backward's three grouped products: dH = dY W_down^T
 // (F columns, reduction D), the recomputed projections (NC, D) and
-// dX = dGU W1^T (D, NC), NC = 2F (GLU) or F.
+// dX = dGU W1^T (D, NC), NC = 2F (GLU) or F; the activation backward takes
+// hidden units 8 at a time within groups of 32 (F % 32 == 0).
 bool mfma_backward_fits(const MoeOp& o) {
   const int NC = o.wpe == 3 ? 2 * o.F : o.F;
-  return o.mfma && mxm_mfma_tile_rows(o.F, o.D, o.family) > 0 &&
+  return o.mfma && o.F % 32 == 0 && mxm_mfma_tile_rows(o.F, o.D, o.family) > 0 &&
          mxm_mfma_tile_rows(NC, o.D, o.family) > 0 && mxm_mfma_tile_rows(o.D, NC, o.family) > 0;
 }
 

@@ -340,52 +340,81 @@ __global__ void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
 // Activation backward on the recomputed bf16 projections gu [N*K, NC] (GLU:
 // NC = 2F, gate and up columns interleaved in groups of 32 as the MFMA
 // family's W1 rows; MLP: NC = F, up only) and dH [N*K, F]: writes dG and dU
-// into dgu at the columns of g and u, rounded to bf16.
+// into dgu at the columns of g and u, rounded to bf16.  One thread takes 8
+// consecutive hidden units (16-byte loads and stores; F is a multiple of 32).
+__device__ __forceinline__ void act_bw_one(int etype, int act, float slope, float g, float u,
+                                           float dh, float& dg, float& du) {
+  if (etype == MXM_EXPERT_MLP) {
+    float d;
+    switch (act) {
+      case MXM_ACT_SILU: {
+        const float sg = 1.0f / (1.0f + expf(-u));
+        d = sg * (1.0f + u * (1.0f - sg));
+        break;
+      }
+      case MXM_ACT_GELU:
+        (void)gelu_t(u, d);
+        break;
+      case MXM_ACT_RELU:
+        d = u > 0.0f ? 1.0f : 0.0f;
+        break;
+      default: {
+        const float y = u > 0.0f ? u : u * slope;
+        d = 2.0f * y * (u > 0.0f ? 1.0f : slope);
+        break;
+      }
+    }
+    dg = 0.0f;
+    du = dh * d;
+  } else {
+    float a, d;
+    if (etype == MXM_EXPERT_SWIGLU) {
+      a = 1.0f / (1.0f + expf(-g));
+      d = a * (1.0f - a);
+    } else {
+      a = gelu_t(g, d);
+    }
+    dg = dh * u * d;
+    du = dh * a;
+  }
+}
+
 __global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dh,
-                                   int F, int etype, int act, float slope, size_t total,
+                                   int F, int etype, int act, float slope, size_t total8,
                                    uint16_t* __restrict__ dgu) {
   const bool glu = etype != MXM_EXPERT_MLP;
   const int NC = glu ? 2 * F : F;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total8;
        i += (size_t)gridDim.x * blockDim.x) {
-    const size_t r = i / F;
-    const int f = (int)(i % F);
-    const float d_h = mxm_bf2f(dh[i]);
+    const size_t e0 = i * 8;  // first element of [N*K, F]
+    const size_t r = e0 / F;
+    const int f = (int)(e0 % F);
+    const uint4 hv = *reinterpret_cast<const uint4*>(dh + e0);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    const size_t cu = r * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
+    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t gw[4] = {0u, 0u, 0u, 0u};
     if (glu) {
-      const size_t cg = r * NC + (f >> 5) * 64 + (f & 31), cu = cg + 32;
-      const float g = mxm_bf2f(gu[cg]), u = mxm_bf2f(gu[cu]);
-      float a, d;
-      if (etype == MXM_EXPERT_SWIGLU) {
-        a = 1.0f / (1.0f + expf(-g));
-        d = a * (1.0f - a);
-      } else {
-        a = gelu_t(g, d);
-      }
-      dgu[cg] = mxm_f2bf(d_h * u * d);
-      dgu[cu] = mxm_f2bf(d_h * a);
-    } else {
-      const float u = mxm_bf2f(gu[i]);
-      float d;
-      switch (act) {
-        case MXM_ACT_SILU: {
-          const float sg = 1.0f / (1.0f + expf(-u));
-          d = sg * (1.0f + u * (1.0f - sg));
-          break;
-        }
-        case MXM_ACT_GELU:
-          (void)gelu_t(u, d);
-          break;
-        case MXM_ACT_RELU:
-          d = u > 0.0f ? 1.0f : 0.0f;
-          break;
-        default: {
-          const float y = u > 0.0f ? u : u * slope;
-          d = 2.0f * y * (u > 0.0f ? 1.0f : slope);
-          break;
-        }
-      }
-      dgu[i] = mxm_f2bf(d_h * d);
+      const uint4 gv = *reinterpret_cast<const uint4*>(gu + cu - 32);
+      gw[0] = gv.x;
+      gw[1] = gv.y;
+      gw[2] = gv.z;
+      gw[3] = gv.w;
     }
+    uint32_t og[4], ou[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float dg0, du0, dg1, du1;
+      act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16),
+                 mxm_u2f(hw[q] << 16), dg0, du0);
+      act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
+                 mxm_u2f(hw[q] & 0xffff0000u), dg1, du1);
+      og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
+      ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
+    }
+    *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+    if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
   }
 }
 
@@ -457,10 +486,12 @@ void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int row
 
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
                             int act, float slope, uint16_t* dgu, hipStream_t s) {
-  const size_t total = (size_t)rows * F;
-  if (total > 0)
-    hipLaunchKernelGGL(act_bw_bf16_kernel, dim3(grid_of(total)), dim3(256), 0, s, gu, dh, F, etype,
-                       act, slope, total, dgu);
+  // F is a multiple of 32 (the MFMA family's GLU interleave), so rows of 8
+  // hidden units never straddle an interleave group or a row
+  const size_t total8 = (size_t)rows * F / 8;
+  if (total8 > 0)
+    hipLaunchKernelGGL(act_bw_bf16_kernel, dim3(grid_of(total8)), dim3(256), 0, s, gu, dh, F, etype,
+                       act, slope, total8, dgu);
 }
 
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
