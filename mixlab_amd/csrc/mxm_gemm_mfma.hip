@@ -333,37 +333,62 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 
   // ---- epilogue: activation, bf16, per-wave LDS staging, 16-byte stores ----
   // 32x32 accumulator layout: register r of lane l holds
-  // C[(r/4)*8 + (l/32)*4 + r%4][l%32].
+  // C[(r/4)*8 + (l/32)*4 + r%4][l%32].  Registers r and r+1 (r even) hold two
+  // consecutive rows of one column; they are converted together and staged
+  // as one 32-bit word (low half the even row) of a row-pair line, so a wave
+  // writes half as many LDS words as it has outputs.  Lines hold C words (the
+  // wave's output columns).  Staging swizzle, with kp the row pair:
+  //   C = 64: line kp, 16-byte chunk ch -> ch ^ (kp & 1) ^ ((kp >> 1 & 1) << 3)
+  //   C = 32: line kp ^ (kp >> 1 & 1), chunk ch -> ch ^ (kp >> 1 & 1)
+  // A write instruction covers 32 columns of row pairs kp and kp + 2 (the two
+  // half-waves), which land in disjoint banks; a read instruction's 16-lane
+  // phases take two 16-byte chunks of four (C = 32) or two (C = 64) row
+  // pairs, also in disjoint banks.
   constexpr int WROWS = TM * 32;
   constexpr int C = (MODE == MXM_GEMM_GLU) ? TN * 16 : TN * 32;  // output columns per wave
-  constexpr int CPR = C / 8;
-  constexpr int SW = CPR < 8 ? CPR : 8;  // chunk swizzle width
-  // Per-wave staging in the (now idle) stage ring.
+  static_assert(C == 32 || C == 64, "staging swizzle covers 32 or 64 columns per wave");
   static_assert(NW * WROWS * C * 2 <= (int)sizeof(u32x4_t) * NS * BUF, "staging fits in LDS");
-  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + (size_t)wave * WROWS * C;
+  uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + (size_t)wave * (WROWS / 2) * C;
+  auto word_at = [](int kp, int c) -> int {
+    const int b1 = (kp >> 1) & 1;
+    if constexpr (C == 64) {
+      const int ch = (c >> 2) ^ (kp & 1) ^ (b1 << 3);
+      return kp * C + ch * 4 + (c & 3);
+    } else {
+      const int ch = (c >> 2) ^ b1;
+      return (kp ^ b1) * C + ch * 4 + (c & 3);
+    }
+  };
   const int col = lane & 31;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    for (int r = 0; r < 16; r += 2) {
+      const int kp = i * 16 + (r >> 2) * 4 + (lane >> 5) * 2 + ((r & 3) >> 1);
       if (MODE == MXM_GEMM_GLU) {
 #pragma unroll
         for (int pj = 0; pj < TN / 2; ++pj) {
-          const float gg = mxm_rbf_fast(acc[i][2 * pj][r]);
-          const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r]);
-          const float h = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
-          const int c = pj * 32 + col;
-          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf_fast(h);
+          float h[2];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float gg = mxm_rbf_fast(acc[i][2 * pj][r + q]);
+            const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r + q]);
+            h[q] = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
+          }
+          stage[word_at(kp, pj * 32 + col)] = mxm_pack_bf2_fast(h[0], h[1]);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          float v = acc[i][j][r];
-          if (MODE == MXM_GEMM_MLP)
-            v = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f, mxm_rbf_fast(v));
-          const int c = j * 32 + col;
-          stage[row * C + (((c >> 3) ^ (row & (SW - 1))) << 3) + (c & 7)] = mxm_f2bf_fast(v);
+          float v[2];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            v[q] = acc[i][j][r + q];
+            if (MODE == MXM_GEMM_MLP)
+              v[q] = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f,
+                                           mxm_rbf_fast(v[q]));
+          }
+          stage[word_at(kp, j * 32 + col)] = mxm_pack_bf2_fast(v[0], v[1]);
         }
       }
     }
@@ -371,19 +396,30 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // each lane takes 8 columns of one row pair: two 16-byte chunks, split by
+  // byte permutes into the even row's and the odd row's 16-byte segments
   const int ldo = (MODE == MXM_GEMM_GLU) ? a.Ncols / 2 : a.Ncols;
   const int c0 = n0 / (MODE == MXM_GEMM_GLU ? 2 : 1) + wn * C;
   uint16_t* __restrict__ out = static_cast<uint16_t*>(a.out);
+  constexpr int SEGS = C / 8;  // 8-column segments per row pair
 #pragma unroll
-  for (int it = 0; it < WROWS * CPR / 64; ++it) {
+  for (int it = 0; it < (WROWS / 2) * SEGS / 64; ++it) {
     const int q = lane + 64 * it;
-    const int row = q / CPR, cc = q % CPR;
-    const int grow = wm * WROWS + row;
-    if (grow < rows) {
-      const u32x4_t v =
-          *reinterpret_cast<const u32x4_t*>(stage + row * C + ((cc ^ (row & (SW - 1))) << 3));
-      *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow) * ldo + c0 + cc * 8) = v;
+    const int kp = q / SEGS, sg = q % SEGS;
+    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(stage + word_at(kp, sg * 8));
+    const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(stage + word_at(kp, sg * 8 + 4));
+    const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    u32x4_t lo, hi;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      lo[m] = __builtin_amdgcn_perm(wv[2 * m + 1], wv[2 * m], 0x05040100u);  // low halves
+      hi[m] = __builtin_amdgcn_perm(wv[2 * m + 1], wv[2 * m], 0x07060302u);  // high halves
     }
+    const int grow = wm * WROWS + 2 * kp;
+    if (grow < rows)
+      *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow) * ldo + c0 + sg * 8) = lo;
+    if (grow + 1 < rows)
+      *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow + 1) * ldo + c0 + sg * 8) = hi;
   }
 }
 

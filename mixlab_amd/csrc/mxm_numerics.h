@@ -143,6 +143,12 @@ __device__ __forceinline__ float mxm_rbf_fast(float f) { return (float)(__bf16)f
 __device__ __forceinline__ uint16_t mxm_f2bf_fast(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
+// Two values to packed bf16 (lo = bf16(a), hi = bf16(b)), one conversion.
+__device__ __forceinline__ uint32_t mxm_pack_bf2_fast(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ float mxm_exp_fast(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
