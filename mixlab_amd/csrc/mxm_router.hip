@@ -55,6 +55,13 @@ __device__ __forceinline__ void unpack16<uint16_t>(const uint4 raw, float* f) {
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return mxm_xor_lane_f(v, m); }
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return mxm_xor_lane_i(v, m); }
 
+// Per-wave LDS scratch of route_token's top-k for E <= 64.
+struct RankScratch {
+  uint64_t key[64];
+  float pick_p[64];
+  int pick_e[64];
+};
+
 // Softmax, stable top-k and renormalised gates of one token on one wave
 // (gpu/ir.cpp:1107-1111).  Lane l holds experts l + 64 j (j < NJ); v[j] is
 // that expert's logit (bf16-rounded in the bf16 flow), ignored past E.  On
@@ -65,7 +72,7 @@ __device__ __forceinline__ int shfl_xor_i(int v, int m) { return mxm_xor_lane_i(
 template <bool BF16, int NJ>
 __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int E, int K,
                                              float (&p)[NJ], int (&pick_e)[NJ],
-                                             float (&pick_g)[NJ]) {
+                                             float (&pick_g)[NJ], RankScratch* rsc) {
   float m = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -97,9 +104,10 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) ent_local = ent_local + shfl_xor_f(ent_local, s);
 
-  // top-k: K rounds of argmax under (p desc, e asc).  The argmax is
-  // wave-uniform, so every lane accumulates the same running sum of the
-  // picked probabilities (k order), and lane k%64 keeps pick k in slot k/64.
+  // top-k under (p desc, e asc) -- the order of a stable argsort(-p).  Every
+  // lane accumulates the same running sum of the picked probabilities (k
+  // order), and lane k%64 keeps pick k in slot k/64.  E > 64: K rounds of a
+  // wave-wide argmax.
   uint32_t taken = 0u;
   float s_top = 0.0f;
   float my_p[NJ];
@@ -108,34 +116,71 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
     my_p[j] = 0.0f;
     pick_e[j] = 0;
   }
-  for (int k = 0; k < K; ++k) {
-    float bp = -2.0f;
-    int be = 0x7fffffff;
+  if constexpr (NJ == 1) {
+    // E <= 64: each lane's rank under the same order, from the wave's 64
+    // keys in LDS (broadcast reads): key = (bits of p) << 6 | (63 - lane), an
+    // integer order equal to (p desc, e asc) on p >= 0; lanes past E (p = -1)
+    // take key 0 and rank after every expert.  The lane of rank k < K leaves
+    // its probability and expert in pick slot k; every lane then reads the K
+    // picks in k order.  (One wave owns rsc; its LDS operations complete in
+    // program order.)
+    const float pl = p[0];
+    const uint64_t key =
+        pl >= 0.0f ? ((uint64_t)__builtin_bit_cast(uint32_t, pl) << 6) | (uint64_t)(63 - lane) : 0ull;
+    rsc->key[lane] = key;
+    __builtin_amdgcn_wave_barrier();
+    int rank = 0;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !((taken >> j) & 1u) && p[j] > bp) {
-        bp = p[j];
-        be = e;
-      }
+    for (int j2 = 0; j2 < 32; ++j2) {
+      const ulonglong2 q = reinterpret_cast<const ulonglong2*>(rsc->key)[j2];
+      rank += (q.x > key) ? 1 : 0;
+      rank += (q.y > key) ? 1 : 0;
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-      const float op = shfl_xor_f(bp, s);
-      const int oe = shfl_xor_i(be, s);
-      if (op > bp || (op == bp && oe < be)) {
-        bp = op;
-        be = oe;
-      }
+    if (rank < K) {
+      rsc->pick_p[rank] = pl;
+      rsc->pick_e[rank] = lane;
     }
-    if ((be & 63) == lane) taken |= 1u << (be >> 6);
-    s_top = (k == 0) ? bp : s_top + bp;
+    __builtin_amdgcn_wave_barrier();
+    for (int k = 0; k < K; ++k) {
+      const float bp = rsc->pick_p[k];
+      s_top = (k == 0) ? bp : s_top + bp;
+    }
+    if (lane < K) {
+      my_p[0] = rsc->pick_p[lane];
+      pick_e[0] = rsc->pick_e[lane];
+    }
+    __builtin_amdgcn_wave_barrier();  // rsc is free for the wave's next token
+    (void)taken;
+  } else {
+    for (int k = 0; k < K; ++k) {
+      float bp = -2.0f;
+      int be = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (k == lane + 64 * j) {
-        my_p[j] = bp;
-        pick_e[j] = be;
+      for (int j = 0; j < NJ; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !((taken >> j) & 1u) && p[j] > bp) {
+          bp = p[j];
+          be = e;
+        }
       }
+#pragma unroll
+      for (int s = 32; s >= 1; s >>= 1) {
+        const float op = shfl_xor_f(bp, s);
+        const int oe = shfl_xor_i(be, s);
+        if (op > bp || (op == bp && oe < be)) {
+          bp = op;
+          be = oe;
+        }
+      }
+      if ((be & 63) == lane) taken |= 1u << (be >> 6);
+      s_top = (k == 0) ? bp : s_top + bp;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (k == lane + 64 * j) {
+          my_p[j] = bp;
+          pick_e[j] = be;
+        }
+    }
   }
   if (BF16) s_top = mxm_rbf(s_top);
   const float den = fmaxf(s_top, 1e-12f);
@@ -163,6 +208,7 @@ __global__ __launch_bounds__(NT) void router_kernel(
   constexpr int NWAVE = THREADS / 64;
   __shared__ float wave_psum[NWAVE][EP];
   __shared__ float wave_ent[NWAVE];
+  __shared__ __attribute__((aligned(16))) RankScratch rank_scr[NWAVE];
 
   float* xs = smem;            // [BK][TM]
   float* ws = smem + BK * TM;  // [BK][EP]
@@ -317,7 +363,7 @@ __global__ __launch_bounds__(NT) void router_kernel(
     }
     float p[NJ], pick_g[NJ];
     int pick_e[NJ];
-    ent_acc = ent_acc + route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g);
+    ent_acc = ent_acc + route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g, &rank_scr[wave]);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int e = lane + 64 * j;
@@ -407,6 +453,7 @@ template <typename TX, bool BF16, int NJ, bool VEC>
 __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   extern __shared__ __attribute__((aligned(16))) float rs_dyn[];  // x row, then the slots
   __shared__ float lg[NJ * 64];
+  __shared__ __attribute__((aligned(16))) RankScratch rank_scr;
   __shared__ int cnt[MXM_MAX_EXPERTS];
   __shared__ int offs[MXM_MAX_EXPERTS];
   __shared__ int runc[MXM_MAX_EXPERTS];
@@ -513,7 +560,7 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
     for (int j = 0; j < NJ; ++j) v[j] = lg[lane + 64 * j];
     float p[NJ], pick_g[NJ];
     int pick_e[NJ];
-    const float ent = route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g);
+    const float ent = route_token<BF16, NJ>(v, lane, E, K, p, pick_e, pick_g, &rank_scr);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int e = lane + 64 * j;
