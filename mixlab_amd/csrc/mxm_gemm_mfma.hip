@@ -416,10 +416,18 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       hi[m] = __builtin_amdgcn_perm(wv[2 * m + 1], wv[2 * m], 0x07060302u);  // high halves
     }
     const int grow = wm * WROWS + 2 * kp;
-    if (grow < rows)
-      *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow) * ldo + c0 + sg * 8) = lo;
-    if (grow + 1 < rows)
-      *reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow + 1) * ldo + c0 + sg * 8) = hi;
+    // Y (down projection) is read once, by the combine, and is several times
+    // the last-level cache: stored nontemporal.  H stays cached for the down
+    // GEMM's re-reads.
+    u32x4_t* d0 = reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow) * ldo + c0 + sg * 8);
+    u32x4_t* d1 = reinterpret_cast<u32x4_t*>(out + (size_t)(row0 + grow + 1) * ldo + c0 + sg * 8);
+    if constexpr (MODE == MXM_GEMM_DOWN) {
+      if (grow < rows) __builtin_nontemporal_store(lo, d0);
+      if (grow + 1 < rows) __builtin_nontemporal_store(hi, d1);
+    } else {
+      if (grow < rows) *d0 = lo;
+      if (grow + 1 < rows) *d1 = hi;
+    }
   }
 }
 
