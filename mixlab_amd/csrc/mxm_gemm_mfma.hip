@@ -260,7 +260,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
           if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 \
         }                                                                                     \
       }                                                                                       \
-      if (DO_DMA && ks < DSTEPS)                                                              \
+      if ((DO_DMA) && ks < DSTEPS)                                                            \
         MXM_DMA_PART(DSTAGE, DK0, ks * LDPS / DSTEPS, (ks + 1) * LDPS / DSTEPS);              \
     }                                                                                         \
   } while (0)
