@@ -98,10 +98,25 @@ def cpu_baseline(w, cfg, target_s: float) -> dict:
         t = run(n)
     times = [t] + [run(n) for _ in range(2)]
     med = float(np.median(times))
+    blas = next((f"{p.get('internal_api', 'blas')} {p.get('version', '')}".strip()
+                 for p in threadpool_info() if p.get("user_api") == "blas"), "BLAS")
     return {"value": n / med, "unit": "tokens/s", "cores": int(cores), "kind": "port",
             "sample": (f"first {n} of {cfg.N} tokens, dense fp32 (all {cfg.E} experts on every "
-                       f"token, gpu/ir.cpp:1118-1148) with numpy/OpenBLAS sgemm; median of 3 "
-                       f"runs of {med:.2f} s after warm-up")}
+                       f"token, gpu/ir.cpp:1118-1148) with numpy sgemm ({blas}, {int(cores)} "
+                       f"threads) on {_cpu_model()}; median of 3 runs of {med:.2f} s after "
+                       f"warm-up")}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), or 'unknown CPU'."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def run_config(cfg, steps: int, warmup: int, flags: int = 0, stage_repeats: int = 1):
