@@ -21,6 +21,8 @@
 // two are 2.7 GB, ten times the last-level cache; 0.52 -> 0.47 ms).
 #include "mxm_kernels.h"
 
+#include <type_traits>
+
 namespace {
 // 16-byte vectors for the nontemporal builtins (which take clang vector
 // types, not HIP's float4 / uint4 structs).
@@ -170,33 +172,28 @@ __device__ __forceinline__ void load_y(const TY* p, float* f, int vec);
 
 template <typename TY, int VEC>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
-  __shared__ int se[MXM_MAX_EXPERTS];
-  __shared__ int sp[MXM_MAX_EXPERTS];
+  __shared__ int sk[MXM_MAX_EXPERTS];  // the token's experts in top-k order
+  __shared__ int sp[MXM_MAX_EXPERTS];  // slot positions, ascending expert id
   __shared__ float sg[MXM_MAX_EXPERTS];
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
-  const int K = a.K;
-  for (int k = tid; k < K; k += 256) {
-    se[k] = a.top_idx[(size_t)n * K + k];
-    sg[k] = a.gates[(size_t)n * K + k];
-    sp[k] = a.slot_pos[(size_t)n * K + k];
+  const int K = a.K;  // K <= E <= 256 = blockDim.x
+  int e = 0, p = 0;
+  float g = 0.0f;
+  if (tid < K) {
+    e = a.top_idx[(size_t)n * K + tid];
+    g = a.gates[(size_t)n * K + tid];
+    p = a.slot_pos[(size_t)n * K + tid];
+    sk[tid] = e;
   }
   __syncthreads();
-  if (tid == 0) {
-    for (int i = 1; i < K; ++i) {
-      const int e = se[i], p = sp[i];
-      const float g = sg[i];
-      int j = i - 1;
-      while (j >= 0 && se[j] > e) {
-        se[j + 1] = se[j];
-        sp[j + 1] = sp[j];
-        sg[j + 1] = sg[j];
-        --j;
-      }
-      se[j + 1] = e;
-      sp[j + 1] = p;
-      sg[j + 1] = g;
-    }
+  // a token's K experts are distinct, so the number of smaller ones is the
+  // slot's place in ascending expert order
+  if (tid < K) {
+    int r = 0;
+    for (int j = 0; j < K; ++j) r += sk[j] < e;
+    sp[r] = p;
+    sg[r] = g;
   }
   __syncthreads();
   const TY* y = static_cast<const TY*>(a.y);
@@ -204,25 +201,43 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     float acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = 0.0f;
-    for (int k = 0; k < K; ++k) {
-      const TY* src = y + (size_t)sp[k] * a.D + d;
-      float f[VEC];
-      if constexpr (sizeof(TY) == 2 && VEC == 8) {
-        const vu4 rv = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(src));
-        const uint4 raw = make_uint4(rv.x, rv.y, rv.z, rv.w);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    if constexpr ((sizeof(TY) == 2 && VEC == 8) || (sizeof(TY) == 4 && VEC == 4)) {
+      // the rows of up to KC slots are requested together, then accumulated
+      // in ascending expert order
+      constexpr int KC = 8;
+      typedef typename std::conditional<sizeof(TY) == 2, vu4, vf4>::type raw_t;
+      for (int k0 = 0; k0 < K; k0 += KC) {
+        const int kn = min(KC, K - k0);
+        raw_t r[KC];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          f[2 * q] = mxm_u2f(w[q] << 16);
-          f[2 * q + 1] = mxm_u2f(w[q] & 0xffff0000u);
+        for (int u = 0; u < KC; ++u)
+          if (u < kn)
+            r[u] = __builtin_nontemporal_load(
+                reinterpret_cast<const raw_t*>(y + (size_t)sp[k0 + u] * a.D + d));
+#pragma unroll
+        for (int u = 0; u < KC; ++u) {
+          if (u < kn) {
+            float f[VEC];
+            if constexpr (sizeof(TY) == 2) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                f[2 * q] = mxm_u2f(r[u][q] << 16);
+                f[2 * q + 1] = mxm_u2f(r[u][q] & 0xffff0000u);
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) f[q] = r[u][q];
+            }
+            const float g = sg[k0 + u];
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], g));
+          }
         }
-      } else if constexpr (sizeof(TY) == 4 && VEC == 4) {
-        const vf4 v = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(src));
-        f[0] = v.x;
-        f[1] = v.y;
-        f[2] = v.z;
-        f[3] = v.w;
-      } else {
+      }
+    } else {
+      for (int k = 0; k < K; ++k) {
+        const TY* src = y + (size_t)sp[k] * a.D + d;
+        float f[VEC];
 #pragma unroll
         for (int q = 0; q < VEC; ++q) {
           if constexpr (sizeof(TY) == 2)
@@ -230,10 +245,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
           else
             f[q] = reinterpret_cast<const float*>(src)[q];
         }
-      }
-      const float g = sg[k];
+        const float g = sg[k];
 #pragma unroll
-      for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], g));
+        for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], g));
+      }
     }
     if (a.resid) {
       // block level: x + delta (* moe_scale), fp32
