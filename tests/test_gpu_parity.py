@@ -382,6 +382,21 @@ def test_backward_fp32(gpu_lib, etype, act, slope, K):
                 assert not np.any(dexp[e][m]), (e, m)
 
 
+@pytest.mark.parametrize("E,K", [(16, 9), (16, 16), (64, 40)])
+@pytest.mark.parametrize("N", [70, 1100])
+def test_large_top_k(gpu_lib, E, K, N):
+    """K past one combine chunk of 8 slots (9, 16, 40): the slots are summed
+    in ascending expert id, so the fp32 delta is bit-exact; on both router
+    paths."""
+    D, F = 128, 64
+    x, wr, experts = random_case(300 + 7 * E + K + N, N, D, E, F)
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K)
+    want = run_oracle(x, wr, experts, K=K)
+    assert_routing_equal(routing, want)
+    assert same_bits(delta, want["delta"])
+    assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
+
+
 @pytest.mark.parametrize("E", [65, 128, 200, 256])
 @pytest.mark.parametrize("N", [130, 1500])
 @pytest.mark.parametrize("bf16", [False, True])
