@@ -235,8 +235,11 @@ struct BlockIO {
   float* aux_scaled;
 };
 
+// pre_out (MFMA family only): also keep the up projections' pre-activation
+// products [N*K, NC] bf16 there (the backward's activation gradient reads
+// them); H is then derived from them with the same activation code.
 void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent,
-                 const BlockIO* blk = nullptr) {
+                 const BlockIO* blk = nullptr, uint16_t* pre_out = nullptr) {
   for (int i = 1; i < o.n_inputs; ++i)
     if (!o.have[i]) fail("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
   if (!o.ws_ready) alloc_workspace(o);
@@ -382,6 +385,15 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     g1.scale1 = o.s1b.as<float>();
     require_operands(g1, glu, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
+  } else if (o.mfma && pre_out) {
+    g1.mode = MXM_GEMM_RAW;
+    g1.out = pre_out;
+    require_operands(g1, false, false);
+    for (int rep = 0; rep < reps; ++rep) {
+      mxm_launch_gemm_mfma(g1, st);
+      mxm_launch_act_fwd_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope, o.H.as<uint16_t>(),
+                              st);
+    }
   } else if (o.mfma) {
     require_operands(g1, false, false);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
@@ -907,8 +919,8 @@ void gemm_at_b(rocblas_handle h, const uint16_t* A, int M, const uint16_t* B, in
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
 // permuted order throughout (expert e owns rows offsets[e] ..).
 //   dH  = dY W_down^T          MFMA grouped GEMM, W_down kept as [F][D] bf16
-//   G|U = Xp W1                MFMA grouped GEMM with the forward's W1 (the
-//                              bf16 flow's projections, recomputed)
+//   G|U = Xp W1                kept by the forward (mode 3 GEMM, from which
+//                              the forward derives H)
 //   dG|dU                      elementwise (act_bw_bf16)
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
 //   dx  = dxr + sum_k dXe      (dx_bf16)
@@ -922,7 +934,6 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_dyb.alloc(NK * D * 2);
     o.bw_xpb.alloc(NK * D * 2);
     o.bw_dhb.alloc(NK * F * 2);
-    o.bw_gub.alloc(NK * NC * 2);
     o.bw_dgub.alloc(NK * NC * 2);
     o.bw_dxeb.alloc(NK * D * 2);
     if (glu) o.bw_dw1cat.alloc((size_t)E * D * NC * 4);
@@ -968,7 +979,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     HIPCK(hipGetLastError());
   };
   product(0, dyb, o.bw_w2o.p, dhb, D, F);
-  product(1, xpb, o.w1.p, gub, D, NC);
+  // gub holds G|U from the forward (run_forward's pre_out)
   mxm_launch_act_bw_bf16(gub, dhb, (int)NK, F, o.etype, o.act, o.slope, dgub, st);
   product(2, dgub, o.bw_w1u.p, dxeb, NC, D);
   mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
@@ -1077,8 +1088,14 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     if (!o.bw_x32.p) o.bw_x32.alloc(N * D * 4);
     x32 = o.bw_x32.as<float>();
   }
+  // the MFMA backward's G|U (pre-activation products) come from the forward
+  uint16_t* gu = nullptr;
+  if (mfma_bw) {
+    if (!o.bw_gub.p) o.bw_gub.alloc(NK * (size_t)(o.wpe == 3 ? 2 * F : F) * 2);
+    gu = o.bw_gub.as<uint16_t>();
+  }
   o.keep_probs = true;
-  run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr);
+  run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
   o.keep_probs = false;
   // x as the forward saw it (rounded to bf16 when given in fp32)
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.xcast.p;

@@ -447,6 +447,10 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
     launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
     return;
   }
+  if (a.mode == MXM_GEMM_RAW) {
+    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_RAW>(a, s, blocks, ngroups);
+    return;
+  }
   switch (mxm_epi_kind(a.expert_type, a.activation)) {
     case EPI_GEGLU:
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_GEGLU>(a, s, blocks, ngroups);

@@ -126,8 +126,10 @@ struct ScatterArgs {
 void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s);
 
 // Grouped expert FFN.  mode: 0 = gate+up with GLU epilogue, 1 = up with MLP
-// activation, 2 = down projection.
-enum { MXM_GEMM_GLU = 0, MXM_GEMM_MLP = 1, MXM_GEMM_DOWN = 2 };
+// activation, 2 = down projection, 3 = the up projections' pre-activation
+// products (A gathered through perm as in 0/1, stored bf16 without the
+// activation; MFMA family only).
+enum { MXM_GEMM_GLU = 0, MXM_GEMM_MLP = 1, MXM_GEMM_DOWN = 2, MXM_GEMM_RAW = 3 };
 
 struct GemmArgs {
   int mode;
@@ -162,12 +164,14 @@ int mxm_simt_bm();
 
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
 // projections, or the plain bf16 store of the down projection.
-enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN };
+enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN,
+       EPI_RAW };
 
 template <int EPI>
 struct Epi {
   static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
                               : EPI == EPI_DOWN ? MXM_GEMM_DOWN
+                              : EPI == EPI_RAW  ? MXM_GEMM_RAW
                                                 : MXM_GEMM_MLP;
   static constexpr int ETYPE = EPI == EPI_SWIGLU ? MXM_EXPERT_SWIGLU
                                : EPI == EPI_GEGLU ? MXM_EXPERT_GEGLU
@@ -301,6 +305,12 @@ void mxm_launch_backward_experts(const BackwardArgs& a, hipStream_t s);
 // the GLU pair's gradient de-interleaved into Op.Inputs order.
 void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
                                  uint16_t* out, hipStream_t s);
+// H [rows, F] (bf16) from the up projections' pre-activation products gu
+// [rows, NC] (mode 3 layout: GLU gate/up interleaved in groups of 32), with
+// the MFMA epilogue's own activation code, so H is the same bits as mode 0/1
+// would store.
+void mxm_launch_act_fwd_bf16(const uint16_t* gu, int rows, int F, int etype, int act, float slope,
+                             uint16_t* h, hipStream_t s);
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
                             int act, float slope, uint16_t* dgu, hipStream_t s);
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
