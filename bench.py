@@ -238,8 +238,9 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     op.close()
     glu = cfg.expert_type != 2
     nkdf = cfg.N * cfg.K * cfg.D * cfg.F
-    # forward (3 or 2 products) + recomputed projections + dH + dX + weight gradients
-    fl = 2 * nkdf * ((3 if glu else 2) + (2 if glu else 1) + 1 + (2 if glu else 1)
+    # algorithmic work: forward (3 or 2 products) + dH + dX + weight gradients,
+    # plus the router's forward and backward; recomputation is not counted
+    fl = 2 * nkdf * ((3 if glu else 2) + 1 + (2 if glu else 1)
                      + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
     tf = fl / (ms * 1e-3) / 1e12
     log(f"backward {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
