@@ -106,11 +106,11 @@ struct MoeOp {
   // backward (fp32 flow): recomputed intermediates, transposed weights
   bool keep_probs = false, bw_ready = false;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
-      bw_dlogits, bw_dxr, bw_w1t, bw_w1bt, bw_w2t, bw_wrt, bw_one, bw_wr_part;
+      bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
   // and of the forward's expert outputs, for the fp32 backward kernels
   bool bw_w32_ready = false;
-  DevBuf bw_w1_32, bw_w1b_32, bw_w2_32, bw_wr32, bw_x32, bw_y32, bw_mstart;
+  DevBuf bw_w1_32, bw_w1b_32, bw_w2_32, bw_wr32, bw_x32, bw_y32;
   // bf16 ops of the MFMA family: bf16 intermediates of the MFMA backward, the
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
@@ -1016,6 +1016,84 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   HIPCK(hipGetLastError());
 }
 
+// The experts' part of the fp32 backward (fp32 compute, or the bf16 flow on
+// fp32 copies where the MFMA tiles do not apply).  Rows are in the forward's
+// permuted order (expert e owns rows offsets[e] ..); per expert, with r rows,
+// all matrices row-major and the weights in the reference's x.W layout:
+//   G = Xp W_gate, U = Xp W_up          (recomputed forward projections)
+//   dH = dY W_down^T
+//   dG, dU, H                           elementwise (mxm_launch_backward_act)
+//   dX = dG W_gate^T + dU W_up^T        (summed per token by mxm_launch_backward_dx)
+//   dW_gate = Xp^T dG, dW_up = Xp^T dU, dW_down = H^T dY
+// each a rocBLAS fp32 GEMM (column-major, so each is issued as its
+// transpose).  The per-expert row counts are read back once.
+void run_backward_blas32(MoeOp& o, BackwardArgs& b) {
+  hipStream_t st = o.stream;
+  const bool glu = o.wpe == 3;
+  const int D = o.D, F = o.F, E = o.E;
+  const size_t DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
+  mxm_launch_backward_gather(b, st);
+  HIPCK(hipGetLastError());
+  std::vector<int32_t> cnt(E);
+  HIPCK(hipMemcpyAsync(cnt.data(), b.counts, (size_t)E * 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  if (!o.bw_blas) check_blas(rocblas_create_handle(&o.bw_blas), "rocblas_create_handle");
+  check_blas(rocblas_set_stream(o.bw_blas, st), "rocblas_set_stream");
+  const float one = 1.0f, zero = 0.0f;
+  auto mm = [&](rocblas_operation ta, rocblas_operation tb, int m, int n, int k, const float* A,
+                int lda, const float* B, int ldb, float* C, int ldc) {
+    check_blas(rocblas_sgemm(o.bw_blas, ta, tb, m, n, k, &one, A, lda, B, ldb, &zero, C, ldc),
+               "fp32 backward GEMM");
+  };
+  constexpr rocblas_operation NO = rocblas_operation_none, TR = rocblas_operation_transpose;
+  size_t off = 0;
+  for (int e = 0; e < E; ++e) {
+    const int r = cnt[e];
+    if (r > 0) {
+      const float* xp = b.xp + off * D;
+      const float* w1 = b.w1 + (size_t)e * DF;
+      if (glu) {
+        mm(NO, NO, F, r, D, w1, F, xp, D, b.g + off * F, F);
+        mm(NO, NO, F, r, D, b.w1b + (size_t)e * DF, F, xp, D, b.u + off * F, F);
+      } else {
+        mm(NO, NO, F, r, D, w1, F, xp, D, b.u + off * F, F);
+      }
+      mm(TR, NO, F, r, D, b.w2 + (size_t)e * DF, D, b.dy + off * D, D, b.dh + off * F, F);
+    }
+    off += (size_t)(r > 0 ? r : 0);
+  }
+  mxm_launch_backward_act(b, st);
+  HIPCK(hipGetLastError());
+  off = 0;
+  for (int e = 0; e < E; ++e) {
+    const int r = cnt[e];
+    float* dwe = b.dw + (size_t)e * stride;
+    if (r <= 0) {
+      HIPCK(hipMemsetAsync(dwe, 0, stride * 4, st));
+      continue;
+    }
+    const float* xp = b.xp + off * D;
+    const float* dy = b.dy + off * D;
+    const float* w1 = b.w1 + (size_t)e * DF;
+    const float* dg = b.dg + off * F;
+    const float* du = b.du + off * F;
+    if (glu) {
+      mm(TR, NO, D, r, F, w1, F, dg, F, b.dxg + off * D, D);
+      mm(TR, NO, D, r, F, b.w1b + (size_t)e * DF, F, du, F, b.dxu + off * D, D);
+      mm(NO, TR, F, D, r, dg, F, xp, D, dwe, F);                          // gate [D][F]
+      mm(NO, TR, F, D, r, du, F, xp, D, dwe + DF, F);                     // up [D][F]
+      mm(NO, TR, D, F, r, dy, D, b.h + off * F, F, dwe + 2 * DF, D);      // down [F][D]
+    } else {
+      mm(TR, NO, D, r, F, w1, F, du, F, b.dxu + off * D, D);
+      mm(NO, TR, F, D, r, du, F, xp, D, dwe, F);                          // up [D][F]
+      mm(NO, TR, D, F, r, dy, D, b.h + off * F, F, dwe + DF, D);          // down [F][D]
+    }
+    off += (size_t)r;
+  }
+  mxm_launch_backward_dx(b, st);
+  HIPCK(hipGetLastError());
+}
+
 void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
                   float d_ent, float* dx, float* dwr, float* dw) {
   if (o.q8) fail("OP_MOE_FEED_FORWARD backward is not available for int8 expert weights");
@@ -1048,9 +1126,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
       o.bw_dh.alloc(NK * F * 4);
       o.bw_dg.alloc(NK * F * 4);
       o.bw_du.alloc(NK * F * 4);
-      o.bw_w1t.alloc(E * D * F * 4);
-      o.bw_w1bt.alloc(E * D * F * 4);
-      o.bw_w2t.alloc(E * D * F * 4);
     }
     o.bw_ready = true;
   }
@@ -1147,17 +1222,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     run_backward_mfma(o, xb, b, dx, dw);
     return;
   }
-  // the experts' products on the SIMT kernels, with their row tiles
-  b.max_mtiles = o.max_mtiles2;
-  b.mstart = o.mstart2.as<int32_t>();
-  if (o.bm2 != mxm_simt_bm()) {
-    if (!o.bw_mstart.p) o.bw_mstart.alloc(((size_t)o.E + 1) * 4);
-    mxm_launch_tile_prefix(o.counts.as<int32_t>(), o.E, mxm_simt_bm(), o.bw_mstart.as<int32_t>(),
-                           o.stream);
-    HIPCK(hipGetLastError());
-    b.mstart = o.bw_mstart.as<int32_t>();
-    b.max_mtiles = (int)((NK + mxm_simt_bm() - 1) / mxm_simt_bm()) + o.E;
-  }
   b.w1 = w1;
   b.w1b = w1b;
   b.w2 = w2;
@@ -1170,11 +1234,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.du = o.bw_du.as<float>();
   b.dxg = o.bw_dxg.as<float>();
   b.dxu = o.bw_dxu.as<float>();
-  b.w1t = o.bw_w1t.as<float>();
-  b.w1bt = o.bw_w1bt.as<float>();
-  b.w2t = o.bw_w2t.as<float>();
-  mxm_launch_backward_experts(b, o.stream);
-  HIPCK(hipGetLastError());
+  run_backward_blas32(o, b);
 }
 
 int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const float* d_delta,

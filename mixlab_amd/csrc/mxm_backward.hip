@@ -16,10 +16,12 @@
 //                   (dG, dU) from the activation's derivative,
 //                   dx += dG W_gate^T + dU W_up^T,
 //                   dW_gate = X^T dG, dW_up = X^T dU.
-// Expert products run on the SIMT grouped GEMM (the forward's kernel, rows
-// grouped by expert through the forward's offsets); the weight gradients
-// reduce over each expert's rows in ascending order (wgrad_kernel), so every
-// result is deterministic.
+// The router part runs here (dgates, router_bw, dy, the router's input and
+// weight gradients; the weight gradient reduces over row chunks in a fixed
+// order).  The experts' fp32 products are one rocBLAS GEMM per expert and
+// product, issued by the library's host code; the elementwise parts (the
+// gathered rows, the activation derivative, dx) are the launchers at the end.
+// Every result is deterministic.
 #include "mxm_kernels.h"
 
 namespace {
@@ -165,58 +167,7 @@ __global__ void act_bw_kernel(BackwardArgs a, size_t total) {
   }
 }
 
-// Weight gradient: for each segment e (rows offsets[e] .. offsets[e+1]-1),
-// out[e][i][j] = sum_r A[r][i] * B[r][j], rows in ascending order.
-constexpr int WG_T = 64, WG_R = 16;
-__global__ __launch_bounds__(256) void wgrad_kernel(const float* __restrict__ A, int M,
-                                                    const float* __restrict__ B, int Nn,
-                                                    const int32_t* __restrict__ offsets,
-                                                    float* __restrict__ out, size_t out_stride) {
-  __shared__ float As[WG_R][WG_T + 4];
-  __shared__ float Bs[WG_R][WG_T + 4];
-  const int e = blockIdx.z;
-  const int i0 = blockIdx.y * WG_T, j0 = blockIdx.x * WG_T;
-  const int r0 = offsets[e], r1 = offsets[e + 1];
-  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  for (int rb = r0; rb < r1; rb += WG_R) {
-    __syncthreads();
-    for (int q = tid; q < WG_R * WG_T; q += 256) {
-      const int rr = q / WG_T, c = q % WG_T;
-      const int r = rb + rr;
-      As[rr][c] = (r < r1 && i0 + c < M) ? A[(size_t)r * M + i0 + c] : 0.0f;
-      Bs[rr][c] = (r < r1 && j0 + c < Nn) ? B[(size_t)r * Nn + j0 + c] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int rr = 0; rr < WG_R; ++rr) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[rr][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[rr][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
-    }
-  }
-  float* o = out + (size_t)e * out_stride;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ii = i0 + ty * 4 + i;
-    if (ii >= M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int jj = j0 + tx * 4 + j;
-      if (jj < Nn) o[(size_t)ii * Nn + jj] = acc[i][j];
-    }
-  }
-}
+constexpr int WG_T = 64, WG_R = 16;  // router weight-gradient tile: 64 x 64, 16 rows per step
 
 // Row-split weight gradient of one segment: part[c][i][j] = sum over rows
 // r in chunk c (rows c*rc .. c*rc+rc-1, ascending) of A[r][i] * B[r][j].
@@ -317,12 +268,6 @@ void grouped(const float* A, const float* B, float* out, int Kd, int NC, const i
   g.max_mtiles = max_mtiles;
   g.y_bf16 = false;
   mxm_launch_gemm_simt(g, false, s);
-}
-
-void wgrad(const float* A, int M, const float* B, int Nn, const int32_t* offsets, int E,
-           float* out, size_t out_stride, hipStream_t s) {
-  hipLaunchKernelGGL(wgrad_kernel, dim3((Nn + WG_T - 1) / WG_T, (M + WG_T - 1) / WG_T, E),
-                     dim3(256), 0, s, A, M, B, Nn, offsets, out, out_stride);
 }
 
 // ---- bf16 flow on the MFMA family --------------------------------------------
@@ -577,46 +522,17 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
 
 // The experts' products on the fp32 SIMT kernels: recomputed projections,
 // activation backward, dx (with the router term) and the weight gradients.
-void mxm_launch_backward_experts(const BackwardArgs& a, hipStream_t s) {
-  const int N = a.N, D = a.D, E = a.E, F = a.F, NK = a.N * a.K;
-  const bool glu = a.etype != MXM_EXPERT_MLP;
-  const size_t DF = (size_t)D * F;
-  if (NK <= 0) return;
-  // gathered rows and the transposed weights
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(NK), dim3(256), 0, s, a.x, a.perm, D, a.xp);
-  transpose_batch(a.w2, E, F, D, a.w2t, s);   // [E][D][F]
-  transpose_batch(a.w1, E, D, F, a.w1t, s);   // [E][F][D]
-  if (glu) transpose_batch(a.w1b, E, D, F, a.w1bt, s);
-  // projections of the forward (recomputed)
-  if (glu) {
-    grouped(a.xp, a.w1, a.g, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
-    grouped(a.xp, a.w1b, a.u, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
-  } else {
-    grouped(a.xp, a.w1, a.u, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
-  }
-  // down projection
-  grouped(a.dy, a.w2t, a.dh, D, F, a.offsets, a.mstart, E, a.max_mtiles, s);
-  const size_t total = (size_t)NK * F;
-  int blocks = (int)((total + 255) / 256);
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(act_bw_kernel, dim3(blocks), dim3(256), 0, s, a, total);
-  // input gradient
-  if (glu) grouped(a.dg, a.w1t, a.dxg, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
-  grouped(a.du, glu ? a.w1bt : a.w1t, a.dxu, F, D, a.offsets, a.mstart, E, a.max_mtiles, s);
-  hipLaunchKernelGGL(dx_kernel, dim3(N), dim3(256), 0, s, a);
-  // weight gradients (per expert blocks of a.dw in Op.Inputs order)
-  const size_t stride = (size_t)a.wpe * DF;
-  if (glu) {
-    wgrad(a.xp, D, a.dg, F, a.offsets, E, a.dw, stride, s);            // gate
-    wgrad(a.xp, D, a.du, F, a.offsets, E, a.dw + DF, stride, s);       // up
-    wgrad(a.h, F, a.dy, D, a.offsets, E, a.dw + 2 * DF, stride, s);    // down
-  } else {
-    wgrad(a.xp, D, a.du, F, a.offsets, E, a.dw, stride, s);            // up
-    wgrad(a.h, F, a.dy, D, a.offsets, E, a.dw + DF, stride, s);        // down
-  }
+void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s) {
+  const int NK = a.N * a.K;
+  if (NK > 0) hipLaunchKernelGGL(gather_rows_kernel, dim3(NK), dim3(256), 0, s, a.x, a.perm, a.D, a.xp);
 }
 
-void mxm_launch_backward(const BackwardArgs& a, hipStream_t s) {
-  mxm_launch_backward_router(a, s);
-  mxm_launch_backward_experts(a, s);
+void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s) {
+  const size_t total = (size_t)a.N * a.K * a.F;
+  if (total > 0)
+    hipLaunchKernelGGL(act_bw_kernel, dim3(grid_of(total)), dim3(256), 0, s, a, total);
+}
+
+void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s) {
+  if (a.N > 0) hipLaunchKernelGGL(dx_kernel, dim3(a.N), dim3(256), 0, s, a);
 }

@@ -260,7 +260,7 @@ int mxm_q8_max_kd();
 // a forward on the same x; every other intermediate is recomputed.  All
 // matrices are fp32 in the x.W layout of the forward's SIMT family.
 struct BackwardArgs {
-  int N, D, E, K, F, etype, act, wpe, max_mtiles;
+  int N, D, E, K, F, etype, act, wpe;
   float slope;
   // forward state
   const float* x;            // [N, D]
@@ -270,7 +270,6 @@ struct BackwardArgs {
   const int32_t* perm;       // [N*K]
   const int32_t* counts;     // [E]
   const int32_t* offsets;    // [E + 1]
-  const int32_t* mstart;     // [E + 1] row tiles of 64
   const float* probs;        // [N, E]
   const float* Y;            // [N*K, D]
   const float* wr;           // [D, E]
@@ -283,7 +282,7 @@ struct BackwardArgs {
   // scratch
   float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
   float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D]
-  float *w1t, *w1bt, *w2t, *wrt;                          // transposed weights
+  float* wrt;                                             // router_w transposed [E][D]
   int32_t* one;                                           // [4]: offsets/mstart of one segment
   float* wr_part;            // [wgrad_router_chunks(N)][D][E]: row-chunk partials of d router_w
   // outputs
@@ -291,14 +290,18 @@ struct BackwardArgs {
   float* dwr;                // [D, E]
   float* dw;                 // per expert, Op.Inputs order, x.W layout
 };
-void mxm_launch_backward(const BackwardArgs& a, hipStream_t s);
 // Row chunks of d router_w's reduction (BackwardArgs::wr_part holds one D x E
 // partial per chunk).
 int wgrad_router_chunks(int N);
-// Its two halves: gate/router gradients, dY, dx's router term and d router_w;
-// then the experts' products on the fp32 SIMT kernels.
+// The router part: gate/router gradients, dY, dx's router term and d router_w.
 void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s);
-void mxm_launch_backward_experts(const BackwardArgs& a, hipStream_t s);
+// The fp32 experts' elementwise parts around their products (which the host
+// issues as per-expert GEMMs): xp = x gathered by perm; dg, du and h from
+// g, u, dh (the activation's derivative, h recomputed); dx = dxr + the
+// experts' input gradients summed over each token's slots, k ascending.
+void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s);
+void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s);
+void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
 // bf16 flow on the MFMA family (products by the MFMA grouped GEMM and, for
 // the weight gradients, rocBLAS): gathered bf16 rows, activation backward on
 // the recomputed bf16 projections, dx from bf16 expert input gradients, and
