@@ -105,6 +105,9 @@ struct MoeOp {
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
   // backward (fp32 flow): recomputed intermediates, transposed weights
   bool keep_probs = false, bw_ready = false;
+  // set by the fp32 backward around its forward: stop after the routing
+  // (router, scan, scatter); the backward computes the experts' products itself
+  bool route_only = false;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
       bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
@@ -359,6 +362,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   }
 
   mark(3);
+  if (o.route_only) return;
   const bool glu = o.etype != MXM_EXPERT_MLP;
   GemmArgs g1{};
   g1.mode = glu ? MXM_GEMM_GLU : MXM_GEMM_MLP;
@@ -1016,18 +1020,22 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   HIPCK(hipGetLastError());
 }
 
-// The experts' part of the fp32 backward (fp32 compute, or the bf16 flow on
+// The fp32 backward after the routing (fp32 compute, or the bf16 flow on
 // fp32 copies where the MFMA tiles do not apply).  Rows are in the forward's
 // permuted order (expert e owns rows offsets[e] ..); per expert, with r rows,
 // all matrices row-major and the weights in the reference's x.W layout:
-//   G = Xp W_gate, U = Xp W_up          (recomputed forward projections)
+//   G = Xp W_gate, U = Xp W_up          (the forward projections)
+//   own_forward (fp32 compute): H elementwise, Y = H W_down (the forward's
+//                                expert outputs, which dgates reads)
+//   the router part (mxm_launch_backward_router: dgates .. dY, d router_w)
 //   dH = dY W_down^T
 //   dG, dU, H                           elementwise (mxm_launch_backward_act)
 //   dX = dG W_gate^T + dU W_up^T        (summed per token by mxm_launch_backward_dx)
 //   dW_gate = Xp^T dG, dW_up = Xp^T dU, dW_down = H^T dY
 // each a rocBLAS fp32 GEMM (column-major, so each is issued as its
-// transpose).  The per-expert row counts are read back once.
-void run_backward_blas32(MoeOp& o, BackwardArgs& b) {
+// transpose).  The per-expert row counts are read back once.  Without
+// own_forward (the bf16 flow) Y comes from the op's forward.
+void run_backward_blas32(MoeOp& o, BackwardArgs& b, bool own_forward) {
   hipStream_t st = o.stream;
   const bool glu = o.wpe == 3;
   const int D = o.D, F = o.F, E = o.E;
@@ -1058,8 +1066,28 @@ void run_backward_blas32(MoeOp& o, BackwardArgs& b) {
       } else {
         mm(NO, NO, F, r, D, w1, F, xp, D, b.u + off * F, F);
       }
-      mm(TR, NO, F, r, D, b.w2 + (size_t)e * DF, D, b.dy + off * D, D, b.dh + off * F, F);
     }
+    off += (size_t)(r > 0 ? r : 0);
+  }
+  if (own_forward) {
+    mxm_launch_backward_hidden(b, st);
+    HIPCK(hipGetLastError());
+    off = 0;
+    for (int e = 0; e < E; ++e) {
+      const int r = cnt[e];
+      if (r > 0)
+        mm(NO, NO, D, r, F, b.w2 + (size_t)e * DF, D, b.h + off * F, F,
+           o.Y.as<float>() + off * D, D);
+      off += (size_t)(r > 0 ? r : 0);
+    }
+  }
+  mxm_launch_backward_router(b, st);
+  HIPCK(hipGetLastError());
+  off = 0;
+  for (int e = 0; e < E; ++e) {
+    const int r = cnt[e];
+    if (r > 0)
+      mm(TR, NO, F, r, D, b.w2 + (size_t)e * DF, D, b.dy + off * D, D, b.dh + off * F, F);
     off += (size_t)(r > 0 ? r : 0);
   }
   mxm_launch_backward_act(b, st);
@@ -1169,9 +1197,18 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     if (!o.bw_gub.p) o.bw_gub.alloc(NK * (size_t)(o.wpe == 3 ? 2 * F : F) * 2);
     gu = o.bw_gub.as<uint16_t>();
   }
+  // fp32 compute: the forward's routing only; the experts' forward products
+  // are computed by run_backward_blas32 (and kept for the backward)
+  const bool own_forward = !o.bf16;
   o.keep_probs = true;
-  run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
-  o.keep_probs = false;
+  o.route_only = own_forward;
+  try {
+    run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
+  } catch (...) {
+    o.keep_probs = o.route_only = false;
+    throw;
+  }
+  o.keep_probs = o.route_only = false;
   // x as the forward saw it (rounded to bf16 when given in fp32)
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.xcast.p;
   if (o.bf16) {
@@ -1216,9 +1253,9 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.dx = dx;
   b.dwr = dwr;
   b.dw = dw;
-  mxm_launch_backward_router(b, o.stream);
-  HIPCK(hipGetLastError());
   if (mfma_bw) {
+    mxm_launch_backward_router(b, o.stream);
+    HIPCK(hipGetLastError());
     run_backward_mfma(o, xb, b, dx, dw);
     return;
   }
@@ -1234,7 +1271,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.du = o.bw_du.as<float>();
   b.dxg = o.bw_dxg.as<float>();
   b.dxu = o.bw_dxu.as<float>();
-  run_backward_blas32(o, b);
+  run_backward_blas32(o, b, own_forward);
 }
 
 int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const float* d_delta,

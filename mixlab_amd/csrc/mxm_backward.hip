@@ -120,50 +120,72 @@ __device__ __forceinline__ float gelu_t(float v, float& deriv) {
   return 0.5f * v * (1.0f + t);
 }
 
+// The hidden unit of one routed row and its derivatives (fp32 flow): h, and
+// dh/dg (GLU only) and dh/du.
+__device__ __forceinline__ void act_eval(int etype, int act, float slope, float g, float u,
+                                         float& h, float& cg, float& cu) {
+  if (etype == MXM_EXPERT_MLP) {
+    float d;
+    switch (act) {
+      case MXM_ACT_SILU: {
+        const float sg = 1.0f / (1.0f + expf(-u));
+        h = u * sg;
+        d = sg * (1.0f + u * (1.0f - sg));
+        break;
+      }
+      case MXM_ACT_GELU:
+        h = gelu_t(u, d);
+        break;
+      case MXM_ACT_RELU:
+        h = u > 0.0f ? u : 0.0f;
+        d = u > 0.0f ? 1.0f : 0.0f;
+        break;
+      default: {
+        const float y = u > 0.0f ? u : u * slope;
+        h = y * y;
+        d = 2.0f * y * (u > 0.0f ? 1.0f : slope);
+        break;
+      }
+    }
+    cg = 0.0f;
+    cu = d;
+  } else {
+    float a, d;
+    if (etype == MXM_EXPERT_SWIGLU) {
+      a = 1.0f / (1.0f + expf(-g));
+      d = a * (1.0f - a);
+    } else {
+      a = gelu_t(g, d);
+    }
+    h = a * u;
+    cg = u * d;
+    cu = a;
+  }
+}
+
 // activation backward per element of [N*K, F]; recomputes H
 __global__ void act_bw_kernel(BackwardArgs a, size_t total) {
+  const bool glu = a.etype != MXM_EXPERT_MLP;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const float dh = a.dh[i];
-    if (a.etype == MXM_EXPERT_MLP) {
-      const float u = a.u[i];
-      float h, d;
-      switch (a.act) {
-        case MXM_ACT_SILU: {
-          const float sg = 1.0f / (1.0f + expf(-u));
-          h = u * sg;
-          d = sg * (1.0f + u * (1.0f - sg));
-          break;
-        }
-        case MXM_ACT_GELU:
-          h = gelu_t(u, d);
-          break;
-        case MXM_ACT_RELU:
-          h = u > 0.0f ? u : 0.0f;
-          d = u > 0.0f ? 1.0f : 0.0f;
-          break;
-        default: {
-          const float y = u > 0.0f ? u : u * a.slope;
-          h = y * y;
-          d = 2.0f * y * (u > 0.0f ? 1.0f : a.slope);
-          break;
-        }
-      }
-      a.h[i] = h;
-      a.du[i] = dh * d;
-    } else {
-      const float g = a.g[i], u = a.u[i];
-      float act, d;
-      if (a.etype == MXM_EXPERT_SWIGLU) {
-        act = 1.0f / (1.0f + expf(-g));
-        d = act * (1.0f - act);
-      } else {
-        act = gelu_t(g, d);
-      }
-      a.h[i] = act * u;
-      a.dg[i] = dh * u * d;
-      a.du[i] = dh * act;
-    }
+    float h, cg, cu;
+    act_eval(a.etype, a.act, a.slope, glu ? a.g[i] : 0.0f, a.u[i], h, cg, cu);
+    a.h[i] = h;
+    if (glu) a.dg[i] = dh * cg;
+    a.du[i] = dh * cu;
+  }
+}
+
+// H per element of [N*K, F] from the projections (the forward's hidden
+// units, for the backward's own expert forward)
+__global__ void hidden_kernel(BackwardArgs a, size_t total) {
+  const bool glu = a.etype != MXM_EXPERT_MLP;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float h, cg, cu;
+    act_eval(a.etype, a.act, a.slope, glu ? a.g[i] : 0.0f, a.u[i], h, cg, cu);
+    a.h[i] = h;
   }
 }
 
@@ -531,6 +553,12 @@ void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s) {
   const size_t total = (size_t)a.N * a.K * a.F;
   if (total > 0)
     hipLaunchKernelGGL(act_bw_kernel, dim3(grid_of(total)), dim3(256), 0, s, a, total);
+}
+
+void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s) {
+  const size_t total = (size_t)a.N * a.K * a.F;
+  if (total > 0)
+    hipLaunchKernelGGL(hidden_kernel, dim3(grid_of(total)), dim3(256), 0, s, a, total);
 }
 
 void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s) {

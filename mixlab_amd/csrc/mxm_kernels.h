@@ -301,6 +301,8 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s);
 // experts' input gradients summed over each token's slots, k ascending.
 void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s);
+// h from g, u alone (the expert forward of an fp32 backward)
+void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
 // bf16 flow on the MFMA family (products by the MFMA grouped GEMM and, for
 // the weight gradients, rocBLAS): gathered bf16 rows, activation backward on
