@@ -103,7 +103,7 @@ struct MoeOp {
       tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits, tok_ent,
       ticket;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
-  // backward (fp32 flow): recomputed intermediates, transposed weights
+  // backward (fp32 flow): the experts' projections, gradients and scratch
   bool keep_probs = false, bw_ready = false;
   // set by the fp32 backward around its forward: stop after the routing
   // (router, scan, scatter); the backward computes the experts' products itself
@@ -894,7 +894,7 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
 // Op.Inputs order (per expert gate, up, down -- or up, down -- in x.W layout).
 
 // Shapes of the MFMA backward's three grouped products: dH = dY W_down^T
-// (F columns, reduction D), the recomputed projections (NC, D) and
+// (F columns, reduction D), the forward's kept projections (NC, D) and
 // dX = dGU W1^T (D, NC), NC = 2F (GLU) or F; the activation backward takes
 // hidden units 8 at a time within groups of 32 (F % 32 == 0).
 bool mfma_backward_fits(const MoeOp& o) {

@@ -304,7 +304,7 @@ __global__ void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
   for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
 }
 
-// Activation backward on the recomputed bf16 projections gu [N*K, NC] (GLU:
+// Activation backward on the forward's bf16 projections gu [N*K, NC] (GLU:
 // NC = 2F, gate and up columns interleaved in groups of 32 as the MFMA
 // family's W1 rows; MLP: NC = F, up only) and dH [N*K, F]: writes dG and dU
 // into dgu at the columns of g and u, rounded to bf16.  One thread takes 8
@@ -542,8 +542,8 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   (void)K;
 }
 
-// The experts' products on the fp32 SIMT kernels: recomputed projections,
-// activation backward, dx (with the router term) and the weight gradients.
+// The fp32 experts' elementwise parts; their products are per-expert rocBLAS
+// GEMMs issued by the library's host code.
 void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s) {
   const int NK = a.N * a.K;
   if (NK > 0) hipLaunchKernelGGL(gather_rows_kernel, dim3(NK), dim3(256), 0, s, a.x, a.perm, a.D, a.xp);

@@ -256,9 +256,11 @@ void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s);
 void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s);
 int mxm_q8_max_kd();
 
-// Backward of op 74 (fp32 flow).  Uses the routing, probabilities and Y of
-// a forward on the same x; every other intermediate is recomputed.  All
-// matrices are fp32 in the x.W layout of the forward's SIMT family.
+// Backward of op 74 (fp32 flow).  Uses the routing and probabilities of a
+// forward on the same x and the expert outputs Y (the forward's, or under
+// fp32 compute the backward's own per-expert products); the projections and
+// hidden units are computed again.  All matrices are fp32 in the x.W layout
+// of the forward's SIMT family.
 struct BackwardArgs {
   int N, D, E, K, F, etype, act, wpe;
   float slope;
@@ -306,7 +308,7 @@ void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
 // bf16 flow on the MFMA family (products by the MFMA grouped GEMM and, for
 // the weight gradients, rocBLAS): gathered bf16 rows, activation backward on
-// the recomputed bf16 projections, dx from bf16 expert input gradients, and
+// the forward's bf16 projections, dx from bf16 expert input gradients, and
 // the GLU pair's gradient de-interleaved into Op.Inputs order.
 void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
                                  uint16_t* out, hipStream_t s);
