@@ -194,9 +194,10 @@ def copy_calibration(mib: int, reps: int = 5) -> int:
 def run_backward(cfg, steps: int, warmup: int) -> dict:
     """Backward of op 74 (mxm_moe_backward: a forward with the routing kept,
     then the gradients of x, the router and every routed expert) on the
-    configuration's compute dtype.  fp32: products on the SIMT kernels; bf16
-    (MFMA weight family): products on MFMA and, for the weight gradients,
-    rocBLAS bf16 GEMMs with fp32 output."""
+    configuration's compute dtype.  fp32: the routing of the forward, then
+    every expert product as a per-expert rocBLAS fp32 GEMM (fp32 matrix
+    cores); bf16 (MFMA weight family): products on MFMA and, for the weight
+    gradients, rocBLAS bf16 GEMMs with fp32 output."""
     from mixlab_amd import _lib
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import make_workload
@@ -249,7 +250,7 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
                 "weight gradients)", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": tf / PEAK_BF16_TFLOPS, "traffic": None}
     else:
-        roof = {"bound": "valu", "kernel": "whole backward (SIMT fp32 products)",
+        roof = {"bound": "mfma", "kernel": "whole backward (per-expert rocBLAS fp32 GEMMs)",
                 "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": tf / PEAK_FP32_TFLOPS, "traffic": None}
     return {"workload": f"{cfg.name} shape, {cfg.dtype} compute", "tokens": cfg.N,

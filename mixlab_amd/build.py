@@ -70,7 +70,8 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
     tmp = LIB.with_suffix(".so.tmp")
-    # rocBLAS: the per-expert weight-gradient GEMMs of the bf16 backward
+    # rocBLAS: the backward's per-expert GEMMs (bf16 weight gradients; the
+    # fp32 flow's products)
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
            "-lrocblas"]
     res = subprocess.run(cmd, capture_output=True, text=True)
