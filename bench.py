@@ -23,7 +23,7 @@ import numpy as np
 METRIC = "MoE layer tokens/sec at d=2048,64e top-8; grouped-GEMM % MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (AMD published)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (AMD published)
-PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 vector (AMD published)
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32, matrix and vector (AMD published)
 
 
 def log(msg: str) -> None:
