@@ -425,6 +425,8 @@ def test_many_experts(gpu_lib, E, N, bf16):
     (200, 100, 16, 4, True),     # bf16 rows not in 16-byte pieces; no full register round
     (96, 300, 40, 3, False),     # full rounds, remainder blocks and a d tail
     (77, 2051, 96, 5, True),     # odd D, two waves of router logits
+    (8, 16384, 64, 4, True),     # D at the one-launch router's limit (64 KB x row in LDS)
+    (8, 16388, 64, 4, False),    # D past it: the tiled router
 ])
 def test_decode_router_shapes(gpu_lib, N, D, E, K, bf16):
     """Decode-sized batches route in one launch (logits, softmax, top-k, then
