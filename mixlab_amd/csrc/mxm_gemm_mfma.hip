@@ -26,7 +26,12 @@
 //
 // Ragged experts: the scan kernel writes `mstart`, the prefix over experts of
 // ceil(count/BM) row tiles, so tile -> (expert, rows) is resolved on device
-// and tiles past the end exit at once.
+// (one round of loads and a ballot) and tiles past the end are skipped.
+//
+// The grid is persistent: as many workgroups as fit on the device at once,
+// each walking launch indices w, w + gridDim.x, ...; a CU goes from one
+// tile's epilogue straight to the next tile while the stores drain, instead
+// of waiting for the workgroup to retire and a new one to be dispatched.
 //
 // Tile order: the hardware hands workgroup L to XCD L % 8.  Row tiles are
 // grouped GM at a time with the column tiles of a group adjacent, and group g
@@ -35,6 +40,8 @@
 // XCDs.  The epilogue applies the activation (hardware exp2 / rcp and bf16
 // conversion), stages each wave's bf16 tile through LDS (chunk-swizzled) and
 // writes 16-byte row segments.
+#include <algorithm>
+
 #include "mxm_kernels.h"
 
 namespace {
@@ -80,6 +87,36 @@ __device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mti
   return lo;
 }
 
+// Row tile mtile -> its expert e, first row row0 and the expert's row end.
+// Returns false for tiles past the last expert's.  For E <= 64 this is one
+// round of independent loads: lane l reads mstart[l + 1], offsets[l] and
+// offsets[l + 1]; since mstart is nondecreasing from mstart[0] = 0, e is the
+// number of i in 1..E-1 with mstart[i] <= mtile (a ballot), and the rest are
+// read from the lanes holding them.  A binary search would be log2(E)
+// dependent loads, each a full L2 round trip, before the tile's first
+// operand load could be issued.
+__device__ __forceinline__ bool locate_tile(const int32_t* mstart, const int32_t* offsets, int E,
+                                            int mtile, int BM, int& e, int& row0, int& rend) {
+  if (E <= 64) {
+    const int lane = threadIdx.x & 63;
+    const bool in = lane < E;
+    const int ms1 = in ? mstart[lane + 1] : 0x7fffffff;
+    const int of0 = in ? offsets[lane] : 0;
+    const int of1 = in ? offsets[lane + 1] : 0;
+    if (mtile >= __builtin_amdgcn_readlane(ms1, E - 1)) return false;
+    e = __popcll(__ballot(lane + 1 < E && ms1 <= mtile));
+    const int ms_e = e == 0 ? 0 : __builtin_amdgcn_readlane(ms1, e - 1);
+    row0 = __builtin_amdgcn_readlane(of0, e) + (mtile - ms_e) * BM;
+    rend = __builtin_amdgcn_readlane(of1, e);
+    return true;
+  }
+  if (mtile >= mstart[E]) return false;
+  e = find_expert(mstart, E, mtile);
+  row0 = offsets[e] + (mtile - mstart[e]) * BM;
+  rend = offsets[e + 1];
+  return true;
+}
+
 // Direct global->LDS load of 16 bytes per lane (global_load_lds_dwordx4):
 // lane l's data lands at LDS address `lds` + 16*l.  Issued as inline asm so
 // the compiler does not track it: its conservative tracking of LDS DMA would
@@ -123,7 +160,8 @@ struct Tile {
 
 template <class TL, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(GemmArgs a,
-                                                                            int ngroups) {
+                                                                            int ngroups,
+                                                                            int nblocks) {
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN;
   constexpr int A_CH = TL::A_CH, BUF = TL::BUF;
@@ -135,17 +173,23 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   // XCD-aware grouped schedule (see the file comment).
   const int ntile_n = a.Ncols / BN;
   const int per_group = GM * ntile_n;
-  const int L = blockIdx.x;
+  // The grid is persistent (as many workgroups as fit at once): workgroup w
+  // takes launch indices w, w + gridDim.x, ..., so the CU goes straight from
+  // one tile's epilogue to the next tile while the epilogue's stores drain.
+  // gridDim.x is a multiple of 8, so every index keeps the workgroup's XCD.
+  for (int L = blockIdx.x; L < nblocks; L += gridDim.x) {
+  // every wave has read the previous tile's epilogue staging out of LDS
+  // (plain s_barrier: no wait for that epilogue's stores)
+  if (L != (int)blockIdx.x) asm volatile("s_barrier" ::: "memory");
   const int local = L >> 3;
   const int g = (local / per_group) * 8 + (L & 7);
-  if (g >= ngroups) return;
+  if (g >= ngroups) break;  // g only grows with L
   const int rr = local % per_group;
   const int mtile = g * GM + rr % GM;
   const int ntile = rr / GM;
-  if (mtile >= a.mstart[a.E]) return;
-  const int e = find_expert(a.mstart, a.E, mtile);
-  const int row0 = a.offsets[e] + (mtile - a.mstart[e]) * BM;
-  const int rows = min(BM, a.offsets[e + 1] - row0);
+  int e, row0, rend;
+  if (!locate_tile(a.mstart, a.offsets, a.E, mtile, BM, e, row0, rend)) continue;
+  const int rows = min(BM, rend - row0);
   const int n0 = ntile * BN;
   const int Kd = a.Kd;
 
@@ -285,8 +329,13 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   constexpr int DSTEPS = (MXM_DMA_STEPS > 0 && MXM_DMA_STEPS < BK / 16) ? MXM_DMA_STEPS : BK / 16;
   constexpr int KS = BK / 16;
   const int nk = Kd / BK;
+  // first stage: the weight rows go out first, they do not wait for perm
+  if (nk > 0) {
+    MXM_DMA_PART(lds, 0, QA, LDPS);
+    MXM_DMA_PART(lds, 0, 0, QA);
+  }
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st)
+  for (int st = 1; st < NS - 1; ++st)
     if (st < nk) MXM_DMA(lds + st * BUF, st * BK);
   if constexpr (NS >= 3) {
     // Deep ring: the barrier of stage kt+1 is taken before the last k step
@@ -429,13 +478,35 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       if (grow + 1 < rows) *d1 = hi;
     }
   }
+  }  // tile loop
+}
+
+// Workgroups resident at once on the current device: CUs x workgroups per
+// CU, rounded down to a multiple of 8 so a workgroup's tiles all map to the
+// XCD it runs on.
+static int persistent_grid(int per_cu) {
+  static int ncu[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (ncu[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    ncu[dev] = n;
+  }
+  return std::max(8, ncu[dev] * per_cu / 8 * 8);
 }
 
 template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK, int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
   using TL = Tile<BM, BN, WM, WN, WPS, NSTG, BKK>;
-  hipLaunchKernelGGL((gemm_kernel<TL, BM, BN, WM, WN, EPI>), dim3(blocks), dim3(TL::NT), 0, s, a,
-                     ngroups);
+  // workgroups per CU: what the launch bounds allow, capped by LDS
+  constexpr int lds_bytes = NSTG * TL::BUF * 16;
+  constexpr int per_cu = std::min(TL::WPS * 256 / TL::NT, 160 * 1024 / lds_bytes);
+  const int grid = std::min(blocks, persistent_grid(std::max(1, per_cu)));
+  hipLaunchKernelGGL((gemm_kernel<TL, BM, BN, WM, WN, EPI>), dim3(grid), dim3(TL::NT), 0, s, a,
+                     ngroups, blocks);
 }
 
 template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK>
