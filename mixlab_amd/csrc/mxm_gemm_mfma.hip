@@ -286,6 +286,9 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 // Per 16-wide k step: the fragment reads of the next step are interleaved
 // one by one between the MFMAs of this step (sched_group_barrier pins the
 // order: 1 MFMA, 1 LDS read, ...), so LDS latency hides behind MFMAs.  After
+// the stage barrier the first step's TM + TN reads are all issued before its
+// first MFMA, so the stage start costs one LDS latency rather than a read,
+// wait, MFMA chain.  After
 // each step, a share of the direct-to-LDS loads of stage DSTAGE (k offset
 // DK0) is issued, so the vector memory path fills in the background instead
 // of stalling every wave right after the stage barrier.
@@ -299,6 +302,8 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfm[ks & 1][j],          \
                                                       acc[i][j], 0, 0, 0);                    \
       if (ks + 1 < BK / 16) {                                                                 \
+        if (ks == 0) /* the first step's fragments all go out before its MFMAs */             \
+          __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);                            \
         _Pragma("unroll") for (int q = 0; q < TM * TN; ++q) {                                 \
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  \
           if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 \
