@@ -278,10 +278,11 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #define MXM_FRAGS(STAGE, P, KS)                                                               \
   do {                                                                                        \
     const int kc_ = (KS) * 2 + (lane >> 5);                                                   \
-    _Pragma("unroll") for (int i = 0; i < TM; ++i) af[P][i] =                                 \
-        __builtin_bit_cast(bf16x8_t, (STAGE)[swz<CH>(arow + i * 32, kc_)]);                       \
+    /* B first: the first MFMA needs b0 and a0, so it waits for TN + 1 reads */               \
     _Pragma("unroll") for (int j = 0; j < TN; ++j) bfm[P][j] =                                \
-        __builtin_bit_cast(bf16x8_t, (STAGE)[A_CH + swz<CH>(brow + j * 32, kc_)]);                \
+        __builtin_bit_cast(bf16x8_t, (STAGE)[A_CH + swz<CH>(brow + j * 32, kc_)]);            \
+    _Pragma("unroll") for (int i = 0; i < TM; ++i) af[P][i] =                                 \
+        __builtin_bit_cast(bf16x8_t, (STAGE)[swz<CH>(arow + i * 32, kc_)]);                   \
   } while (0)
 // Per 16-wide k step: the fragment reads of the next step are interleaved
 // one by one between the MFMAs of this step (sched_group_barrier pins the
