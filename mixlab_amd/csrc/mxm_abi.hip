@@ -101,7 +101,7 @@ struct MoeOp {
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
       tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits, tok_ent,
-      ticket;
+      ticket, expert_count, expert_pmean, scan_ticket;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
   // backward (fp32 flow): the experts' projections, gradients and scratch
   bool keep_probs = false, bw_ready = false;
@@ -204,6 +204,10 @@ void alloc_workspace(MoeOp& o) {
   A(o.mstart2, (E + 1) * 4);
   A(o.aux, 4);
   A(o.ent, 4);
+  A(o.expert_count, E * 4);
+  A(o.expert_pmean, E * 4);
+  A(o.scan_ticket, 4);
+  HIPCK(hipMemsetAsync(o.scan_ticket.p, 0, 4, o.stream));
   const size_t esz = (o.mfma || o.q8) ? 2 : 4;
   A(o.H, NK * (size_t)o.F * esz);
   A(o.Y, NK * (size_t)o.D * esz);
@@ -347,6 +351,9 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     sa.entropy = ent_p;
     sa.aux_weight = blk ? blk->aux_weight : 1.0f;
     sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
+    sa.expert_count = o.expert_count.as<int32_t>();
+    sa.expert_pmean = o.expert_pmean.as<float>();
+    sa.ticket = o.scan_ticket.as<int32_t>();
     for (int rep = 0; rep < reps; ++rep) mxm_launch_scan(sa, o.bf16, st);
     HIPCK(hipGetLastError());
 
@@ -354,6 +361,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     sc.top_idx = ra.top_idx;
     sc.slot_rank = ra.slot_rank;
     sc.tile_base = sa.tile_base;
+    sc.offsets = sa.offsets;
     sc.N = o.N;
     sc.K = o.K;
     sc.ntiles = o.ntiles;

@@ -9,8 +9,8 @@
 //   offsets        = exclusive scan of counts (offsets[E] = N*K)
 //   perm[offsets[e] + r] = the r-th such token
 // The router leaves per-tile counts and per-slot in-tile ranks; the scan
-// kernel below turns the counts into offsets and per-(expert, tile) bases,
-// and the scatter kernel places every slot.  Nothing here uses atomics, so
+// kernel below turns the counts into offsets and per-(expert, tile) bases
+// (one workgroup per expert), and the scatter kernel places every slot.  Nothing here uses atomics, so
 // the result does not depend on scheduling.
 //
 // The combine sums, per token, gate * y over its K slots in ascending expert
@@ -35,124 +35,123 @@ __device__ __forceinline__ float wave_sum_fixed(float v) {
   return v;
 }
 
-__device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
-  return v;
-}
+constexpr int SCAN_NT = 256;
 
-constexpr int SCAN_NT = 1024;
-
+// Workgroup e < E: expert e's total, its mean probability and the exclusive
+// prefix of its per-tile counts (relative to the expert's first row);
+// workgroup E: the entropy.  The last expert workgroup to finish (agent-scope
+// release fence, atomic ticket; agent-scope acquire) computes counts,
+// offsets, both row-tile prefixes and aux from the per-expert totals and
+// resets the ticket.  No workgroup waits for another, so the grid always
+// drains.  The floating-point sums keep one fixed order: per expert (and for
+// the entropy) lane-strided sequential partial sums over the tiles, then an
+// xor butterfly over the wave; aux over experts in ascending order.
 template <bool BF16>
 __global__ __launch_bounds__(SCAN_NT) void scan_kernel(ScanArgs a) {
-  __shared__ int cnt[MXM_MAX_EXPERTS];
-  __shared__ int offs[MXM_MAX_EXPERTS + 1];
-  __shared__ float pmean[MXM_MAX_EXPERTS];
+  __shared__ int wtot[SCAN_NT / 64];
+  __shared__ int s_last;
+  __shared__ int scount[MXM_MAX_EXPERTS];
+  __shared__ float spmean[MXM_MAX_EXPERTS];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  constexpr int NW = SCAN_NT / 64;
   const int T = a.ntiles;
+  const int e = blockIdx.x;
+  constexpr int SB = 16;  // loads per lane issued together
 
-  // pass 1: per-expert totals and probability sums (lane-strided sequential
-  // partial sums, then a fixed butterfly); the loads of SB tiles per lane are
-  // issued together
-  constexpr int SB = 16;
-  for (int e = wave; e < a.E; e += NW) {
-    int c = 0;
+  if (e == a.E) {
+    if (wave == 0) {
+      float sum = 0.0f;
+      for (int t0 = lane; t0 < T; t0 += 64 * SB) {
+        float ev[SB];
+#pragma unroll
+        for (int b = 0; b < SB; ++b) ev[b] = t0 + 64 * b < T ? a.tile_ent[t0 + 64 * b] : 0.0f;
+#pragma unroll
+        for (int b = 0; b < SB; ++b)
+          if (t0 + 64 * b < T) sum = sum + ev[b];
+      }
+      sum = wave_sum_fixed(sum);
+      if (lane == 0) a.entropy[0] = -(sum / (float)a.N);
+    }
+    return;
+  }
+
+  const int32_t* tc = a.tile_counts + (size_t)e * T;
+  if (wave == 0) {
+    const float* tp = a.tile_psum + (size_t)e * T;
     float ps = 0.0f;
     for (int t0 = lane; t0 < T; t0 += 64 * SB) {
-      int cv[SB];
       float pv[SB];
 #pragma unroll
-      for (int b = 0; b < SB; ++b) {
-        const int t = t0 + 64 * b;
-        cv[b] = t < T ? a.tile_counts[(size_t)e * T + t] : 0;
-        pv[b] = t < T ? a.tile_psum[(size_t)e * T + t] : 0.0f;
-      }
+      for (int b = 0; b < SB; ++b) pv[b] = t0 + 64 * b < T ? tp[t0 + 64 * b] : 0.0f;
 #pragma unroll
       for (int b = 0; b < SB; ++b)
-        if (t0 + 64 * b < T) {
-          c += cv[b];
-          ps = ps + pv[b];
-        }
+        if (t0 + 64 * b < T) ps = ps + pv[b];
     }
-    c = wave_sum_int(c);
     ps = wave_sum_fixed(ps);
     if (lane == 0) {
-      cnt[e] = c;
       const float mean = ps / (float)a.N;
-      pmean[e] = BF16 ? mxm_rbf(mean) : mean;
+      a.expert_pmean[e] = BF16 ? mxm_rbf(mean) : mean;
     }
   }
-  if (wave == NW - 1) {
-    float s = 0.0f;
-    for (int t0 = lane; t0 < T; t0 += 64 * SB) {
-      float ev[SB];
+  // thread i owns tiles [i*R, i*R + R): its run total, the workgroup's
+  // exclusive scan of the run totals, then the tiles' bases
+  const int R = (T + SCAN_NT - 1) / SCAN_NT;
+  const int t_lo = min(T, tid * R), t_hi = min(T, t_lo + R);
+  int run = 0;
+  for (int t = t_lo; t < t_hi; ++t) run += tc[t];
+  int incl = run;
 #pragma unroll
-      for (int b = 0; b < SB; ++b) ev[b] = t0 + 64 * b < T ? a.tile_ent[t0 + 64 * b] : 0.0f;
-#pragma unroll
-      for (int b = 0; b < SB; ++b)
-        if (t0 + 64 * b < T) s = s + ev[b];
-    }
-    s = wave_sum_fixed(s);
-    if (lane == 0) a.entropy[0] = -(s / (float)a.N);
+  for (int sh = 1; sh < 64; sh <<= 1) {
+    const int up = __shfl_up(incl, sh, 64);
+    if (lane >= sh) incl += up;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int base = incl - run;
+  for (int w = 0; w < wave; ++w) base += wtot[w];
+  for (int t = t_lo; t < t_hi; ++t) {
+    a.tile_base[(size_t)e * T + t] = base;
+    base += tc[t];
+  }
+  if (tid == SCAN_NT - 1) a.expert_count[e] = base;  // the expert's total
+
+  // ---- ticket: the last expert workgroup continues ----
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(a.ticket, 1) == a.E - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  // every expert's total read in one round of loads
+  for (int x = tid; x < a.E; x += SCAN_NT) {
+    scount[x] = a.expert_count[x];
+    spmean[x] = a.expert_pmean[x];
   }
   __syncthreads();
-
   if (tid == 0) {
     int o = 0, m1 = 0, m2 = 0;
     float aux = 0.0f;
-    for (int e = 0; e < a.E; ++e) {
-      const int c = cnt[e];
-      offs[e] = o;
-      a.offsets[e] = o;
-      a.counts[e] = c;
-      a.mstart1[e] = m1;
-      a.mstart2[e] = m2;
+    for (int x = 0; x < a.E; ++x) {
+      const int c = scount[x];
+      a.offsets[x] = o;
+      a.counts[x] = c;
+      a.mstart1[x] = m1;
+      a.mstart2[x] = m2;
       o += c;
       m1 += (c + a.bm1 - 1) / a.bm1;
       m2 += (c + a.bm2 - 1) / a.bm2;
       const float frac = ((float)c / (float)a.K) / (float)a.N;
-      const float term = pmean[e] * frac;
-      aux = (e == 0) ? term : aux + term;
+      const float term = spmean[x] * frac;
+      aux = (x == 0) ? term : aux + term;
     }
-    offs[a.E] = o;
     a.offsets[a.E] = o;
     a.mstart1[a.E] = m1;
     a.mstart2[a.E] = m2;
     const float raw = aux * (float)a.E;
     a.aux[0] = raw;
     if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
-  }
-  __syncthreads();
-
-  // pass 2: exclusive scan over tiles, per expert (SB chunks of 64 tiles
-  // loaded together, then scanned in order)
-  for (int e = wave; e < a.E; e += NW) {
-    int carry = offs[e];
-    for (int c0 = 0; c0 < T; c0 += 64 * SB) {
-      int cv[SB];
-#pragma unroll
-      for (int b = 0; b < SB; ++b) {
-        const int t = c0 + 64 * b + lane;
-        cv[b] = t < T ? a.tile_counts[(size_t)e * T + t] : 0;
-      }
-#pragma unroll
-      for (int b = 0; b < SB; ++b) {
-        if (c0 + 64 * b < T) {  // wave-uniform
-          const int t = c0 + 64 * b + lane;
-          int incl = cv[b];
-#pragma unroll
-          for (int s = 1; s < 64; s <<= 1) {
-            const int up = __shfl_up(incl, s, 64);
-            if (lane >= s) incl += up;
-          }
-          if (t < T) a.tile_base[(size_t)e * T + t] = carry + incl - cv[b];
-          carry += __shfl(incl, 63, 64);
-        }
-      }
-    }
+    __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -162,7 +161,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(ScatterArgs a) {
   const int n = (int)(s / a.K);
   const int e = a.top_idx[s];
   const int tile = n / MXM_ROUTER_TM;
-  const int pos = a.tile_base[(size_t)e * a.ntiles + tile] + a.slot_rank[s];
+  const int pos = a.offsets[e] + a.tile_base[(size_t)e * a.ntiles + tile] + a.slot_rank[s];
   a.perm[pos] = n;
   a.slot_pos[s] = pos;
 }
@@ -283,9 +282,9 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 
 void mxm_launch_scan(const ScanArgs& a, bool bf16, hipStream_t s) {
   if (bf16)
-    hipLaunchKernelGGL(scan_kernel<true>, dim3(1), dim3(SCAN_NT), 0, s, a);
+    hipLaunchKernelGGL(scan_kernel<true>, dim3(a.E + 1), dim3(SCAN_NT), 0, s, a);
   else
-    hipLaunchKernelGGL(scan_kernel<false>, dim3(1), dim3(SCAN_NT), 0, s, a);
+    hipLaunchKernelGGL(scan_kernel<false>, dim3(a.E + 1), dim3(SCAN_NT), 0, s, a);
 }
 
 void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s) {

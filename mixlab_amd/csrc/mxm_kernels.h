@@ -105,20 +105,24 @@ struct ScanArgs {
   int bm1, bm2;         // row-tile heights of the two grouped GEMMs
   int32_t* counts;      // [E]
   int32_t* offsets;     // [E + 1]
-  int32_t* tile_base;   // [E, ntiles] first permuted position of the tile's rows on e
+  int32_t* tile_base;   // [E, ntiles] first position of the tile's rows on e, relative to offsets[e]
   int32_t* mstart1;     // [E + 1] prefix of ceil(counts / bm1)
   int32_t* mstart2;     // [E + 1] prefix of ceil(counts / bm2)
   float* aux;           // [1]
   float* entropy;       // [1]
   float aux_weight;     // block level: aux_scaled = aux * aux_weight
   float* aux_scaled;    // [1] or null
+  int32_t* expert_count;  // [E] scratch: each workgroup's expert total
+  float* expert_pmean;    // [E] scratch: each workgroup's mean probability
+  int32_t* ticket;        // [1], zero between calls (the last workgroup resets it)
 };
 void mxm_launch_scan(const ScanArgs& a, bool bf16, hipStream_t s);
 
 struct ScatterArgs {
   const int32_t* top_idx;
   const int32_t* slot_rank;
-  const int32_t* tile_base;
+  const int32_t* tile_base;  // relative to offsets[e]
+  const int32_t* offsets;
   int N, K, ntiles;
   int32_t* perm;      // [N*K] permuted position -> token
   int32_t* slot_pos;  // [N*K] slot (n, k) -> permuted position
