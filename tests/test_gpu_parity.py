@@ -156,6 +156,36 @@ def test_ragged_token_counts(gpu_lib, B, T, D, F):
     assert rel_l2(delta, want["delta"]) <= BF16_TOL
 
 
+@pytest.mark.parametrize("E,K", [(1, 1), (2, 1), (2, 2), (3, 2)])
+@pytest.mark.parametrize("N", [1100, 2049])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_tiled_scan_few_experts(gpu_lib, E, K, N, bf16):
+    """The tiled router and the scan's one workgroup per expert at the
+    smallest expert counts (E = 1: the only expert workgroup is also the
+    last ticket), a ragged last token tile, and two calls on one op (the last
+    workgroup resets the ticket for the next call)."""
+    from mixlab_amd.op import MoEFeedForward
+
+    D, F = 128, 128
+    x, wr, experts = random_case(900 + 10 * E + K + N, N, D, E, F)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    conv = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
+    want = run_oracle(x, wr, experts, K=K, bf16=bf16)
+    with MoEFeedForward([1, N, D, E, K, 0, F, 0], [0.0],
+                        compute_dtype="bf16" if bf16 else "fp32") as op:
+        op.set_weights(conv(wr), [[conv(w) for w in ws] for ws in experts])
+        for call in range(2):
+            delta, aux, ent = op.forward_host(conv(x))
+            routing = op.routing()
+            assert_routing_equal(routing, want)
+            assert rel_l2(delta, want["delta"]) <= (BF16_TOL if bf16 else FP32_TOL), call
+            assert abs(aux - want["aux"]) <= (1e-2 if bf16 else 1e-5) * abs(want["aux"]), call
+            if E > 1:
+                assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"]), call
+
+
 def test_k_equals_e_and_k1(gpu_lib):
     x, wr, experts = random_case(21, 128, 128, 4, 128)
     for K in (1, 4):
