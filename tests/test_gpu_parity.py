@@ -156,6 +156,28 @@ def test_ragged_token_counts(gpu_lib, B, T, D, F):
     assert rel_l2(delta, want["delta"]) <= BF16_TOL
 
 
+@pytest.mark.parametrize("flow", ["bf16_mfma", "bf16_mfma128", "bf16_mfma256x128"])
+def test_mfma_families_many_tiles(gpu_lib, flow):
+    """Every MFMA tile family with more tiles than workgroups resident at once
+    (272 / 1056 / 544 gate+up tiles against a persistent grid of 256 / 512 /
+    512), so workgroups walk several tiles: routing bit-exact, delta on a
+    sample of rows within the bf16 bar."""
+    N, D, E, F, K = 16384, 256, 8, 256, 2
+    x, wr, experts = random_case(4242, N, D, E, F)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(m) for m in ws] for ws in experts]
+    flags = {"bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128,
+             "bf16_mfma256x128": _lib.MXM_FLAG_MFMA_TILE256x128}.get(flow, 0)
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=True,
+                                             flags=flags)
+    rows = np.sort(np.random.default_rng(5).choice(N, size=512, replace=False)).astype(np.int32)
+    want = run_oracle(x, wr, experts, K=K, bf16=True, rows=rows)
+    assert info["mfma"]
+    assert_routing_equal(routing, want)
+    err = rel_l2(delta[rows], want["delta"][rows])
+    assert err <= BF16_TOL, err
+
+
 @pytest.mark.parametrize("E,K", [(1, 1), (2, 1), (2, 2), (3, 2)])
 @pytest.mark.parametrize("N", [1100, 2049])
 @pytest.mark.parametrize("bf16", [False, True])
