@@ -10,6 +10,11 @@ metas of arch/moe.go:112-150 at the block's offset: ``moe_norm_scale``,
 ``moe_scale`` with block scales.  The reader and writer here follow the same
 layout and the same checks, with the reference's error messages.
 
+HF export (train/export_hf.go): an MoE block's weights keep their shapes
+and data and are renamed ``blocks.{b}.norm.weight``, ``blocks.{b}.router_w``
+and ``blocks.{b}.experts.{e}.w_{gate,up,down}.weight`` (``hf_moe_weight_map``,
+``export_hf_safetensors``).
+
 int8: the reference quantises for export per input row with clipping
 (train/quantize.go:99-118; ``DequantizePerRow`` :191-200 undoes it); the
 int8 executor (``mxm_moe_set_input_q8``) takes symmetric per-output-channel
@@ -22,11 +27,11 @@ import json
 import os
 import struct
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from .moe import BlockSpec, WeightMeta, moe_weight_shapes
+from .moe import BlockSpec, WeightMeta, effective_moe_expert_block, moe_weight_shapes
 
 
 class CheckpointError(ValueError):
@@ -135,6 +140,78 @@ def export_safetensors(path: str, metas: Sequence[WeightMeta], weights: Sequence
         offset += a.nbytes
         arrays.append(a)
     meta = {"format": "mixlab_v1"}
+    meta.update(metadata or {})
+    header["__metadata__"] = meta
+    hb = json.dumps(header, separators=(",", ":")).encode()
+    hb += b" " * ((8 - len(hb) % 8) % 8)
+    tmp = f"{path}.tmp{os.getpid()}"
+    with open(tmp, "wb") as f:
+        f.write(struct.pack("<Q", len(hb)))
+        f.write(hb)
+        for a in arrays:
+            f.write(a.tobytes())
+    os.replace(tmp, path)
+
+
+def hf_moe_weight_map(block_index: int, spec: BlockSpec, metas: Sequence[WeightMeta],
+                      first_index: int = 0) -> List[Tuple[str, str, List[int]]]:
+    """The HF export names of one MoE block (train/export_hf.go:544-604, with
+    the positional checks of ``addExpected`` :247-255): walks the block's
+    weight metas from global index ``first_index`` and returns
+    (native checkpoint name, HF name, shape) per mapped weight.  The block's
+    optional ``moe_scale`` is not mapped here, as in the reference's moe case."""
+    mapping: List[Tuple[str, str, List[int]]] = []
+    prefix = f"blocks.{block_index}"
+    wi = 0
+
+    def expect(want: str, hf: str, what: str) -> None:
+        nonlocal wi
+        if wi >= len(metas):
+            raise CheckpointError(f"weight map exhausted while mapping {what}")
+        got = metas[wi].name
+        if got != want:
+            raise CheckpointError(f"HF export weight map expected Mixlab weight {want!r} at index "
+                                  f"{first_index + wi}, got {got!r}")
+        mapping.append((checkpoint_name(first_index + wi, got), f"{prefix}.{hf}",
+                        list(metas[wi].shape)))
+        wi += 1
+
+    for mix, hf in (("moe_norm_scale", "norm.weight"), ("router_w", "router_w")):
+        expect(mix, hf, f"moe block {block_index}")
+    expert_type = effective_moe_expert_block(spec).type.strip().lower() or "swiglu"
+    if expert_type in ("swiglu", "geglu"):
+        kinds = ("gate", "up", "down")
+    elif expert_type == "mlp":
+        kinds = ("up", "down")
+    else:
+        raise CheckpointError(f"unsupported HF export moe expert type "
+                              f"{effective_moe_expert_block(spec).type!r}")
+    for e in range(spec.num_experts):
+        for k in kinds:
+            expect(f"expert_{e}_w_{k}", f"experts.{e}.w_{k}.weight",
+                   f"moe block {block_index} expert {e}")
+    return mapping
+
+
+def export_hf_safetensors(path: str, mapping: Sequence[Tuple[str, str, List[int]]],
+                          weights: Sequence[np.ndarray],
+                          metadata: Optional[Dict[str, str]] = None) -> None:
+    """train/export_hf.go:772-800: F32 tensors under their HF names with the
+    mapped shapes (no transposes), ``__metadata__`` format "pt" plus the
+    model fields the caller passes (name, model_dim, vocab_size, seq_len)."""
+    if len(mapping) != len(weights):
+        raise CheckpointError(f"mapping/weights count mismatch: {len(mapping)} vs {len(weights)}")
+    header = {}
+    offset = 0
+    arrays = []
+    for (_, hf, shape), w in zip(mapping, weights):
+        a = np.ascontiguousarray(w, dtype="<f4")
+        if list(a.shape) != list(shape):
+            raise CheckpointError(f"weight {hf} has shape {list(a.shape)}, want {list(shape)}")
+        header[hf] = {"dtype": "F32", "shape": list(shape), "data_offsets": [offset, offset + a.nbytes]}
+        offset += a.nbytes
+        arrays.append(a)
+    meta = {"format": "pt"}
     meta.update(metadata or {})
     header["__metadata__"] = meta
     hb = json.dumps(header, separators=(",", ":")).encode()

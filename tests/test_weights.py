@@ -126,3 +126,67 @@ def test_aux_entropy_aggregation():
     assert vals["loss"] == float(f(2.5) + f(vals["moe_aux_loss"]))
     # no MoE block: nothing emitted
     assert not moe.emit_moe_auxiliary_aggregates_ir(moe.Program(), False)
+
+
+# ---- HF export names (train/export_hf.go:544-604) ----
+
+def _moe_metas(expert_type="swiglu", E=2, D=8):
+    from mixlab_amd.weights import moe_block_metas
+    spec = moe.BlockSpec(type="moe", num_experts=E, top_k=min(2, E),
+                         expert_block=moe.BlockSpec(type=expert_type))
+    return spec, moe_block_metas(spec, D, 4.0)
+
+
+@pytest.mark.parametrize("expert_type,kinds", [("swiglu", ("gate", "up", "down")),
+                                               ("geglu", ("gate", "up", "down")),
+                                               ("mlp", ("up", "down"))])
+def test_hf_moe_names(expert_type, kinds):
+    from mixlab_amd.weights import hf_moe_weight_map
+    spec, metas = _moe_metas(expert_type)
+    got = hf_moe_weight_map(4, spec, metas, first_index=10)
+    want_hf = ["blocks.4.norm.weight", "blocks.4.router_w"] + [
+        f"blocks.4.experts.{e}.w_{k}.weight" for e in range(2) for k in kinds]
+    assert [g[1] for g in got] == want_hf
+    assert [g[0] for g in got] == [f"w{10 + i}_{m.name}" for i, m in enumerate(metas)]
+    assert [g[2] for g in got] == [list(m.shape) for m in metas]
+
+
+def test_hf_moe_default_expert_is_swiglu():
+    from mixlab_amd.weights import hf_moe_weight_map, moe_block_metas
+    spec = moe.BlockSpec(type="moe", num_experts=1, top_k=1)
+    got = hf_moe_weight_map(0, spec, moe_block_metas(spec, 8, 4.0))
+    assert got[2][1] == "blocks.0.experts.0.w_gate.weight"
+
+
+def test_hf_moe_errors():
+    from mixlab_amd.weights import hf_moe_weight_map
+    spec, metas = _moe_metas("swiglu")
+    with pytest.raises(CheckpointError, match="weight map exhausted while mapping moe block 1 expert 1"):
+        hf_moe_weight_map(1, spec, metas[:-1])
+    with pytest.raises(CheckpointError, match="weight map exhausted while mapping moe block 1$"):
+        hf_moe_weight_map(1, spec, metas[:1])
+    swapped = [metas[1], metas[0]] + list(metas[2:])
+    with pytest.raises(CheckpointError, match="expected Mixlab weight 'moe_norm_scale' at index 3, got 'router_w'"):
+        hf_moe_weight_map(1, spec, swapped, first_index=3)
+    bad = moe.BlockSpec(type="moe", num_experts=1, top_k=1, expert_block=moe.BlockSpec(type="conv"))
+    with pytest.raises(CheckpointError, match="unsupported HF export moe expert type 'conv'"):
+        hf_moe_weight_map(0, bad, metas)
+
+
+def test_hf_export_round_trip(tmp_path):
+    from mixlab_amd.weights import export_hf_safetensors, hf_moe_weight_map, load_safetensors
+    spec, metas = _moe_metas("mlp", E=3)
+    rng = np.random.default_rng(3)
+    ws = [rng.standard_normal(m.shape).astype(np.float32) for m in metas]
+    mapping = hf_moe_weight_map(2, spec, metas)
+    path = str(tmp_path / "hf.safetensors")
+    export_hf_safetensors(path, mapping, ws, {"name": "t", "model_dim": "8"})
+    tensors = load_safetensors(path)
+    for (_, hf, shape), w in zip(mapping, ws):
+        assert tensors[hf].dtype == "F32" and tensors[hf].shape == shape
+        np.testing.assert_array_equal(np.frombuffer(tensors[hf].data, "<f4").reshape(shape), w)
+    with open(path, "rb") as f:
+        import json, struct
+        n = struct.unpack("<Q", f.read(8))[0]
+        meta = json.loads(f.read(n))["__metadata__"]
+    assert meta == {"format": "pt", "name": "t", "model_dim": "8"}
