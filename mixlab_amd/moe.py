@@ -325,6 +325,17 @@ def emit_moe_ir(prog: Program, spec: BlockSpec, x: str, wi: int, D: int, T: int,
     return next_wi
 
 
+def emit_moe_parallel_delta_ir(prog: Program, spec: BlockSpec, x_norm: str, wi: int, D: int, T: int,
+                               B: int, idx: int, mlp_mult: float = DEFAULT_FFN_MULTIPLIER,
+                               block_scales: bool = False, dropout: float = 0.0) -> tuple[str, int]:
+    """arch/moe.go:168-171, the MoE member of a parallel-residual pair
+    (arch/parallel_residual.go:461-462): the pair's shared normalised rows
+    go straight into op 74 and the delta is returned for the pair to add."""
+    prefix = tmp_name(x_norm + "_parallel_moe", idx)
+    return emit_moe_delta_ir(prog, spec, x_norm, wi, D, T, B, idx, mlp_mult, block_scales,
+                             dropout, prefix)
+
+
 def estimate_moe_block_flops(block: BlockSpec, B: int, T: int, D: int, mlp_mult: float) -> int:
     """arch/moe.go:215-236: router + top_k active experts (the algorithmic count)."""
     if block.num_experts <= 0:

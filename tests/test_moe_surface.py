@@ -119,6 +119,30 @@ def test_op_encoding_and_block_emission():
     assert next_wi == 16
 
 
+def test_parallel_residual_member_emission():
+    """arch/moe.go:168-171 (arch/parallel_residual.go:461-462): no norm and no
+    residual add of its own; op 74 on the pair's normalised rows, the aux
+    scaling, optional moe_scale, the delta returned under the
+    `<x_norm>_parallel_moe_<idx>` prefix."""
+    spec = _block('{"type":"moe","num_experts":2,"top_k":2}')
+    prog = moe.Program()
+    delta, next_wi = moe.emit_moe_parallel_delta_ir(prog, spec, "h_norm", 3, 16, 4, 1, 5,
+                                                    mlp_mult=2.0, block_scales=True)
+    codes = [op.code for op in prog.ops]
+    assert codes == [moe.OP_MOE_FEED_FORWARD, moe.OP_SCALAR_MUL, moe.OP_MUL]
+    ff, scal, mul = prog.ops
+    assert ff.inputs == ["h_norm"] + [f"w{i}" for i in range(3, 3 + 1 + 2 * 3)]
+    assert ff.outputs == ["h_norm_parallel_moe_5_delta", "h_norm_parallel_moe_5_moe_aux_loss_raw",
+                          "h_norm_parallel_moe_5_moe_router_entropy"]
+    assert scal.outputs == ["h_norm_parallel_moe_5_moe_aux_loss"]
+    assert mul.inputs == ["h_norm_parallel_moe_5_delta", "w10"]
+    assert delta == "h_norm_parallel_moe_5_scaled" and next_wi == 11
+    prog2 = moe.Program()
+    delta2, wi2 = moe.emit_moe_parallel_delta_ir(prog2, spec, "h_norm", 0, 16, 4, 1, 0,
+                                                 mlp_mult=2.0)
+    assert delta2 == "h_norm_parallel_moe_0_delta" and wi2 == 7
+
+
 def test_flop_estimates():
     """arch/moe.go:215-236 counts the router and top_k active experts."""
     spec = _block('{"type":"moe","num_experts":64,"top_k":8}')
