@@ -404,6 +404,25 @@ def emit_moe_auxiliary_aggregates_ir(prog: Program, task_loss_has_eval_loss: boo
     return True
 
 
+def training_step_output_names(prog: Program, loss_name: str = "loss") -> list:
+    """gpu/ir_trainer.cpp:1540-1585: the outputs a training step reads back --
+    the loss, then each of magnitudes, x_hidden, logits, qr, moe_aux_loss and
+    moe_router_entropy that some op of the program writes, in that order."""
+    written = {out for op in prog.ops for out in op.outputs}
+    names = [loss_name]
+    for name in ("magnitudes", "x_hidden", "logits", "qr", "moe_aux_loss", "moe_router_entropy"):
+        if name in written:
+            names.append(name)
+    return names
+
+
+def moe_component_losses(values: dict) -> dict:
+    """The MoE entry of the telemetry's ``component_losses`` object
+    (train/telemetry.go:48, docs/performance.md:158-163): ``moe_aux_loss``
+    when the graph produced it; absent objectives add no key."""
+    return {"moe_aux_loss": float(values["moe_aux_loss"])} if "moe_aux_loss" in values else {}
+
+
 def evaluate_scalar_ops(prog: Program, values: dict, start: int = 0) -> dict:
     """Evaluate the scalar Add / ScalarMul ops of prog (from op index start)
     in fp32, as the interpreter does for [1]-shaped tensors; values maps

@@ -190,3 +190,21 @@ def test_hf_export_round_trip(tmp_path):
         n = struct.unpack("<Q", f.read(8))[0]
         meta = json.loads(f.read(n))["__metadata__"]
     assert meta == {"format": "pt", "name": "t", "model_dim": "8"}
+
+
+def test_training_step_outputs_and_component_losses():
+    """gpu/ir_trainer.cpp:1540-1585: the loss first, then the captured scalars
+    the program writes; the telemetry's component_losses carries
+    moe_aux_loss only when the graph has it."""
+    spec = moe.BlockSpec.from_json('{"type":"moe","num_experts":4,"top_k":2}')
+    prog = moe.Program()
+    assert moe.training_step_output_names(prog) == ["loss"]
+    wi = moe.emit_moe_ir(prog, spec, "x", 0, 16, 4, 1, 0, mlp_mult=2.0)
+    moe.emit_moe_ir(prog, spec, "x", wi, 16, 4, 1, 1, mlp_mult=2.0)
+    assert moe.training_step_output_names(prog) == ["loss"]  # per-block names only so far
+    assert moe.emit_moe_auxiliary_aggregates_ir(prog, task_loss_has_eval_loss=False)
+    assert moe.training_step_output_names(prog) == ["loss", "moe_aux_loss", "moe_router_entropy"]
+    assert moe.training_step_output_names(prog, "total") == ["total", "moe_aux_loss",
+                                                             "moe_router_entropy"]
+    assert moe.moe_component_losses({"loss": 1.0}) == {}
+    assert moe.moe_component_losses({"moe_aux_loss": np.float32(0.25)}) == {"moe_aux_loss": 0.25}
