@@ -18,7 +18,14 @@ Parity pins (see tests/test_oracle.py):
   * closed forms: K = E (dense softmax mixture), K = 1 (argmax, gate 1),
     E = K = 1 (plain sigmoid-GLU FFN), tie order of a stable argsort;
   * exp within 2 ulp of the correctly rounded value on a dense sweep;
-  * dense (every expert on every row) == sparse bit for bit.
+  * dense (every expert on every row) == sparse bit for bit;
+  * the bf16 dtype flow step by step (tests/test_oracle_bf16.py): bf16 logits
+    and probabilities against float64 dot products and softmax, top-k against
+    a lexsort of the bf16 probabilities, gates against the bf16 top-p sum,
+    aux against the bf16 per-expert means, entropy over the bf16
+    probabilities, each expert kind's activation against float64 rounded at
+    the flow's rounding points, and the delta against a float64 restatement
+    of the flow -- each shown to reject a planted slip (build_planted).
 """
 from __future__ import annotations
 
@@ -32,7 +39,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "libmoe_oracle.so"
 
-_lib = None
+_libs: dict = {}
 
 
 def build() -> Path:
@@ -40,12 +47,24 @@ def build() -> Path:
     return LIB_PATH
 
 
-def _load():
-    global _lib
-    if _lib is None:
-        if not LIB_PATH.exists():
+def build_planted(plant: str, outdir) -> Path:
+    """Compile a copy of the restatement with one planted mistake
+    (ORACLE_PLANT_<plant>, see the list at the top of moe_oracle.c) into
+    outdir; the tests use it to show that a pin rejects that mistake."""
+    out = Path(outdir) / f"libmoe_oracle_plant_{plant.lower()}.so"
+    cmd = ["gcc", "-O2", "-mfma", "-mavx2", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
+           "-fPIC", "-std=c11", "-shared", f"-DORACLE_PLANT_{plant.upper()}",
+           "-o", str(out), str(HERE / "moe_oracle.c"), "-lm"]
+    subprocess.run(cmd, check=True)
+    return out
+
+
+def _load(path=None):
+    path = str(LIB_PATH if path is None else path)
+    if path not in _libs:
+        if path == str(LIB_PATH) and not LIB_PATH.exists():
             build()
-        lib = ctypes.CDLL(str(LIB_PATH))
+        lib = ctypes.CDLL(path)
         f32p = ctypes.POINTER(ctypes.c_float)
         i32p = ctypes.POINTER(ctypes.c_int32)
         lib.oracle_moe_forward.restype = ctypes.c_int
@@ -67,8 +86,8 @@ def _load():
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, f32p, f32p, f32p,
             ctypes.c_int64,
         ]
-        _lib = lib
-    return _lib
+        _libs[path] = lib
+    return _libs[path]
 
 
 def _p(a, ctype=ctypes.c_float):
@@ -107,11 +126,14 @@ def exp(x: np.ndarray) -> np.ndarray:
     return y
 
 
-def hidden(bf16: bool, expert_type: int, activation: int, slope: float, g, u) -> np.ndarray:
+def hidden(bf16: bool, expert_type: int, activation: int, slope: float, g, u,
+           lib=None) -> np.ndarray:
+    """Hidden unit act(g, u) of gpu/ir.cpp:1130-1145 elementwise; g and u are
+    the projections (bf16 values in the bf16 flow).  lib: a planted build."""
     g = np.ascontiguousarray(g, dtype=np.float32)
     u = np.ascontiguousarray(u, dtype=np.float32)
     h = np.empty_like(u)
-    _load().oracle_hidden_array(int(bf16), expert_type, activation, slope, _p(g), _p(u), _p(h), u.size)
+    _load(lib).oracle_hidden_array(int(bf16), expert_type, activation, slope, _p(g), _p(u), _p(h), u.size)
     return h
 
 
@@ -125,12 +147,12 @@ def pack_experts(expert_weights) -> np.ndarray:
 def moe_forward(x, router_w, expert_weights, *, top_k: int, expert_type: int = 0,
                 activation: int = 0, leaky_slope: float = 0.0, bf16: bool = False,
                 dense: bool = False, rows=None, want_delta: bool = True,
-                prerounded: bool = False) -> dict:
+                prerounded: bool = False, lib=None) -> dict:
     """Run the restatement.  x [N, D]; router_w [D, E]; expert_weights as in
     pack_experts (or already packed).  In the bf16 flow inputs are rounded to
     bf16 here.  Returns delta, aux, entropy, top_idx, gates, probs, logits,
-    counts, offsets, perm (numpy arrays)."""
-    lib = _load()
+    counts, offsets, perm (numpy arrays).  lib: a planted build (tests)."""
+    lib = _load(lib)
     x = np.ascontiguousarray(x, dtype=np.float32)
     router_w = np.ascontiguousarray(router_w, dtype=np.float32)
     N, D = x.shape

@@ -43,6 +43,83 @@
 #include <omp.h>
 #endif
 
+/* Planted mistakes.  tests/test_oracle_bf16.py compiles copies of this file
+ * with one ORACLE_PLANT_<NAME> macro defined and checks that its pins reject
+ * each; the default build (oracle/Makefile) defines none, and then every
+ * PLANT(...) below is 0.  Each names one plausible slip in the bf16 dtype
+ * flow: a rounding dropped, or a decision taken on unrounded values. */
+#define PLANT(name) PLANT_##name
+#ifdef ORACLE_PLANT_LOGITS_FP32
+#define PLANT_LOGITS_FP32 1 /* logits not rounded to bf16 */
+#else
+#define PLANT_LOGITS_FP32 0
+#endif
+#ifdef ORACLE_PLANT_PROBS_FP32
+#define PLANT_PROBS_FP32 1 /* probabilities not rounded to bf16 */
+#else
+#define PLANT_PROBS_FP32 0
+#endif
+#ifdef ORACLE_PLANT_TOPK_FP32
+#define PLANT_TOPK_FP32 1 /* top-k ranked on the unrounded fp32 probabilities */
+#else
+#define PLANT_TOPK_FP32 0
+#endif
+#ifdef ORACLE_PLANT_TOPSUM_FP32
+#define PLANT_TOPSUM_FP32 1 /* the top-p sum left in fp32 */
+#else
+#define PLANT_TOPSUM_FP32 0
+#endif
+#ifdef ORACLE_PLANT_AUX_MEAN_FP32
+#define PLANT_AUX_MEAN_FP32 1 /* the per-expert mean probability left in fp32 */
+#else
+#define PLANT_AUX_MEAN_FP32 0
+#endif
+#ifdef ORACLE_PLANT_ENTROPY_FP32
+#define PLANT_ENTROPY_FP32 1 /* entropy from the unrounded probabilities */
+#else
+#define PLANT_ENTROPY_FP32 0
+#endif
+#ifdef ORACLE_PLANT_PROJ_FP32
+#define PLANT_PROJ_FP32 1 /* expert projections not rounded to bf16 */
+#else
+#define PLANT_PROJ_FP32 0
+#endif
+#ifdef ORACLE_PLANT_SWIGLU_SIG
+#define PLANT_SWIGLU_SIG 1 /* swiglu: sigmoid(g) not rounded */
+#else
+#define PLANT_SWIGLU_SIG 0
+#endif
+#ifdef ORACLE_PLANT_SWIGLU_PROD
+#define PLANT_SWIGLU_PROD 1 /* swiglu: sigmoid(g) * u not rounded */
+#else
+#define PLANT_SWIGLU_PROD 0
+#endif
+#ifdef ORACLE_PLANT_GEGLU_SQ
+#define PLANT_GEGLU_SQ 1 /* geglu: square(g) not rounded */
+#else
+#define PLANT_GEGLU_SQ 0
+#endif
+#ifdef ORACLE_PLANT_SILU_SIG
+#define PLANT_SILU_SIG 1 /* mlp silu: sigmoid(u) not rounded */
+#else
+#define PLANT_SILU_SIG 0
+#endif
+#ifdef ORACLE_PLANT_GELU_SQ
+#define PLANT_GELU_SQ 1 /* mlp gelu: square(u) not rounded */
+#else
+#define PLANT_GELU_SQ 0
+#endif
+#ifdef ORACLE_PLANT_Y_FP32
+#define PLANT_Y_FP32 1 /* expert output y of a bf16-hidden kind left in fp32 */
+#else
+#define PLANT_Y_FP32 0
+#endif
+#ifdef ORACLE_PLANT_Y_BF16
+#define PLANT_Y_BF16 1 /* expert output y rounded to bf16 for every kind */
+#else
+#define PLANT_Y_BF16 0
+#endif
+
 static inline uint32_t f2u(float f) {
   uint32_t u;
   memcpy(&u, &f, 4);
@@ -111,13 +188,14 @@ static inline float R(int bf16, float v) { return bf16 ? oracle_round_bf16(v) : 
 
 /* Hidden unit of one expert row (gpu/ir.cpp:1130-1145 and 1057-1068). */
 float oracle_hidden(int bf16, int etype, int act, float slope, float g, float u) {
-  if (etype == SWIGLU) return R(bf16, R(bf16, oracle_sigmoid(g)) * u);
-  if (etype == GEGLU) return oracle_gelu_tanh(g, R(bf16, g * g)) * u;
+  if (etype == SWIGLU)
+    return R(bf16 && !PLANT(SWIGLU_PROD), R(bf16 && !PLANT(SWIGLU_SIG), oracle_sigmoid(g)) * u);
+  if (etype == GEGLU) return oracle_gelu_tanh(g, R(bf16 && !PLANT(GEGLU_SQ), g * g)) * u;
   switch (act) {
     case SILU:
-      return R(bf16, u * R(bf16, oracle_sigmoid(u)));
+      return R(bf16, u * R(bf16 && !PLANT(SILU_SIG), oracle_sigmoid(u)));
     case GELU:
-      return oracle_gelu_tanh(u, R(bf16, u * u));
+      return oracle_gelu_tanh(u, R(bf16 && !PLANT(GELU_SQ), u * u));
     case RELU:
       return u > 0.0f ? u : 0.0f;
     default: {
@@ -128,6 +206,8 @@ float oracle_hidden(int bf16, int etype, int act, float slope, float g, float u)
 }
 
 static int hidden_is_bf16(int etype, int act) {
+  if (PLANT(Y_FP32)) return 0;
+  if (PLANT(Y_BF16)) return 1;
   if (etype == SWIGLU) return 1;
   if (etype == GEGLU) return 0;
   return act == SILU || act == RELU;
@@ -150,8 +230,8 @@ static void gemm_rows(const float* const* arows, int nr, const float* b, int inn
 
 /* Router for rows [n0, n1): logits, probs, top-k, gates. */
 static void route_rows(int n0, int n1, int D, int E, int K, int bf16, const float* x,
-                       const float* wr, float* logits, float* probs, int32_t* top_idx,
-                       float* gates) {
+                       const float* wr, float* logits, float* probs, float* probs_raw,
+                       int32_t* top_idx, float* gates) {
   float* acc = (float*)malloc(sizeof(float) * (size_t)E);
   float* ex = (float*)malloc(sizeof(float) * (size_t)E);
   unsigned char* taken = (unsigned char*)malloc((size_t)E);
@@ -164,9 +244,10 @@ static void route_rows(int n0, int n1, int D, int E, int K, int bf16, const floa
     }
     float* lg = logits + (size_t)n * E;
     float* p = probs + (size_t)n * E;
+    float* praw = probs_raw + (size_t)n * E;
     float m = -INFINITY;
     for (int e = 0; e < E; ++e) {
-      lg[e] = R(bf16, acc[e]);
+      lg[e] = R(bf16 && !PLANT(LOGITS_FP32), acc[e]);
       m = fmaxf(m, lg[e]);
     }
     for (int e = 0; e < E; ++e) ex[e] = oracle_exp(lg[e] - m);
@@ -182,19 +263,23 @@ static void route_rows(int n0, int n1, int D, int E, int K, int bf16, const floa
       memcpy(lane, nx, sizeof lane);
     }
     const float sum = lane[0];
-    for (int e = 0; e < E; ++e) p[e] = R(bf16, ftz(ex[e] / sum));
+    for (int e = 0; e < E; ++e) {
+      praw[e] = ftz(ex[e] / sum);
+      p[e] = R(bf16 && !PLANT(PROBS_FP32), praw[e]);
+    }
     /* stable argsort(-p): largest first, ties to the lower expert index */
+    const float* rank = PLANT(TOPK_FP32) ? praw : p;
     memset(taken, 0, (size_t)E);
     float s_top = 0.0f;
     for (int k = 0; k < K; ++k) {
       int best = -1;
       for (int e = 0; e < E; ++e)
-        if (!taken[e] && (best < 0 || p[e] > p[best])) best = e;
+        if (!taken[e] && (best < 0 || rank[e] > rank[best])) best = e;
       taken[best] = 1;
       top_idx[(size_t)n * K + k] = best;
       s_top = (k == 0) ? p[best] : s_top + p[best];
     }
-    const float den = fmaxf(R(bf16, s_top), 1e-12f);
+    const float den = fmaxf(R(bf16 && !PLANT(TOPSUM_FP32), s_top), 1e-12f);
     for (int k = 0; k < K; ++k) gates[(size_t)n * K + k] = p[top_idx[(size_t)n * K + k]] / den;
   }
   free(acc);
@@ -227,6 +312,7 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
   float* probs = probs_out ? probs_out : (float*)malloc(sizeof(float) * NE);
   int32_t* top_idx = top_idx_out ? top_idx_out : (int32_t*)malloc(sizeof(int32_t) * NK);
   float* gates = gates_out ? gates_out : (float*)malloc(sizeof(float) * NK);
+  float* probs_raw = (float*)malloc(sizeof(float) * NE); /* before the bf16 rounding */
 
 #pragma omp parallel
   {
@@ -237,7 +323,8 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
 #endif
     const int chunk = (N + nt - 1) / nt;
     const int a = it * chunk, b = (a + chunk < N) ? a + chunk : N;
-    if (a < b) route_rows(a, b, D, E, K, bf16, x, router_w, logits, probs, top_idx, gates);
+    if (a < b)
+      route_rows(a, b, D, E, K, bf16, x, router_w, logits, probs, probs_raw, top_idx, gates);
   }
 
   /* aux and entropy (gpu/ir.cpp:1150-1162) */
@@ -248,7 +335,7 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
     for (int e = 0; e < E; ++e) {
       double s = 0.0;
       for (int n = 0; n < N; ++n) s += probs[(size_t)n * E + e];
-      const float pm = R(bf16, (float)(s / N));
+      const float pm = R(bf16 && !PLANT(AUX_MEAN_FP32), (float)(s / N));
       const float frac = ((float)cnt[e] / (float)K) / (float)N;
       const float term = pm * frac;
       acc = (e == 0) ? term : acc + term;
@@ -260,7 +347,7 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
     for (int n = 0; n < N; ++n) {
       float rs = 0.0f;
       for (int e = 0; e < E; ++e) {
-        const float q = probs[(size_t)n * E + e];
+        const float q = (PLANT(ENTROPY_FP32) ? probs_raw : probs)[(size_t)n * E + e];
         rs += q * logf(fmaxf(q, 1e-12f));
       }
       tot += rs;
@@ -328,9 +415,10 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
         for (int r = 0; r < nb; ++r) ar[r] = x + (size_t)list[b0 + r] * D;
         if (wg) gemm_rows(ar, nb, wg, D, F, g);
         gemm_rows(ar, nb, wu, D, F, u);
+        const int rp = bf16 && !PLANT(PROJ_FP32); /* projections are bf16 matmuls */
         for (int i = 0; i < nb * F; ++i) {
-          const float gi = wg ? R(bf16, g[i]) : 0.0f;
-          u[i] = oracle_hidden(bf16, etype, act, slope, gi, R(bf16, u[i]));
+          const float gi = wg ? R(rp, g[i]) : 0.0f;
+          u[i] = oracle_hidden(bf16, etype, act, slope, gi, R(rp, u[i]));
         }
         const float* hr[8];
         for (int r = 0; r < nb; ++r) hr[r] = u + (size_t)r * F;
@@ -360,6 +448,7 @@ int oracle_moe_forward(int N, int D, int E, int K, int etype, int F, int act, fl
   free(cnt);
   free(off);
   free(grp);
+  free(probs_raw);
   if (!logits_out) free(logits);
   if (!probs_out) free(probs);
   if (!top_idx_out) free(top_idx);
