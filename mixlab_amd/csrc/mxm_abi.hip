@@ -677,6 +677,10 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     if (o->B <= 0 || o->T <= 0 || o->D <= 0 || o->E <= 0 || o->K <= 0 || o->K > o->E || o->F <= 0)
       fail("OP_MOE_FEED_FORWARD invalid dimensions");
     if ((int64_t)o->B * o->T > (int64_t)1 << 30) fail("OP_MOE_FEED_FORWARD invalid dimensions");
+    // slot indices (perm, slot_pos, offsets, row tiles) are int32
+    if ((int64_t)o->B * o->T * o->K > (int64_t)INT32_MAX)
+      fail("OP_MOE_FEED_FORWARD B*T*topK = %lld routed slots exceeds %d",
+           (long long)((int64_t)o->B * o->T * o->K), INT32_MAX);
     if (o->etype < MXM_EXPERT_SWIGLU || o->etype > MXM_EXPERT_MLP)
       fail("OP_MOE_FEED_FORWARD unsupported expert type");
     if (o->etype == MXM_EXPERT_MLP && (o->act < MXM_ACT_SILU || o->act > MXM_ACT_LEAKY_RELU_SQ))

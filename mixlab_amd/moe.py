@@ -51,6 +51,12 @@ class BlockSpec:
     weight_group: str = ""
     parallel_residual: Optional[bool] = None
     heads: int = 0
+    residual_scale_init: Optional[float] = None
+    # keys outside the fields above.  arch.BlockSpec has its own UnmarshalJSON
+    # (arch/config.go:229-249), which re-decodes the block with a plain
+    # json.Unmarshal: the outer decoder's DisallowUnknownFields
+    # (arch/config_load.go:115) does not reach into a block, so unknown keys
+    # inside a block are ignored by the reference, not rejected.
     extra: dict = field(default_factory=dict)
     # presence flag recorded by BlockSpec.UnmarshalJSON (arch/config.go:229-249)
     load_balance_loss_weight_set: bool = False
@@ -59,7 +65,8 @@ class BlockSpec:
     def from_dict(cls, raw: dict) -> "BlockSpec":
         known = {"type", "num_experts", "top_k", "expert_block", "router",
                  "load_balance_loss_weight", "activation", "leaky_slope", "weight_group",
-                 "parallel_residual", "heads"}
+                 "parallel_residual", "heads", "residual_scale_init"}
+        rsi = raw.get("residual_scale_init")
         spec = cls(
             type=str(raw.get("type", "")),
             num_experts=int(raw.get("num_experts", 0)),
@@ -72,6 +79,7 @@ class BlockSpec:
             weight_group=str(raw.get("weight_group", "")),
             parallel_residual=raw.get("parallel_residual"),
             heads=int(raw.get("heads", 0)),
+            residual_scale_init=None if rsi is None else float(rsi),
             extra={k: v for k, v in raw.items() if k not in known},
         )
         spec.load_balance_loss_weight_set = "load_balance_loss_weight" in raw
@@ -160,10 +168,28 @@ def ffn_dim(D: int, multiplier: float) -> int:
 
 @dataclass
 class WeightMeta:
+    """The fields of arch.WeightMeta this block sets (arch/weight_shapes.go)."""
+
     name: str
     shape: list
     is_norm_scale: bool = False
     init_one: bool = False
+    init_zero: bool = False
+    init_value: float = 0.0
+
+
+def residual_scale_weight_meta(spec: BlockSpec, name: str, dim: int) -> WeightMeta:
+    """arch/weight_shapes.go:75-87: init 1 unless residual_scale_init is set;
+    an explicit 0 inits to zero, any other value inits to that value (fp32)."""
+    meta = WeightMeta(name, [dim], init_one=True)
+    if spec.residual_scale_init is None:
+        return meta
+    meta.init_one = False
+    if spec.residual_scale_init == 0:
+        meta.init_zero = True
+        return meta
+    meta.init_value = float(np.float32(spec.residual_scale_init))
+    return meta
 
 
 def moe_weight_shapes(spec: BlockSpec, D: int, mlp_mult: float = DEFAULT_FFN_MULTIPLIER,
@@ -184,8 +210,30 @@ def moe_weight_shapes(spec: BlockSpec, D: int, mlp_mult: float = DEFAULT_FFN_MUL
             metas += [WeightMeta(f"expert_{i}_w_up", [D, F]),
                       WeightMeta(f"expert_{i}_w_down", [F, D])]
     if block_scales:
-        metas.append(WeightMeta("moe_scale", [D], init_one=True))
+        metas.append(residual_scale_weight_meta(spec, "moe_scale", D))
     return metas
+
+
+def moe_parallel_weight_shapes(spec: BlockSpec, paired_second: bool, D: int,
+                               mlp_mult: float = DEFAULT_FFN_MULTIPLIER,
+                               block_scales: bool = False) -> list[WeightMeta]:
+    """arch/weight_shapes.go:498-551 for an MoE block: the second block of a
+    parallel-residual pair runs on the pair's shared normalised rows, so its
+    own moe_norm_scale is stripped (pinned by arch/moe_test.go:160-198)."""
+    metas = moe_weight_shapes(spec, D, mlp_mult, block_scales)
+    if paired_second:
+        if not metas or metas[0].name != "moe_norm_scale":
+            raise ConfigError("parallel_residual FFN block has unexpected weight layout")
+        metas = metas[1:]
+    return metas
+
+
+def moe_parallel_weight_count(spec: BlockSpec, paired_second: bool,
+                              block_scales: bool = False) -> int:
+    """arch/parallel_residual.go:242-264: a paired MoE follower omits one
+    weight (its norm scale)."""
+    n = moe_weight_count(spec, block_scales)
+    return n - 1 if paired_second else n
 
 
 def validate_moe_block(b: BlockSpec, source: str = "config", group: str = "blocks",
@@ -226,6 +274,91 @@ def parse_moe_block(text: str, source: str = "config", idx: int = 0) -> BlockSpe
     spec = BlockSpec.from_json(text)
     validate_moe_block(spec, source=source, idx=idx)
     return spec
+
+
+# JSON names of arch.ArchConfig's fields (arch/config.go:18-87): the
+# top-level keys ParseArchConfig accepts; any other top-level key is an error
+# (DisallowUnknownFields, arch/config_load.go:115).
+ARCH_CONFIG_FIELDS = frozenset((
+    "name", "model_dim", "vocab_size", "seq_len", "mlp_mult", "tie_embeddings", "block_scales",
+    "resid_mix", "parallel_residual", "unet", "rc_equivariant", "smear_embeddings",
+    "smear_embeddings_gate_shape", "char_vocab_size", "char_dim", "char_max_per_token",
+    "positional_embedding", "max_positions", "embedding_dropout", "input_adapter",
+    "hf_export_format", "bigram_vocab_size", "bigram_dim", "trigram_vocab_size", "trigram_dim",
+    "logit_softcap", "dropout", "attn_dropout", "hidden_dropout", "tie_dropout", "mlm_head",
+    "norm_type", "norm_eps", "norm_affine", "batchnorm_momentum", "norm_placement", "final_norm",
+    "ffn_internal_norm", "layer_aggregation", "mtp", "backout", "data", "blocks", "recurrence",
+    "recurrence_phases", "execution_order", "recurrence_phase_activations", "training", "eval"))
+
+
+@dataclass
+class ModelConfig:
+    """The top-level fields of arch.ArchConfig that size and place MoE blocks."""
+
+    name: str
+    model_dim: int
+    seq_len: int
+    mlp_mult: float
+    block_scales: bool
+    parallel_residual: bool
+    batch_tokens: int
+    blocks: list
+
+
+def _strip_json_comments(text: str) -> str:
+    """arch/config_load.go stripJSONComments: drop // line comments outside
+    strings (JSONC)."""
+    out, in_str, esc, i = [], False, False, 0
+    while i < len(text):
+        c = text[i]
+        if in_str:
+            out.append(c)
+            if esc:
+                esc = False
+            elif c == "\\":
+                esc = True
+            elif c == '"':
+                in_str = False
+        elif c == '"':
+            in_str = True
+            out.append(c)
+        elif c == "/" and text[i + 1:i + 2] == "/":
+            while i < len(text) and text[i] != "\n":
+                i += 1
+            continue
+        else:
+            out.append(c)
+        i += 1
+    return "".join(out)
+
+
+def parse_model_config(text: str, source: str = "config") -> ModelConfig:
+    """The part of ParseArchConfig (arch/config_load.go:98-136, comments per
+    stripJSONComments at :49-92) this path
+    needs: JSONC comments stripped, unknown top-level keys rejected with the
+    reference's wording, then each MoE block validated
+    (arch/config_validate.go:519-556).  Other block kinds are returned
+    unvalidated; the nested objects (training, data, ...) are not checked."""
+    try:
+        raw = json.loads(_strip_json_comments(text))
+    except json.JSONDecodeError as err:
+        raise ConfigError(f'parse config "{source}": {err}') from None
+    if not isinstance(raw, dict):
+        raise ConfigError(f'parse config "{source}": top level is not an object')
+    for key in raw:
+        if key not in ARCH_CONFIG_FIELDS:
+            raise ConfigError(f'parse config "{source}": json: unknown field "{key}" '
+                              "(check field names against docs/config-reference.md)")
+    blocks = [BlockSpec.from_dict(b) for b in raw.get("blocks", [])]
+    for i, b in enumerate(blocks):
+        validate_moe_block(b, source=source, idx=i)
+    training = raw.get("training") or {}
+    return ModelConfig(name=str(raw.get("name", "")), model_dim=int(raw.get("model_dim", 0)),
+                       seq_len=int(raw.get("seq_len", 0)),
+                       mlp_mult=float(raw.get("mlp_mult", 0.0)),
+                       block_scales=bool(raw.get("block_scales", False)),
+                       parallel_residual=bool(raw.get("parallel_residual", False)),
+                       batch_tokens=int(training.get("batch_tokens", 0)), blocks=blocks)
 
 
 @dataclass

@@ -78,6 +78,7 @@ def _create(int_params, n_inputs, dtype=_lib.MXM_DTYPE_F32, flags=0, floats=(0.0
     ([1, 4, 64, 3, 2, 0, 64, 0], 11, 1, 16, "int8 weights need bf16 compute"),
     ([1, 4, 96, 3, 2, 0, 64, 0], 11, 2, 16, "multiples of 64"),
     ([1, 4, 3, 3, 2, 0, 4, 0], 11, 7, 0, "compute dtype"),
+    ([32768, 32768, 3, 3, 2, 0, 4, 0], 11, 1, 0, "routed slots exceeds 2147483647"),
 ])
 def test_create_rejects_bad_parameters(int_params, n_inputs, dtype, flags, want):
     handle = _create(int_params, n_inputs, dtype, flags)

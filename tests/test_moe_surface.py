@@ -158,3 +158,96 @@ def test_parse_round_trip():
     raw = {"type": "moe", "num_experts": 8, "top_k": 2, "expert_block": {"type": "swiglu"}}
     spec = moe.parse_moe_block(json.dumps(raw))
     assert spec.num_experts == 8 and spec.expert_block.type == "swiglu"
+
+
+# ---- parallel-residual follower, residual scale init, config loading ----
+
+def test_parallel_residual_follower_omits_norm_scale():
+    """arch/moe_test.go:160-198 and arch/weight_shapes.go:498-551: the second
+    block of a parallel-residual pair drops moe_norm_scale; the first keeps
+    it, and the counts follow (arch/parallel_residual.go:242-264)."""
+    spec = _block('{"type":"moe","num_experts":2,"top_k":1}')
+    lead = moe.moe_parallel_weight_shapes(spec, False, 32)
+    follow = moe.moe_parallel_weight_shapes(spec, True, 32)
+    assert lead[0].name == "moe_norm_scale"
+    assert "moe_norm_scale" not in [m.name for m in follow]
+    assert [m.name for m in follow] == [m.name for m in lead[1:]]
+    for scales in (False, True):
+        assert moe.moe_parallel_weight_count(spec, True, scales) == len(
+            moe.moe_parallel_weight_shapes(spec, True, 32, block_scales=scales))
+        assert moe.moe_parallel_weight_count(spec, False, scales) == len(
+            moe.moe_parallel_weight_shapes(spec, False, 32, block_scales=scales))
+    # the follower's metas still end with moe_scale under block scales
+    assert moe.moe_parallel_weight_shapes(spec, True, 32, block_scales=True)[-1].name == "moe_scale"
+
+
+@pytest.mark.parametrize("body,one,zero,value", [
+    ('{"type":"moe","num_experts":2}', True, False, 0.0),
+    ('{"type":"moe","num_experts":2,"residual_scale_init":0}', False, True, 0.0),
+    ('{"type":"moe","num_experts":2,"residual_scale_init":0.1}', False, False,
+     float(__import__("numpy").float32(0.1))),
+])
+def test_moe_scale_follows_residual_scale_init(body, one, zero, value):
+    """arch/weight_shapes.go:75-87: moe_scale inits to 1, to zero for an
+    explicit 0, else to the given value as fp32."""
+    meta = moe.moe_weight_shapes(_block(body), 16, block_scales=True)[-1]
+    assert meta.name == "moe_scale" and meta.shape == [16]
+    assert (meta.init_one, meta.init_zero, meta.init_value) == (one, zero, value)
+
+
+MOE_TINY = """{
+  "name": "moe-tiny",
+  "model_dim": 64,
+  "vocab_size": 1024,
+  "seq_len": 128,
+  "mlp_mult": 2.0,
+  // a JSONC comment, as stripJSONComments allows
+  "blocks": [
+    {"type": "plain", "heads": 4},
+    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"},
+     "router": "linear", "load_balance_loss_weight": 0.01},
+    {"type": "plain", "heads": 4},
+    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"}}
+  ],
+  "training": {"steps": 200, "lr": 0.0003, "batch_tokens": 1024, "grad_clip": 1.0,
+               "weight_decay": 0.01}
+}"""
+
+
+def test_parse_model_config_moe_tiny():
+    """examples/moe_tiny.json: two MoE blocks of D 64, F = ffnDim(64, 2.0) =
+    128, 4 experts, top-2; 1024 tokens per step."""
+    cfg = moe.parse_model_config(MOE_TINY, "moe_tiny.json")
+    assert (cfg.model_dim, cfg.seq_len, cfg.batch_tokens, cfg.mlp_mult) == (64, 128, 1024, 2.0)
+    blocks = [b for b in cfg.blocks if moe.block_type_key(b) == "moe"]
+    assert len(blocks) == 2
+    assert moe.ffn_dim(cfg.model_dim, cfg.mlp_mult) == 128
+    assert [moe.effective_moe_load_balance_loss_weight(b) for b in blocks] == [0.01, 0.01]
+
+
+def test_parse_model_config_rejects_unknown_top_level_field():
+    """arch/config_test.go:934-943 (TestUnknownFieldRejected)."""
+    bad = MOE_TINY.replace('"seq_len": 128,', '"seq_len": 128, "bogus_field": true,')
+    with pytest.raises(ConfigError, match='parse config "t": json: unknown field "bogus_field"'):
+        moe.parse_model_config(bad, "t")
+
+
+def test_unknown_block_keys_are_ignored_like_the_reference():
+    """Inside a block the reference does not reject unknown keys: BlockSpec's
+    own UnmarshalJSON (arch/config.go:229-249) re-decodes with a plain
+    json.Unmarshal, which the outer DisallowUnknownFields does not reach.  A
+    misspelled MoE key therefore falls back to its default, as there."""
+    cfg = moe.parse_model_config(MOE_TINY.replace('"top_k": 2, "expert_block": {"type": "swiglu"}}',
+                                                  '"topk": 3, "expert_block": {"type": "swiglu"}}'))
+    spec = cfg.blocks[3]
+    assert spec.extra == {"topk": 3}
+    assert moe.effective_moe_top_k(spec) == 2
+
+
+def test_parse_model_config_validates_moe_blocks():
+    bad = MOE_TINY.replace('"num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"},\n'
+                           '     "router": "linear"',
+                           '"num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"},\n'
+                           '     "router": "hash"')
+    with pytest.raises(ConfigError, match=r'blocks\[1\] type=moe has invalid router="hash"'):
+        moe.parse_model_config(bad, "t")
