@@ -171,6 +171,13 @@ def test_hf_moe_errors():
     bad = moe.BlockSpec(type="moe", num_experts=1, top_k=1, expert_block=moe.BlockSpec(type="conv"))
     with pytest.raises(CheckpointError, match="unsupported HF export moe expert type 'conv'"):
         hf_moe_weight_map(0, bad, metas)
+    # block scales: moe_scale has no HF name, so the map stops short of the
+    # block's metas and the export fails (train/export_hf.go:733-735)
+    scaled = moe.moe_weight_shapes(spec, 8, 4.0, block_scales=True)
+    assert scaled[-1].name == "moe_scale"
+    with pytest.raises(CheckpointError, match="did not consume all weights: next_unmapped=10 "
+                                              "total=11"):
+        hf_moe_weight_map(0, spec, scaled, first_index=2)
 
 
 def test_hf_export_round_trip(tmp_path):
