@@ -263,6 +263,7 @@ class MoEBlock:
         self.metas = moe_weight_shapes(spec, D, mlp_mult, block_scales)
         self.block_scales = block_scales
         self.bf16 = compute_dtype in ("bf16", "bfloat16")
+        self._int8 = bool(flags & _lib.MXM_FLAG_INT8_WEIGHTS)
         self.op = MoEFeedForward.from_op(ff, compute_dtype=compute_dtype, flags=flags)
         self.norm_scale = None
         self.moe_scale = None
@@ -291,6 +292,28 @@ class MoEBlock:
         w{first_index + i}_{meta name}, train/import.go:71-89)."""
         from .weights import load_weights
         self.set_weights(load_weights(path, self.metas, first_index))
+
+    def load_quantized(self, path: str, first_index: int = 0) -> None:
+        """Bind the block's weights from a checkpoint the reference's quantized
+        export wrote (train/export.go:203-352: I8 matrices with per-row F32
+        scales, small and 1-D tensors F32).  The block's op must use int8
+        weights (MXM_FLAG_INT8_WEIGHTS): each expert matrix goes to the
+        executor in its per-output-channel form (requantised from the
+        dequantised values); the router, norm and moe_scale are bound as
+        their dequantised values."""
+        from .weights import QuantizedWeight, load_quantized_weights, quantize_per_channel
+        if self.op.info()["mfma"] or not self._int8:
+            raise ValueError("load_quantized needs a block created with int8 expert weights")
+        got = load_quantized_weights(path, self.metas, first_index)
+        dense = [g.dequantize() if isinstance(g, QuantizedWeight) else g for g in got]
+        self.norm_scale = self._conv(dense[0])
+        self.op.set_input(1, self._conv(dense[1]))
+        n_exp = len(self.metas) - 2 - (1 if self.block_scales else 0)
+        for i in range(n_exp):
+            g = got[2 + i]
+            q, sc = g.per_channel() if isinstance(g, QuantizedWeight) else quantize_per_channel(g)
+            self.op.set_input_q8(2 + i, q, sc)
+        self.moe_scale = self._conv(dense[-1]) if self.block_scales else None
 
     def forward_host(self, x: np.ndarray):
         """x [B*T, D] (fp32, or bf16 bits) -> (x + delta [B*T, D] fp32,

@@ -9,6 +9,27 @@ from mixlab_amd import _lib
 from mixlab_amd.workloads import bf16_bits
 
 
+# examples/moe_tiny.json of the reference (two MoE blocks: D 64, mlp_mult 2.0,
+# 4 experts, top-2; 1024 tokens per step), with one JSONC comment added
+MOE_TINY = """{
+  "name": "moe-tiny",
+  "model_dim": 64,
+  "vocab_size": 1024,
+  "seq_len": 128,
+  "mlp_mult": 2.0,
+  // a JSONC comment, as stripJSONComments allows
+  "blocks": [
+    {"type": "plain", "heads": 4},
+    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"},
+     "router": "linear", "load_balance_loss_weight": 0.01},
+    {"type": "plain", "heads": 4},
+    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"}}
+  ],
+  "training": {"steps": 200, "lr": 0.0003, "batch_tokens": 1024, "grad_clip": 1.0,
+               "weight_decay": 0.01}
+}"""
+
+
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -9,6 +9,7 @@ import pytest
 
 from mixlab_amd import moe
 from mixlab_amd.moe import BlockSpec, ConfigError
+from tests.moe_testutil import MOE_TINY
 
 
 def _block(body: str) -> BlockSpec:
@@ -195,23 +196,7 @@ def test_moe_scale_follows_residual_scale_init(body, one, zero, value):
     assert (meta.init_one, meta.init_zero, meta.init_value) == (one, zero, value)
 
 
-MOE_TINY = """{
-  "name": "moe-tiny",
-  "model_dim": 64,
-  "vocab_size": 1024,
-  "seq_len": 128,
-  "mlp_mult": 2.0,
-  // a JSONC comment, as stripJSONComments allows
-  "blocks": [
-    {"type": "plain", "heads": 4},
-    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"},
-     "router": "linear", "load_balance_loss_weight": 0.01},
-    {"type": "plain", "heads": 4},
-    {"type": "moe", "num_experts": 4, "top_k": 2, "expert_block": {"type": "swiglu"}}
-  ],
-  "training": {"steps": 200, "lr": 0.0003, "batch_tokens": 1024, "grad_clip": 1.0,
-               "weight_decay": 0.01}
-}"""
+
 
 
 def test_parse_model_config_moe_tiny():
