@@ -68,18 +68,15 @@ struct DevBuf {
   T* as() const { return static_cast<T*>(p); }
 };
 
-bool hidden_is_bf16(int etype, int act) {
-  if (etype == MXM_EXPERT_SWIGLU) return true;
-  if (etype == MXM_EXPERT_GEGLU) return false;
-  return act == MXM_ACT_SILU || act == MXM_ACT_RELU;
-}
-
 struct MoeOp {
   // op parameters (arch/ir.go:697)
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
   float slope = 0.0f;
   int N = 0, wpe = 0, n_inputs = 0;
   bool bf16 = false, mfma = false, debug_probs = false, q8 = false;
+  // MFMA / int8 families with a kind whose hidden is fp32 in the bf16 flow:
+  // H holds two bf16 planes [N*K][2F] and Y is fp32 (GemmArgs::h_split)
+  bool hsplit = false;
   int family = MXM_TILE_AUTO;
   hipStream_t stream = nullptr;
 
@@ -176,7 +173,7 @@ void alloc_workspace(MoeOp& o) {
     o.bm1 = o.bm2 = 256;  // tile schedules are not used by the int8 kernels
   } else if (o.mfma) {
     o.bm1 = mxm_mfma_tile_rows(glu ? 2 * o.F : o.F, o.D, o.family);
-    o.bm2 = mxm_mfma_tile_rows(o.D, o.F, o.family);
+    o.bm2 = mxm_mfma_tile_rows(o.D, o.hsplit ? 2 * o.F : o.F, o.family);
   } else {
     o.bm1 = o.bm2 = mxm_simt_bm();
   }
@@ -209,8 +206,8 @@ void alloc_workspace(MoeOp& o) {
   A(o.scan_ticket, 4);
   HIPCK(hipMemsetAsync(o.scan_ticket.p, 0, 4, o.stream));
   const size_t esz = (o.mfma || o.q8) ? 2 : 4;
-  A(o.H, NK * (size_t)o.F * esz);
-  A(o.Y, NK * (size_t)o.D * esz);
+  A(o.H, NK * (size_t)o.F * esz * (o.hsplit ? 2 : 1));
+  A(o.Y, NK * (size_t)o.D * (o.hsplit ? 4 : esz));
   if (o.debug_probs) A(o.probs, N * E * 4);
   if (o.small_route) {
     A(o.logits, N * E * 4);  // probabilities when no caller copy is kept
@@ -424,14 +421,16 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g2.offsets = sa.offsets;
   g2.mstart = sa.mstart2;
   g2.E = o.E;
-  g2.Kd = o.F;
+  // the split MFMA down projection reduces over both planes of H
+  g2.Kd = (o.hsplit && o.mfma) ? 2 * o.F : o.F;
+  g2.h_split = o.hsplit;
   g2.Ncols = o.D;
   g2.max_mtiles = o.max_mtiles2;
   g2.family = o.family;
   g2.expert_type = o.etype;
   g2.activation = o.act;
   g2.slope = o.slope;
-  g2.y_bf16 = o.bf16 && hidden_is_bf16(o.etype, o.act);
+  g2.y_bf16 = o.bf16 && mxm_hidden_is_bf16(o.etype, o.act);
   g2.rows_total = o.N * o.K;
   if (o.q8) {
     g2.b0 = o.q2.p;
@@ -463,7 +462,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     ca.rscale = blk->moe_scale;
     ca.rscale_bf16 = blk->scale_bf16;
   }
-  for (int rep = 0; rep < reps; ++rep) mxm_launch_combine(ca, o.mfma || o.q8, st);
+  for (int rep = 0; rep < reps; ++rep) mxm_launch_combine(ca, (o.mfma || o.q8) && !o.hsplit, st);
   HIPCK(hipGetLastError());
   mark(6);
 }
@@ -711,6 +710,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
       o->mfma = false;
     }
     o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
+    o->hsplit = (o->mfma || o->q8) && !mxm_hidden_is_bf16(o->etype, o->act);
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
@@ -923,10 +923,11 @@ void check_blas(rocblas_status st, const char* what) {
 // dst[rows][C] (row-major, fp32) = A^T B over `rows`, A [rows][M], B [rows][C]
 // bf16 row-major (rocBLAS is column-major: dst^T = B^T A).
 void gemm_at_b(rocblas_handle h, const uint16_t* A, int M, const uint16_t* B, int C, int rows,
-               float* dst) {
-  const float one = 1.0f, zero = 0.0f;
+               float* dst, int lda = 0, float beta = 0.0f) {
+  const float one = 1.0f;
   check_blas(rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, C, M, rows, &one,
-                             B, rocblas_datatype_bf16_r, C, A, rocblas_datatype_bf16_r, M, &zero, dst,
+                             B, rocblas_datatype_bf16_r, C, A, rocblas_datatype_bf16_r,
+                             lda > 0 ? lda : M, &beta, dst,
                              rocblas_datatype_f32_r, C, dst, rocblas_datatype_f32_r, C,
                              rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
              "weight-gradient GEMM");
@@ -1024,8 +1025,14 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     // gate|up (interleaved, GLU) or up (MLP): [D][NC] = Xp^T dGU
     gemm_at_b(o.bw_blas, xpb + off * D, D, dgub + off * NC, NC, rows,
               glu ? w1g + (size_t)e * D * NC : dwe);
-    // down: [F][D] = H^T dY
-    gemm_at_b(o.bw_blas, hb + off * F, F, dyb + off * D, D, rows, dwe + (glu ? 2 : 1) * DF);
+    // down: [F][D] = H^T dY (a split hidden: hi^T dY + lo^T dY)
+    float* dwd = dwe + (glu ? 2 : 1) * DF;
+    if (o.hsplit) {
+      gemm_at_b(o.bw_blas, hb + off * 2 * F, F, dyb + off * D, D, rows, dwd, 2 * F);
+      gemm_at_b(o.bw_blas, hb + off * 2 * F + F, F, dyb + off * D, D, rows, dwd, 2 * F, 1.0f);
+    } else {
+      gemm_at_b(o.bw_blas, hb + off * F, F, dyb + off * D, D, rows, dwd);
+    }
     off += (size_t)rows;
   }
   if (glu) mxm_launch_deinterleave(w1g, E, D, F, dw, stride, st);
@@ -1225,7 +1232,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.xcast.p;
   if (o.bf16) {
     mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
-    if (o.mfma) {
+    if (o.mfma && !o.hsplit) {  // (a split hidden's y is fp32 already)
       if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
       mxm_launch_to_f32(o.Y.p, MXM_DTYPE_BF16, o.bw_y32.as<float>(), (int64_t)(NK * D), o.stream);
       y32 = o.bw_y32.as<float>();

@@ -392,6 +392,7 @@ __global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16
 __global__ void act_fwd_bf16_kernel(const uint16_t* __restrict__ gu, int F, int etype, int act,
                                     float slope, size_t total8, uint16_t* __restrict__ h) {
   const bool glu = etype != MXM_EXPERT_MLP;
+  const bool split = !mxm_hidden_is_bf16(etype, act);
   const int NC = glu ? 2 * F : F;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total8;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -409,7 +410,7 @@ __global__ void act_fwd_bf16_kernel(const uint16_t* __restrict__ gu, int F, int 
       gw[2] = gv.z;
       gw[3] = gv.w;
     }
-    uint32_t o[4];
+    uint32_t o[4], ol[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float h0 = mxm_hidden_fast<true>(etype, act, slope, mxm_u2f(gw[q] << 16),
@@ -417,8 +418,16 @@ __global__ void act_fwd_bf16_kernel(const uint16_t* __restrict__ gu, int F, int 
       const float h1 = mxm_hidden_fast<true>(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u),
                                              mxm_u2f(uw[q] & 0xffff0000u));
       o[q] = mxm_pack_bf2_fast(h0, h1);
+      ol[q] = mxm_pack_bf2_fast(h0 - mxm_rbf_fast(h0), h1 - mxm_rbf_fast(h1));
     }
-    *reinterpret_cast<uint4*>(h + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+    if (split) {
+      // the two planes of an fp32 hidden: hi at r*2F + f, lo at r*2F + F + f
+      uint16_t* hr = h + r * 2 * F + f;
+      *reinterpret_cast<uint4*>(hr) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(hr + F) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+    } else {
+      *reinterpret_cast<uint4*>(h + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 

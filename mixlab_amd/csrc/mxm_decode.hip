@@ -19,6 +19,12 @@
 // an integer in [0, 255], which bf16 holds exactly; the +128 offset is
 // removed after the loop with the rows' sums (an MFMA against ones).
 //
+// Split hidden (kinds whose hidden is fp32 in the bf16 flow, GemmArgs::
+// h_split): the up projection stores H as the planes hi | lo, and the down
+// projection stages a pass's 16 rows twice -- row group 0 from the hi
+// plane, row group 1 from the lo plane -- so each converted weight block
+// feeds both, and y = (hi . W + lo . W) * scale is stored in fp32.
+//
 // Work split: a workgroup = NW waves = NW consecutive column blocks of one
 // expert.  Each wave requests the first P blocks of its weight stream, the
 // workgroup stages 16 of the expert's rows (all Kd) in LDS, and each wave
@@ -71,6 +77,10 @@ __device__ __forceinline__ int clamp_kb(int kb, int kblocks) {
 template <int EPI, int P, int RG>
 __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
   constexpr int MODE = Epi<EPI>::MODE;
+  constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // up: store H as hi | lo planes
+  constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // down: row group = plane, y fp32
+  static_assert(!DOWN_SPLIT || RG == 2, "the split down projection stages both planes");
+  constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 16 : 16 * RG;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
   constexpr int ASZ = MAX_KD / 64 * 2 * 64;  // pieces of one row group
   // A rows of the current pass, per row group: [kb][half][lane] 16-byte
@@ -103,6 +113,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
   }
   const uint16_t* X = static_cast<const uint16_t*>(a.a);
+  const size_t ldx = DOWN_SPLIT ? 2 * (size_t)Kd : (size_t)Kd;  // A row stride
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
@@ -119,15 +130,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   // staged, so HBM is busy from the workgroup's start
   if (active) prologue();
 
-  for (int rc = 0; rc < count; rc += 16 * RG) {
+  for (int rc = 0; rc < count; rc += ROWS_PER_PASS) {
     __syncthreads();  // the previous pass has finished reading ash
     for (int i = tid; i < 16 * RG * pieces; i += NW * 64) {
       const int r = i / pieces, c8 = i - r * pieces;
+      // staged row r: row group r / 16 (the plane, when split), row r % 16
+      const int rr = DOWN_SPLIT ? (r & 15) : r;
+      const int col0 = DOWN_SPLIT ? (r >> 4) * Kd : 0;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-      if (rc + r < count) {
-        const int p = row_begin + rc + r;
+      if (rc + rr < count) {
+        const int p = row_begin + rc + rr;
         const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
-        v = *reinterpret_cast<const u32x4_t*>(X + (size_t)src * Kd + 8 * c8);
+        v = *reinterpret_cast<const u32x4_t*>(X + (size_t)src * ldx + col0 + 8 * c8);
       }
       ash[(r >> 4) * ASZ + ((c8 >> 3) * 2 + (c8 & 1)) * 64 + ((c8 >> 1) & 3) * 16 + (r & 15)] = v;
     }
@@ -179,6 +193,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 #undef MXM_Q8_STEP
 
     // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
+    if constexpr (DOWN_SPLIT) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = rc + 4 * g + i;
+        if (r >= count) continue;
+        const float hi = acc[0][0][i] - 128.0f * rs[0][i];
+        const float lo = acc[1][0][i] - 128.0f * rs[1][i];
+        static_cast<float*>(a.out)[(size_t)(row_begin + r) * NC + c] = (hi + lo) * sc[0];
+      }
+      continue;
+    }
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
@@ -197,7 +222,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       } else {
         out = v[0];
       }
-      static_cast<uint16_t*>(a.out)[(size_t)(row_begin + r) * NC + c] = mxm_f2bf_fast(out);
+      uint16_t* H = static_cast<uint16_t*>(a.out);
+      if constexpr (H_SPLIT) {
+        const size_t o = (size_t)(row_begin + r) * (2 * NC) + c;
+        const float hi = mxm_rbf_fast(out);
+        H[o] = mxm_f2bf_fast(hi);
+        H[o + NC] = mxm_f2bf_fast(out - hi);
+      } else {
+        H[(size_t)(row_begin + r) * NC + c] = mxm_f2bf_fast(out);
+      }
     }
   }
 }
@@ -245,7 +278,10 @@ int mxm_q8_max_kd() { return MAX_KD; }
 
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
   if (a.mode == MXM_GEMM_DOWN) {
-    launch_epi<EPI_DOWN>(a, s);
+    if (a.h_split)
+      launch_q8<EPI_DOWN_F32, MXM_Q8_DEPTH_ONE, 2>(a, s);
+    else
+      launch_epi<EPI_DOWN>(a, s);
     return;
   }
   switch (mxm_epi_kind(a.expert_type, a.activation)) {

@@ -163,6 +163,8 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
                                                                             int ngroups,
                                                                             int nblocks) {
   constexpr int MODE = Epi<EPI>::MODE;
+  constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // A = [hi | lo] planes, y in fp32
+  constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // H stored as [hi | lo] planes
   constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN;
   constexpr int A_CH = TL::A_CH, BUF = TL::BUF;
   constexpr int NW = NT / 64;
@@ -199,8 +201,11 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   const int wm = wave / WN, wn = wave % WN;
 
   const uint16_t* __restrict__ A = static_cast<const uint16_t*>(a.a);
+  // B rows hold Kb k values; the split down projection reads W_down [D][F]
+  // twice along its reduction over the hi and lo planes (k wraps at F)
+  const int Kb = DOWN_SPLIT ? Kd / 2 : Kd;
   const uint16_t* __restrict__ B =
-      static_cast<const uint16_t*>(a.b0) + (size_t)e * a.Ncols * Kd;
+      static_cast<const uint16_t*>(a.b0) + (size_t)e * a.Ncols * Kb;
 
   // Global->LDS: global_load_lds_dwordx4 writes lane l's 16 bytes to
   // LDS base + 16*l, so one wave-load fills 1 KB = 64/CH consecutive tile
@@ -227,8 +232,8 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
     const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
     aoff[i] = (size_t)src * Kd + lkc * 8;
   }
-  const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kd + lkc * 8;
-  const size_t bstep = (size_t)(NW * RPW) * Kd;
+  const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kb + lkc * 8;
+  const size_t bstep = (size_t)(NW * RPW) * Kb;
 
 // Direct-to-LDS loads Q0 .. Q1-1 of one stage (load q < QA fills A rows,
 // the rest B rows).
@@ -238,7 +243,8 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       if (q_ < QA) {                                                                          \
         dma16(A + aoff[q_] + (K0), STAGE + (wave + NW * q_) * 64);                            \
       } else {                                                                                \
-        dma16(bsrc + (q_ - QA) * bstep + (K0), STAGE + A_CH + (wave + NW * (q_ - QA)) * 64); \
+        dma16(bsrc + (q_ - QA) * bstep + (DOWN_SPLIT && (K0) >= Kb ? (K0) - Kb : (K0)),     \
+              STAGE + A_CH + (wave + NW * (q_ - QA)) * 64);                                   \
       }                                                                                       \
     }                                                                                         \
   } while (0)
@@ -386,6 +392,26 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #undef MXM_COMPUTE
 #undef MXM_KSTEP
 
+  if constexpr (DOWN_SPLIT) {
+    // y in fp32, straight from the accumulators: register r of lane l holds
+    // C[(r/4)*8 + (l/32)*4 + r%4][l%32], so each store instruction writes
+    // 32 consecutive floats of two rows
+    float* __restrict__ yo = static_cast<float*>(a.out);
+    const int ycol = n0 + wn * TN * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = wm * TM * 32 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (lr < rows) {
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            __builtin_nontemporal_store(acc[i][j][r],
+                                        yo + (size_t)(row0 + lr) * a.Ncols + ycol + j * 32);
+        }
+      }
+    continue;
+  }
   // ---- epilogue: activation, bf16, per-wave LDS staging, 16-byte stores ----
   // 32x32 accumulator layout: register r of lane l holds
   // C[(r/4)*8 + (l/32)*4 + r%4][l%32].  Registers r and r+1 (r even) hold two
@@ -415,6 +441,16 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
     }
   };
   const int col = lane & 31;
+  // kinds whose hidden is fp32 store it as two bf16 planes (hi, then lo =
+  // bf16(h - hi)) through the same staging, one plane after the other
+  constexpr int NPLANE = H_SPLIT ? 2 : 1;
+#pragma unroll
+  for (int plane = 0; plane < NPLANE; ++plane) {
+  if (plane > 0) {
+    // this wave's reads of the previous plane's staging are complete
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -429,6 +465,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
             const float gg = mxm_rbf_fast(acc[i][2 * pj][r + q]);
             const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r + q]);
             h[q] = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
+            if (H_SPLIT && plane == 1) h[q] = h[q] - mxm_rbf_fast(h[q]);
           }
           stage[word_at(kp, pj * 32 + col)] = mxm_pack_bf2_fast(h[0], h[1]);
         }
@@ -439,9 +476,11 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
             v[q] = acc[i][j][r + q];
-            if (MODE == MXM_GEMM_MLP)
+            if (MODE == MXM_GEMM_MLP) {
               v[q] = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f,
                                            mxm_rbf_fast(v[q]));
+              if (H_SPLIT && plane == 1) v[q] = v[q] - mxm_rbf_fast(v[q]);
+            }
           }
           stage[word_at(kp, j * 32 + col)] = mxm_pack_bf2_fast(v[0], v[1]);
         }
@@ -453,8 +492,9 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // each lane takes 8 columns of one row pair: two 16-byte chunks, split by
   // byte permutes into the even row's and the odd row's 16-byte segments
-  const int ldo = (MODE == MXM_GEMM_GLU) ? a.Ncols / 2 : a.Ncols;
-  const int c0 = n0 / (MODE == MXM_GEMM_GLU ? 2 : 1) + wn * C;
+  const int hcols = (MODE == MXM_GEMM_GLU) ? a.Ncols / 2 : a.Ncols;  // F (up) or D (down)
+  const int ldo = H_SPLIT ? 2 * hcols : hcols;
+  const int c0 = n0 / (MODE == MXM_GEMM_GLU ? 2 : 1) + wn * C + plane * hcols;
   uint16_t* __restrict__ out = static_cast<uint16_t*>(a.out);
   constexpr int SEGS = C / 8;  // 8-column segments per row pair
 #pragma unroll
@@ -484,6 +524,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       if (grow + 1 < rows) *d1 = hi;
     }
   }
+  }  // plane loop
   }  // tile loop
 }
 
@@ -521,7 +562,10 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
   const int per_group = GM * (a.Ncols / BN);
   const int blocks = ((ngroups + 7) / 8) * 8 * per_group;
   if (a.mode == MXM_GEMM_DOWN) {
-    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
+    if (a.h_split)
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN_F32>(a, s, blocks, ngroups);
+    else
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
     return;
   }
   if (a.mode == MXM_GEMM_RAW) {

@@ -153,12 +153,21 @@ struct GemmArgs {
   bool y_bf16;            // SIMT down: round y to bf16
   int family;             // MFMA tile family (MXM_TILE_*), MXM_TILE_AUTO picks
   int rows_total;         // N*K routed rows (int8 family: picks rows per pass)
+  // Split hidden (MFMA and int8 families, kinds whose hidden is fp32 in the
+  // bf16 flow, !mxm_hidden_is_bf16): the up GEMM stores each fp32 hidden
+  // value h as two bf16 planes of H [rows][2F], hi = bf16(h) in columns
+  // 0..F-1 and lo = bf16(h - hi) in F..2F-1, and the down GEMM (h_split)
+  // reduces over both planes (Kd = 2F for the MFMA family, W_down's k index
+  // wrapping at F) and stores y in fp32 -- the fp32 matmul of the reference
+  // to within 2^-16 relative, since bf16 x bf16 products are exact in fp32.
+  bool h_split;
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
 void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s);
 // MFMA family: bf16 weights stored transposed ([out, in]); GLU gate/up rows
-// interleaved in groups of 32; H and Y are bf16.
+// interleaved in groups of 32; H and Y are bf16 (split hidden: H is the two
+// planes and Y fp32, see GemmArgs::h_split).
 void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s);
 enum { MXM_TILE_AUTO = 0, MXM_TILE_128x128 = 1, MXM_TILE_256x128 = 2, MXM_TILE_256x256 = 3 };
 // Row-tile height the MFMA launcher uses for a GEMM with these dimensions
@@ -169,14 +178,18 @@ int mxm_simt_bm();
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
 // projections, or the plain bf16 store of the down projection.
 enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN,
-       EPI_RAW };
+       EPI_RAW, EPI_DOWN_F32 };
 
 template <int EPI>
 struct Epi {
-  static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
-                              : EPI == EPI_DOWN ? MXM_GEMM_DOWN
-                              : EPI == EPI_RAW  ? MXM_GEMM_RAW
-                                                : MXM_GEMM_MLP;
+  static constexpr int MODE = EPI <= EPI_GEGLU                         ? MXM_GEMM_GLU
+                              : (EPI == EPI_DOWN || EPI == EPI_DOWN_F32) ? MXM_GEMM_DOWN
+                              : EPI == EPI_RAW                          ? MXM_GEMM_RAW
+                                                                        : MXM_GEMM_MLP;
+  // up projections whose hidden is fp32 in the bf16 flow: H in two planes
+  static constexpr bool H_SPLIT = EPI == EPI_GEGLU || EPI == EPI_MLP_GELU || EPI == EPI_MLP_LEAKY;
+  // down projection over the two planes, y stored in fp32
+  static constexpr bool DOWN_SPLIT = EPI == EPI_DOWN_F32;
   static constexpr int ETYPE = EPI == EPI_SWIGLU ? MXM_EXPERT_SWIGLU
                                : EPI == EPI_GEGLU ? MXM_EXPERT_GEGLU
                                                   : MXM_EXPERT_MLP;
@@ -319,7 +332,8 @@ void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int row
 // H [rows, F] (bf16) from the up projections' pre-activation products gu
 // [rows, NC] (mode 3 layout: GLU gate/up interleaved in groups of 32), with
 // the MFMA epilogue's own activation code, so H is the same bits as mode 0/1
-// would store.
+// would store (for kinds with an fp32 hidden, the two planes [rows, 2F] of
+// GemmArgs::h_split).
 void mxm_launch_act_fwd_bf16(const uint16_t* gu, int rows, int F, int etype, int act, float slope,
                              uint16_t* h, hipStream_t s);
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,

@@ -99,6 +99,15 @@ enum {
   MXM_ACT_LEAKY_RELU_SQ = 3,
 };
 
+// Whether the bf16 flow keeps the hidden (and so y) in bf16: MLX promotes
+// it to fp32 for geglu, mlp gelu and mlp leaky_relu_sq, whose float scalar
+// arrays are fp32 (gpu/ir.cpp:1053-1066, 1133-1145).
+MXM_HD bool mxm_hidden_is_bf16(int expert_type, int activation) {
+  if (expert_type == 0) return true;   // swiglu
+  if (expert_type == 1) return false;  // geglu
+  return activation == 0 || activation == 2;  // mlp silu, relu
+}
+
 // Hidden activation h = act(g, u) of one expert row element, following the
 // dtype flow of gpu/ir.cpp:1130-1145 under MLX's promotion rules.
 //   bf16 flow (BF16 = true), g and u are the bf16-rounded projections:

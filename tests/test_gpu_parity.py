@@ -8,6 +8,8 @@ benchmark plan); the exact-order SIMT kernels are additionally bit-exact.
 import numpy as np
 import pytest
 
+import oracle
+
 from mixlab_amd import _lib
 from mixlab_amd.workloads import CONFIGS, bf16_bits, make_workload, round_bf16
 from tests.moe_testutil import (assert_routing_equal, random_case, rel_l2, run_gpu,
@@ -17,6 +19,11 @@ pytestmark = pytest.mark.gpu
 
 FP32_TOL = 1e-5
 BF16_TOL = 2e-2
+# The MFMA kernels against the restatement of the same bf16 dtype flow: only
+# the accumulation order differs (measured 1e-6 to 7e-5 relative L2 over the
+# six expert kinds at 320 tokens, D = F = 256; 1.5e-4 at C2).  A bf16
+# rounding the flow does not make -- e.g. of an fp32 hidden -- is ~2e-3.
+MFMA_TIGHT = 1e-3
 
 
 def _patterned(n, scale):
@@ -115,7 +122,7 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
     if flow.startswith("bf16_mfma"):
         err = rel_l2(delta, want["delta"])
         print(f"{name} bf16 mfma rel L2 = {err:.3e}")
-        assert err <= BF16_TOL
+        assert err <= MFMA_TIGHT
     else:
         assert same_bits(delta, want["delta"])
 
@@ -300,8 +307,16 @@ def test_int8_expert_types(gpu_lib, name, etype, act, slope):
     assert_routing_equal(routing, want)
     assert routing["counts"][5] == 0 and routing["counts"].max() > 48
     err = rel_l2(delta, want["delta"])
-    print(f"int8 {name} rel L2 = {err:.3e}")
+    # the kernels apply the scale in fp32 to the exact q * s; fed those exact
+    # products (not rounded to bf16), the restatement differs from them only
+    # in accumulation order
+    exact = [[(q.astype(np.float32) * s[None, :]).astype(np.float32) for q, s in ws] for ws in q8]
+    want_exact = oracle.moe_forward(x, wr, exact, top_k=K, expert_type=etype, activation=act,
+                                    leaky_slope=slope, bf16=True, prerounded=True)
+    err_exact = rel_l2(delta, want_exact["delta"])
+    print(f"int8 {name} rel L2 = {err:.3e} (bf16(q*s) weights), {err_exact:.3e} (exact q*s)")
     assert err <= BF16_TOL
+    assert err_exact <= MFMA_TIGHT
 
 
 def _block_case(seed, N, D, E, F, bf16, x_fp32_in_bf16_flow=False):
