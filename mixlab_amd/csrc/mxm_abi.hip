@@ -68,6 +68,39 @@ struct DevBuf {
   T* as() const { return static_cast<T*>(p); }
 };
 
+// Every device buffer a forward writes besides its outputs.  layout_workspace
+// places the pieces at 256-byte aligned offsets from one base; the two
+// tickets share the first piece and must be zero between calls (the kernels
+// that take them leave them zero).
+struct Workspace {
+  int32_t* scan_ticket = nullptr;  // [1] scan kernel (N > 1024)
+  int32_t* ticket = nullptr;       // [1] one-launch router (decode sizes)
+  void* xcast = nullptr;           // [N, D] bf16 copy of fp32 x (bf16 compute)
+  int32_t* top_idx = nullptr;      // [N*K]
+  float* gates = nullptr;          // [N*K]
+  int32_t* slot_rank = nullptr;    // [N*K]
+  int32_t* slot_pos = nullptr;     // [N*K]
+  int32_t* perm = nullptr;         // [N*K]
+  int32_t* tile_counts = nullptr;  // [E, ntiles]
+  float* tile_psum = nullptr;      // [E, ntiles]
+  float* tile_ent = nullptr;       // [ntiles]
+  int32_t* tile_base = nullptr;    // [E, ntiles]
+  int32_t* counts = nullptr;       // [E]
+  int32_t* offsets = nullptr;      // [E + 1]
+  int32_t* mstart1 = nullptr;      // [E + 1]
+  int32_t* mstart2 = nullptr;      // [E + 1]
+  float* aux = nullptr;            // [1] when the caller passes none
+  float* ent = nullptr;            // [1]
+  int32_t* expert_count = nullptr; // [E]
+  float* expert_pmean = nullptr;   // [E]
+  void* H = nullptr;               // [N*K, F] (split hidden: [N*K, 2F])
+  void* Y = nullptr;               // [N*K, D]
+  float* probs = nullptr;          // [N, E] (MXM_FLAG_DEBUG_PROBS)
+  float* small_probs = nullptr;    // [N, E] one-launch router's probabilities
+  float* tok_ent = nullptr;        // [N]
+  size_t bytes = 0;
+};
+
 struct MoeOp {
   // op parameters (arch/ir.go:697)
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
@@ -93,13 +126,16 @@ struct MoeOp {
   DevBuf q1, q1b, q2, s1, s1b, s2;
   std::vector<char> have;
 
-  // workspace, sized for N at the first forward
-  bool ws_ready = false;
+  // tile schedule of the forward (set at create from the op's parameters)
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
-  DevBuf xcast, top_idx, gates, slot_rank, slot_pos, perm, tile_counts, tile_psum, tile_ent,
-      tile_base, counts, offsets, mstart1, mstart2, aux, ent, H, Y, probs, logits, tok_ent,
-      ticket, expert_count, expert_pmean, scan_ticket;
+  // the op's own workspace, allocated at the first forward; `last` is the
+  // workspace the latest forward used (the op's own, or the device scratch
+  // of mxm_moe_forward_noalloc), which the routing queries read
+  bool ws_ready = false, have_last = false;
+  DevBuf wsbuf;
+  Workspace ws, last;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
+  DevBuf bw_probs;        // the backward's forward keeps its probabilities here
   // backward (fp32 flow): the experts' projections, gradients and scratch
   bool keep_probs = false, bw_ready = false;
   // set by the fp32 backward around its forward: stop after the routing
@@ -118,7 +154,6 @@ struct MoeOp {
   DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_dw1cat, bw_ms, bw_w2o, bw_w1u;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
-  size_t ws_bytes = 0;
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
   bool profiling = false;
@@ -165,9 +200,11 @@ int fenced(F&& f) {
     return MXM_ERR_OP;                                  \
   }
 
-void alloc_workspace(MoeOp& o) {
-  const size_t N = (size_t)o.N, K = (size_t)o.K, E = (size_t)o.E, NK = N * K;
-  o.ntiles = (int)((N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
+// Row-tile heights and tile counts of the forward's kernels; a function of
+// the op's parameters only.
+void set_schedule(MoeOp& o) {
+  const size_t NK = (size_t)o.N * o.K;
+  o.ntiles = (int)(((size_t)o.N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
   const bool glu = o.etype != MXM_EXPERT_MLP;
   if (o.q8) {
     o.bm1 = o.bm2 = 256;  // tile schedules are not used by the int8 kernels
@@ -179,43 +216,57 @@ void alloc_workspace(MoeOp& o) {
   }
   o.max_mtiles1 = (int)((NK + o.bm1 - 1) / o.bm1) + o.E;
   o.max_mtiles2 = (int)((NK + o.bm2 - 1) / o.bm2) + o.E;
+}
+
+// Place the forward's workspace for op o at base (nullptr: sizes only).
+Workspace layout_workspace(const MoeOp& o, char* base) {
+  const size_t N = (size_t)o.N, K = (size_t)o.K, E = (size_t)o.E, NK = N * K;
   const size_t T = (size_t)o.ntiles;
-  size_t total = 0;
-  auto A = [&](DevBuf& b, size_t bytes) {
-    b.alloc(bytes);
-    total += b.bytes;
+  Workspace w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+    return p;
   };
-  if (o.bf16) A(o.xcast, N * o.D * 2);
-  A(o.top_idx, NK * 4);
-  A(o.gates, NK * 4);
-  A(o.slot_rank, NK * 4);
-  A(o.slot_pos, NK * 4);
-  A(o.perm, NK * 4);
-  A(o.tile_counts, E * T * 4);
-  A(o.tile_psum, E * T * 4);
-  A(o.tile_ent, T * 4);
-  A(o.tile_base, E * T * 4);
-  A(o.counts, E * 4);
-  A(o.offsets, (E + 1) * 4);
-  A(o.mstart1, (E + 1) * 4);
-  A(o.mstart2, (E + 1) * 4);
-  A(o.aux, 4);
-  A(o.ent, 4);
-  A(o.expert_count, E * 4);
-  A(o.expert_pmean, E * 4);
-  A(o.scan_ticket, 4);
-  HIPCK(hipMemsetAsync(o.scan_ticket.p, 0, 4, o.stream));
+  char* tickets = take(8);
+  w.scan_ticket = reinterpret_cast<int32_t*>(tickets);
+  w.ticket = base ? reinterpret_cast<int32_t*>(tickets + 4) : nullptr;
+  if (o.bf16) w.xcast = take(N * o.D * 2);
+  w.top_idx = reinterpret_cast<int32_t*>(take(NK * 4));
+  w.gates = reinterpret_cast<float*>(take(NK * 4));
+  w.slot_rank = reinterpret_cast<int32_t*>(take(NK * 4));
+  w.slot_pos = reinterpret_cast<int32_t*>(take(NK * 4));
+  w.perm = reinterpret_cast<int32_t*>(take(NK * 4));
+  w.tile_counts = reinterpret_cast<int32_t*>(take(E * T * 4));
+  w.tile_psum = reinterpret_cast<float*>(take(E * T * 4));
+  w.tile_ent = reinterpret_cast<float*>(take(T * 4));
+  w.tile_base = reinterpret_cast<int32_t*>(take(E * T * 4));
+  w.counts = reinterpret_cast<int32_t*>(take(E * 4));
+  w.offsets = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  w.mstart1 = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  w.mstart2 = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  w.aux = reinterpret_cast<float*>(take(4));
+  w.ent = reinterpret_cast<float*>(take(4));
+  w.expert_count = reinterpret_cast<int32_t*>(take(E * 4));
+  w.expert_pmean = reinterpret_cast<float*>(take(E * 4));
   const size_t esz = (o.mfma || o.q8) ? 2 : 4;
-  A(o.H, NK * (size_t)o.F * esz * (o.hsplit ? 2 : 1));
-  A(o.Y, NK * (size_t)o.D * (o.hsplit ? 4 : esz));
-  if (o.debug_probs) A(o.probs, N * E * 4);
+  w.H = take(NK * (size_t)o.F * esz * (o.hsplit ? 2 : 1));
+  w.Y = take(NK * (size_t)o.D * (o.hsplit ? 4 : esz));
+  if (o.debug_probs) w.probs = reinterpret_cast<float*>(take(N * E * 4));
   if (o.small_route) {
-    A(o.logits, N * E * 4);  // probabilities when no caller copy is kept
-    A(o.tok_ent, N * 4);
-    A(o.ticket, 4);
-    HIPCK(hipMemsetAsync(o.ticket.p, 0, 4, o.stream));
+    w.small_probs = reinterpret_cast<float*>(take(N * E * 4));
+    w.tok_ent = reinterpret_cast<float*>(take(N * 4));
   }
-  o.ws_bytes = total;
+  w.bytes = off;
+  return w;
+}
+
+void alloc_workspace(MoeOp& o) {
+  const size_t bytes = layout_workspace(o, nullptr).bytes;
+  o.wsbuf.alloc(bytes);
+  o.ws = layout_workspace(o, o.wsbuf.as<char>());
+  HIPCK(hipMemsetAsync(o.ws.scan_ticket, 0, 8, o.stream));  // both tickets
   o.ws_ready = true;
 }
 
@@ -242,23 +293,28 @@ struct BlockIO {
 // pre_out (MFMA family only): also keep the up projections' pre-activation
 // products [N*K, NC] bf16 there (the backward's activation gradient reads
 // them); H is then derived from them with the same activation code.
-void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux, float* ent,
-                 const BlockIO* blk = nullptr, uint16_t* pre_out = nullptr) {
+// w is the workspace the forward writes (the op's own, or the device
+// scratch of the no-allocation entry point); with events = false no
+// profiling events are recorded (they are created on demand).
+void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float* delta, float* aux,
+                 float* ent, const BlockIO* blk = nullptr, uint16_t* pre_out = nullptr,
+                 bool events = true) {
   for (int i = 1; i < o.n_inputs; ++i)
     if (!o.have[i]) fail("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
-  if (!o.ws_ready) alloc_workspace(o);
   hipStream_t st = o.stream;
+  o.last = w;
+  o.have_last = true;
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
-    mxm_launch_to_bf16(x, MXM_DTYPE_F32, o.xcast.as<uint16_t>(), (int64_t)o.N * o.D, st);
-    xin = o.xcast.p;
+    mxm_launch_to_bf16(x, MXM_DTYPE_F32, static_cast<uint16_t*>(w.xcast), (int64_t)o.N * o.D, st);
+    xin = w.xcast;
   } else if ((o.bf16 && x_dtype != MXM_DTYPE_BF16) || (!o.bf16 && x_dtype != MXM_DTYPE_F32)) {
     fail("OP_MOE_FEED_FORWARD unsupported x dtype %d for this compute dtype", x_dtype);
   }
-  float* aux_p = aux ? aux : o.aux.as<float>();
-  float* ent_p = ent ? ent : o.ent.as<float>();
+  float* aux_p = aux ? aux : w.aux;
+  float* ent_p = ent ? ent : w.ent;
   hipEvent_t* evs = nullptr;
-  if (o.profiling) {
+  if (o.profiling && events) {
     if (o.ev_used == o.ev_sets.size()) {
       std::array<hipEvent_t, MXM_NUM_STAGES + 1> set{};
       for (auto& e : set) HIPCK(hipEventCreate(&e));
@@ -275,15 +331,15 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   const int reps = evs ? o.prof_reps : 1;
 
   mark(0);
-  float* probs_keep = (o.debug_probs || o.keep_probs) ? o.probs.as<float>() : nullptr;
+  float* probs_keep = o.keep_probs ? o.bw_probs.as<float>() : w.probs;
   ScanArgs sa{};
-  sa.counts = o.counts.as<int32_t>();
-  sa.offsets = o.offsets.as<int32_t>();
-  sa.mstart1 = o.mstart1.as<int32_t>();
-  sa.mstart2 = o.mstart2.as<int32_t>();
+  sa.counts = w.counts;
+  sa.offsets = w.offsets;
+  sa.mstart1 = w.mstart1;
+  sa.mstart2 = w.mstart2;
   ScatterArgs sc{};
-  sc.perm = o.perm.as<int32_t>();
-  sc.slot_pos = o.slot_pos.as<int32_t>();
+  sc.perm = w.perm;
+  sc.slot_pos = w.slot_pos;
   if (o.small_route) {
     // one launch: router, scan and scatter (stages 1 and 2 are empty)
     RouteSmallArgs rs{};
@@ -296,10 +352,10 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     rs.K = o.K;
     rs.bm1 = o.bm1;
     rs.bm2 = o.bm2;
-    rs.top_idx = o.top_idx.as<int32_t>();
-    rs.gates = o.gates.as<float>();
-    rs.probs = probs_keep ? probs_keep : o.logits.as<float>();
-    rs.tok_ent = o.tok_ent.as<float>();
+    rs.top_idx = w.top_idx;
+    rs.gates = w.gates;
+    rs.probs = probs_keep ? probs_keep : w.small_probs;
+    rs.tok_ent = w.tok_ent;
     rs.counts = sa.counts;
     rs.offsets = sa.offsets;
     rs.mstart1 = sa.mstart1;
@@ -310,7 +366,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     rs.entropy = ent_p;
     rs.aux_weight = blk ? blk->aux_weight : 1.0f;
     rs.aux_scaled = blk ? blk->aux_scaled : nullptr;
-    rs.ticket = o.ticket.as<int32_t>();
+    rs.ticket = w.ticket;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_route_small(rs, o.bf16, st);
     HIPCK(hipGetLastError());
     mark(1);
@@ -323,12 +379,12 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     ra.D = o.D;
     ra.E = o.E;
     ra.K = o.K;
-    ra.top_idx = o.top_idx.as<int32_t>();
-    ra.gates = o.gates.as<float>();
-    ra.slot_rank = o.slot_rank.as<int32_t>();
-    ra.tile_counts = o.tile_counts.as<int32_t>();
-    ra.tile_psum = o.tile_psum.as<float>();
-    ra.tile_ent = o.tile_ent.as<float>();
+    ra.top_idx = w.top_idx;
+    ra.gates = w.gates;
+    ra.slot_rank = w.slot_rank;
+    ra.tile_counts = w.tile_counts;
+    ra.tile_psum = w.tile_psum;
+    ra.tile_ent = w.tile_ent;
     ra.probs_out = probs_keep;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_router(ra, o.bf16, st);
     HIPCK(hipGetLastError());
@@ -343,14 +399,14 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     sa.ntiles = o.ntiles;
     sa.bm1 = o.bm1;
     sa.bm2 = o.bm2;
-    sa.tile_base = o.tile_base.as<int32_t>();
+    sa.tile_base = w.tile_base;
     sa.aux = aux_p;
     sa.entropy = ent_p;
     sa.aux_weight = blk ? blk->aux_weight : 1.0f;
     sa.aux_scaled = blk ? blk->aux_scaled : nullptr;
-    sa.expert_count = o.expert_count.as<int32_t>();
-    sa.expert_pmean = o.expert_pmean.as<float>();
-    sa.ticket = o.scan_ticket.as<int32_t>();
+    sa.expert_count = w.expert_count;
+    sa.expert_pmean = w.expert_pmean;
+    sa.ticket = w.scan_ticket;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_scan(sa, o.bf16, st);
     HIPCK(hipGetLastError());
 
@@ -375,7 +431,7 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   g1.perm = sc.perm;
   g1.b0 = o.w1.p;
   g1.b1 = o.w1b.p;
-  g1.out = o.H.p;
+  g1.out = w.H;
   g1.offsets = sa.offsets;
   g1.mstart = sa.mstart1;
   g1.E = o.E;
@@ -400,8 +456,8 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
     require_operands(g1, false, false);
     for (int rep = 0; rep < reps; ++rep) {
       mxm_launch_gemm_mfma(g1, st);
-      mxm_launch_act_fwd_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope, o.H.as<uint16_t>(),
-                              st);
+      mxm_launch_act_fwd_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope,
+                              static_cast<uint16_t*>(w.H), st);
     }
   } else if (o.mfma) {
     require_operands(g1, false, false);
@@ -415,9 +471,9 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
   mark(4);
   GemmArgs g2{};
   g2.mode = MXM_GEMM_DOWN;
-  g2.a = o.H.p;
+  g2.a = w.H;
   g2.b0 = o.w2.p;
-  g2.out = o.Y.p;
+  g2.out = w.Y;
   g2.offsets = sa.offsets;
   g2.mstart = sa.mstart2;
   g2.E = o.E;
@@ -448,9 +504,9 @@ void run_forward(MoeOp& o, const void* x, int x_dtype, float* delta, float* aux,
 
   mark(5);
   CombineArgs ca{};
-  ca.y = o.Y.p;
-  ca.top_idx = o.top_idx.as<int32_t>();
-  ca.gates = o.gates.as<float>();
+  ca.y = w.Y;
+  ca.top_idx = w.top_idx;
+  ca.gates = w.gates;
   ca.slot_pos = sc.slot_pos;
   ca.N = o.N;
   ca.D = o.D;
@@ -716,6 +772,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K);
+    set_schedule(*o);
     if (o->small_route) {
       o->ldw = (o->D + 3) / 4 * 4;
       o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * 4);
@@ -786,7 +843,8 @@ int mxm_moe_forward(int64_t h, const void* x, int x_dtype, int64_t rows, float* 
   return fenced([&] {
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
     if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
-    run_forward(*op, x, x_dtype, delta, aux, entropy);
+    if (!op->ws_ready) alloc_workspace(*op);
+    run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy);
     return MXM_OK;
   });
 }
@@ -803,10 +861,10 @@ int mxm_moe_forward_host(int64_t h, const void* x, int x_dtype, int64_t rows, fl
     dd.alloc((size_t)op->N * op->D * 4);
     HIPCK(hipMemcpyAsync(dx.p, x, dx.bytes, hipMemcpyHostToDevice, op->stream));
     if (!op->ws_ready) alloc_workspace(*op);
-    run_forward(*op, dx.p, x_dtype, dd.as<float>(), op->aux.as<float>(), op->ent.as<float>());
+    run_forward(*op, op->ws, dx.p, x_dtype, dd.as<float>(), op->ws.aux, op->ws.ent);
     HIPCK(hipMemcpyAsync(delta, dd.p, (size_t)op->N * op->D * 4, hipMemcpyDeviceToHost, op->stream));
-    if (aux) HIPCK(hipMemcpyAsync(aux, op->aux.p, 4, hipMemcpyDeviceToHost, op->stream));
-    if (entropy) HIPCK(hipMemcpyAsync(entropy, op->ent.p, 4, hipMemcpyDeviceToHost, op->stream));
+    if (aux) HIPCK(hipMemcpyAsync(aux, op->ws.aux, 4, hipMemcpyDeviceToHost, op->stream));
+    if (entropy) HIPCK(hipMemcpyAsync(entropy, op->ws.ent, 4, hipMemcpyDeviceToHost, op->stream));
     HIPCK(hipStreamSynchronize(op->stream));
     return MXM_OK;
   });
@@ -846,7 +904,7 @@ void run_block(MoeOp& o, const void* x, int x_dtype, const void* norm_scale, con
   b.scale_bf16 = na.scale_bf16;
   b.aux_weight = aux_weight;
   b.aux_scaled = aux;
-  run_forward(o, o.xn.p, o.bf16 ? MXM_DTYPE_BF16 : MXM_DTYPE_F32, x_out, nullptr, ent, &b);
+  run_forward(o, o.ws, o.xn.p, o.bf16 ? MXM_DTYPE_BF16 : MXM_DTYPE_F32, x_out, nullptr, ent, &b);
 }
 
 int mxm_moe_block_forward(int64_t h, const void* x, int x_dtype, int64_t rows,
@@ -1011,7 +1069,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     check_blas(rocblas_create_handle(&o.bw_blas), "rocblas_create_handle");
   }
   check_blas(rocblas_set_stream(o.bw_blas, st), "rocblas_set_stream");
-  const uint16_t* hb = o.H.as<uint16_t>();
+  const uint16_t* hb = static_cast<const uint16_t*>(o.ws.H);
   float* w1g = glu ? o.bw_dw1cat.as<float>() : nullptr;
   size_t off = 0;
   for (int e = 0; e < E; ++e) {
@@ -1096,7 +1154,7 @@ void run_backward_blas32(MoeOp& o, BackwardArgs& b, bool own_forward) {
       const int r = cnt[e];
       if (r > 0)
         mm(NO, NO, D, r, F, b.w2 + (size_t)e * DF, D, b.h + off * F, F,
-           o.Y.as<float>() + off * D, D);
+           static_cast<float*>(o.ws.Y) + off * D, D);
       off += (size_t)(r > 0 ? r : 0);
     }
   }
@@ -1150,7 +1208,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   if (!o.ws_ready) alloc_workspace(o);
   const size_t N = o.N, D = o.D, E = o.E, F = o.F, NK = (size_t)o.N * o.K;
   const bool mfma_bw = mfma_backward_fits(o);
-  if (!o.probs.p) o.probs.alloc(N * E * 4);
+  if (!o.bw_probs.p) o.bw_probs.alloc(N * E * 4);
   if (!o.bw_ready) {
     o.bw_delta.alloc(N * D * 4);
     o.bw_dy.alloc(NK * D * 4);
@@ -1179,7 +1237,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   const float *w1 = o.w1.as<float>(), *w1b = o.w1b.as<float>(), *w2 = o.w2.as<float>();
   const float* wr = o.router.as<float>();
   const float* x32 = static_cast<const float*>(x);
-  const float* y32 = o.Y.as<float>();
+  const float* y32 = static_cast<const float*>(o.ws.Y);
   if (o.bf16) {
     // The bf16 flow's values (x and weights rounded to bf16, the forward's
     // bf16 expert outputs) in fp32 for the fp32 kernels.
@@ -1222,19 +1280,19 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   o.keep_probs = true;
   o.route_only = own_forward;
   try {
-    run_forward(o, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
+    run_forward(o, o.ws, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
   } catch (...) {
     o.keep_probs = o.route_only = false;
     throw;
   }
   o.keep_probs = o.route_only = false;
   // x as the forward saw it (rounded to bf16 when given in fp32)
-  const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.xcast.p;
+  const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.ws.xcast;
   if (o.bf16) {
     mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
     if (o.mfma && !o.hsplit) {  // (a split hidden's y is fp32 already)
       if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
-      mxm_launch_to_f32(o.Y.p, MXM_DTYPE_BF16, o.bw_y32.as<float>(), (int64_t)(NK * D), o.stream);
+      mxm_launch_to_f32(o.ws.Y, MXM_DTYPE_BF16, o.bw_y32.as<float>(), (int64_t)(NK * D), o.stream);
       y32 = o.bw_y32.as<float>();
     }
     HIPCK(hipGetLastError());
@@ -1250,13 +1308,13 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.wpe = o.wpe;
   b.slope = o.slope;
   b.x = x32;
-  b.top_idx = o.top_idx.as<int32_t>();
-  b.gates = o.gates.as<float>();
-  b.slot_pos = o.slot_pos.as<int32_t>();
-  b.perm = o.perm.as<int32_t>();
-  b.counts = o.counts.as<int32_t>();
-  b.offsets = o.offsets.as<int32_t>();
-  b.probs = o.probs.as<float>();
+  b.top_idx = o.ws.top_idx;
+  b.gates = o.ws.gates;
+  b.slot_pos = o.ws.slot_pos;
+  b.perm = o.ws.perm;
+  b.counts = o.ws.counts;
+  b.offsets = o.ws.offsets;
+  b.probs = o.bw_probs.as<float>();
   b.Y = y32;
   b.wr = wr;
   b.d_delta = d_delta;
@@ -1347,17 +1405,18 @@ int mxm_moe_routing(int64_t h, int32_t* top_idx, float* gates, int32_t* counts, 
                     int32_t* perm, int to_host) {
   OP_OR_RETURN(h);
   return fenced([&] {
-    if (!op->ws_ready) fail("OP_MOE_FEED_FORWARD routing requested before any forward");
+    if (!op->have_last) fail("OP_MOE_FEED_FORWARD routing requested before any forward");
     const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
     const size_t NK = (size_t)op->N * op->K;
-    auto cp = [&](void* dst, const DevBuf& src, size_t bytes) {
-      if (dst) HIPCK(hipMemcpyAsync(dst, src.p, bytes, kind, op->stream));
+    const Workspace& w = op->last;
+    auto cp = [&](void* dst, const void* src, size_t bytes) {
+      if (dst) HIPCK(hipMemcpyAsync(dst, src, bytes, kind, op->stream));
     };
-    cp(top_idx, op->top_idx, NK * 4);
-    cp(gates, op->gates, NK * 4);
-    cp(counts, op->counts, (size_t)op->E * 4);
-    cp(offsets, op->offsets, ((size_t)op->E + 1) * 4);
-    cp(perm, op->perm, NK * 4);
+    cp(top_idx, w.top_idx, NK * 4);
+    cp(gates, w.gates, NK * 4);
+    cp(counts, w.counts, (size_t)op->E * 4);
+    cp(offsets, w.offsets, ((size_t)op->E + 1) * 4);
+    cp(perm, w.perm, NK * 4);
     HIPCK(hipStreamSynchronize(op->stream));
     return MXM_OK;
   });
@@ -1367,8 +1426,8 @@ int mxm_moe_probs(int64_t h, float* probs) {
   OP_OR_RETURN(h);
   return fenced([&] {
     if (!op->debug_probs) fail("OP_MOE_FEED_FORWARD probabilities need MXM_FLAG_DEBUG_PROBS");
-    if (!op->ws_ready) fail("OP_MOE_FEED_FORWARD probabilities requested before any forward");
-    HIPCK(hipMemcpyAsync(probs, op->probs.p, (size_t)op->N * op->E * 4, hipMemcpyDeviceToHost,
+    if (!op->have_last) fail("OP_MOE_FEED_FORWARD probabilities requested before any forward");
+    HIPCK(hipMemcpyAsync(probs, op->last.probs, (size_t)op->N * op->E * 4, hipMemcpyDeviceToHost,
                          op->stream));
     HIPCK(hipStreamSynchronize(op->stream));
     return MXM_OK;
@@ -1411,7 +1470,8 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t vals[4] = {op->q8 ? 2 : op->mfma ? 1 : 0, (int64_t)op->ws_bytes, (int64_t)op->bm1,
+  const int64_t vals[4] = {op->q8 ? 2 : op->mfma ? 1 : 0,
+                           (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM)};
   int w = 0;
   for (; w < n && w < 4; ++w) info[w] = vals[w];
