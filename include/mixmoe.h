@@ -140,6 +140,25 @@ int mxm_moe_forward(int64_t op, const void* x, int x_dtype, int64_t rows, float*
 int mxm_moe_forward_host(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
                          float* aux, float* entropy);
 
+/* Device scratch of mxm_moe_forward_noalloc, per GPU (64 MiB). */
+#define MXM_NOALLOC_MAX_BYTES (64ll << 20)
+
+/* mxm_moe_forward that allocates nothing.  It has no counterpart in the
+ * reference: it is for callers that cannot call hipMalloc -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation.
+ * Every buffer the forward writes besides its outputs (routing, dispatch,
+ * H, Y) lives in one file-scope device array per GPU of
+ * MXM_NOALLOC_MAX_BYTES, held until the process ends; an op whose workspace
+ * is larger is rejected with an error.  Same arguments, kernels and results
+ * as mxm_moe_forward (device pointers, asynchronous on the op's stream).
+ * All calls on one GPU share that array: calls that overlap on one GPU (two
+ * streams, two threads) race; each call leaves it ready for the next.  Call
+ * mxm_init on each device before capturing (it looks up and clears the
+ * array).  After this call mxm_moe_routing reads the array, which the next
+ * no-allocation call on that GPU overwrites. */
+int mxm_moe_forward_noalloc(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
+                            float* aux, float* entropy);
+
 /* The whole MoE block of arch/moe.go:152-213 (emitMoEIR + emitMoEDeltaIR):
  *   xn     = RMSNorm(x, norm_scale, eps)        gpu/ir.cpp:4949-4960 (OP_RMSNORM)
  *   (delta, aux_raw, entropy) = op 74 on xn     gpu/ir.cpp:1073-1164

@@ -25,6 +25,7 @@ MXM_FLAG_MFMA_TILE256x128 = 8
 MXM_FLAG_MFMA_TILE256x256 = 12
 MXM_FLAG_INT8_WEIGHTS = 16
 MXM_NUM_STAGES = 6
+MXM_NOALLOC_MAX_BYTES = 64 << 20
 STAGE_NAMES = ("router", "scan", "scatter", "gemm_up", "gemm_down", "combine")
 
 # name -> (restype, argtypes); every function declared in include/mixmoe.h
@@ -53,6 +54,8 @@ SIGNATURES = {
                                        _VP, _VP]),
     "mxm_moe_forward_host": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64,
                                             _VP, _VP, _VP]),
+    "mxm_moe_forward_noalloc": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int,
+                                               ctypes.c_int64, _VP, _VP, _VP]),
     "mxm_moe_block_forward": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64,
                                              _VP, _VP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _VP, _VP, _VP]),

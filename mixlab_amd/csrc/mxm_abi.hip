@@ -112,6 +112,7 @@ struct MoeOp {
   bool hsplit = false;
   int family = MXM_TILE_AUTO;
   hipStream_t stream = nullptr;
+  int device = 0;  // the device current at create (the stream's)
 
   // weights.  SIMT family: w1 = gate (GLU) or up (MLP) fp32 [E][D][F], w1b =
   // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
@@ -639,6 +640,52 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   o.bw_wbf_ready = false;
 }
 
+// ---- device scratch of the no-allocation forward ----
+// One array per GPU (each device holds its own copy at its own address), kept
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// never device memory: host code uses only the address hipGetSymbolAddress
+// returns for the current device (device_scratch below).
+static __device__ __align__(256) unsigned char scratch[MXM_NOALLOC_MAX_BYTES];
+
+__global__ void zero_words_kernel(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch[kMaxDevices] = {};
+
+// This device's scratch address.  The first call on a device looks it up and
+// clears the tickets (the first 256 bytes of every workspace layout; the
+// kernels leave them zero after each call) with a fill kernel, then waits for
+// the device, so it must not run under stream capture: mxm_init does it
+// before any capture.
+char* device_scratch(hipStream_t capturing) {
+  int dev = 0;
+  HIPCK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) fail("OP_MOE_FEED_FORWARD device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    if (capturing) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      HIPCK(hipStreamIsCapturing(capturing, &cs));
+      if (cs != hipStreamCaptureStatusNone)
+        fail("OP_MOE_FEED_FORWARD no-allocation forward: call mxm_init on device %d before "
+             "capturing",
+             dev);
+    }
+    void* p = nullptr;
+    HIPCK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) fail("OP_MOE_FEED_FORWARD device scratch has no address on device %d", dev);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, nullptr, static_cast<int32_t*>(p),
+                       64);
+    HIPCK(hipGetLastError());
+    HIPCK(hipDeviceSynchronize());
+    g_scratch[dev] = static_cast<char*>(p);
+  }
+  return g_scratch[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -652,9 +699,12 @@ int mxm_init(void) {
     HIPCK(hipGetDevice(&dev));
     hipDeviceProp_t prop;
     HIPCK(hipGetDeviceProperties(&prop, dev));
-    std::lock_guard<std::mutex> lk(g_mu);
-    g_device_name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
-                    std::to_string(prop.multiProcessorCount) + " CUs)";
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      g_device_name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
+                      std::to_string(prop.multiProcessorCount) + " CUs)";
+    }
+    device_scratch(nullptr);  // the no-allocation forward's scratch on this device
     return MXM_OK;
   });
 }
@@ -768,6 +818,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
     o->hsplit = (o->mfma || o->q8) && !mxm_hidden_is_bf16(o->etype, o->act);
     o->have.assign((size_t)n_inputs, 0);
+    HIPCK(hipGetDevice(&o->device));
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
@@ -866,6 +917,28 @@ int mxm_moe_forward_host(int64_t h, const void* x, int x_dtype, int64_t rows, fl
     if (aux) HIPCK(hipMemcpyAsync(aux, op->ws.aux, 4, hipMemcpyDeviceToHost, op->stream));
     if (entropy) HIPCK(hipMemcpyAsync(entropy, op->ws.ent, 4, hipMemcpyDeviceToHost, op->stream));
     HIPCK(hipStreamSynchronize(op->stream));
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_forward_noalloc(int64_t h, const void* x, int x_dtype, int64_t rows, float* delta,
+                            float* aux, float* entropy) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
+    if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
+    int dev = 0;
+    HIPCK(hipGetDevice(&dev));
+    if (dev != op->device)
+      fail("OP_MOE_FEED_FORWARD no-allocation forward called on device %d for an op of device %d",
+           dev, op->device);
+    const size_t need = layout_workspace(*op, nullptr).bytes;
+    if (need > (size_t)MXM_NOALLOC_MAX_BYTES)
+      fail("OP_MOE_FEED_FORWARD no-allocation forward needs %zu bytes of scratch for B*T=%d "
+           "D=%d ffn=%d topK=%d, above the %zu-byte device scratch",
+           need, op->N, op->D, op->F, op->K, (size_t)MXM_NOALLOC_MAX_BYTES);
+    const Workspace w = layout_workspace(*op, device_scratch(op->stream));
+    run_forward(*op, w, x, x_dtype, delta, aux, entropy, nullptr, nullptr, /*events=*/false);
     return MXM_OK;
   });
 }
