@@ -4,9 +4,12 @@
 A step is one forward of the MoE feed-forward op (router, dispatch, grouped
 expert FFN, combine) over the whole batch, with inputs and weights resident
 in HBM.  The headline workload is C4: d_model 2048, 64 experts, top-8, gated
-expert hidden 1024, 65,536 tokens, bf16.  The same run also measures C5, the
-decode shape with int8 expert weights (64 tokens; HBM-bound), and reports it
-under "decode_int8".  Prints one JSON line.
+expert hidden 1024, 65,536 tokens, bf16; `roofline` is its grouped GEMM
+(both launches) against the bf16 MFMA peak.  The same run also measures C2
+and C3 (the near-uniform and the Zipf-ragged MFMA-bound configurations,
+under "configs"), C5, the decode shape with int8 expert weights (64 tokens;
+HBM-bound, under "decode_int8"), the backward on the C2 shape, and the CPU
+baseline.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
 """
@@ -68,15 +71,30 @@ def measured_traffic(workload: str, stage: str, flags: int):
     return None if entry is None else int(entry["fetch_bytes"] + entry["write_bytes"])
 
 
+CPU_RUNS = 5         # timed runs of the CPU baseline after one warm-up (median reported)
+CPU_MIN_TOKENS = 4096  # smallest contiguous token slice timed
+
+
+def gemm_traffic(workload: str, flags: int):
+    """HBM bytes of the grouped GEMM of one forward (both launches)."""
+    up, down = measured_traffic(workload, "gemm_up", flags), measured_traffic(workload,
+                                                                               "gemm_down", flags)
+    return None if up is None or down is None else up + down
+
+
 def cpu_baseline(w, cfg, target_s: float) -> dict:
-    """Time the dense fp32 BLAS restatement of the reference algorithm on a
-    bounded prefix of the same tokens (oracle/dense_blas.py)."""
+    """Time the dense fp32 BLAS restatement of the reference algorithm
+    (oracle/dense_blas.py: every expert on every token, gpu/ir.cpp:1118-1148)
+    on the first n tokens of the same workload: n is at least 4,096 and
+    grows until one run takes about target_s (the whole N if that fits); one
+    warm-up, then the median of 5 runs, scaled to tokens/s (the dense cost is
+    linear in n).  All host cores run the BLAS threads."""
     from threadpoolctl import threadpool_info
 
     from oracle.dense_blas import dense_forward
 
-    cores = max((p.get("num_threads", 1) for p in threadpool_info()
-                 if p.get("user_api") == "blas"), default=1)
+    blas_threads = max((p.get("num_threads", 1) for p in threadpool_info()
+                        if p.get("user_api") == "blas"), default=1)
     mats = {}
 
     def mat(e, j):
@@ -90,21 +108,25 @@ def cpu_baseline(w, cfg, target_s: float) -> dict:
                       cfg.leaky_slope)
         return time.perf_counter() - t0
 
-    n = min(cfg.N, 64)
-    t = run(n)  # warm-up (also converts the weights once)
+    run(min(cfg.N, 64))  # converts the weights once
+    n = min(cfg.N, 256)
     t = run(n)
-    while t < target_s / 4 and n < cfg.N:
-        n = min(cfg.N, n * 4)
-        t = run(n)
-    times = [t] + [run(n) for _ in range(2)]
+    # the run time is linear in n: size the slice for target_s per run
+    n = int(min(cfg.N, max(CPU_MIN_TOKENS, n * target_s / max(t, 1e-6))))
+    n = min(cfg.N, max(CPU_MIN_TOKENS, n // 256 * 256))
+    run(n)  # warm-up at the timed size
+    times = [run(n) for _ in range(CPU_RUNS)]
     med = float(np.median(times))
     blas = next((f"{p.get('internal_api', 'blas')} {p.get('version', '')}".strip()
                  for p in threadpool_info() if p.get("user_api") == "blas"), "BLAS")
-    return {"value": n / med, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+    nproc = os.cpu_count() or 1
+    return {"value": n / med, "unit": "tokens/s", "cores": int(blas_threads), "kind": "port",
+            "nproc": int(nproc), "blas_threads": int(blas_threads), "cpu_model": _cpu_model(),
+            "blas": blas, "runs": CPU_RUNS, "run_s": [round(x, 3) for x in times],
             "sample": (f"first {n} of {cfg.N} tokens, dense fp32 (all {cfg.E} experts on every "
-                       f"token, gpu/ir.cpp:1118-1148) with numpy sgemm ({blas}, {int(cores)} "
-                       f"threads) on {_cpu_model()}; median of 3 runs of {med:.2f} s after "
-                       f"warm-up")}
+                       f"token, gpu/ir.cpp:1118-1148) with numpy sgemm ({blas}, "
+                       f"{int(blas_threads)} threads; nproc {nproc}) on {_cpu_model()}; median "
+                       f"of {CPU_RUNS} runs of {med:.2f} s after one warm-up")}
 
 
 def _cpu_model() -> str:
@@ -117,6 +139,20 @@ def _cpu_model() -> str:
     except OSError:
         pass
     return "unknown CPU"
+
+
+def grouped_gemm_summary(cfg, stages) -> dict:
+    """The grouped GEMM of one forward (gate+up launch, then down launch):
+    algorithmic FLOPs (6 K N D F for a GLU expert, 4 K N D F for an mlp
+    expert; arch/moe.go:215-236) over the two launches' event times."""
+    fl = cfg.flops()
+    up = fl["up"] / (stages["gemm_up"] * 1e-3) / 1e12
+    down = fl["down"] / (stages["gemm_down"] * 1e-3) / 1e12
+    ms = stages["gemm_up"] + stages["gemm_down"]
+    tf = fl["experts"] / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS, "up_tflops": up,
+            "down_tflops": down, "up_frac": up / PEAK_BF16_TFLOPS,
+            "down_frac": down / PEAK_BF16_TFLOPS, "flops": fl["experts"]}
 
 
 def run_config(cfg, steps: int, warmup: int, flags: int = 0, stage_repeats: int = 1):
@@ -264,8 +300,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4", help="C1..C4 (C4 is the headline configuration)")
     ap.add_argument("--flags", type=int, default=0, help="mxm_moe_create flags (include/mixmoe.h)")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+    ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C2 / C3 sections")
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -288,12 +325,8 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     log(f"device: {_lib.device_name()}")
     w, r = run_config(cfg, args.steps, args.warmup, args.flags)
+    gg = grouped_gemm_summary(cfg, r["stages"])
     stages = r["stages"]
-    fl = cfg.flops()
-    up_tflops = fl["up"] / (stages["gemm_up"] * 1e-3) / 1e12
-    down_tflops = fl["down"] / (stages["gemm_down"] * 1e-3) / 1e12
-    gg_ms = stages["gemm_up"] + stages["gemm_down"]
-    gg_tflops = fl["experts"] / (gg_ms * 1e-3) / 1e12
     sb = stage_bytes(cfg)
     hbm = {k: sb[k] / (stages[k] * 1e-3) / 1e9 for k in sb}
 
@@ -313,11 +346,15 @@ def main() -> int:
         xb = c5.N * c5.D * 2
         total = wb["gemm_up"] + wb["gemm_down"] + sum(stage_bytes(c5).values()) + xb
         up_gbs = (wb["gemm_up"] + xb) / (ds["gemm_up"] * 1e-3) / 1e9
+        layer_gbs = total / (d["ms_per_step"] * 1e-3) / 1e9
         decode = {
             "workload": "C5", "tokens": c5.N, "tokens_per_s": d["tokens_per_s"],
             "ms_per_step": d["ms_per_step"],
             "routed_experts": wb["routed_experts"],
-            "hbm_gbs_forward": total / (d["ms_per_step"] * 1e-3) / 1e9,
+            "hbm_gbs_forward": layer_gbs,
+            "layer_roofline": {"bound": "hbm", "kernel": "whole decode forward (all launches)",
+                               "achieved": layer_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                               "frac": layer_gbs / PEAK_HBM_GBS, "traffic": None},
             "roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
                          "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": up_gbs / PEAK_HBM_GBS,
@@ -325,6 +362,23 @@ def main() -> int:
             "gemm_down_gbs": (wb["gemm_down"]) / (ds["gemm_down"] * 1e-3) / 1e9,
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
+
+    # the other MFMA-bound configurations: near-uniform C2 and Zipf-ragged C3
+    extra = {}
+    if not args.no_configs:
+        for name in ("C2", "C3"):
+            if name == cfg.name:
+                continue
+            c = CONFIGS[name]
+            _, rc = run_config(c, args.steps, args.warmup)
+            counts = np.asarray(rc["counts"])
+            extra[name] = {"tokens": c.N, "d_model": c.D, "experts": c.E, "top_k": c.K,
+                           "expert_hidden": c.F, "tokens_per_s": rc["tokens_per_s"],
+                           "ms_per_step": rc["ms_per_step"],
+                           "grouped_gemm": grouped_gemm_summary(c, rc["stages"]),
+                           "stages_ms": {k: v for k, v in rc["stages"].items() if k != "forwards"},
+                           "expert_rows": {"max": int(counts.max()), "min": int(counts.min()),
+                                           "mean": float(counts.mean())}}
 
     backward = backward_bf16 = None
     if not args.no_backward:
@@ -349,14 +403,15 @@ def main() -> int:
                    "top_k": cfg.K, "expert_hidden": cfg.F,
                    "expert": "sigmoid-GLU (swiglu)" if cfg.expert_type == 0 else str(cfg.expert_type),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_up (gate+up grouped GEMM, GLU epilogue)",
-                     "achieved": up_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": up_tflops / PEAK_BF16_TFLOPS,
-                     "traffic": measured_traffic(cfg.name, "gemm_up", args.flags)},
-        "grouped_gemm": {"ms": gg_ms, "tflops": gg_tflops, "frac": gg_tflops / PEAK_BF16_TFLOPS,
-                         "up_tflops": up_tflops, "down_tflops": down_tflops},
+        "roofline": {"bound": "mfma",
+                     "kernel": "gemm_kernel, the grouped GEMM of one forward (gate+up launch "
+                               "with GLU epilogue + down launch)",
+                     "achieved": gg["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gg["frac"], "traffic": gemm_traffic(cfg.name, args.flags)},
+        "grouped_gemm": gg,
         "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
         "hbm_gbs": hbm,
+        "configs": extra,
         "decode_int8": decode,
         "backward_fp32": backward,
         "backward_bf16": backward_bf16,
