@@ -212,6 +212,50 @@ def run_config(cfg, steps: int, warmup: int, flags: int = 0, stage_repeats: int 
                "counts": counts}
 
 
+def vendor_gemm(cfg) -> dict:
+    """The vendor library's dense bf16 GEMM (torch.matmul -> hipBLASLt) on the
+    dense shapes of the grouped GEMM's two launches: [N*K, D] x [D, 2F] (gate
+    and up together) and [N*K, F] x [F, D], every row one expert's, no gather.
+    A reference point for the grouped kernel, not part of the op.  torch
+    carries its own HIP runtime, so this runs in a child process that never
+    loads libmixmoe (bench.py --vendor-gemm-only)."""
+    import subprocess
+
+    res = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-gemm-only",
+                          "--config", cfg.name], capture_output=True, text=True, timeout=600)
+    sys.stderr.write(res.stderr)
+    if res.returncode != 0:
+        raise RuntimeError(f"vendor GEMM child exited with {res.returncode}")
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def vendor_gemm_child(cfg, reps: int = 10) -> int:
+    """--vendor-gemm-only: time torch.matmul on the two dense shapes and print
+    one JSON line (this process loads torch and never libmixmoe)."""
+    import torch
+
+    out = {}
+    M = cfg.N * cfg.K
+    for name, (k, n) in {"gemm_up": (cfg.D, (2 if cfg.wpe == 3 else 1) * cfg.F),
+                         "gemm_down": (cfg.F, cfg.D)}.items():
+        a = torch.randn(M, k, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16)
+        for _ in range(3):
+            c = a @ b
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            c = a @ b
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        tf = 2.0 * M * k * n / (ms * 1e-3) / 1e12
+        out[name] = {"shape": [M, k, n], "ms": ms, "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS}
+        log(f"vendor dense GEMM {name} {M}x{k}x{n}: {ms:.3f} ms, {tf:.1f} TFLOP/s")
+        del a, b, c
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def copy_calibration(mib: int, reps: int = 5) -> int:
     """Copies of a known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this
     run gives the counter-to-bytes factors used for roofline.traffic."""
@@ -303,6 +347,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
     ap.add_argument("--no-configs", action="store_true", help="skip the C2 / C3 sections")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time hipBLASLt (torch.matmul) on the dense equivalents of the "
+                         "grouped GEMM's two launches (in a child process)")
+    ap.add_argument("--vendor-gemm-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -311,6 +359,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.vendor_gemm_only:
+        from mixlab_amd.workloads import CONFIGS
+        return vendor_gemm_child(CONFIGS[args.config])
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -380,6 +431,8 @@ def main() -> int:
                            "expert_rows": {"max": int(counts.max()), "min": int(counts.min()),
                                            "mean": float(counts.mean())}}
 
+    vendor = vendor_gemm(cfg) if args.vendor_gemm else None
+
     backward = backward_bf16 = None
     if not args.no_backward:
         import dataclasses
@@ -412,6 +465,7 @@ def main() -> int:
         "stages_ms": {k: v for k, v in stages.items() if k != "forwards"},
         "hbm_gbs": hbm,
         "configs": extra,
+        "vendor_gemm": vendor,
         "decode_int8": decode,
         "backward_fp32": backward,
         "backward_bf16": backward_bf16,

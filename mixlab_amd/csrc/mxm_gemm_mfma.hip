@@ -444,6 +444,27 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   // kinds whose hidden is fp32 store it as two bf16 planes (hi, then lo =
   // bf16(h - hi)) through the same staging, one plane after the other
   constexpr int NPLANE = H_SPLIT ? 2 : 1;
+  if constexpr (H_SPLIT) {
+    // the fp32 hidden, computed once in place: h overwrites the gate
+    // accumulator (GLU) or the projection's (MLP), which are dead after it
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (MODE == MXM_GEMM_GLU) {
+#pragma unroll
+          for (int pj = 0; pj < TN / 2; ++pj)
+            acc[i][2 * pj][r] = mxm_hidden_fast<true>(
+                Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(acc[i][2 * pj][r]),
+                mxm_rbf_fast(acc[i][2 * pj + 1][r]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j][r] = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f,
+                                                 mxm_rbf_fast(acc[i][j][r]));
+        }
+      }
+  }
 #pragma unroll
   for (int plane = 0; plane < NPLANE; ++plane) {
   if (plane > 0) {
@@ -462,10 +483,14 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
           float h[2];
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            const float gg = mxm_rbf_fast(acc[i][2 * pj][r + q]);
-            const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r + q]);
-            h[q] = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
-            if (H_SPLIT && plane == 1) h[q] = h[q] - mxm_rbf_fast(h[q]);
+            if constexpr (H_SPLIT) {  // h computed above; plane 1 holds h - bf16(h)
+              h[q] = acc[i][2 * pj][r + q];
+              if (plane == 1) h[q] = h[q] - mxm_rbf_fast(h[q]);
+            } else {
+              const float gg = mxm_rbf_fast(acc[i][2 * pj][r + q]);
+              const float u = mxm_rbf_fast(acc[i][2 * pj + 1][r + q]);
+              h[q] = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, gg, u);
+            }
           }
           stage[word_at(kp, pj * 32 + col)] = mxm_pack_bf2_fast(h[0], h[1]);
         }
@@ -476,10 +501,11 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
             v[q] = acc[i][j][r + q];
-            if (MODE == MXM_GEMM_MLP) {
+            if constexpr (H_SPLIT) {  // h computed above
+              if (plane == 1) v[q] = v[q] - mxm_rbf_fast(v[q]);
+            } else if (MODE == MXM_GEMM_MLP) {
               v[q] = mxm_hidden_fast<true>(MXM_EXPERT_MLP, Epi<EPI>::ACT, a.slope, 0.0f,
                                            mxm_rbf_fast(v[q]));
-              if (H_SPLIT && plane == 1) v[q] = v[q] - mxm_rbf_fast(v[q]);
             }
           }
           stage[word_at(kp, j * 32 + col)] = mxm_pack_bf2_fast(v[0], v[1]);
