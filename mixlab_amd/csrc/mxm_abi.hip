@@ -345,7 +345,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     // one launch: router, scan and scatter (stages 1 and 2 are empty)
     RouteSmallArgs rs{};
     rs.x = xin;
-    rs.wr_t = o.router_t.as<float>();
+    rs.wr_t = o.router_t.p;
     rs.ldw = o.ldw;
     rs.N = o.N;
     rs.D = o.D;
@@ -567,8 +567,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
     else
       mxm_launch_to_f32(src, dtype, o.router.as<float>(), (int64_t)n, st);
     if (o.small_route)
-      mxm_launch_router_t(o.router.p, o.bf16 ? MXM_DTYPE_BF16 : MXM_DTYPE_F32, o.D, o.E, o.ldw,
-                          o.router_t.as<float>(), st);
+      mxm_launch_router_t(o.router.p, o.bf16, o.D, o.E, o.ldw, o.router_t.p, st);
   } else if (o.mfma) {
     const bool glu = o.wpe == 3;
     if (j == o.wpe - 1) {
@@ -825,8 +824,8 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
     if (o->small_route) {
-      o->ldw = (o->D + 3) / 4 * 4;
-      o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * 4);
+      o->ldw = (o->D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
+      o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * (o->bf16 ? 2 : 4));
     }
     if (o->q8) {
       o->q1.alloc(EE * DF);

@@ -73,9 +73,10 @@ void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s);
 #define MXM_SMALL_D 16384
 struct RouteSmallArgs {
   const void* x;       // [N, D], bf16 bits or fp32
-  const float* wr_t;   // fp32 [ceil(E/64)][ldw/4][64][4]: element (g, c, l, q) =
-                       // router_w[4c + q][64g + l], zero past D or E
-  int ldw;             // D rounded up to a multiple of 4
+  const void* wr_t;    // the flow's dtype, [ceil(E/64)][ldw/P][64][P] with P = 16 bytes
+                       // of it (4 fp32, 8 bf16): element (g, c, l, q) =
+                       // router_w[Pc + q][64g + l], zero past D or E
+  int ldw;             // D rounded up to a multiple of MXM_LOGIT_CHUNK
   int N, D, E, K;
   int bm1, bm2;        // row-tile heights of the two grouped GEMMs
   int32_t* top_idx;    // [N, K]
@@ -258,7 +259,9 @@ void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n
 // interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up.
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
                                uint16_t* dst, hipStream_t s);
-void mxm_launch_router_t(const void* src, int src_dtype, int D, int E, int ldw, float* dst,
+// The decode router's copy of router_w [D, E] (stored in the flow's dtype:
+// bf16 when bf16, else fp32), in RouteSmallArgs::wr_t's layout.
+void mxm_launch_router_t(const void* src, bool bf16, int D, int E, int ldw, void* dst,
                          hipStream_t s);
 // MFMA-family expert weights back to fp32 x.W layout (backward of bf16 ops).
 void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int slot, float* dst,

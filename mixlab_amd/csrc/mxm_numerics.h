@@ -6,6 +6,10 @@
 // that a C compiler on the host reproduces exactly:
 //   * the library is compiled with -ffp-contract=off; fused multiply-adds are
 //     written as explicit fmaf where intended;
+//   * router logits split d into chunks of MXM_LOGIT_CHUNK from d = 0: each
+//     chunk's partial is an fmaf chain over its d in ascending order from +0,
+//     and the logit is +0 plus the partials added in ascending chunk order
+//     (chunks can be computed in parallel; the additions are sequential);
 //   * exp is not the device libm's: mxm_exp below is Cody & Waite (1980)
 //     argument reduction e^x = 2^n e^r, n = rint(x log2 e), r = x - n ln2
 //     with ln2 split into a 17-bit head and a tail (the split published with
@@ -21,6 +25,9 @@
 #include <stdint.h>
 
 #define MXM_HD __host__ __device__ __forceinline__
+
+// d per chunk of the router logits' summation order (see above)
+#define MXM_LOGIT_CHUNK 64
 
 MXM_HD uint32_t mxm_f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 MXM_HD float mxm_u2f(uint32_t u) { return __builtin_bit_cast(float, u); }

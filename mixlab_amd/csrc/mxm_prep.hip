@@ -66,33 +66,38 @@ void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, in
 
 namespace {
 
-// router_w [D, E] (x.W layout, stored bf16 or fp32) -> fp32 in the decode
-// router's lane-interleaved layout [ceil(E/64)][ldw/4][64][4]: element
-// (g, c, l, q) = router_w[4c + q][64g + l], zero past D or E.  Lane l of the
-// wave for expert group g reads its expert's next four d values as one 16-byte
-// piece, and the 64 lanes' pieces are one contiguous 1 KB line set.  bf16
-// values are exact in fp32.
-__global__ void router_t_kernel(const void* src, int dtype, int D, int E, int ldw, float* dst) {
+// router_w [D, E] (x.W layout, in the flow's dtype T) -> the decode router's
+// lane-interleaved layout [ceil(E/64)][ldw/P][64][P], P = 16 / sizeof(T):
+// element (g, c, l, q) = router_w[Pc + q][64g + l], zero past D or E.  Lane l
+// of a wave for expert group g reads its expert's next P d values as one
+// 16-byte piece, and the 64 lanes' pieces are one contiguous 1 KB line set.
+template <typename T>
+__global__ void router_t_kernel(const T* src, int D, int E, int ldw, T* dst) {
+  constexpr int P = 16 / (int)sizeof(T);
   const int G = (E + 63) / 64;
   const int64_t n = (int64_t)G * ldw * 64;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int q = (int)(i & 3), l = (int)((i >> 2) & 63);
-    const int64_t gc = i >> 8;  // g * (ldw / 4) + c
-    const int c = (int)(gc % (ldw / 4)), g = (int)(gc / (ldw / 4));
-    const int d = 4 * c + q, e = 64 * g + l;
-    dst[i] = (d < D && e < E) ? src_at(src, dtype, (size_t)d * E + e) : 0.0f;
+    const int q = (int)(i % P), l = (int)((i / P) & 63);
+    const int64_t gc = i / (64 * P);  // g * (ldw / P) + c
+    const int c = (int)(gc % (ldw / P)), g = (int)(gc / (ldw / P));
+    const int d = P * c + q, e = 64 * g + l;
+    dst[i] = (d < D && e < E) ? src[(size_t)d * E + e] : T(0);
   }
 }
 
 }  // namespace
 
-void mxm_launch_router_t(const void* src, int src_dtype, int D, int E, int ldw, float* dst,
+void mxm_launch_router_t(const void* src, bool bf16, int D, int E, int ldw, void* dst,
                          hipStream_t s) {
   const int64_t n = (int64_t)((E + 63) / 64) * ldw * 64;
-  if (n > 0)
-    hipLaunchKernelGGL(router_t_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, D, E,
-                       ldw, dst);
+  if (n <= 0) return;
+  if (bf16)
+    hipLaunchKernelGGL(router_t_kernel<uint16_t>, dim3(grid_for(n)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(src), D, E, ldw, static_cast<uint16_t*>(dst));
+  else
+    hipLaunchKernelGGL(router_t_kernel<float>, dim3(grid_for(n)), dim3(256), 0, s,
+                       static_cast<const float*>(src), D, E, ldw, static_cast<float*>(dst));
 }
 
 namespace {

@@ -3,8 +3,9 @@
 // the aux / entropy outputs (gpu/ir.cpp:1150-1162).
 //
 // One workgroup owns a tile of MXM_ROUTER_TM consecutive tokens and all E
-// experts.  Phase 1 is a register-tiled SIMT product: each output logit is
-// accumulated in fp32 by fmaf over d = 0..D-1 in ascending order, which is
+// experts.  Phase 1 is a register-tiled SIMT product in the logits'
+// summation order (mxm_numerics.h): per 64-d chunk of d, a partial by fmaf
+// over the chunk's d ascending from +0, added to the logit in chunk order --
 // the order the CPU restatement uses, so logits are bit-identical.  Phase 2
 // gives each wavefront 16 tokens: one lane per expert (lane l holds experts
 // l, l+64, ...), softmax with a fixed xor-butterfly sum, top-k by K rounds of
@@ -18,6 +19,8 @@
 // router, scan and scatter; see below).  Both kernels run the per-token
 // softmax / top-k / gate code of route_token, so their routing is the same
 // bit for bit.
+#include <type_traits>
+
 #include "mxm_kernels.h"
 
 namespace {
@@ -228,8 +231,15 @@ __global__ __launch_bounds__(NT) void router_kernel(
 #pragma unroll
     for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
 
-  // products of one BK chunk held in LDS
+  // products of one BK chunk held in LDS (BK is the logits' 64-d summation
+  // chunk): a partial from +0, then added to the logit
+  static_assert(BK == MXM_LOGIT_CHUNK, "one LDS chunk per summation chunk");
   auto compute = [&]() {
+    float part[4][EPT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) part[i][j] = 0.0f;
 #pragma unroll 4
     for (int dd = 0; dd < BK; ++dd) {
       const float4 xv = *reinterpret_cast<const float4*>(&xs[dd * TM + ty * 4]);
@@ -238,12 +248,16 @@ __global__ __launch_bounds__(NT) void router_kernel(
       for (int j = 0; j < EPT; ++j) wv[j] = ws[dd * EP + tx * EPT + j];
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
-        acc[0][j] = __builtin_fmaf(xv.x, wv[j], acc[0][j]);
-        acc[1][j] = __builtin_fmaf(xv.y, wv[j], acc[1][j]);
-        acc[2][j] = __builtin_fmaf(xv.z, wv[j], acc[2][j]);
-        acc[3][j] = __builtin_fmaf(xv.w, wv[j], acc[3][j]);
+        part[0][j] = __builtin_fmaf(xv.x, wv[j], part[0][j]);
+        part[1][j] = __builtin_fmaf(xv.y, wv[j], part[1][j]);
+        part[2][j] = __builtin_fmaf(xv.z, wv[j], part[2][j]);
+        part[3][j] = __builtin_fmaf(xv.w, wv[j], part[3][j]);
       }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) acc[i][j] = acc[i][j] + part[i][j];
   };
   if constexpr (VEC) {
     // 16-byte pieces of x (token-fastest across lanes, so the transposed LDS
@@ -421,27 +435,30 @@ __global__ __launch_bounds__(NT) void router_kernel(
 }
 
 // Decode-sized batches: routing in one launch.  Workgroup n owns token n.
-// Its x row is staged in LDS as fp32; wave w < NJ computes the logits of
-// experts 64 w + lane by fmaf over d = 0..D-1 ascending from 0 -- the tiled
-// kernel's accumulation order, so the bits are the same.  The fp32 router
-// weights are stored lane-interleaved (each wave load is 1 KB contiguous,
-// 16 bytes = the next four d of the lane's expert) and stream through a ring
-// of RS_RD register blocks (RS_RD - 1 blocks in flight); x is broadcast from
-// LDS through a ring of RS_XR blocks.  Wave 0 then runs route_token and writes the token's
-// picks, gates, probabilities and entropy term.  Every workgroup then takes a
-// ticket (agent-scope fence, atomic add); the one that takes the last ticket
-// reads all tokens' results back and computes what the scan and scatter
-// kernels compute for larger batches: per-expert counts (LDS histogram),
-// offsets and row-tile prefixes (one wave's scan), aux and entropy, and the
-// stable permutation (per 64-token chunk, the rank of a slot among the
-// chunk's tokens on its expert from a 64-bit token mask, plus the running
-// count of earlier chunks).  It resets the ticket for the next call.  No
-// workgroup waits on another, so the kernel always drains.
-constexpr int RS_NT = 256;
-constexpr int RS_BD = 16;  // d per register block
-constexpr int RS_RD = 8;   // weight blocks in the register ring
-constexpr int RS_XR = 4;   // x blocks in the register ring
-static_assert(RS_RD % RS_XR == 0, "x slots repeat with the weight ring");
+// Its x row is staged in LDS as fp32, zero-padded to whole 64-d chunks.  The
+// logits follow the chunked summation order of mxm_numerics.h, so the bits
+// are those of the tiled kernel: the waves of an expert group (one expert per
+// lane) compute chunk partials in rounds, each an fmaf chain from +0 with x
+// broadcast from LDS, and the group's first wave adds them in chunk order.
+// The router weights are a copy in the flow's dtype, lane-interleaved (each
+// wave load is 1 KB contiguous: 16 bytes = the lane's expert's next 4 or 8 d),
+// and the next pieces are in flight while a chunk is summed.  Wave 0 then
+// runs route_token and writes the token's picks, gates, probabilities and
+// entropy term.  Every workgroup then takes a ticket (wave 0: agent-scope
+// fence, atomic add); the one that takes the last ticket reads all tokens'
+// results back and computes what the scan and scatter kernels compute for
+// larger batches: per-expert counts (LDS histogram), offsets and row-tile
+// prefixes (wave scans), aux and entropy, and the stable permutation (per
+// 64-token chunk, the rank of a slot among the chunk's tokens on its expert
+// from a 64-bit token mask, plus the running count of earlier chunks).  It
+// resets the ticket for the next call.  No workgroup waits on another, so
+// the kernel always drains.
+constexpr int RS_NT = 1024;  // 16 waves: four per SIMD hide the LDS and load latency
+constexpr int RS_WAVES = RS_NT / 64;
+constexpr int RS_RING = 2;   // items in the logits' register ring (128 VGPRs a lane)
+// LDS for a round's chunk partials [RPC][NJ * 64] and, in the last
+// workgroup, the per-wave probability sums [RS_WAVES][MXM_MAX_EXPERTS]
+constexpr int RS_PART_FLOATS = 4096;
 
 __device__ __forceinline__ float rs_wave_sum(float v) {
 #pragma unroll
@@ -450,14 +467,14 @@ __device__ __forceinline__ float rs_wave_sum(float v) {
 }
 
 template <typename TX, bool BF16, int NJ, bool VEC>
-__global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
+__global__ __launch_bounds__(RS_NT, 1) void route_small_kernel(RouteSmallArgs a) {
   extern __shared__ __attribute__((aligned(16))) float rs_dyn[];  // x row, then the slots
   __shared__ float lg[NJ * 64];
+  __shared__ float rs_part[RS_PART_FLOATS];  // a round's chunk partials [RPC][NJ * 64]
   __shared__ __attribute__((aligned(16))) RankScratch rank_scr;
   __shared__ int cnt[MXM_MAX_EXPERTS];
   __shared__ int offs[MXM_MAX_EXPERTS];
   __shared__ int runc[MXM_MAX_EXPERTS];
-  __shared__ float pmean[MXM_MAX_EXPERTS];
   __shared__ uint32_t msk[MXM_MAX_EXPERTS][2];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -480,76 +497,107 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   } else {
     for (int d = tid; d < D; d += RS_NT) xl[d] = ld_as_f32<TX>(xrow + d);
   }
+  // the dispatch's counters (used by the last workgroup only)
+  for (int e = tid; e < E; e += RS_NT) {
+    cnt[e] = 0;
+    runc[e] = 0;
+    msk[e][0] = 0u;
+    msk[e][1] = 0u;
+  }
+  // zeros up to whole 64-d chunks (the padded weights are zero too)
+  for (int d = D + tid; d < (D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
+       d += RS_NT)
+    xl[d] = 0.0f;
   __syncthreads();
 
   // ---- logits ---------------------------------------------------------------
-  if (wave < NJ) {
-    const int e = wave * 64 + lane;
-    // the lane's 16-byte piece of chunk c (d = 4c .. 4c+3) is wlane[256 c]
-    const float* wlane = a.wr_t + (size_t)wave * a.ldw * 64 + lane * 4;
+  // The logits' summation order (mxm_numerics.h): 64-d chunks, each a partial
+  // from +0, added in chunk order.  WPG = 16 / NJ waves share an expert group
+  // (64 experts, one per lane).  Chunks go in rounds of up to RPC: wave
+  // (g, sub) takes chunks sub, sub + WPG, ... of the round, streams their
+  // weight pieces through a register ring of RS_RING items (an item is 32
+  // registers of pieces: one bf16 chunk or half an fp32 chunk; the next item
+  // is in flight while one is summed), and parks each chunk's partial in LDS.
+  // After the round's barrier the group's first wave adds the partials in
+  // chunk order.
+  {
+    constexpr int WPG = RS_WAVES / NJ;                  // waves per expert group
+    constexpr int PER = 16 / (int)sizeof(TX);           // d per 16-byte weight piece
+    constexpr int PPC = MXM_LOGIT_CHUNK / PER;          // pieces per chunk (8 or 16)
+    constexpr int IP = 8;                               // pieces per item
+    constexpr int IPC = PPC / IP;                       // items per chunk (1 or 2)
+    constexpr int RPC = RS_PART_FLOATS / (NJ * 64);     // chunks per round
+    static_assert(PPC % IP == 0 && RPC >= WPG, "items and rounds");
+    // wave-uniform values in scalar registers, so every condition below is a
+    // scalar branch and the loads sit outside divergent control flow
+    const int swave = __builtin_amdgcn_readfirstlane(wave);
+    const int g = swave / WPG, sub = swave % WPG;
+    const bool active = g < NJ;  // NJ == 3 leaves the last wave idle
+    const int nchunks = (D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK;
+    // this lane's piece p of chunk c: wlane + (c * PPC + p) * 64 * PER
+    const TX* wlane = static_cast<const TX*>(a.wr_t) +
+                      ((size_t)(active ? g : 0) * (a.ldw / PER) * 64 + lane) * PER;
+    float* part_lds = rs_part + g * 64 + lane;  // chunk i of the round at i * NJ * 64
     float acc = 0.0f;
-    const int nblk = D / RS_BD;
-    float4 w[RS_RD][RS_BD / 4];
-    float4 xv[RS_XR][RS_BD / 4];  // x of the current and the next RS_XR - 1 blocks
-    auto ld = [&](float4 (&dst)[RS_BD / 4], int b) {
-      const float* src = wlane + (size_t)b * (RS_BD / 4) * 256;
+    for (int r0 = 0; r0 < nchunks; r0 += RPC) {
+      const int rc = min(RPC, nchunks - r0);               // chunks in this round
+      const int mine = active && sub < rc ? (rc - sub + WPG - 1) / WPG : 0;
+      const int nit = mine * IPC;                           // this wave's items
+      // Workgroups n and n + 8 run on one XCD (round-robin dispatch); they
+      // walk their chunk lists from different starting points, so the XCD's
+      // L2 fills from HBM in parallel instead of every CU missing on the same
+      // lines at once.  The partials land in chunk slots, so the order of the
+      // walk does not change the sum.
+      const int rot = (int)((blockIdx.x >> 3) & 7) * mine / 8;
+      auto chunk_of = [&](int it) {  // chunk of the round of item it
+        int j = it / IPC + rot;
+        if (j >= mine) j -= mine;
+        return sub + j * WPG;
+      };
+      uint4 ring[RS_RING][IP];
+      // item it: chunk chunk_of(it), pieces (it % IPC) * IP ..
+      auto load = [&](auto S, int it) {
+        it = min(it, nit - 1);  // past the end: the last item again, unused
+        const int c = r0 + chunk_of(it);
+        const TX* p = wlane + ((size_t)c * PPC + (it % IPC) * IP) * 64 * PER;
 #pragma unroll
-      for (int q = 0; q < RS_BD / 4; ++q) dst[q] = *reinterpret_cast<const float4*>(src + q * 256);
-    };
-    auto ldx = [&](float4 (&dst)[RS_BD / 4], int b) {
-      const float4* src = reinterpret_cast<const float4*>(xl + b * RS_BD);
+        for (int q = 0; q < IP; ++q)
+          ring[S()][q] = *reinterpret_cast<const uint4*>(p + (size_t)q * 64 * PER);
+      };
+      float part = 0.0f;
+      auto step = [&](auto S, int it) {
+        load(std::integral_constant<int, (S() + RS_RING - 1) % RS_RING>{}, it + RS_RING - 1);
+        if (it < nit) {
+          const int i = chunk_of(it), h = it % IPC;  // chunk of the round, half
+          const float* xc = xl + (r0 + i) * MXM_LOGIT_CHUNK + h * IP * PER;
 #pragma unroll
-      for (int q = 0; q < RS_BD / 4; ++q) dst[q] = src[q];
-    };
-    auto fma_blk = [&](const float4 (&wv)[RS_BD / 4], const float4 (&xb)[RS_BD / 4]) {
+          for (int q = 0; q < IP; ++q) {
+            float w[PER];
+            unpack16<TX>(ring[S()][q], w);
 #pragma unroll
-      for (int q = 0; q < RS_BD / 4; ++q) {
-        acc = __builtin_fmaf(xb[q].x, wv[q].x, acc);
-        acc = __builtin_fmaf(xb[q].y, wv[q].y, acc);
-        acc = __builtin_fmaf(xb[q].z, wv[q].z, acc);
-        acc = __builtin_fmaf(xb[q].w, wv[q].w, acc);
-      }
-    };
-    const int nround = nblk / RS_RD;
-    if (nround > 0) {
-#pragma unroll
-      for (int r = 0; r < RS_RD - 1; ++r) ld(w[r], r);
-#pragma unroll
-      for (int r = 0; r < RS_XR - 1; ++r) ldx(xv[r], r);
-      // step b refills the weight slot consumed at step b - 1 with block
-      // b + RS_RD - 1 and the x slot with block b + RS_XR - 1 (RS_RD is a
-      // multiple of RS_XR, so step r's x slot is r % RS_XR).  The scheduling
-      // barrier keeps the LDS reads ahead of the block's FMAs.
-      for (int it = 0; it + 1 < nround; ++it) {
-#pragma unroll
-        for (int r = 0; r < RS_RD; ++r) {
-          const int b = it * RS_RD + r;
-          ld(w[(r + RS_RD - 1) % RS_RD], b + RS_RD - 1);
-          ldx(xv[(r + RS_XR - 1) % RS_XR], b + RS_XR - 1);
-          __builtin_amdgcn_sched_barrier(0);
-          fma_blk(w[r], xv[r % RS_XR]);
+            for (int t = 0; t < PER; ++t) part = __builtin_fmaf(xc[q * PER + t], w[t], part);
+          }
+          if (h == IPC - 1) {
+            part_lds[i * NJ * 64] = part;
+            part = 0.0f;
+          }
+        }
+      };
+      if (nit > 0) {
+        load(std::integral_constant<int, 0>{}, 0);
+        static_assert(RS_RING == 2, "two slots in the loop below");
+        for (int it = 0; it < nit; it += RS_RING) {
+          step(std::integral_constant<int, 0>{}, it);
+          step(std::integral_constant<int, 1>{}, it + 1);
         }
       }
-      // last full round: only its first step has a block of the full rounds
-      // left to fetch
-      const int bl = (nround - 1) * RS_RD;
-#pragma unroll
-      for (int r = 0; r < RS_RD; ++r) {
-        if (r == 0) ld(w[RS_RD - 1], bl + RS_RD - 1);
-        if (r + RS_XR - 1 < RS_RD) ldx(xv[(r + RS_XR - 1) % RS_XR], bl + r + RS_XR - 1);
-        __builtin_amdgcn_sched_barrier(0);
-        fma_blk(w[r], xv[r % RS_XR]);
+      __syncthreads();
+      if (active && sub == 0) {
+        for (int i = 0; i < rc; ++i) acc = acc + part_lds[i * NJ * 64];
       }
+      if (r0 + RPC < nchunks) __syncthreads();  // the next round reuses the partials
     }
-    for (int b = nround * RS_RD; b < nblk; ++b) {
-      float4 wv[RS_BD / 4], xb[RS_BD / 4];
-      ld(wv, b);
-      ldx(xb, b);
-      fma_blk(wv, xb);
-    }
-    for (int d = nblk * RS_BD; d < D; ++d)
-      acc = __builtin_fmaf(xl[d], wlane[(size_t)(d >> 2) * 256 + (d & 3)], acc);
-    lg[e] = BF16 ? mxm_rbf(acc) : acc;
+    if (active && sub == 0) lg[g * 64 + lane] = BF16 ? mxm_rbf(acc) : acc;
   }
   __syncthreads();
 
@@ -574,129 +622,117 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   }
 
   // ---- ticket: the last workgroup continues --------------------------------
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
+  // Wave 0 wrote all of this token's results, so it alone releases them; in
+  // the last workgroup wave 0 alone acquires the others' (the caches it
+  // invalidates are the CU's and the XCD's, shared by the workgroup's waves,
+  // and the barrier orders the other waves' reads after it).
+  if (wave == 0) {
+    __threadfence();
+    if (lane == 0) s_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
+  }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
+  if (wave == 0) __threadfence();
+  __syncthreads();
 
   // ---- dispatch, aux, entropy (one workgroup) -----------------------------
+  // One round trip reads the batch's results back: each thread's first slots
+  // (top_idx), its wave's tokens' probabilities and, on the last wave, the
+  // entropy terms are loaded together.  Slots go to LDS and straight into the
+  // per-expert counts and, for the first 64 tokens, the expert masks of the
+  // stable permutation.  Probabilities are summed per wave over a fixed token
+  // subset, then over the waves in wave order.
   const int NK = N * K;
   int* sidx = reinterpret_cast<int*>(rs_dyn);  // the x row is no longer needed
-  // The first loads of all three inputs are issued together, so a decode
-  // batch (N <= 64, N*K <= 2048) reads them in one round trip: slots, the
-  // probabilities of the first 64 tokens, their entropy terms.
-  int sv[8];
+  constexpr int SV = 4;  // slots per thread loaded in the first pass
+  int sv[SV];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < SV; ++q) {
     const int sl = q * RS_NT + tid;
     sv[q] = sl < NK ? a.top_idx[sl] : 0;
   }
-  const int t_first = min(N, 64);
-  float pv[64];
+  float ps[NJ];
 #pragma unroll
-  for (int q = 0; q < 64; ++q)
-    pv[q] = (tid < E && q < t_first) ? a.probs[(size_t)q * E + tid] : 0.0f;
-  constexpr int ENT_WAVE = RS_NT / 64 - 1;
-  const float ev = (wave == ENT_WAVE && lane < N) ? a.tok_ent[lane] : 0.0f;
-  for (int e = tid; e < E; e += RS_NT) {
-    cnt[e] = 0;
-    runc[e] = 0;
-  }
+  for (int j = 0; j < NJ; ++j) ps[j] = 0.0f;
+#pragma unroll 4
+  for (int t = wave; t < N; t += RS_WAVES) {
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int sl = q * RS_NT + tid;
-    if (sl < NK) sidx[sl] = sv[q];
-  }
-  for (int s0 = RS_NT * 8; s0 < NK; s0 += RS_NT * 8) {
-    int v[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int sl = s0 + q * RS_NT + tid;
-      v[q] = sl < NK ? a.top_idx[sl] : 0;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int sl = s0 + q * RS_NT + tid;
-      if (sl < NK) sidx[sl] = v[q];
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) ps[j] = ps[j] + a.probs[(size_t)t * E + e];
     }
   }
-  // per-expert probability sums over tokens in ascending order
-  if (tid < E) {
-    float ps = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 64; ++q)
-      if (q < t_first) ps = ps + pv[q];
-    for (int t0 = 64; t0 < N; t0 += 64) {
-      float v[64];
-#pragma unroll
-      for (int q = 0; q < 64; ++q) v[q] = (t0 + q < N) ? a.probs[(size_t)(t0 + q) * E + tid] : 0.0f;
-#pragma unroll
-      for (int q = 0; q < 64; ++q)
-        if (t0 + q < N) ps = ps + v[q];
-    }
-    const float mean = ps / (float)N;
-    pmean[tid] = BF16 ? mxm_rbf(mean) : mean;
-  }
+  constexpr int ENT_WAVE = RS_WAVES - 1;
   if (wave == ENT_WAVE) {
-    float es = ev;
-    for (int t = lane + 64; t < N; t += 64) es = es + a.tok_ent[t];
+    float es = 0.0f;
+    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
     es = rs_wave_sum(es);
     if (lane == 0) a.entropy[0] = -(es / (float)N);
   }
-  __syncthreads();
-  for (int sl = tid; sl < NK; sl += RS_NT) atomicAdd(&cnt[sidx[sl]], 1);
+  auto take_slot = [&](int sl, int e) {
+    sidx[sl] = e;
+    atomicAdd(&cnt[e], 1);
+    const int t = sl / K;
+    if (t < 64) atomicOr(&msk[e][t >> 5], 1u << (t & 31));
+  };
+#pragma unroll
+  for (int q = 0; q < SV; ++q) {
+    const int sl = q * RS_NT + tid;
+    if (sl < NK) take_slot(sl, sv[q]);
+  }
+  for (int sl = SV * RS_NT + tid; sl < NK; sl += RS_NT) take_slot(sl, a.top_idx[sl]);
+  static_assert(RS_WAVES * MXM_MAX_EXPERTS <= RS_PART_FLOATS, "per-wave probability sums");
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) rs_part[wave * MXM_MAX_EXPERTS + e] = ps[j];
+  }
   __syncthreads();
 
   if (wave == 0) {
-    // lane l takes experts 4l .. 4l+3 (E <= 256): exclusive prefixes of the
-    // counts and of the row tiles of both GEMM families
-    int c[4], t0 = 0, t1 = 0, t2 = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = 4 * lane + q;
-      c[q] = e < E ? cnt[e] : 0;
-      t0 += c[q];
-      t1 += (c[q] + a.bm1 - 1) / a.bm1;
-      t2 += (c[q] + a.bm2 - 1) / a.bm2;
-    }
-    int i0 = t0, i1 = t1, i2 = t2;
-#pragma unroll
-    for (int sh = 1; sh < 64; sh <<= 1) {
-      const int u0 = __shfl_up(i0, sh, 64), u1 = __shfl_up(i1, sh, 64), u2 = __shfl_up(i2, sh, 64);
-      if (lane >= sh) {
-        i0 += u0;
-        i1 += u1;
-        i2 += u2;
-      }
-    }
-    int o = i0 - t0, m1 = i1 - t1, m2 = i2 - t2;
+    // expert e = lane + 64 j: exclusive prefixes of the counts and of the row
+    // tiles of both GEMM families (one wave scan per j), the mean
+    // probabilities and the aux terms
+    int run0 = 0, run1 = 0, run2 = 0;
     float aux = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = 4 * lane + q;
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      const int c = e < E ? cnt[e] : 0;
+      const int u1 = (c + a.bm1 - 1) / a.bm1, u2 = (c + a.bm2 - 1) / a.bm2;
+      int i0 = c, i1 = u1, i2 = u2;
+#pragma unroll
+      for (int sh = 1; sh < 64; sh <<= 1) {
+        const int v0 = __shfl_up(i0, sh, 64), v1 = __shfl_up(i1, sh, 64), v2 = __shfl_up(i2, sh, 64);
+        if (lane >= sh) {
+          i0 += v0;
+          i1 += v1;
+          i2 += v2;
+        }
+      }
       if (e < E) {
+        const int o = run0 + i0 - c;
         offs[e] = o;
         a.offsets[e] = o;
-        a.counts[e] = c[q];
-        a.mstart1[e] = m1;
-        a.mstart2[e] = m2;
-        o += c[q];
-        m1 += (c[q] + a.bm1 - 1) / a.bm1;
-        m2 += (c[q] + a.bm2 - 1) / a.bm2;
-        const float frac = ((float)c[q] / (float)K) / (float)N;
-        const float term = pmean[e] * frac;
-        aux = (q == 0) ? term : aux + term;
+        a.counts[e] = c;
+        a.mstart1[e] = run1 + i1 - u1;
+        a.mstart2[e] = run2 + i2 - u2;
+        float pm = 0.0f;
+#pragma unroll
+        for (int w = 0; w < RS_WAVES; ++w) pm = pm + rs_part[w * MXM_MAX_EXPERTS + e];
+        const float mean = pm / (float)N;
+        const float frac = ((float)c / (float)K) / (float)N;
+        aux = aux + (BF16 ? mxm_rbf(mean) : mean) * frac;
       }
+      run0 += __shfl(i0, 63, 64);
+      run1 += __shfl(i1, 63, 64);
+      run2 += __shfl(i2, 63, 64);
     }
     aux = rs_wave_sum(aux);
-    if (lane == 63) {
-      a.offsets[E] = i0;
-      a.mstart1[E] = i1;
-      a.mstart2[E] = i2;
-    }
     if (lane == 0) {
+      a.offsets[E] = run0;
+      a.mstart1[E] = run1;
+      a.mstart2[E] = run2;
       const float raw = aux * (float)E;
       a.aux[0] = raw;
       if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
@@ -704,19 +740,23 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
   }
   __syncthreads();
 
-  // stable permutation, 64 tokens at a time
+  // stable permutation, 64 tokens at a time (chunk 0's masks are built above):
+  // the rank of a slot among the chunk's tokens on its expert from the
+  // expert's 64-bit token mask, plus the running count of earlier chunks
   for (int c0 = 0; c0 < N; c0 += 64) {
     const int ct = min(64, N - c0);
-    for (int e = tid; e < E; e += RS_NT) {
-      msk[e][0] = 0u;
-      msk[e][1] = 0u;
+    if (c0 > 0) {
+      for (int e = tid; e < E; e += RS_NT) {
+        msk[e][0] = 0u;
+        msk[e][1] = 0u;
+      }
+      __syncthreads();
+      for (int i = tid; i < ct * K; i += RS_NT) {
+        const int t = i / K;
+        atomicOr(&msk[sidx[c0 * K + i]][t >> 5], 1u << (t & 31));
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    for (int i = tid; i < ct * K; i += RS_NT) {
-      const int t = i / K;
-      atomicOr(&msk[sidx[c0 * K + i]][t >> 5], 1u << (t & 31));
-    }
-    __syncthreads();
     for (int i = tid; i < ct * K; i += RS_NT) {
       const int t = i / K, sl = c0 * K + i;
       const int e = sidx[sl];
@@ -727,9 +767,11 @@ __global__ __launch_bounds__(RS_NT) void route_small_kernel(RouteSmallArgs a) {
       a.perm[pos] = c0 + t;
       a.slot_pos[sl] = pos;
     }
-    __syncthreads();
-    for (int e = tid; e < E; e += RS_NT) runc[e] += __popc(msk[e][0]) + __popc(msk[e][1]);
-    __syncthreads();
+    if (c0 + 64 < N) {
+      __syncthreads();
+      for (int e = tid; e < E; e += RS_NT) runc[e] += __popc(msk[e][0]) + __popc(msk[e][1]);
+      __syncthreads();
+    }
   }
   if (tid == 0) __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -738,7 +780,7 @@ template <typename TX, bool BF16, int NJ>
 void launch_route_small_t(const RouteSmallArgs& a, hipStream_t s) {
   constexpr int PER = 16 / (int)sizeof(TX);
   const bool vec = a.D % PER == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
-  size_t lds = (size_t)a.D * 4;
+  size_t lds = (size_t)(a.D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK * 4;
   const size_t slots = (size_t)a.N * a.K * 4;
   if (slots > lds) lds = slots;
   lds = (lds + 15) / 16 * 16;

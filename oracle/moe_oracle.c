@@ -27,8 +27,11 @@
  * already rounded to bf16 in the bf16 flow.
  *
  * Arithmetic contract (what MLX leaves unspecified, fixed here and in the
- * device code alike): dot products accumulate in fp32 by fmaf over the
- * reduction index in ascending order; exp is Cody-Waite reduction with a
+ * device code alike): the router logits split d into chunks of 64 from d = 0,
+ * each chunk's partial an fmaf chain over its d in ascending order from +0,
+ * and the logit is +0 plus the chunk partials added in ascending chunk order;
+ * the expert FFN's dot products accumulate in fp32 by fmaf over the reduction
+ * index in ascending order; exp is Cody-Waite reduction with a
  * degree-7 Taylor polynomial; the softmax denominator is summed lane-wise
  * (lane l holds experts l, l+64, ...) and then by an xor butterfly over 64
  * lanes; probabilities below 2^-126 flush to +0; bf16 rounding is
@@ -181,6 +184,9 @@ float oracle_gelu_tanh(float v, float sq) {
   return f * e;
 }
 
+/* d per chunk of the router logits' summation order */
+#define ORACLE_LOGIT_CHUNK 64
+
 enum { SWIGLU = 0, GEGLU = 1, MLP = 2 };
 enum { SILU = 0, GELU = 1, RELU = 2, LEAKY_RELU_SQ = 3 };
 
@@ -233,14 +239,22 @@ static void route_rows(int n0, int n1, int D, int E, int K, int bf16, const floa
                        const float* wr, float* logits, float* probs, float* probs_raw,
                        int32_t* top_idx, float* gates) {
   float* acc = (float*)malloc(sizeof(float) * (size_t)E);
+  float* part = (float*)malloc(sizeof(float) * (size_t)E);
   float* ex = (float*)malloc(sizeof(float) * (size_t)E);
   unsigned char* taken = (unsigned char*)malloc((size_t)E);
   for (int n = n0; n < n1; ++n) {
+    /* logits: chunks of ORACLE_LOGIT_CHUNK d, each an fmaf chain from +0,
+       the partials added to +0 in chunk order */
     for (int e = 0; e < E; ++e) acc[e] = 0.0f;
-    for (int d = 0; d < D; ++d) {
-      const float xv = x[(size_t)n * D + d];
-      const float* w = wr + (size_t)d * E;
-      for (int e = 0; e < E; ++e) acc[e] = fmaf(xv, w[e], acc[e]);
+    for (int d0 = 0; d0 < D; d0 += ORACLE_LOGIT_CHUNK) {
+      const int d1 = (d0 + ORACLE_LOGIT_CHUNK < D) ? d0 + ORACLE_LOGIT_CHUNK : D;
+      for (int e = 0; e < E; ++e) part[e] = 0.0f;
+      for (int d = d0; d < d1; ++d) {
+        const float xv = x[(size_t)n * D + d];
+        const float* w = wr + (size_t)d * E;
+        for (int e = 0; e < E; ++e) part[e] = fmaf(xv, w[e], part[e]);
+      }
+      for (int e = 0; e < E; ++e) acc[e] = acc[e] + part[e];
     }
     float* lg = logits + (size_t)n * E;
     float* p = probs + (size_t)n * E;
@@ -283,6 +297,7 @@ static void route_rows(int n0, int n1, int D, int E, int K, int bf16, const floa
     for (int k = 0; k < K; ++k) gates[(size_t)n * K + k] = p[top_idx[(size_t)n * K + k]] / den;
   }
   free(acc);
+  free(part);
   free(ex);
   free(taken);
 }

@@ -464,7 +464,7 @@ def test_large_top_k(gpu_lib, E, K, N):
     assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"])
 
 
-@pytest.mark.parametrize("E", [65, 128, 200, 256])
+@pytest.mark.parametrize("E", [65, 128, 150, 200, 256])
 @pytest.mark.parametrize("N", [130, 1500])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_many_experts(gpu_lib, E, N, bf16):
@@ -489,9 +489,11 @@ def test_many_experts(gpu_lib, E, N, bf16):
     (1, 64, 8, 2, False),        # one token: one workgroup takes the only ticket
     (1024, 128, 64, 16, True),   # N*K at the one-launch router's slot limit
     (1024, 128, 64, 17, True),   # one slot row past it: the tiled router
-    (200, 100, 16, 4, True),     # bf16 rows not in 16-byte pieces; no full register round
-    (96, 300, 40, 3, False),     # full rounds, remainder blocks and a d tail
-    (77, 2051, 96, 5, True),     # odd D, two waves of router logits
+    (200, 100, 16, 4, True),     # bf16 rows not in 16-byte pieces; 2 of a round's 8 chunks
+    (96, 300, 40, 3, False),     # 5 chunks: a full round of 4, then 1 with a zero-padded tail
+    (77, 2051, 96, 5, True),     # odd D, 2 waves per expert group, 9 rounds (odd: slot 0 last)
+    (5, 64, 150, 3, False),      # one chunk, 3 expert groups (one wave idle in the logits)
+    (40, 2048, 64, 6, False),    # 32 chunks in 8 full rounds of 4 (fp32: 1 chunk per wave)
     (8, 16384, 64, 4, True),     # D at the one-launch router's limit (64 KB x row in LDS)
     (8, 16388, 64, 4, False),    # D past it: the tiled router
 ])

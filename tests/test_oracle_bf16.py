@@ -18,8 +18,8 @@ reject a planted slip (a build of oracle/moe_oracle.c with one ORACLE_PLANT_*
 macro defined): a rounding dropped or a decision taken on unrounded values.
 Where an independent float64 value lies within the fp32 evaluation error of a
 bf16 rounding boundary, the two roundings may legitimately differ; such
-elements are held to one bf16 ulp and every other element must match bit for
-bit.  No GPU is used here.
+elements are held to one bf16 ulp plus that error bound, and every other
+element must match bit for bit.  No GPU is used here.
 """
 from __future__ import annotations
 
@@ -79,14 +79,17 @@ def near_bf16_boundary(v, tol) -> np.ndarray:
 
 
 def match_rounding(got, exact64, tol) -> bool:
-    """got == rb(exact64) except within tol of a midpoint, where one bf16
-    ulp is allowed."""
+    """got == rb(exact64) except within tol (the fp32 evaluation's error
+    bound) of a midpoint, where got may be the rounding of any value within
+    tol of exact64: one bf16 ulp plus tol."""
     got = np.asarray(got, np.float64)
+    tol = np.broadcast_to(np.asarray(tol, np.float64), np.shape(exact64))
     want = rb(exact64)
     near = near_bf16_boundary(exact64, tol)
     if not np.array_equal(got[~near], want[~near]):
         return False
-    return bool(np.all(np.abs(got[near] - exact64[near]) <= bf16_ulp(exact64[near])))
+    return bool(np.all(np.abs(got[near] - exact64[near])
+                       <= bf16_ulp(exact64[near]) + tol[near]))
 
 
 # ---- routing pins (gpu/ir.cpp:1106-1111, 1150-1162) ----
