@@ -276,8 +276,8 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     then the gradients of x, the router and every routed expert) on the
     configuration's compute dtype.  fp32: the routing of the forward, then
     every expert product as a per-expert rocBLAS fp32 GEMM (fp32 matrix
-    cores); bf16 (MFMA weight family): products on MFMA and, for the weight
-    gradients, rocBLAS bf16 GEMMs with fp32 output."""
+    cores); bf16 (MFMA weight family): every product on MFMA, the weight
+    gradients on the ragged grouped weight-gradient kernel (fp32 out)."""
     from mixlab_amd import _lib
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import make_workload
@@ -326,7 +326,7 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     tf = fl / (ms * 1e-3) / 1e12
     log(f"backward {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
     if bf16 and mfma:
-        roof = {"bound": "mfma", "kernel": "whole backward (MFMA grouped products, rocBLAS "
+        roof = {"bound": "mfma", "kernel": "whole backward (MFMA grouped products and "
                 "weight gradients)", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": tf / PEAK_BF16_TFLOPS, "traffic": None}
     else:

@@ -24,6 +24,7 @@ SOURCES = [
     "mxm_dispatch.hip",
     "mxm_gemm_simt.hip",
     "mxm_gemm_mfma.hip",
+    "mxm_wgrad.hip",
     "mxm_decode.hip",
     "mxm_prep.hip",
     "mxm_block.hip",

@@ -152,7 +152,7 @@ struct MoeOp {
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
   bool bw_wbf_ready = false;
-  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_dw1cat, bw_ms, bw_w2o, bw_w1u;
+  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
 
@@ -1050,19 +1050,6 @@ void check_blas(rocblas_status st, const char* what) {
     fail("OP_MOE_FEED_FORWARD backward: %s failed (rocBLAS status %d)", what, (int)st);
 }
 
-// dst[rows][C] (row-major, fp32) = A^T B over `rows`, A [rows][M], B [rows][C]
-// bf16 row-major (rocBLAS is column-major: dst^T = B^T A).
-void gemm_at_b(rocblas_handle h, const uint16_t* A, int M, const uint16_t* B, int C, int rows,
-               float* dst, int lda = 0, float beta = 0.0f) {
-  const float one = 1.0f;
-  check_blas(rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, C, M, rows, &one,
-                             B, rocblas_datatype_bf16_r, C, A, rocblas_datatype_bf16_r,
-                             lda > 0 ? lda : M, &beta, dst,
-                             rocblas_datatype_f32_r, C, dst, rocblas_datatype_f32_r, C,
-                             rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
-             "weight-gradient GEMM");
-}
-
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
 // permuted order throughout (expert e owns rows offsets[e] ..).
 //   dH  = dY W_down^T          MFMA grouped GEMM, W_down kept as [F][D] bf16
@@ -1071,7 +1058,7 @@ void gemm_at_b(rocblas_handle h, const uint16_t* A, int M, const uint16_t* B, in
 //   dG|dU                      elementwise (act_bw_bf16)
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
 //   dx  = dxr + sum_k dXe      (dx_bf16)
-//   dW1 = Xp^T dG|dU, dW_down = H^T dY   per expert, rocBLAS bf16 -> fp32
+//   dW1 = Xp^T dG|dU, dW_down = H^T dY   MFMA weight-gradient kernel (fp32 out)
 void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* dx, float* dw) {
   hipStream_t st = o.stream;
   const bool glu = o.wpe == 3;
@@ -1083,7 +1070,8 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_dhb.alloc(NK * F * 2);
     o.bw_dgub.alloc(NK * NC * 2);
     o.bw_dxeb.alloc(NK * D * 2);
-    if (glu) o.bw_dw1cat.alloc((size_t)E * D * NC * 4);
+    o.bw_zero.alloc(512);  // 256 zero bf16: the weight gradients' rows past an expert's end
+    HIPCK(hipMemsetAsync(o.bw_zero.p, 0, 512, st));
     o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
     o.bw_w2o.alloc((size_t)E * DF * 2);
     o.bw_w1u.alloc((size_t)E * D * NC * 2);
@@ -1132,40 +1120,42 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
   HIPCK(hipGetLastError());
 
-  // weight gradients: one rocBLAS GEMM per expert and matrix pair, sized by
-  // the expert's row count
-  std::vector<int32_t> cnt(E);
-  HIPCK(hipMemcpyAsync(cnt.data(), b.counts, (size_t)E * 4, hipMemcpyDeviceToHost, st));
-  HIPCK(hipStreamSynchronize(st));
-  if (!o.bw_blas) {
-    check_blas(rocblas_create_handle(&o.bw_blas), "rocblas_create_handle");
-  }
-  check_blas(rocblas_set_stream(o.bw_blas, st), "rocblas_set_stream");
-  const uint16_t* hb = static_cast<const uint16_t*>(o.ws.H);
-  float* w1g = glu ? o.bw_dw1cat.as<float>() : nullptr;
-  size_t off = 0;
-  for (int e = 0; e < E; ++e) {
-    const int rows = cnt[e];
-    float* dwe = dw + (size_t)e * stride;
-    if (rows <= 0) {
-      HIPCK(hipMemsetAsync(dwe, 0, stride * 4, st));
-      if (glu) HIPCK(hipMemsetAsync(w1g + (size_t)e * D * NC, 0, (size_t)D * NC * 4, st));
-      continue;
-    }
-    // gate|up (interleaved, GLU) or up (MLP): [D][NC] = Xp^T dGU
-    gemm_at_b(o.bw_blas, xpb + off * D, D, dgub + off * NC, NC, rows,
-              glu ? w1g + (size_t)e * D * NC : dwe);
-    // down: [F][D] = H^T dY (a split hidden: hi^T dY + lo^T dY)
-    float* dwd = dwe + (glu ? 2 : 1) * DF;
-    if (o.hsplit) {
-      gemm_at_b(o.bw_blas, hb + off * 2 * F, F, dyb + off * D, D, rows, dwd, 2 * F);
-      gemm_at_b(o.bw_blas, hb + off * 2 * F + F, F, dyb + off * D, D, rows, dwd, 2 * F, 1.0f);
-    } else {
-      gemm_at_b(o.bw_blas, hb + off * F, F, dyb + off * D, D, rows, dwd);
-    }
-    off += (size_t)rows;
-  }
-  if (glu) mxm_launch_deinterleave(w1g, E, D, F, dw, stride, st);
+  // weight gradients on MFMA, each reduced over its expert's rows (ragged,
+  // from the device-side offsets): dW1 = Xp^T dG|dU, its GLU columns landing
+  // de-interleaved in the gate and up matrices (x.W layout), and
+  // dW_down = H^T dY over the hidden's planes (hi and lo for a split hidden)
+  if (!mxm_wgrad_fits(D, NC) || !mxm_wgrad_fits(F, D))
+    fail("OP_MOE_FEED_FORWARD backward: weight-gradient tiles need D, F multiples of 128 "
+         "(D=%d F=%d)", D, F);
+  WgradArgs wa{};
+  wa.offsets = b.offsets;
+  wa.zero = o.bw_zero.as<uint16_t>();
+  wa.E = E;
+  wa.out_estride = stride;
+  wa.a = xpb;
+  wa.lda = D;
+  wa.planes = 1;
+  wa.b = dgub;
+  wa.ldb = NC;
+  wa.M = D;
+  wa.C = NC;
+  wa.out = dw;
+  wa.out_slot = DF;
+  wa.glu_f = glu ? F : 0;
+  mxm_launch_wgrad(wa, st);
+  HIPCK(hipGetLastError());
+  wa.a = static_cast<const uint16_t*>(o.ws.H);
+  wa.lda = o.hsplit ? 2 * F : F;
+  wa.aplane = F;
+  wa.planes = o.hsplit ? 2 : 1;
+  wa.b = dyb;
+  wa.ldb = D;
+  wa.M = F;
+  wa.C = D;
+  wa.out = dw + (glu ? 2 : 1) * DF;
+  wa.out_slot = 0;
+  wa.glu_f = 0;
+  mxm_launch_wgrad(wa, st);
   HIPCK(hipGetLastError());
 }
 

@@ -444,22 +444,6 @@ __global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __
   }
 }
 
-// The GLU pair's weight gradient from the interleaved product src [E][D][2F]
-// (column c: gate (c/32 even) or up of hidden unit (c/64)*32 + c%32) into
-// the gate and up blocks of each expert's gradients (stride floats apart).
-__global__ void deinterleave_kernel(const float* __restrict__ src, int E, int D, int F,
-                                    float* __restrict__ dw, size_t stride) {
-  const size_t total = (size_t)E * D * 2 * F;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % (2 * F));
-    const size_t ed = i / (2 * F);
-    const int d = (int)(ed % D), e = (int)(ed / D);
-    const int m = (c >> 5) & 1, f = (c >> 6) * 32 + (c & 31);
-    dw[(size_t)e * stride + (size_t)m * D * F + (size_t)d * F + f] = src[i];
-  }
-}
-
 int grid_of(size_t n) {
   size_t b = (n + 255) / 256;
   if (b > 65536) b = 65536;
@@ -519,14 +503,6 @@ void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, in
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
                         int D, int K, float* dx, hipStream_t s) {
   if (N > 0) hipLaunchKernelGGL(dx_bf16_kernel, dim3(N), dim3(256), 0, s, dxr, dxe, slot_pos, D, K, dx);
-}
-
-void mxm_launch_deinterleave(const float* src, int E, int D, int F, float* dw, size_t stride,
-                             hipStream_t s) {
-  const size_t total = (size_t)E * D * 2 * F;
-  if (total > 0)
-    hipLaunchKernelGGL(deinterleave_kernel, dim3(grid_of(total)), dim3(256), 0, s, src, E, D, F, dw,
-                       stride);
 }
 
 // Gate, renorm, aux / entropy and softmax gradients, the router's products

@@ -174,6 +174,29 @@ enum { MXM_TILE_AUTO = 0, MXM_TILE_128x128 = 1, MXM_TILE_256x128 = 2, MXM_TILE_2
 // Row-tile height the MFMA launcher uses for a GEMM with these dimensions
 // (0: the family does not tile them).
 int mxm_mfma_tile_rows(int Ncols, int Kd, int family);
+
+// Weight gradients on MFMA (mxm_wgrad.hip): per expert e,
+//   out[e][m][c] = sum_p sum_k A[k][p * aplane + m] * B[k][c]   (fp32)
+// over rows k = offsets[e] .. offsets[e+1]-1 and planes p < planes.  With
+// glu_f > 0 the C columns are GLU-interleaved in groups of 32 (gate, up) and
+// land de-interleaved: column c -> out[e] + ((c/32) % 2) * out_slot +
+// m * glu_f + (c/64)*32 + c%32; else out[e] + m * C + c.
+struct WgradArgs {
+  const uint16_t* a;        // bf16 [rows][lda]
+  int lda, aplane, planes;
+  const uint16_t* b;        // bf16 [rows][ldb]
+  int ldb;
+  const int32_t* offsets;   // [E + 1]
+  const uint16_t* zero;     // 256 zero bf16 (rows past an expert's end)
+  int E, M, C;
+  float* out;
+  size_t out_estride;       // floats between experts' outputs
+  size_t out_slot;          // floats from the gate matrix to the up matrix (GLU)
+  int glu_f;                // F for GLU de-interleaving, else 0
+};
+// M and C multiples of 128.
+bool mxm_wgrad_fits(int M, int C);
+void mxm_launch_wgrad(const WgradArgs& a, hipStream_t s);
 int mxm_simt_bm();
 
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
@@ -343,7 +366,5 @@ void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, in
                             int act, float slope, uint16_t* dgu, hipStream_t s);
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
                         int D, int K, float* dx, hipStream_t s);
-void mxm_launch_deinterleave(const float* src, int E, int D, int F, float* dw, size_t stride,
-                             hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);

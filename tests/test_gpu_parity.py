@@ -537,30 +537,47 @@ def test_decode_router_repeated_calls(gpu_lib):
             assert abs(ent - want["entropy"]) <= 1e-5 * abs(want["entropy"])
 
 
-@pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0), (2, 1, 0.0), (2, 3, 0.4)])
-@pytest.mark.parametrize("flow", ["bf16_mfma", "bf16_simt"])
-def test_backward_bf16(gpu_lib, etype, act, slope, flow):
-    """mxm_moe_backward under bf16 compute: the fp32 backward kernels take
-    the bf16 flow's values (x and weights rounded to bf16, the forward's bf16
-    expert outputs); against the float64 restatement on the bf16-rounded
-    inputs with the bf16 routing, within the bf16 bar (2e-2 relative L2)."""
+def _backward_bf16(etype, act, slope, shape, simt):
     from mixlab_amd.op import MoEFeedForward
-    from oracle.backward import backward64
 
-    B, T, D, E, F, K = 2, 96, 256, 6, 256, 2
+    B, T, D, E, F, K = shape
     x, wr, experts = random_case(81 + etype * 7 + act, B * T, D, E, F, expert_type=etype,
                                  wscale=0.1)
     x, wr = round_bf16(x), round_bf16(wr)
     experts = [[round_bf16(w) for w in ws] for ws in experts]
     rng = np.random.default_rng(82)
     dD = rng.standard_normal((B * T, D), dtype=np.float32)
-    flags = _lib.MXM_FLAG_FORCE_SIMT if flow == "bf16_simt" else 0
+    flags = _lib.MXM_FLAG_FORCE_SIMT if simt else 0
     with MoEFeedForward([B, T, D, E, K, etype, F, act], [slope], compute_dtype="bf16",
                         flags=flags) as op:
         op.set_weights(bf16_bits(wr), [[bf16_bits(w) for w in ws] for ws in experts])
         dx, dwr, dexp = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
         routing = op.routing()
-        assert op.info()["mfma"] == (flow == "bf16_mfma")
+        assert op.info()["mfma"] == (not simt)
+    return x, wr, experts, dD, dx, dwr, dexp, routing
+
+
+@pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0), (2, 1, 0.0), (2, 3, 0.4)])
+@pytest.mark.parametrize("flow", ["bf16_mfma", "bf16_simt"])
+@pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 40, 384, 16, 128, 2)])
+def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
+    """mxm_moe_backward under bf16 compute: the fp32 backward kernels take
+    the bf16 flow's values (x and weights rounded to bf16, the forward's bf16
+    expert outputs); against the float64 restatement on the bf16-rounded
+    inputs with the bf16 routing, within the bf16 bar (2e-2 relative L2).
+    Experts with few rows (the second shape has about 5 per expert) carry
+    the bf16 flow's error unaveraged (up to 3e-2 on both paths), so there
+    each weight-gradient kind is checked over all experts together and per
+    expert only from 16 rows up; experts without rows get exact zeros.  On
+    MFMA the weight gradients are the ragged grouped kernel's (256-wide
+    tiles for the first shape, 128-wide for the second, D = 384, F = 128),
+    and every expert's matrices are also held to 1e-2 against the fp32 SIMT
+    backward on the same op, which shares the bf16 forward."""
+    from oracle.backward import backward64
+
+    simt = flow == "bf16_simt"
+    x, wr, experts, dD, dx, dwr, dexp, routing = _backward_bf16(etype, act, slope, shape, simt)
+    B, T, D, E, F, K = shape
     want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
                       bf16=True)
     assert_routing_equal(routing, want)
@@ -568,12 +585,29 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow):
                                   etype, act, slope)
     assert rel_l2(dx, rdx) <= BF16_TOL
     assert rel_l2(dwr, rdwr) <= BF16_TOL
+    rows = np.bincount(want["top_idx"].ravel(), minlength=E)
+    nmat = len(experts[0])
+    for m in range(nmat):
+        got = np.concatenate([dexp[e][m].ravel() for e in range(E)])
+        ref = np.concatenate([np.asarray(rdexp[e][m], np.float64).ravel() for e in range(E)])
+        assert rel_l2(got, ref) <= BF16_TOL, m
     for e in range(E):
-        for m in range(len(experts[e])):
-            if np.any(rdexp[e][m]):
-                assert rel_l2(dexp[e][m], rdexp[e][m]) <= BF16_TOL, (e, m)
-            else:
+        for m in range(nmat):
+            if rows[e] == 0:
                 assert not np.any(dexp[e][m]), (e, m)
+            elif rows[e] >= 16:
+                assert rel_l2(dexp[e][m], rdexp[e][m]) <= BF16_TOL, (e, m)
+    if not simt:
+        sdexp = _backward_bf16(etype, act, slope, shape, True)[6]
+        worst = 0.0
+        for e in range(E):
+            for m in range(nmat):
+                if rows[e] > 0:
+                    err = rel_l2(dexp[e][m], sdexp[e][m])
+                    worst = max(worst, err)
+                    assert err <= 1e-2, (e, m)
+        print(f"etype {etype} act {act} {shape}: dx {rel_l2(dx, rdx):.2e}, "
+              f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
 @pytest.mark.parametrize("T", [64, 1536])
