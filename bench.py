@@ -82,6 +82,12 @@ def gemm_traffic(workload: str, flags: int):
     return None if up is None or down is None else up + down
 
 
+def layer_traffic(workload: str, stages, flags: int):
+    """HBM bytes of one whole forward: the sum over its launches."""
+    parts = [measured_traffic(workload, s, flags) for s in stages]
+    return None if any(p is None for p in parts) else sum(parts)
+
+
 def cpu_baseline(w, cfg, target_s: float) -> dict:
     """Time the dense fp32 BLAS restatement of the reference algorithm
     (oracle/dense_blas.py: every expert on every token, gpu/ir.cpp:1118-1148)
@@ -353,6 +359,9 @@ def main() -> int:
     ap.add_argument("--vendor-gemm-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
+    ap.add_argument("--backward-only", action="store_true",
+                    help="only time the bf16 backward at the C2 shape (10 steps after 3 warm-up) "
+                         "and print its JSON object (for profiling)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -362,6 +371,10 @@ def main() -> int:
     if args.vendor_gemm_only:
         from mixlab_amd.workloads import CONFIGS
         return vendor_gemm_child(CONFIGS[args.config])
+    if args.backward_only:
+        from mixlab_amd.workloads import CONFIGS
+        print(json.dumps({"backward_bf16": run_backward(CONFIGS["C2"], 10, 3)}), flush=True)
+        return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -405,7 +418,9 @@ def main() -> int:
             "hbm_gbs_forward": layer_gbs,
             "layer_roofline": {"bound": "hbm", "kernel": "whole decode forward (all launches)",
                                "achieved": layer_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                               "frac": layer_gbs / PEAK_HBM_GBS, "traffic": None},
+                               "frac": layer_gbs / PEAK_HBM_GBS,
+                               "traffic": layer_traffic("C5", ("route_small", "gemm_up",
+                                                               "gemm_down", "combine"), 0)},
             "roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
                          "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": up_gbs / PEAK_HBM_GBS,

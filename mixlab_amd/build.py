@@ -71,8 +71,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
     tmp = LIB.with_suffix(".so.tmp")
-    # rocBLAS: the backward's per-expert GEMMs (bf16 weight gradients; the
-    # fp32 flow's products)
+    # rocBLAS: the fp32 flow's backward products (per-expert fp32 GEMMs)
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
            "-lrocblas"]
     res = subprocess.run(cmd, capture_output=True, text=True)
