@@ -1064,8 +1064,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   const bool glu = o.wpe == 3;
   const int D = o.D, F = o.F, E = o.E, NC = glu ? 2 * F : F;
   const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
-  if (!o.bw_dyb.p) {
-    o.bw_dyb.alloc(NK * D * 2);
+  if (!o.bw_xpb.p) {
     o.bw_xpb.alloc(NK * D * 2);
     o.bw_dhb.alloc(NK * F * 2);
     o.bw_dgub.alloc(NK * NC * 2);
@@ -1090,7 +1089,6 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *xpb = o.bw_xpb.as<uint16_t>(),
            *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
            *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>();
-  mxm_launch_to_bf16(b.dy, MXM_DTYPE_F32, dyb, (int64_t)(NK * D), st);
   mxm_launch_gather_rows_bf16(static_cast<const uint16_t*>(xb), b.perm, (int)NK, D, xpb, st);
   auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols) {
     const int bm = mxm_mfma_tile_rows(Ncols, Kd, o.family);
@@ -1273,7 +1271,10 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   if (!o.bw_probs.p) o.bw_probs.alloc(N * E * 4);
   if (!o.bw_ready) {
     o.bw_delta.alloc(N * D * 4);
-    o.bw_dy.alloc(NK * D * 4);
+    if (mfma_bw)
+      o.bw_dyb.alloc(NK * D * 2);  // dY straight in bf16
+    else
+      o.bw_dy.alloc(NK * D * 4);
     o.bw_dgates.alloc(NK * 4);
     o.bw_dlogits.alloc(N * E * 4);
     o.bw_dxr.alloc(N * D * 4);
@@ -1327,8 +1328,10 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
       w1b = o.bw_w1b_32.as<float>();
       w2 = o.bw_w2_32.as<float>();
     }
-    if (!o.bw_x32.p) o.bw_x32.alloc(N * D * 4);
-    x32 = o.bw_x32.as<float>();
+    if (!mfma_bw) {  // (the MFMA backward reads the bf16 x)
+      if (!o.bw_x32.p) o.bw_x32.alloc(N * D * 4);
+      x32 = o.bw_x32.as<float>();
+    }
   }
   // the MFMA backward's G|U (pre-activation products) come from the forward
   uint16_t* gu = nullptr;
@@ -1350,7 +1353,10 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   o.keep_probs = o.route_only = false;
   // x as the forward saw it (rounded to bf16 when given in fp32)
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.ws.xcast;
-  if (o.bf16) {
+  // The MFMA backward's router part reads x and a bf16 Y as they are; the
+  // fp32 kernels of the other paths take fp32 copies.
+  const bool read_bf16 = o.bf16 && mfma_bw;
+  if (o.bf16 && !read_bf16) {
     mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
     if (o.mfma && !o.hsplit) {  // (a split hidden's y is fp32 already)
       if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
@@ -1378,11 +1384,16 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.offsets = o.ws.offsets;
   b.probs = o.bw_probs.as<float>();
   b.Y = y32;
+  if (read_bf16) {
+    b.xb16 = static_cast<const uint16_t*>(xb);
+    if (!o.hsplit) b.Yb16 = static_cast<const uint16_t*>(o.ws.Y);
+  }
   b.wr = wr;
   b.d_delta = d_delta;
   b.d_aux = d_aux;
   b.d_ent = d_ent;
   b.dy = o.bw_dy.as<float>();
+  if (mfma_bw) b.dyb16 = o.bw_dyb.as<uint16_t>();
   b.dgates = o.bw_dgates.as<float>();
   b.dlogits = o.bw_dlogits.as<float>();
   b.dxr = o.bw_dxr.as<float>();

@@ -26,6 +26,9 @@
 
 namespace {
 
+__device__ __forceinline__ float ld_x(const float* p) { return *p; }
+__device__ __forceinline__ float ld_x(const uint16_t* p) { return mxm_bf2f(*p); }
+
 __global__ void gather_rows_kernel(const float* __restrict__ x, const int32_t* __restrict__ perm,
                                    int D, float* __restrict__ out) {
   const int s = blockIdx.x;
@@ -58,9 +61,13 @@ __global__ __launch_bounds__(256) void dgates_kernel(BackwardArgs a) {
   if (s >= a.N * a.K) return;
   const int n = s / a.K;
   const float* dd = a.d_delta + (size_t)n * a.D;
-  const float* y = a.Y + (size_t)a.slot_pos[s] * a.D;
+  const size_t yo = (size_t)a.slot_pos[s] * a.D;
   float acc = 0.0f;
-  for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], y[d], acc);
+  if (a.Yb16) {
+    for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], mxm_bf2f(a.Yb16[yo + d]), acc);
+  } else {
+    for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], a.Y[yo + d], acc);
+  }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc = acc + mxm_xor_lane_f(acc, m);
   if (lane == 0) a.dgates[s] = acc;
@@ -108,8 +115,12 @@ __global__ void dy_kernel(BackwardArgs a) {
   const int n = s / a.K;
   const float g = a.gates[s];
   const float* dd = a.d_delta + (size_t)n * a.D;
-  float* dst = a.dy + (size_t)a.slot_pos[s] * a.D;
-  for (int d = threadIdx.x; d < a.D; d += blockDim.x) dst[d] = g * dd[d];
+  const size_t o = (size_t)a.slot_pos[s] * a.D;
+  if (a.dyb16) {
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) a.dyb16[o + d] = mxm_f2bf(g * dd[d]);
+  } else {
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) a.dy[o + d] = g * dd[d];
+  }
 }
 
 __device__ __forceinline__ float gelu_t(float v, float& deriv) {
@@ -189,57 +200,55 @@ __global__ void hidden_kernel(BackwardArgs a, size_t total) {
   }
 }
 
-constexpr int WG_T = 64, WG_R = 16;  // router weight-gradient tile: 64 x 64, 16 rows per step
-
-// Row-split weight gradient of one segment: part[c][i][j] = sum over rows
-// r in chunk c (rows c*rc .. c*rc+rc-1, ascending) of A[r][i] * B[r][j].
-__global__ __launch_bounds__(256) void wgrad_part_kernel(const float* __restrict__ A, int M,
-                                                         const float* __restrict__ B, int Nn,
-                                                         int rows, int rc,
-                                                         float* __restrict__ part) {
-  __shared__ float As[WG_R][WG_T + 4];
-  __shared__ float Bs[WG_R][WG_T + 4];
-  const int c = blockIdx.z;
-  const int i0 = blockIdx.y * WG_T, j0 = blockIdx.x * WG_T;
+// d router_w = x^T dlogits, a D x E output reduced over all N rows: row
+// chunk c's partial part[c][d][e] = sum over its rows n ascending of
+// fmaf(x[n][d], dlogits[n][e], .).  Lane l of a workgroup takes column
+// d = 64 * blockIdx.x + l (coalesced x reads), wave w experts
+// 4 JT * blockIdx.z + JT w .. +JT-1 (wave-uniform, so dlogits comes in by scalar
+// loads); JT = 8 experts per wave for E <= 8, else 16; idle waves (past E)
+// return at once.
+template <typename TX, int JT>
+__global__ __launch_bounds__(256) void router_wgrad_kernel(const TX* __restrict__ x, int D,
+                                                           const float* __restrict__ dl, int E,
+                                                           int rows, int rc,
+                                                           float* __restrict__ part) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e0 = blockIdx.z * (4 * JT) + wave * JT;
+  if (e0 >= E) return;
+  const int c = blockIdx.y;
+  const int d = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int dc = min(d, D - 1);  // lanes past D read a valid column and store nothing
   const int r0 = c * rc, r1 = min(rows, r0 + rc);
-  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  float acc[4][4];
+  const int ne = min(JT, E - e0);
+  float acc[JT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < JT; ++j) acc[j] = 0.0f;
+  // rows 8 at a time: the 8 loads go out together, then the FMAs in row order
+  constexpr int RU = 8;
+  for (int n0 = r0; n0 < r1; n0 += RU) {
+    float xv[RU];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  for (int rb = r0; rb < r1; rb += WG_R) {
-    __syncthreads();
-    for (int q = tid; q < WG_R * WG_T; q += 256) {
-      const int rr = q / WG_T, cc = q % WG_T;
-      const int r = rb + rr;
-      As[rr][cc] = (r < r1 && i0 + cc < M) ? A[(size_t)r * M + i0 + cc] : 0.0f;
-      Bs[rr][cc] = (r < r1 && j0 + cc < Nn) ? B[(size_t)r * Nn + j0 + cc] : 0.0f;
-    }
-    __syncthreads();
+    for (int u = 0; u < RU; ++u) xv[u] = ld_x(x + (size_t)min(n0 + u, r1 - 1) * D + dc);
 #pragma unroll
-    for (int rr = 0; rr < WG_R; ++rr) {
-      float av[4], bv[4];
+    for (int u = 0; u < RU; ++u) {
+      if (n0 + u < r1) {
+        const float* dr = dl + (size_t)(n0 + u) * E + e0;
+        if (ne == JT) {  // a full block: one contiguous scalar load of the row's JT values
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[rr][ty * 4 + i];
+          for (int j = 0; j < JT; ++j) acc[j] = __builtin_fmaf(xv[u], dr[j], acc[j]);
+        } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[rr][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+          for (int j = 0; j < JT; ++j)
+            if (j < ne) acc[j] = __builtin_fmaf(xv[u], dr[j], acc[j]);
+        }
+      }
     }
   }
-  float* o = part + (size_t)c * M * Nn;
+  if (d < D) {
+    float* o = part + ((size_t)c * D + d) * E + e0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ii = i0 + ty * 4 + i;
-    if (ii >= M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int jj = j0 + tx * 4 + j;
-      if (jj < Nn) o[(size_t)ii * Nn + jj] = acc[i][j];
-    }
+    for (int j = 0; j < JT; ++j)
+      if (j < ne) o[j] = acc[j];
   }
 }
 
@@ -520,8 +529,23 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   // chunk) to spread the reduction over the GPU
   const int nch = wgrad_router_chunks(N);
   const int rc = (N + nch - 1) / nch;
-  hipLaunchKernelGGL(wgrad_part_kernel, dim3((E + WG_T - 1) / WG_T, (D + WG_T - 1) / WG_T, nch),
-                     dim3(256), 0, s, a.x, D, a.dlogits, E, N, rc, a.wr_part);
+  if (E <= 8) {
+    const dim3 wg((D + 63) / 64, nch, 1);
+    if (a.xb16)
+      hipLaunchKernelGGL((router_wgrad_kernel<uint16_t, 8>), wg, dim3(256), 0, s, a.xb16, D,
+                         a.dlogits, E, N, rc, a.wr_part);
+    else
+      hipLaunchKernelGGL((router_wgrad_kernel<float, 8>), wg, dim3(256), 0, s, a.x, D, a.dlogits,
+                         E, N, rc, a.wr_part);
+  } else {
+    const dim3 wg((D + 63) / 64, nch, (E + 63) / 64);
+    if (a.xb16)
+      hipLaunchKernelGGL((router_wgrad_kernel<uint16_t, 16>), wg, dim3(256), 0, s, a.xb16, D,
+                         a.dlogits, E, N, rc, a.wr_part);
+    else
+      hipLaunchKernelGGL((router_wgrad_kernel<float, 16>), wg, dim3(256), 0, s, a.x, D, a.dlogits,
+                         E, N, rc, a.wr_part);
+  }
   const size_t n = (size_t)D * E;
   hipLaunchKernelGGL(wgrad_sum_kernel, dim3(grid_of(n)), dim3(256), 0, s, a.wr_part, nch, n, a.dwr);
   (void)K;

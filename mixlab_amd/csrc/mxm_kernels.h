@@ -317,6 +317,10 @@ struct BackwardArgs {
   const int32_t* offsets;    // [E + 1]
   const float* probs;        // [N, E]
   const float* Y;            // [N*K, D]
+  // bf16 flow: x and Y as the forward holds them (bf16); when set, the router
+  // part reads these instead of x and Y
+  const uint16_t* xb16;      // [N, D]
+  const uint16_t* Yb16;      // [N*K, D]
   const float* wr;           // [D, E]
   const float* w1;           // [E][D][F] gate (GLU) or up (MLP)
   const float* w1b;          // [E][D][F] up (GLU)
@@ -327,6 +331,7 @@ struct BackwardArgs {
   // scratch
   float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
   float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D]
+  uint16_t* dyb16;           // [N*K, D]: when set, dY is written here in bf16 instead of dy
   float* wrt;                                             // router_w transposed [E][D]
   int32_t* one;                                           // [4]: offsets/mstart of one segment
   float* wr_part;            // [wgrad_router_chunks(N)][D][E]: row-chunk partials of d router_w
