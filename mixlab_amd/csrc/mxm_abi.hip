@@ -451,16 +451,8 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     g1.scale1 = o.s1b.as<float>();
     require_operands(g1, glu, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
-  } else if (o.mfma && pre_out) {
-    g1.mode = MXM_GEMM_RAW;
-    g1.out = pre_out;
-    require_operands(g1, false, false);
-    for (int rep = 0; rep < reps; ++rep) {
-      mxm_launch_gemm_mfma(g1, st);
-      mxm_launch_act_fwd_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope,
-                              static_cast<uint16_t*>(w.H), st);
-    }
   } else if (o.mfma) {
+    g1.out2 = pre_out;  // the backward keeps the raw projections too
     require_operands(g1, false, false);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
   } else {
@@ -1053,8 +1045,8 @@ void check_blas(rocblas_status st, const char* what) {
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
 // permuted order throughout (expert e owns rows offsets[e] ..).
 //   dH  = dY W_down^T          MFMA grouped GEMM, W_down kept as [F][D] bf16
-//   G|U = Xp W1                kept by the forward (mode 3 GEMM, from which
-//                              the forward derives H)
+//   G|U = Xp W1                kept by the forward (its gate+up GEMM stores
+//                              the raw projections beside H, GemmArgs::out2)
 //   dG|dU                      elementwise (act_bw_bf16)
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
 //   dx  = dxr + sum_k dXe      (dx_bf16)

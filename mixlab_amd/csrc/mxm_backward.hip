@@ -394,52 +394,6 @@ __global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16
   }
 }
 
-// H from the pre-activation products gu, 8 hidden units per thread: the
-// values, the activation (mxm_hidden_fast<true>) and the packing are those of
-// the MFMA GEMM's mode 0/1 epilogue, which sees the same bf16-rounded
-// accumulators, so H matches it bit for bit.
-__global__ void act_fwd_bf16_kernel(const uint16_t* __restrict__ gu, int F, int etype, int act,
-                                    float slope, size_t total8, uint16_t* __restrict__ h) {
-  const bool glu = etype != MXM_EXPERT_MLP;
-  const bool split = !mxm_hidden_is_bf16(etype, act);
-  const int NC = glu ? 2 * F : F;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total8;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const size_t e0 = i * 8;  // first element of [rows, F]
-    const size_t r = e0 / F;
-    const int f = (int)(e0 % F);
-    const size_t cu = r * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
-    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
-    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    uint32_t gw[4] = {0u, 0u, 0u, 0u};
-    if (glu) {
-      const uint4 gv = *reinterpret_cast<const uint4*>(gu + cu - 32);
-      gw[0] = gv.x;
-      gw[1] = gv.y;
-      gw[2] = gv.z;
-      gw[3] = gv.w;
-    }
-    uint32_t o[4], ol[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float h0 = mxm_hidden_fast<true>(etype, act, slope, mxm_u2f(gw[q] << 16),
-                                             mxm_u2f(uw[q] << 16));
-      const float h1 = mxm_hidden_fast<true>(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u),
-                                             mxm_u2f(uw[q] & 0xffff0000u));
-      o[q] = mxm_pack_bf2_fast(h0, h1);
-      ol[q] = mxm_pack_bf2_fast(h0 - mxm_rbf_fast(h0), h1 - mxm_rbf_fast(h1));
-    }
-    if (split) {
-      // the two planes of an fp32 hidden: hi at r*2F + f, lo at r*2F + F + f
-      uint16_t* hr = h + r * 2 * F + f;
-      *reinterpret_cast<uint4*>(hr) = make_uint4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<uint4*>(hr + F) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
-    } else {
-      *reinterpret_cast<uint4*>(h + e0) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-  }
-}
-
 // dx[n] = dxr[n] + sum_k dxe[slot_pos(n, k)] (bf16 rows), k ascending
 __global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __restrict__ dxe,
                                const int32_t* __restrict__ slot_pos, int D, int K,
@@ -488,15 +442,6 @@ void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstar
 void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
                                  uint16_t* out, hipStream_t s) {
   if (rows > 0) hipLaunchKernelGGL(gather_rows_bf16_kernel, dim3(rows), dim3(256), 0, s, x, perm, D, out);
-}
-
-void mxm_launch_act_fwd_bf16(const uint16_t* gu, int rows, int F, int etype, int act, float slope,
-                             uint16_t* h, hipStream_t s) {
-  // F is a multiple of 32 (see below)
-  const size_t total8 = (size_t)rows * F / 8;
-  if (total8 > 0)
-    hipLaunchKernelGGL(act_fwd_bf16_kernel, dim3(grid_of(total8)), dim3(256), 0, s, gu, F, etype,
-                       act, slope, total8, h);
 }
 
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,

@@ -441,6 +441,57 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
     }
   };
   const int col = lane & 31;
+  if constexpr (Epi<EPI>::KEEP_RAW) {
+    // the raw bf16 projections (all TN column tiles: gate and up interleaved
+    // as W1's rows) to out2, through the same staging with 64 columns per
+    // wave, before the activation overwrites the accumulators
+    constexpr int CR = TN * 32;
+    static_assert(CR == 64 && NW * WROWS * CR * 2 <= (int)sizeof(u32x4_t) * NS * BUF,
+                  "raw staging fits in LDS");
+    uint32_t* rst = reinterpret_cast<uint32_t*>(lds) + (size_t)wave * (WROWS / 2) * CR;
+    auto rword = [](int kp, int c) -> int {
+      const int b1 = (kp >> 1) & 1;
+      const int ch = (c >> 2) ^ (kp & 1) ^ (b1 << 3);
+      return kp * CR + ch * 4 + (c & 3);
+    };
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const int kp = i * 16 + (r >> 2) * 4 + (lane >> 5) * 2 + ((r & 3) >> 1);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          rst[rword(kp, j * 32 + col)] = mxm_pack_bf2_fast(acc[i][j][r], acc[i][j][r + 1]);
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint16_t* __restrict__ rout = static_cast<uint16_t*>(a.out2);
+    constexpr int RSEGS = CR / 8;
+#pragma unroll
+    for (int it = 0; it < (WROWS / 2) * RSEGS / 64; ++it) {
+      const int q = lane + 64 * it;
+      const int kp = q / RSEGS, sg = q % RSEGS;
+      const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(rst + rword(kp, sg * 8));
+      const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(rst + rword(kp, sg * 8 + 4));
+      const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      u32x4_t lo, hi;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        lo[m] = __builtin_amdgcn_perm(wv[2 * m + 1], wv[2 * m], 0x05040100u);
+        hi[m] = __builtin_amdgcn_perm(wv[2 * m + 1], wv[2 * m], 0x07060302u);
+      }
+      const int grow = wm * WROWS + 2 * kp;
+      const int c0r = n0 + wn * CR + sg * 8;
+      if (grow < rows)
+        *reinterpret_cast<u32x4_t*>(rout + (size_t)(row0 + grow) * a.Ncols + c0r) = lo;
+      if (grow + 1 < rows)
+        *reinterpret_cast<u32x4_t*>(rout + (size_t)(row0 + grow + 1) * a.Ncols + c0r) = hi;
+    }
+    // every wave's staging reads are done before the hidden's staging writes
+    // (the hidden's per-wave regions are laid out at another stride)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
   // kinds whose hidden is fp32 store it as two bf16 planes (hi, then lo =
   // bf16(h - hi)) through the same staging, one plane after the other
   constexpr int NPLANE = H_SPLIT ? 2 : 1;
@@ -583,6 +634,18 @@ void launch_epi(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
 }
 
 template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK>
+void launch_family(const GemmArgs& a, hipStream_t s);
+
+// An up projection that also keeps its raw projections (GemmArgs::out2).
+template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK, int EPI>
+void launch_up(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
+  if (a.out2)
+    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_KEEP + EPI>(a, s, blocks, ngroups);
+  else
+    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI>(a, s, blocks, ngroups);
+}
+
+template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK>
 void launch_family(const GemmArgs& a, hipStream_t s) {
   const int ngroups = (a.max_mtiles + GM - 1) / GM;
   const int per_group = GM * (a.Ncols / BN);
@@ -594,28 +657,24 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
     return;
   }
-  if (a.mode == MXM_GEMM_RAW) {
-    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_RAW>(a, s, blocks, ngroups);
-    return;
-  }
   switch (mxm_epi_kind(a.expert_type, a.activation)) {
     case EPI_GEGLU:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_GEGLU>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_GEGLU>(a, s, blocks, ngroups);
       break;
     case EPI_MLP_SILU:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_SILU>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_SILU>(a, s, blocks, ngroups);
       break;
     case EPI_MLP_GELU:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_GELU>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_GELU>(a, s, blocks, ngroups);
       break;
     case EPI_MLP_RELU:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_RELU>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_RELU>(a, s, blocks, ngroups);
       break;
     case EPI_MLP_LEAKY:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_MLP_LEAKY>(a, s, blocks, ngroups);
       break;
     default:
-      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SWIGLU>(a, s, blocks, ngroups);
+      launch_up<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SWIGLU>(a, s, blocks, ngroups);
       break;
   }
 }

@@ -131,10 +131,8 @@ struct ScatterArgs {
 void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s);
 
 // Grouped expert FFN.  mode: 0 = gate+up with GLU epilogue, 1 = up with MLP
-// activation, 2 = down projection, 3 = the up projections' pre-activation
-// products (A gathered through perm as in 0/1, stored bf16 without the
-// activation; MFMA family only).
-enum { MXM_GEMM_GLU = 0, MXM_GEMM_MLP = 1, MXM_GEMM_DOWN = 2, MXM_GEMM_RAW = 3 };
+// activation, 2 = down projection.
+enum { MXM_GEMM_GLU = 0, MXM_GEMM_MLP = 1, MXM_GEMM_DOWN = 2 };
 
 struct GemmArgs {
   int mode;
@@ -145,6 +143,8 @@ struct GemmArgs {
   const float* scale0;    // int8 weights: per-output-channel scales
   const float* scale1;
   void* out;              // mode 0/1: H [N*K, F]; mode 2: Y [N*K, D]
+  void* out2;             // MFMA up projections: if set, the raw bf16 projections too,
+                          // [N*K, Ncols] in W1's column order (the backward's G|U)
   const int32_t* offsets; // [E + 1]
   const int32_t* mstart;  // [E + 1]
   int E, Kd, Ncols;       // reduction length, output columns (per matrix)
@@ -202,13 +202,18 @@ int mxm_simt_bm();
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
 // projections, or the plain bf16 store of the down projection.
 enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN,
-       EPI_RAW, EPI_DOWN_F32 };
+       EPI_DOWN_F32 };
 
-template <int EPI>
+// EPI_KEEP + an up-projection kind: the same epilogue, which first also
+// stores the raw projections to GemmArgs::out2.
+constexpr int EPI_KEEP = 16;
+
+template <int EPI_>
 struct Epi {
+  static constexpr int EPI = EPI_ % EPI_KEEP;
+  static constexpr bool KEEP_RAW = EPI_ >= EPI_KEEP;
   static constexpr int MODE = EPI <= EPI_GEGLU                         ? MXM_GEMM_GLU
                               : (EPI == EPI_DOWN || EPI == EPI_DOWN_F32) ? MXM_GEMM_DOWN
-                              : EPI == EPI_RAW                          ? MXM_GEMM_RAW
                                                                         : MXM_GEMM_MLP;
   // up projections whose hidden is fp32 in the bf16 flow: H in two planes
   static constexpr bool H_SPLIT = EPI == EPI_GEGLU || EPI == EPI_MLP_GELU || EPI == EPI_MLP_LEAKY;
@@ -354,19 +359,11 @@ void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s);
 // h from g, u alone (the expert forward of an fp32 backward)
 void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
-// bf16 flow on the MFMA family (products by the MFMA grouped GEMM and, for
-// the weight gradients, rocBLAS): gathered bf16 rows, activation backward on
-// the forward's bf16 projections, dx from bf16 expert input gradients, and
-// the GLU pair's gradient de-interleaved into Op.Inputs order.
+// bf16 flow on the MFMA family (products by the MFMA grouped GEMM, weight
+// gradients by mxm_launch_wgrad): gathered bf16 rows, activation backward on
+// the forward's bf16 projections, dx from bf16 expert input gradients.
 void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
                                  uint16_t* out, hipStream_t s);
-// H [rows, F] (bf16) from the up projections' pre-activation products gu
-// [rows, NC] (mode 3 layout: GLU gate/up interleaved in groups of 32), with
-// the MFMA epilogue's own activation code, so H is the same bits as mode 0/1
-// would store (for kinds with an fp32 hidden, the two planes [rows, 2F] of
-// GemmArgs::h_split).
-void mxm_launch_act_fwd_bf16(const uint16_t* gu, int rows, int F, int etype, int act, float slope,
-                             uint16_t* h, hipStream_t s);
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
                             int act, float slope, uint16_t* dgu, hipStream_t s);
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
