@@ -247,6 +247,21 @@ def _check_large(name, sample_rows=256):
     assert err <= BF16_TOL
     assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
     assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"])
+    # every row: the exact-order SIMT kernels on the same op shape compute
+    # the restatement's arithmetic (bit for bit on the sampled rows), so the
+    # MFMA delta is checked against them at full size
+    sdelta, _, _, srouting, sinfo = run_gpu_workload(w, flags=_lib.MXM_FLAG_FORCE_SIMT)
+    assert not sinfo["mfma"]
+    assert_routing_equal(srouting, want)
+    assert same_bits(sdelta[rows], want["delta"][rows])
+    err_all = rel_l2(delta, sdelta)
+    num = np.linalg.norm((delta - sdelta).astype(np.float64), axis=1)
+    den = np.linalg.norm(sdelta.astype(np.float64), axis=1)
+    worst = float(np.max(num / np.maximum(den, 1e-30)))
+    print(f"{name} all {cfg.N} rows against the SIMT kernels: rel L2 {err_all:.3e}, "
+          f"worst row {worst:.3e}")
+    assert err_all <= MFMA_TIGHT
+    assert worst <= BF16_TOL
     return routing
 
 
