@@ -109,6 +109,7 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
         x, wr = round_bf16(x), round_bf16(wr)
         experts = [[round_bf16(m) for m in ws] for ws in experts]
     flags = {"bf16_simt": _lib.MXM_FLAG_FORCE_SIMT,
+             "bf16_mfma": _lib.MXM_FLAG_MFMA_TILE256x256,
              "bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128,
              "bf16_mfma256x128": _lib.MXM_FLAG_MFMA_TILE256x128}.get(flow, 0)
     delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=320, K=2, expert_type=etype,
@@ -173,7 +174,8 @@ def test_mfma_families_many_tiles(gpu_lib, flow):
     x, wr, experts = random_case(4242, N, D, E, F)
     x, wr = round_bf16(x), round_bf16(wr)
     experts = [[round_bf16(m) for m in ws] for ws in experts]
-    flags = {"bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128,
+    flags = {"bf16_mfma": _lib.MXM_FLAG_MFMA_TILE256x256,
+             "bf16_mfma128": _lib.MXM_FLAG_MFMA_TILE128,
              "bf16_mfma256x128": _lib.MXM_FLAG_MFMA_TILE256x128}.get(flow, 0)
     delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=True,
                                              flags=flags)
@@ -183,6 +185,25 @@ def test_mfma_families_many_tiles(gpu_lib, flow):
     assert_routing_equal(routing, want)
     err = rel_l2(delta[rows], want["delta"][rows])
     assert err <= BF16_TOL, err
+
+
+@pytest.mark.parametrize("N,F,bm", [(2048, 256, 128), (16384, 1024, 256)])
+def test_mfma_family_auto(gpu_lib, N, F, bm):
+    """Without a family flag a GEMM takes 256 x 256 tiles only when that
+    gives at least two tiles per CU (2048 tokens x 2 slots, 2F = 512:
+    16 x 2 = 32 tiles -> 128 x 128; 16384 x 2, 2F = 2048: 128 x 8 = 1024
+    tiles -> 256 x 256); either way routing is bit-exact and the delta
+    within the bf16 bar."""
+    D, E, K = 256, 8, 2
+    x, wr, experts = random_case(4343 + N, N, D, E, F)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(m) for m in ws] for ws in experts]
+    delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=True)
+    assert info["mfma"] and info["gemm_bm"] == bm
+    rows = np.sort(np.random.default_rng(6).choice(N, size=256, replace=False)).astype(np.int32)
+    want = run_oracle(x, wr, experts, K=K, bf16=True, rows=rows)
+    assert_routing_equal(routing, want)
+    assert rel_l2(delta[rows], want["delta"][rows]) <= MFMA_TIGHT
 
 
 @pytest.mark.parametrize("E,K", [(1, 1), (2, 1), (2, 2), (3, 2)])
