@@ -8,8 +8,9 @@ expert hidden 1024, 65,536 tokens, bf16; `roofline` is its grouped GEMM
 (both launches) against the bf16 MFMA peak.  The same run also measures C2
 and C3 (the near-uniform and the Zipf-ragged MFMA-bound configurations,
 under "configs"), C5, the decode shape with int8 expert weights (64 tokens;
-HBM-bound, under "decode_int8"), the backward on the C2 shape, and the CPU
-baseline.  Prints one JSON line.
+HBM-bound, under "decode_int8"), the backward on the C2 shape (fp32 and
+bf16) and on the Zipf-ragged C3 shape (bf16), and the CPU baseline.  Prints
+one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
 """
@@ -448,11 +449,13 @@ def main() -> int:
 
     vendor = vendor_gemm(cfg) if args.vendor_gemm else None
 
-    backward = backward_bf16 = None
+    backward = backward_bf16 = backward_bf16_c3 = None
     if not args.no_backward:
         import dataclasses
         backward = run_backward(dataclasses.replace(CONFIGS["C2"], dtype="fp32"), 5, 2)
         backward_bf16 = run_backward(CONFIGS["C2"], 10, 3)
+        # skewed routing: one expert holds 37 % of the rows
+        backward_bf16_c3 = run_backward(CONFIGS["C3"], 3, 2)
 
     line = {
         "metric": METRIC,
@@ -484,6 +487,7 @@ def main() -> int:
         "decode_int8": decode,
         "backward_fp32": backward,
         "backward_bf16": backward_bf16,
+        "backward_bf16_c3": backward_bf16_c3,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

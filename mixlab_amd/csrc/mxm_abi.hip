@@ -154,7 +154,7 @@ struct MoeOp {
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
   bool bw_wbf_ready = false;
-  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u;
+  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
 
@@ -1080,6 +1080,9 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_zero.alloc(512);  // 256 zero bf16: the weight gradients' rows past an expert's end
     HIPCK(hipMemsetAsync(o.bw_zero.p, 0, 512, st));
     o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
+    // the weight gradients' schedule and split-reduction partials (both
+    // launches run in stream order and share it)
+    o.bw_wscr.alloc(std::max(mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(F, D)));
     o.bw_w2o.alloc((size_t)E * DF * 2);
     o.bw_w1u.alloc((size_t)E * D * NC * 2);
   }
@@ -1136,6 +1139,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   WgradArgs wa{};
   wa.offsets = b.offsets;
   wa.zero = o.bw_zero.as<uint16_t>();
+  wa.scratch = o.bw_wscr.p;
   wa.E = E;
   wa.out_estride = stride;
   wa.a = xpb;

@@ -193,9 +193,11 @@ struct WgradArgs {
   size_t out_estride;       // floats between experts' outputs
   size_t out_slot;          // floats from the gate matrix to the up matrix (GLU)
   int glu_f;                // F for GLU de-interleaving, else 0
+  void* scratch;            // mxm_wgrad_scratch_bytes(M, C): the schedule and split partials
 };
 // M and C multiples of 128.
 bool mxm_wgrad_fits(int M, int C);
+size_t mxm_wgrad_scratch_bytes(int M, int C);
 void mxm_launch_wgrad(const WgradArgs& a, hipStream_t s);
 int mxm_simt_bm();
 

@@ -646,6 +646,42 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
+@pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0)])
+def test_backward_bf16_split_reduction(gpu_lib, etype, act, slope):
+    """Weight gradients with few tiles but long reductions: 8,192 tokens top-2
+    over 4 experts (about 4,096 rows = 64 stages of 64 rows each) at D = F =
+    256 give dW1 8 tiles and dW_down 4 tiles for a grid of hundreds of
+    workgroups, so the schedule cuts each expert's rows into chunks (chunk 0
+    into the output, the others into scratch partials that the reduction
+    kernel adds in chunk order).  The second case has a split hidden (two
+    planes), so chunks also start inside the lo plane.  Every expert matrix
+    against the float64 restatement (2e-2) and the SIMT backward (1e-2), and
+    the MFMA result bitwise identical on a second op (the chunk order does
+    not depend on timing)."""
+    from oracle.backward import backward64
+
+    shape = (1, 8192, 256, 4, 256, 2)
+    B, T, D, E, F, K = shape
+    print(f"split reduction etype {etype} act {act} {shape}", flush=True)
+    x, wr, experts, dD, dx, dwr, dexp, routing = _backward_bf16(etype, act, slope, shape, False)
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
+                      bf16=True)
+    assert_routing_equal(routing, want)
+    rows = np.bincount(want["top_idx"].ravel(), minlength=E)
+    assert rows.min() >= 2048, rows  # long reductions on every expert
+    rdx, rdwr, rdexp = backward64(x, wr, experts, want["top_idx"].astype(np.int64), dD, 0.3, -0.2,
+                                  etype, act, slope)
+    assert rel_l2(dx, rdx) <= BF16_TOL
+    assert rel_l2(dwr, rdwr) <= BF16_TOL
+    sdexp = _backward_bf16(etype, act, slope, shape, True)[6]
+    again = _backward_bf16(etype, act, slope, shape, False)[6]
+    for e in range(E):
+        for m in range(len(experts[0])):
+            assert rel_l2(dexp[e][m], rdexp[e][m]) <= BF16_TOL, (e, m)
+            assert rel_l2(dexp[e][m], sdexp[e][m]) <= 1e-2, (e, m)
+            assert np.array_equal(dexp[e][m].view(np.uint32), again[e][m].view(np.uint32)), (e, m)
+
+
 @pytest.mark.parametrize("T", [64, 1536])
 def test_stage_profiling_repeats(gpu_lib, T):
     """Profiled forwards that launch each stage several times between its
