@@ -1065,7 +1065,8 @@ void check_blas(rocblas_status st, const char* what) {
 //                              the raw projections beside H, GemmArgs::out2)
 //   dG|dU                      elementwise (act_bw_bf16)
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
-//   dx  = dxr + sum_k dXe      (dx_bf16)
+//   dx  = dlogits Wr^T + sum_k dXe   (dx_fused_bf16; with a dx that is not
+//                              16-byte aligned: dxr + sum_k dXe, dx_bf16)
 //   dW1 = Xp^T dG|dU, dW_down = H^T dY   MFMA weight-gradient kernel (fp32 out)
 void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* dx, float* dw) {
   hipStream_t st = o.stream;
@@ -1126,7 +1127,10 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // gub holds G|U from the forward (run_forward's pre_out)
   mxm_launch_act_bw_bf16(gub, dhb, (int)NK, F, o.etype, o.act, o.slope, dgub, st);
   product(2, dgub, o.bw_w1u.p, dxeb, NC, D);
-  mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
+  if (b.dxr)
+    mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
+  else
+    mxm_launch_dx_fused_bf16(b.dlogits, b.wrt, E, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
   HIPCK(hipGetLastError());
 
   // weight gradients on MFMA, each reduced over its expert's rows (ragged,
@@ -1289,9 +1293,8 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
       o.bw_dy.alloc(NK * D * 4);
     o.bw_dgates.alloc(NK * 4);
     o.bw_dlogits.alloc(N * E * 4);
-    o.bw_dxr.alloc(N * D * 4);
     o.bw_wrt.alloc(D * E * 4);
-    o.bw_wr_part.alloc((size_t)wgrad_router_chunks(o.N) * D * E * 4);
+    o.bw_wr_part.alloc((size_t)wgrad_router_chunks(o.N, D, E) * D * E * 4);
     o.bw_one.alloc(16);
     o.bw_one_host[1] = o.N;
     o.bw_one_host[3] = (o.N + 63) / 64;
@@ -1408,7 +1411,11 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   if (mfma_bw) b.dyb16 = o.bw_dyb.as<uint16_t>();
   b.dgates = o.bw_dgates.as<float>();
   b.dlogits = o.bw_dlogits.as<float>();
-  b.dxr = o.bw_dxr.as<float>();
+  // the MFMA path fuses dx's router term dlogits . Wr^T into the dx sum
+  // (16-byte aligned dx); otherwise it is a separate product into dxr
+  const bool fuse_dx = mfma_bw && reinterpret_cast<uintptr_t>(dx) % 16 == 0;
+  if (!fuse_dx && !o.bw_dxr.p) o.bw_dxr.alloc(N * D * 4);
+  b.dxr = fuse_dx ? nullptr : o.bw_dxr.as<float>();
   b.wrt = o.bw_wrt.as<float>();
   b.one = o.bw_one.as<int32_t>();
   b.wr_part = o.bw_wr_part.as<float>();

@@ -22,6 +22,8 @@
 // product, issued by the library's host code; the elementwise parts (the
 // gathered rows, the activation derivative, dx) are the launchers at the end.
 // Every result is deterministic.
+#include <algorithm>
+
 #include "mxm_kernels.h"
 
 namespace {
@@ -54,23 +56,68 @@ __global__ void transpose_f32_kernel(const float* __restrict__ src, int R, int C
   }
 }
 
-// one wave per slot: dgates[n*K+k] = <dD[n], Y[slot_pos]>
-__global__ __launch_bounds__(256) void dgates_kernel(BackwardArgs a) {
-  const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (s >= a.N * a.K) return;
-  const int n = s / a.K;
-  const float* dd = a.d_delta + (size_t)n * a.D;
-  const size_t yo = (size_t)a.slot_pos[s] * a.D;
-  float acc = 0.0f;
-  if (a.Yb16) {
-    for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], mxm_bf2f(a.Yb16[yo + d]), acc);
-  } else {
-    for (int d = lane; d < a.D; d += 64) acc = __builtin_fmaf(dd[d], a.Y[yo + d], acc);
-  }
+// One workgroup per token n, for each of its slots s = n*K + k in order:
+// dgates[s] = <dD[n], Y[slot_pos[s]]> and dY[slot_pos[s]] = gates[s] * dD[n]
+// (bf16 or fp32).  V = 4: 4 consecutive d per thread (16-byte dD loads, 8 or
+// 16-byte Y loads and dY stores); V = 1 for shapes or pointers that do not
+// allow it.  The dot product is reduced over the workgroup in a fixed order.
+template <int V>
+__global__ __launch_bounds__(256) void dgates_dy_kernel(BackwardArgs a) {
+  __shared__ float red[4];
+  const int n = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const int D = a.D, K = a.K;
+  const float* dd = a.d_delta + (size_t)n * D;
+  for (int k = 0; k < K; ++k) {
+    const int s = n * K + k;
+    const size_t o = (size_t)a.slot_pos[s] * D;
+    const float g = a.gates[s];
+    float acc = 0.0f;
+    for (int d = tid * V; d < D; d += nt * V) {
+      float dv[V], yv[V];
+      if constexpr (V == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(dd + d);
+        dv[0] = t.x; dv[1] = t.y; dv[2] = t.z; dv[3] = t.w;
+        if (a.Yb16) {
+          const uint2 w = *reinterpret_cast<const uint2*>(a.Yb16 + o + d);
+          yv[0] = mxm_u2f(w.x << 16); yv[1] = mxm_u2f(w.x & 0xffff0000u);
+          yv[2] = mxm_u2f(w.y << 16); yv[3] = mxm_u2f(w.y & 0xffff0000u);
+        } else {
+          const float4 y = *reinterpret_cast<const float4*>(a.Y + o + d);
+          yv[0] = y.x; yv[1] = y.y; yv[2] = y.z; yv[3] = y.w;
+        }
+      } else {
+        dv[0] = dd[d];
+        yv[0] = a.Yb16 ? mxm_bf2f(a.Yb16[o + d]) : a.Y[o + d];
+      }
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc = acc + mxm_xor_lane_f(acc, m);
-  if (lane == 0) a.dgates[s] = acc;
+      for (int q = 0; q < V; ++q) acc = __builtin_fmaf(dv[q], yv[q], acc);
+      if (a.dyb16) {
+        if constexpr (V == 4) {
+          const uint32_t lo = (uint32_t)mxm_f2bf(g * dv[0]) | (uint32_t)mxm_f2bf(g * dv[1]) << 16;
+          const uint32_t hi = (uint32_t)mxm_f2bf(g * dv[2]) | (uint32_t)mxm_f2bf(g * dv[3]) << 16;
+          *reinterpret_cast<uint2*>(a.dyb16 + o + d) = uint2{lo, hi};
+        } else {
+          a.dyb16[o + d] = mxm_f2bf(g * dv[0]);
+        }
+      } else {
+        if constexpr (V == 4)
+          *reinterpret_cast<float4*>(a.dy + o + d) =
+              float4{g * dv[0], g * dv[1], g * dv[2], g * dv[3]};
+        else
+          a.dy[o + d] = g * dv[0];
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc = acc + mxm_xor_lane_f(acc, m);
+    if ((tid & 63) == 0) red[tid >> 6] = acc;
+    __syncthreads();
+    if (tid == 0) {
+      float t = red[0];
+      for (int w = 1; w < nt / 64; ++w) t = t + red[w];
+      a.dgates[s] = t;
+    }
+    __syncthreads();
+  }
 }
 
 // one thread per token: renorm, aux / entropy and softmax backward
@@ -107,20 +154,6 @@ __global__ void router_bw_kernel(BackwardArgs a) {
   for (int e = 0; e < E; ++e) s = s + p[e] * dp_of(e);
   float* out = a.dlogits + (size_t)n * E;
   for (int e = 0; e < E; ++e) out[e] = p[e] * (dp_of(e) - s);
-}
-
-// dY[slot_pos] = gate * dD[n]
-__global__ void dy_kernel(BackwardArgs a) {
-  const int s = blockIdx.x;
-  const int n = s / a.K;
-  const float g = a.gates[s];
-  const float* dd = a.d_delta + (size_t)n * a.D;
-  const size_t o = (size_t)a.slot_pos[s] * a.D;
-  if (a.dyb16) {
-    for (int d = threadIdx.x; d < a.D; d += blockDim.x) a.dyb16[o + d] = mxm_f2bf(g * dd[d]);
-  } else {
-    for (int d = threadIdx.x; d < a.D; d += blockDim.x) a.dy[o + d] = g * dd[d];
-  }
 }
 
 __device__ __forceinline__ float gelu_t(float v, float& deriv) {
@@ -200,67 +233,153 @@ __global__ void hidden_kernel(BackwardArgs a, size_t total) {
   }
 }
 
-// d router_w = x^T dlogits, a D x E output reduced over all N rows: row
-// chunk c's partial part[c][d][e] = sum over its rows n ascending of
-// fmaf(x[n][d], dlogits[n][e], .).  Lane l of a workgroup takes column
-// d = 64 * blockIdx.x + l (coalesced x reads), wave w experts
-// 4 JT * blockIdx.z + JT w .. +JT-1 (wave-uniform, so dlogits comes in by scalar
-// loads); JT = 8 experts per wave for E <= 8, else 16; idle waves (past E)
-// return at once.
+// d router_w = x^T dlogits, a D x E output reduced over all N rows.  Row
+// group c (one workgroup) produces part[c][d][e]; its 4 waves take 4
+// consecutive quarters of the group's rows, each summing fmaf(x[n][d],
+// dlogits[n][e], .) over its rows ascending, and the workgroup adds the
+// waves' sums in wave order through LDS.  The work is a stream of x (N x D)
+// against a few FMAs per element, so the kernel is built to keep loads in
+// flight: 8 consecutive d per lane (one 16-byte bf16 or two 16-byte fp32
+// loads per row), JT experts per wave (dlogits rows by scalar loads), 16
+// (bf16) or 8 (fp32) rows' loads issued together before their FMAs.  Lanes
+// past D store nothing; rows past a quarter reload its last row and add
+// nothing; empty quarters add zeros.
 template <typename TX, int JT>
 __global__ __launch_bounds__(256) void router_wgrad_kernel(const TX* __restrict__ x, int D,
                                                            const float* __restrict__ dl, int E,
-                                                           int rows, int rc,
+                                                           int rows, int rg,
                                                            float* __restrict__ part) {
+  constexpr int DV = 8;                          // d per lane
+  constexpr int RU = sizeof(TX) == 2 ? 16 : 8;   // rows in flight
+  constexpr int W = DV * (int)sizeof(TX) / 16;   // 16-byte words per lane and row
+  __shared__ float xch[DV * JT * 64];            // one wave's sums, [i][j][lane]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int e0 = blockIdx.z * (4 * JT) + wave * JT;
-  if (e0 >= E) return;
+  const int lane = threadIdx.x & 63;
   const int c = blockIdx.y;
-  const int d = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int dc = min(d, D - 1);  // lanes past D read a valid column and store nothing
-  const int r0 = c * rc, r1 = min(rows, r0 + rc);
+  const int e0 = blockIdx.z * JT;
   const int ne = min(JT, E - e0);
-  float acc[JT];
+  const int d0 = blockIdx.x * (64 * DV) + lane * DV;
+  const int rw = (rg + 3) / 4;
+  const int g0 = c * rg, g1 = min(rows, g0 + rg);
+  const int r0 = min(g1, g0 + wave * rw), r1 = min(g1, r0 + rw);
+  // whole 16-byte words need the lane's 8 d inside the row and D % 8 == 0
+  const bool vec = d0 + DV <= D && (D % DV) == 0;
+  float acc[DV][JT];
 #pragma unroll
-  for (int j = 0; j < JT; ++j) acc[j] = 0.0f;
-  // rows 8 at a time: the 8 loads go out together, then the FMAs in row order
-  constexpr int RU = 8;
+  for (int i = 0; i < DV; ++i)
+#pragma unroll
+    for (int j = 0; j < JT; ++j) acc[i][j] = 0.0f;
   for (int n0 = r0; n0 < r1; n0 += RU) {
-    float xv[RU];
-#pragma unroll
-    for (int u = 0; u < RU; ++u) xv[u] = ld_x(x + (size_t)min(n0 + u, r1 - 1) * D + dc);
+    uint4 raw[RU][W];
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
-      if (n0 + u < r1) {
-        const float* dr = dl + (size_t)(n0 + u) * E + e0;
-        if (ne == JT) {  // a full block: one contiguous scalar load of the row's JT values
+      const TX* src = x + (size_t)min(n0 + u, r1 - 1) * D + d0;
+      if (vec) {
 #pragma unroll
-          for (int j = 0; j < JT; ++j) acc[j] = __builtin_fmaf(xv[u], dr[j], acc[j]);
+        for (int q = 0; q < W; ++q) raw[u][q] = reinterpret_cast<const uint4*>(src)[q];
+      } else {
+        float f[DV];
+#pragma unroll
+        for (int i = 0; i < DV; ++i) f[i] = d0 + i < D ? ld_x(src + i) : 0.0f;
+        if constexpr (sizeof(TX) == 4) {
+          raw[u][0] = uint4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                            __float_as_uint(f[3])};
+          raw[u][1] = uint4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]),
+                            __float_as_uint(f[7])};
         } else {
+          // bf16 values are exact in the high half of their fp32 words
+          uint32_t wv[4];
 #pragma unroll
-          for (int j = 0; j < JT; ++j)
-            if (j < ne) acc[j] = __builtin_fmaf(xv[u], dr[j], acc[j]);
+          for (int q = 0; q < 4; ++q)
+            wv[q] = (__float_as_uint(f[2 * q]) >> 16) | (__float_as_uint(f[2 * q + 1]) & 0xffff0000u);
+          raw[u][0] = uint4{wv[0], wv[1], wv[2], wv[3]};
         }
       }
     }
-  }
-  if (d < D) {
-    float* o = part + ((size_t)c * D + d) * E + e0;
 #pragma unroll
-    for (int j = 0; j < JT; ++j)
-      if (j < ne) o[j] = acc[j];
+    for (int u = 0; u < RU; ++u) {
+      if (n0 + u < r1) {
+        float xv[DV];
+        if constexpr (sizeof(TX) == 2) {
+          const uint32_t ws[4] = {raw[u][0].x, raw[u][0].y, raw[u][0].z, raw[u][0].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            xv[2 * q] = mxm_u2f(ws[q] << 16);
+            xv[2 * q + 1] = mxm_u2f(ws[q] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            xv[4 * q] = __uint_as_float(raw[u][q].x);
+            xv[4 * q + 1] = __uint_as_float(raw[u][q].y);
+            xv[4 * q + 2] = __uint_as_float(raw[u][q].z);
+            xv[4 * q + 3] = __uint_as_float(raw[u][q].w);
+          }
+        }
+        const float* dr = dl + (size_t)(n0 + u) * E + e0;
+        float g[JT];
+#pragma unroll
+        for (int j = 0; j < JT; ++j) g[j] = (ne == JT || j < ne) ? dr[j] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < DV; ++i)
+#pragma unroll
+          for (int j = 0; j < JT; ++j) acc[i][j] = __builtin_fmaf(xv[i], g[j], acc[i][j]);
+      }
+    }
+  }
+  // wave 0 adds the other waves' sums in wave order
+  for (int w = 1; w < 4; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int i = 0; i < DV; ++i)
+#pragma unroll
+        for (int j = 0; j < JT; ++j) xch[(i * JT + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < DV; ++i)
+#pragma unroll
+        for (int j = 0; j < JT; ++j) acc[i][j] = acc[i][j] + xch[(i * JT + j) * 64 + lane];
+    }
+    __syncthreads();
+  }
+  if (wave != 0) return;
+#pragma unroll
+  for (int i = 0; i < DV; ++i) {
+    if (d0 + i < D) {
+      float* o = part + ((size_t)c * D + d0 + i) * E + e0;
+#pragma unroll
+      for (int j = 0; j < JT; ++j)
+        if (j < ne) o[j] = acc[i][j];
+    }
   }
 }
 
-// out[q] = sum over chunks c ascending of part[c][q]
-__global__ void wgrad_sum_kernel(const float* __restrict__ part, int nchunks, size_t n,
-                                 float* __restrict__ out) {
-  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n;
-       q += (size_t)gridDim.x * blockDim.x) {
-    float acc = part[q];
-    for (int c = 1; c < nchunks; ++c) acc = acc + part[(size_t)c * n + q];
-    out[q] = acc;
+// out[q] = sum over the partials p of part[p][q], in a fixed order: thread
+// group g (of 4) sums p = g, g + 4, ... ascending for 64 consecutive q, then
+// out = ((s0 + s1) + s2) + s3.
+__global__ __launch_bounds__(256) void wgrad_sum_kernel(const float* __restrict__ part, int np,
+                                                        size_t n, float* __restrict__ out) {
+  __shared__ float sg[4][64];
+  const int g = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const size_t q = (size_t)blockIdx.x * 64 + l;
+  float acc = 0.0f;
+  if (q < n) {
+    constexpr int U = 8;
+    int p = g;
+    for (; p + 4 * (U - 1) < np; p += 4 * U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = part[(size_t)(p + 4 * u) * n + q];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc = acc + v[u];
+    }
+    for (; p < np; p += 4) acc = acc + part[(size_t)p * n + q];
   }
+  sg[g][l] = acc;
+  __syncthreads();
+  if (g == 0 && q < n) out[q] = ((sg[0][l] + sg[1][l]) + sg[2][l]) + sg[3][l];
 }
 
 // dx[n] = dxr[n] + sum_k (dxg + dxu)[slot_pos(n, k)], k ascending
@@ -303,14 +422,73 @@ void grouped(const float* A, const float* B, float* out, int Kd, int NC, const i
 
 // ---- bf16 flow on the MFMA family --------------------------------------------
 
-// out[s] = x[perm[s]] (bf16 rows, permuted order)
-__global__ void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
-                                        const int32_t* __restrict__ perm, int D,
-                                        uint16_t* __restrict__ out) {
-  const int s = blockIdx.x;
-  const uint16_t* src = x + (size_t)perm[s] * D;
-  uint16_t* dst = out + (size_t)s * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
+// out[s] = x[perm[s]] (bf16 rows, permuted order).  VEC: one wave per row,
+// 16-byte pieces (D % 8 == 0 and 16-byte aligned rows).
+template <bool VEC>
+__global__ __launch_bounds__(256) void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
+                                                               const int32_t* __restrict__ perm,
+                                                               int rows, int D,
+                                                               uint16_t* __restrict__ out) {
+  if constexpr (VEC) {
+    const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (s >= rows) return;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)perm[s] * D);
+    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)s * D);
+    for (int i = threadIdx.x & 63; i < D / 8; i += 64) dst[i] = src[i];
+  } else {
+    const int s = blockIdx.x;
+    const uint16_t* src = x + (size_t)perm[s] * D;
+    uint16_t* dst = out + (size_t)s * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
+  }
+}
+
+// dx[n] = dlogits[n] . Wr^T + sum_k dXe[slot_pos(n, k)], k ascending: the
+// router's input gradient (e ascending, fmaf) fused with the sum over the
+// token's slots.  A workgroup takes TT tokens; a thread 4 consecutive d of
+// each 4 * blockDim.x wide block (Wr^T rows [E][D] as float4, shared by the
+// TT tokens).  D % 4 == 0.
+template <int TT>
+__global__ __launch_bounds__(256) void dx_fused_bf16_kernel(const float* __restrict__ dlogits,
+                                                            const float* __restrict__ wrt, int E,
+                                                            const uint16_t* __restrict__ dxe,
+                                                            const int32_t* __restrict__ slot_pos,
+                                                            int N, int D, int K,
+                                                            float* __restrict__ dx) {
+  const int n0 = blockIdx.x * TT;
+  for (int d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {
+    float acc[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[t][q] = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      const float4 w = *reinterpret_cast<const float4*>(wrt + (size_t)e * D + d);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const float l = n0 + t < N ? dlogits[(size_t)(n0 + t) * E + e] : 0.0f;
+        acc[t][0] = __builtin_fmaf(l, w.x, acc[t][0]);
+        acc[t][1] = __builtin_fmaf(l, w.y, acc[t][1]);
+        acc[t][2] = __builtin_fmaf(l, w.z, acc[t][2]);
+        acc[t][3] = __builtin_fmaf(l, w.w, acc[t][3]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int n = n0 + t;
+      if (n >= N) break;
+      for (int k = 0; k < K; ++k) {
+        const uint2 v =
+            *reinterpret_cast<const uint2*>(dxe + (size_t)slot_pos[(size_t)n * K + k] * D + d);
+        acc[t][0] = acc[t][0] + mxm_u2f(v.x << 16);
+        acc[t][1] = acc[t][1] + mxm_u2f(v.x & 0xffff0000u);
+        acc[t][2] = acc[t][2] + mxm_u2f(v.y << 16);
+        acc[t][3] = acc[t][3] + mxm_u2f(v.y & 0xffff0000u);
+      }
+      *reinterpret_cast<float4*>(dx + (size_t)n * D + d) =
+          float4{acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+    }
+  }
 }
 
 // Activation backward on the forward's bf16 projections gu [N*K, NC] (GLU:
@@ -407,16 +585,25 @@ __global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __
   }
 }
 
+// Threads for a row of D elements taken V at a time: whole waves, at most 256.
+int block_for(int D, int V) {
+  const int t = (D + V - 1) / V;
+  return std::min(256, std::max(64, (t + 63) / 64 * 64));
+}
+
 int grid_of(size_t n) {
   size_t b = (n + 255) / 256;
   if (b > 65536) b = 65536;
   return (int)(b < 1 ? 1 : b);
 }
 
-// Row chunks of the router's weight gradient: at most 64, of at least 256 rows.
-int wgrad_router_chunks_impl(int N) {
-  int c = (N + 255) / 256;
-  return c < 1 ? 1 : (c > 64 ? 64 : c);
+// Row groups of the router's weight gradient (one partial each): at least
+// 64 rows each, at most 256 groups and 8 M partial floats in all.
+int wgrad_router_chunks_impl(int N, int D, int E) {
+  long long c = ((long long)N + 63) / 64;
+  const long long budget = (8LL << 20) / std::max(1LL, (long long)D * E);
+  c = std::max(1LL, std::min(c, std::min(256LL, budget)));
+  return (int)c;
 }
 
 // Row-tile prefix of a grouped GEMM family with tile height bm:
@@ -433,7 +620,7 @@ __global__ void tile_prefix_kernel(const int32_t* counts, int E, int bm, int32_t
 
 }  // namespace
 
-int wgrad_router_chunks(int N) { return wgrad_router_chunks_impl(N); }
+int wgrad_router_chunks(int N, int D, int E) { return wgrad_router_chunks_impl(N, D, E); }
 
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s) {
   hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, counts, E, bm, mstart);
@@ -441,7 +628,24 @@ void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstar
 
 void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
                                  uint16_t* out, hipStream_t s) {
-  if (rows > 0) hipLaunchKernelGGL(gather_rows_bf16_kernel, dim3(rows), dim3(256), 0, s, x, perm, D, out);
+  if (rows <= 0) return;
+  const bool vec = D % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL(gather_rows_bf16_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, s, x,
+                       perm, rows, D, out);
+  else
+    hipLaunchKernelGGL(gather_rows_bf16_kernel<false>, dim3(rows), dim3(256), 0, s, x, perm, rows,
+                       D, out);
+}
+
+void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
+                              const int32_t* slot_pos, int N, int D, int K, float* dx,
+                              hipStream_t s) {
+  constexpr int TT = 4;
+  if (N > 0)
+    hipLaunchKernelGGL(dx_fused_bf16_kernel<TT>, dim3((N + TT - 1) / TT), dim3(block_for(D, 4)),
+                       0, s, dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
 }
 
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
@@ -465,34 +669,43 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   const int N = a.N, D = a.D, E = a.E, K = a.K, NK = a.N * a.K;
   if (NK <= 0) return;
   transpose_batch(a.wr, 1, D, E, a.wrt, s);  // [E][D]
-  hipLaunchKernelGGL(dgates_kernel, dim3((NK + 3) / 4), dim3(256), 0, s, a);
+  const auto al = [](const void* p, int b) { return reinterpret_cast<uintptr_t>(p) % b == 0; };
+  const bool vec = D % 4 == 0 && al(a.d_delta, 16) &&
+                   (a.Yb16 ? al(a.Yb16, 8) : al(a.Y, 16)) &&
+                   (a.dyb16 ? al(a.dyb16, 8) : al(a.dy, 16));
+  if (vec)
+    hipLaunchKernelGGL(dgates_dy_kernel<4>, dim3(N), dim3(block_for(D, 4)), 0, s, a);
+  else
+    hipLaunchKernelGGL(dgates_dy_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, a);
   hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
-  hipLaunchKernelGGL(dy_kernel, dim3(NK), dim3(256), 0, s, a);
-  grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
+  // dx's router term; fused into the dx sum by the caller when dxr is unset
+  if (a.dxr) grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
   // router: d router_w = x^T dlogits over all N rows -- a D x E output, so
   // the rows are split in chunks (fixed chunk order, rows ascending within a
   // chunk) to spread the reduction over the GPU
-  const int nch = wgrad_router_chunks(N);
-  const int rc = (N + nch - 1) / nch;
+  const int nch = wgrad_router_chunks(N, D, E);
+  const int rg = (N + nch - 1) / nch;
+  const int dblk = (D + 511) / 512;
   if (E <= 8) {
-    const dim3 wg((D + 63) / 64, nch, 1);
+    const dim3 wg(dblk, nch, 1);
     if (a.xb16)
       hipLaunchKernelGGL((router_wgrad_kernel<uint16_t, 8>), wg, dim3(256), 0, s, a.xb16, D,
-                         a.dlogits, E, N, rc, a.wr_part);
+                         a.dlogits, E, N, rg, a.wr_part);
     else
       hipLaunchKernelGGL((router_wgrad_kernel<float, 8>), wg, dim3(256), 0, s, a.x, D, a.dlogits,
-                         E, N, rc, a.wr_part);
+                         E, N, rg, a.wr_part);
   } else {
-    const dim3 wg((D + 63) / 64, nch, (E + 63) / 64);
+    const dim3 wg(dblk, nch, (E + 15) / 16);
     if (a.xb16)
       hipLaunchKernelGGL((router_wgrad_kernel<uint16_t, 16>), wg, dim3(256), 0, s, a.xb16, D,
-                         a.dlogits, E, N, rc, a.wr_part);
+                         a.dlogits, E, N, rg, a.wr_part);
     else
       hipLaunchKernelGGL((router_wgrad_kernel<float, 16>), wg, dim3(256), 0, s, a.x, D, a.dlogits,
-                         E, N, rc, a.wr_part);
+                         E, N, rg, a.wr_part);
   }
   const size_t n = (size_t)D * E;
-  hipLaunchKernelGGL(wgrad_sum_kernel, dim3(grid_of(n)), dim3(256), 0, s, a.wr_part, nch, n, a.dwr);
+  hipLaunchKernelGGL(wgrad_sum_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, s, a.wr_part,
+                     nch, n, a.dwr);
   (void)K;
 }
 

@@ -337,11 +337,12 @@ struct BackwardArgs {
   float d_aux, d_ent;
   // scratch
   float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
-  float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D]
+  float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D] (dxr unset:
+                                                          // the caller fuses dx's router term)
   uint16_t* dyb16;           // [N*K, D]: when set, dY is written here in bf16 instead of dy
   float* wrt;                                             // router_w transposed [E][D]
   int32_t* one;                                           // [4]: offsets/mstart of one segment
-  float* wr_part;            // [wgrad_router_chunks(N)][D][E]: row-chunk partials of d router_w
+  float* wr_part;            // [wgrad_router_chunks(N, D, E)][D][E]: row-chunk partials of d router_w
   // outputs
   float* dx;                 // [N, D]
   float* dwr;                // [D, E]
@@ -349,7 +350,7 @@ struct BackwardArgs {
 };
 // Row chunks of d router_w's reduction (BackwardArgs::wr_part holds one D x E
 // partial per chunk).
-int wgrad_router_chunks(int N);
+int wgrad_router_chunks(int N, int D, int E);
 // The router part: gate/router gradients, dY, dx's router term and d router_w.
 void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s);
 // The fp32 experts' elementwise parts around their products (which the host
@@ -370,5 +371,10 @@ void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, in
                             int act, float slope, uint16_t* dgu, hipStream_t s);
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
                         int D, int K, float* dx, hipStream_t s);
+// dx = dlogits . Wr^T (wrt = Wr^T [E][D]) + the bf16 expert input gradients
+// summed over each token's slots; D % 4 == 0 and 16-byte aligned rows.
+void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
+                              const int32_t* slot_pos, int N, int D, int K, float* dx,
+                              hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);

@@ -646,6 +646,49 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
+def test_backward_bf16_unaligned_dx(gpu_lib):
+    """mxm_moe_backward on device pointers with dx 4 bytes off 16-byte
+    alignment: the MFMA backward then computes dx's router term as a separate
+    product instead of inside the dx sum.  dx agrees with the aligned call's
+    within fp32 rounding of the two summation orders; d router_w and the
+    expert gradients, computed the same way in both calls, are bitwise
+    equal."""
+    import ctypes
+
+    from mixlab_amd.op import MoEFeedForward
+
+    B, T, D, E, F, K = 2, 96, 256, 6, 256, 2
+    N = B * T
+    x, wr, experts = random_case(83, N, D, E, F, wscale=0.1)
+    rng = np.random.default_rng(84)
+    dD = rng.standard_normal((N, D), dtype=np.float32)
+    lib = _lib.init()
+    outs = []
+    with MoEFeedForward([B, T, D, E, K, 0, F, 0], [0.0], compute_dtype="bf16") as op:
+        op.set_weights(bf16_bits(round_bf16(wr)),
+                       [[bf16_bits(round_bf16(w)) for w in ws] for ws in experts])
+        assert op.info()["mfma"]
+        xdev = _lib.DeviceBuffer.from_array(bf16_bits(round_bf16(x)))
+        ddev = _lib.DeviceBuffer.from_array(dD)
+        for off in (0, 4):
+            dx = _lib.DeviceBuffer(N * D * 4 + 16)
+            dwr = _lib.DeviceBuffer(D * E * 4)
+            dw = _lib.DeviceBuffer(E * 3 * D * F * 4)
+            _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, _lib.MXM_DTYPE_BF16, N,
+                                            ddev.value, 0.3, -0.2, dx.value + off, dwr.value,
+                                            dw.value), "mxm_moe_backward")
+            op.synchronize()
+            hx = np.empty((N, D), np.float32)
+            _lib.check(lib.mxm_memcpy_d2h(hx.ctypes.data, ctypes.c_void_p(dx.value + off),
+                                          hx.nbytes), "mxm_memcpy_d2h")
+            outs.append((hx, dwr.download(np.float32, (D * E,)),
+                         dw.download(np.float32, (E * 3 * D * F,))))
+    (dx0, dwr0, dw0), (dx1, dwr1, dw1) = outs
+    assert rel_l2(dx1, dx0) <= 1e-5
+    assert np.array_equal(dwr0.view(np.uint32), dwr1.view(np.uint32))
+    assert np.array_equal(dw0.view(np.uint32), dw1.view(np.uint32))
+
+
 @pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0)])
 def test_backward_bf16_split_reduction(gpu_lib, etype, act, slope):
     """Weight gradients with few tiles but long reductions: 8,192 tokens top-2
