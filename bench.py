@@ -360,9 +360,10 @@ def main() -> int:
     ap.add_argument("--vendor-gemm-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
-    ap.add_argument("--backward-only", action="store_true",
-                    help="only time the bf16 backward at the C2 shape (10 steps after 3 warm-up) "
-                         "and print its JSON object (for profiling)")
+    ap.add_argument("--backward-only", nargs="?", const="C2", default=None, metavar="CONFIG",
+                    help="only time the bf16 backward at the shape of CONFIG (default C2; 10 "
+                         "steps after 3 warm-up, C3: 3 after 2) and print its JSON object (for "
+                         "profiling)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -374,7 +375,9 @@ def main() -> int:
         return vendor_gemm_child(CONFIGS[args.config])
     if args.backward_only:
         from mixlab_amd.workloads import CONFIGS
-        print(json.dumps({"backward_bf16": run_backward(CONFIGS["C2"], 10, 3)}), flush=True)
+        cfg = CONFIGS[args.backward_only]
+        steps, warm = (10, 3) if cfg.N <= 16384 else (3, 2)
+        print(json.dumps({"backward_bf16": run_backward(cfg, steps, warm)}), flush=True)
         return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -197,7 +197,9 @@ int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t r
  * the MFMA weight family the call is asynchronous on the op's stream (the
  * weight gradients are reduced over each expert's rows on the device); the
  * other flows wait once for the op's stream (the per-expert row counts size
- * their per-expert GEMMs) and leave the rest of their work queued on it. */
+ * their per-expert GEMMs) and leave the rest of their work queued on it.  The
+ * first call allocates the backward's workspace (on MI355X, 128 MiB of it
+ * holds the weight gradients' split-reduction partials). */
 int mxm_moe_backward(int64_t op, const void* x, int x_dtype, int64_t rows, const float* d_delta,
                      float d_aux, float d_entropy, float* dx, float* d_router_w, float* d_experts);
 
