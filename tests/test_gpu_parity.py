@@ -599,7 +599,8 @@ def _backward_bf16(etype, act, slope, shape, simt, skew=0.0):
 
 @pytest.mark.parametrize("etype,act,slope", [(0, 0, 0.0), (1, 1, 0.0), (2, 1, 0.0), (2, 3, 0.4)])
 @pytest.mark.parametrize("flow", ["bf16_mfma", "bf16_simt"])
-@pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 40, 384, 16, 128, 2)])
+@pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 40, 384, 16, 128, 2),
+                                   (1, 2048, 256, 64, 256, 8)])
 def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
     """mxm_moe_backward under bf16 compute: the fp32 backward kernels take
     the bf16 flow's values (x and weights rounded to bf16, the forward's bf16
@@ -608,9 +609,11 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
     Experts with few rows (the second shape has about 5 per expert) carry
     the bf16 flow's error unaveraged (up to 3e-2 on both paths), so there
     each weight-gradient kind is checked over all experts together and per
-    expert only from 16 rows up; experts without rows get exact zeros.  On
+    expert only from 16 rows up; experts without rows get exact zeros.  The
+    third shape has the headline's routing width (64 experts, top-8).  On
     MFMA the weight gradients are the ragged grouped kernel's (256-wide
-    tiles for the first shape, 128-wide for the second, D = 384, F = 128),
+    tiles for the first and third shapes, 128-wide for the second, D = 384,
+    F = 128),
     and every expert's matrices are also held to 1e-2 against the fp32 SIMT
     backward on the same op, which shares the bf16 forward."""
     from oracle.backward import backward64
