@@ -127,6 +127,7 @@ struct MoeOp {
   DevBuf q1, q1b, q2, s1, s1b, s2;
   int n_cu = 256;        // CUs of the op's device
   int fam1 = 0, fam2 = 0;  // MFMA tile families of the up and down GEMMs
+  int fam_dh = 0;           // ... of the backward's dH = dY W_down^T (dX uses fam2)
   std::vector<char> have;
 
   // tile schedule of the forward (set at create from the op's parameters)
@@ -225,6 +226,7 @@ void set_schedule(MoeOp& o) {
     const int nc1 = glu ? 2 * o.F : o.F;
     o.fam1 = pick(nc1);
     o.fam2 = pick(o.D);
+    o.fam_dh = pick(o.F);
     o.bm1 = mxm_mfma_tile_rows(nc1, o.D, o.fam1);
     o.bm2 = mxm_mfma_tile_rows(o.D, o.hsplit ? 2 * o.F : o.F, o.fam2);
   } else {
@@ -1102,8 +1104,11 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
            *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
            *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>();
   mxm_launch_gather_rows_bf16(static_cast<const uint16_t*>(xb), b.perm, (int)NK, D, xpb, st);
-  auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols) {
-    const int bm = mxm_mfma_tile_rows(Ncols, Kd, o.family);
+  // families as the forward picks them for the same output width (dX has
+  // the down projection's, D)
+  auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols,
+                     int family) {
+    const int bm = mxm_mfma_tile_rows(Ncols, Kd, family);
     int32_t* ms = o.bw_ms.as<int32_t>() + (size_t)which * (E + 1);
     mxm_launch_tile_prefix(b.counts, E, bm, ms, st);
     GemmArgs g{};
@@ -1117,16 +1122,16 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     g.Kd = Kd;
     g.Ncols = Ncols;
     g.max_mtiles = (int)((NK + bm - 1) / bm) + E;
-    g.family = o.family;
+    g.family = family;
     g.rows_total = (int)NK;
     require_operands(g, false, false);
     mxm_launch_gemm_mfma(g, st);
     HIPCK(hipGetLastError());
   };
-  product(0, dyb, o.bw_w2o.p, dhb, D, F);
+  product(0, dyb, o.bw_w2o.p, dhb, D, F, o.fam_dh);
   // gub holds G|U from the forward (run_forward's pre_out)
   mxm_launch_act_bw_bf16(gub, dhb, (int)NK, F, o.etype, o.act, o.slope, dgub, st);
-  product(2, dgub, o.bw_w1u.p, dxeb, NC, D);
+  product(2, dgub, o.bw_w1u.p, dxeb, NC, D, o.fam2);
   if (b.dxr)
     mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
   else
