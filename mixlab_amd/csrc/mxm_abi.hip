@@ -145,6 +145,7 @@ struct MoeOp {
   // set by the fp32 backward around its forward: stop after the routing
   // (router, scan, scatter); the backward computes the experts' products itself
   bool route_only = false;
+  bool up_only = false;  // the forward stops after the up projection (MFMA backward)
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
       bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
@@ -155,7 +156,8 @@ struct MoeOp {
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
   bool bw_wbf_ready = false;
-  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr;
+  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
+      bw_ddb, bw_gp, bw_dgp;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
 
@@ -477,6 +479,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_simt(g1, o.bf16, st);
   }
   HIPCK(hipGetLastError());
+  if (o.up_only) return;
 
   mark(4);
   GemmArgs g2{};
@@ -1061,11 +1064,15 @@ void check_blas(rocblas_status st, const char* what) {
 }
 
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
-// permuted order throughout (expert e owns rows offsets[e] ..).
-//   dH  = dY W_down^T          MFMA grouped GEMM, W_down kept as [F][D] bf16
-//   G|U = Xp W1                kept by the forward (its gate+up GEMM stores
+// permuted order throughout (expert e owns rows offsets[e] ..).  The forward
+// stops after its up projection: Y is never formed.
+//   G|U = Xp W1, H             kept by the forward (its gate+up GEMM stores
 //                              the raw projections beside H, GemmArgs::out2)
-//   dG|dU                      elementwise (act_bw_bf16)
+//   dH' = dD[token] W_down^T   MFMA grouped GEMM on the bf16 dD rows gathered
+//                              through perm, W_down kept as [F][D] bf16; not
+//                              yet gated
+//   dgates = <dH', h>          (= <dD, Y>), dH = gate * dH', dG|dU: one pass
+//                              (act_bw_gated_bf16), then the router part
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
 //   dx  = dlogits Wr^T + sum_k dXe   (dx_fused_bf16; with a dx that is not
 //                              16-byte aligned: dxr + sum_k dXe, dx_bf16)
@@ -1088,6 +1095,9 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_wscr.alloc(std::max(mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(F, D)));
     o.bw_w2o.alloc((size_t)E * DF * 2);
     o.bw_w1u.alloc((size_t)E * D * NC * 2);
+    o.bw_ddb.alloc((size_t)o.N * D * 2);
+    o.bw_gp.alloc(NK * 4);
+    o.bw_dgp.alloc(NK * 4);
   }
   if (!o.bw_wbf_ready) {
     for (int e = 0; e < E; ++e) {
@@ -1102,12 +1112,17 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   }
   uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *xpb = o.bw_xpb.as<uint16_t>(),
            *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
-           *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>();
+           *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>(),
+           *ddb = o.bw_ddb.as<uint16_t>();
+  // dD in bf16 per token, dY = gate * dD per slot (for dW_down), the gates by
+  // slot position
+  mxm_launch_dy_gate(b.d_delta, b.gates, b.slot_pos, o.N, D, o.K, ddb, dyb, o.bw_gp.as<float>(),
+                     st);
   mxm_launch_gather_rows_bf16(static_cast<const uint16_t*>(xb), b.perm, (int)NK, D, xpb, st);
   // families as the forward picks them for the same output width (dX has
   // the down projection's, D)
   auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols,
-                     int family) {
+                     int family, bool gather) {
     const int bm = mxm_mfma_tile_rows(Ncols, Kd, family);
     int32_t* ms = o.bw_ms.as<int32_t>() + (size_t)which * (E + 1);
     mxm_launch_tile_prefix(b.counts, E, bm, ms, st);
@@ -1123,15 +1138,27 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     g.Ncols = Ncols;
     g.max_mtiles = (int)((NK + bm - 1) / bm) + E;
     g.family = family;
+    g.gather_a = gather;  // A rows = token rows through perm
+    g.perm = b.perm;
     g.rows_total = (int)NK;
     require_operands(g, false, false);
     mxm_launch_gemm_mfma(g, st);
     HIPCK(hipGetLastError());
   };
-  product(0, dyb, o.bw_w2o.p, dhb, D, F, o.fam_dh);
+  // dH' = dD W_down^T for each slot's token, ungated: with H it gives the
+  // gate gradients <dD, Y> = <dH', h>, and dH = gate * dH'
+  product(0, ddb, o.bw_w2o.p, dhb, D, F, o.fam_dh, true);
   // gub holds G|U from the forward (run_forward's pre_out)
-  mxm_launch_act_bw_bf16(gub, dhb, (int)NK, F, o.etype, o.act, o.slope, dgub, st);
-  product(2, dgub, o.bw_w1u.p, dxeb, NC, D, o.fam2);
+  mxm_launch_act_bw_gated_bf16(gub, dhb, static_cast<const uint16_t*>(o.ws.H), o.hsplit,
+                               o.bw_gp.as<float>(), (int)NK, F, o.etype, o.act, o.slope, dgub,
+                               o.bw_dgp.as<float>(), st);
+  HIPCK(hipGetLastError());
+  // the router part from those gate gradients
+  BackwardArgs br = b;
+  br.dgp = o.bw_dgp.as<float>();
+  mxm_launch_backward_router(br, st);
+  HIPCK(hipGetLastError());
+  product(2, dgub, o.bw_w1u.p, dxeb, NC, D, o.fam2, false);
   if (b.dxr)
     mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);
   else
@@ -1364,13 +1391,16 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   const bool own_forward = !o.bf16;
   o.keep_probs = true;
   o.route_only = own_forward;
+  // the MFMA backward needs the routing, H and G|U only: its gate gradients
+  // come from dD W_down^T (the product that also gives dH), not from Y
+  o.up_only = mfma_bw;
   try {
     run_forward(o, o.ws, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
   } catch (...) {
-    o.keep_probs = o.route_only = false;
+    o.keep_probs = o.route_only = o.up_only = false;
     throw;
   }
-  o.keep_probs = o.route_only = false;
+  o.keep_probs = o.route_only = o.up_only = false;
   // x as the forward saw it (rounded to bf16 when given in fp32)
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.ws.xcast;
   // The MFMA backward's router part reads x and a bf16 Y as they are; the
@@ -1428,8 +1458,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.dwr = dwr;
   b.dw = dw;
   if (mfma_bw) {
-    mxm_launch_backward_router(b, o.stream);
-    HIPCK(hipGetLastError());
     run_backward_mfma(o, xb, b, dx, dw);
     return;
   }

@@ -127,7 +127,11 @@ __global__ void router_bw_kernel(BackwardArgs a) {
   const int K = a.K, E = a.E;
   const float* p = a.probs + (size_t)n * E;
   const int32_t* sel = a.top_idx + (size_t)n * K;
-  const float* dg = a.dgates + (size_t)n * K;
+  // gate gradient of the token's slot k (by slot position when the caller
+  // computed them there)
+  const float* dgs = a.dgates + (size_t)n * K;
+  const int32_t* sp = a.slot_pos + (size_t)n * K;
+  auto dg = [&](int k) { return a.dgp ? a.dgp[sp[k]] : dgs[k]; };
   float S = 0.0f;
   for (int k = 0; k < K; ++k) S = S + p[sel[k]];
   const float Sc = fmaxf(S, 1e-12f);
@@ -135,9 +139,9 @@ __global__ void router_bw_kernel(BackwardArgs a) {
   // d(tp_k) = dg_k / S - sum_j dg_j tp_j / S^2 = sum_j tp_j (dg_k - dg_j) / S^2,
   // the second form free of the cancellation of the first (exactly 0 at K = 1)
   auto dtp_of = [&](int k) {
-    if (!renorm) return dg[k] / Sc;
+    if (!renorm) return dg(k) / Sc;
     float t = 0.0f;
-    for (int j = 0; j < K; ++j) t = t + p[sel[j]] * (dg[k] - dg[j]);
+    for (int j = 0; j < K; ++j) t = t + p[sel[j]] * (dg(k) - dg(j));
     return t / (Sc * Sc);
   };
   const float inv_n = 1.0f / (float)a.N;
@@ -533,6 +537,109 @@ __device__ __forceinline__ void act_bw_one(int etype, int act, float slope, floa
   }
 }
 
+// One workgroup per token n: ddb[n] = bf16(dD[n]); for each slot s = n*K + k
+// at position p = slot_pos[s]: dyb[p] = bf16(gates[s] * dD[n]), gp[p] =
+// gates[s].  V = 4: 4 consecutive d per thread (16-byte dD loads, 8-byte
+// stores).
+template <int V>
+__global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ dd,
+                                                      const float* __restrict__ gates,
+                                                      const int32_t* __restrict__ slot_pos, int D,
+                                                      int K, uint16_t* __restrict__ ddb,
+                                                      uint16_t* __restrict__ dyb,
+                                                      float* __restrict__ gp) {
+  const int n = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const float* src = dd + (size_t)n * D;
+  for (int k = tid; k < K; k += nt) gp[slot_pos[(size_t)n * K + k]] = gates[(size_t)n * K + k];
+  for (int d = tid * V; d < D; d += nt * V) {
+    float v[V];
+    if constexpr (V == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(src + d);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+      *reinterpret_cast<uint2*>(ddb + (size_t)n * D + d) =
+          uint2{(uint32_t)mxm_f2bf(v[0]) | (uint32_t)mxm_f2bf(v[1]) << 16,
+                (uint32_t)mxm_f2bf(v[2]) | (uint32_t)mxm_f2bf(v[3]) << 16};
+    } else {
+      v[0] = src[d];
+      ddb[(size_t)n * D + d] = mxm_f2bf(v[0]);
+    }
+    for (int k = 0; k < K; ++k) {
+      const float g = gates[(size_t)n * K + k];
+      uint16_t* o = dyb + (size_t)slot_pos[(size_t)n * K + k] * D + d;
+      if constexpr (V == 4)
+        *reinterpret_cast<uint2*>(o) =
+            uint2{(uint32_t)mxm_f2bf(g * v[0]) | (uint32_t)mxm_f2bf(g * v[1]) << 16,
+                  (uint32_t)mxm_f2bf(g * v[2]) | (uint32_t)mxm_f2bf(g * v[3]) << 16};
+      else
+        *o = mxm_f2bf(g * v[0]);
+    }
+  }
+}
+
+// One wave per routed row p (4 rows per workgroup), 8 hidden units per lane
+// and step: dH = gp[p] * dhr (dhr = dD W_down^T for the row's token, not yet
+// gated), dG and dU from dH and the forward's raw projections gu exactly as
+// act_bw_bf16_kernel, and the gate gradient dgp[p] = <dhr[p], h[p]> with h
+// the forward's hidden (two bf16 planes hi + lo for a split hidden), summed
+// per lane in f order and then over the wave by a fixed butterfly.
+__global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
+    const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dhr,
+    const uint16_t* __restrict__ H, bool hsplit, const float* __restrict__ gp, int rows, int F,
+    int etype, int act, float slope, uint16_t* __restrict__ dgu, float* __restrict__ dgp) {
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (p >= rows) return;  // (the whole wave)
+  const bool glu = etype != MXM_EXPERT_MLP;
+  const int NC = glu ? 2 * F : F;
+  const float gate = gp[p];
+  float dot = 0.0f;
+  for (int f = lane * 8; f < F; f += 512) {
+    const size_t e0 = (size_t)p * F + f;
+    const uint4 hv = *reinterpret_cast<const uint4*>(dhr + e0);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    const size_t cu = (size_t)p * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
+    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t gw[4] = {0u, 0u, 0u, 0u};
+    if (glu) {
+      const uint4 gv = *reinterpret_cast<const uint4*>(gu + cu - 32);
+      gw[0] = gv.x; gw[1] = gv.y; gw[2] = gv.z; gw[3] = gv.w;
+    }
+    const size_t hrow = (size_t)p * (hsplit ? 2 * F : F) + f;
+    const uint4 xv = *reinterpret_cast<const uint4*>(H + hrow);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t lw[4] = {0u, 0u, 0u, 0u};
+    if (hsplit) {
+      const uint4 lv = *reinterpret_cast<const uint4*>(H + hrow + F);
+      lw[0] = lv.x; lw[1] = lv.y; lw[2] = lv.z; lw[3] = lv.w;
+    }
+    uint32_t og[4], ou[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float r0 = mxm_u2f(hw[q] << 16), r1 = mxm_u2f(hw[q] & 0xffff0000u);
+      float h0 = mxm_u2f(xw[q] << 16), h1 = mxm_u2f(xw[q] & 0xffff0000u);
+      if (hsplit) {
+        h0 = h0 + mxm_u2f(lw[q] << 16);
+        h1 = h1 + mxm_u2f(lw[q] & 0xffff0000u);
+      }
+      dot = __builtin_fmaf(r0, h0, dot);
+      dot = __builtin_fmaf(r1, h1, dot);
+      float dg0, du0, dg1, du1;
+      act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0, dg0,
+                 du0);
+      act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
+                 gate * r1, dg1, du1);
+      og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
+      ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
+    }
+    *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+    if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) dot = dot + mxm_xor_lane_f(dot, m);
+  if (lane == 0) dgp[p] = dot;
+}
+
 __global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dh,
                                    int F, int etype, int act, float slope, size_t total8,
                                    uint16_t* __restrict__ dgu) {
@@ -648,6 +755,27 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
                        0, s, dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
 }
 
+void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
+                        int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s) {
+  if (N <= 0) return;
+  const bool vec = D % 4 == 0 && reinterpret_cast<uintptr_t>(dd) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL(dy_gate_kernel<4>, dim3(N), dim3(block_for(D, 4)), 0, s, dd, gates,
+                       slot_pos, D, K, ddb, dyb, gp);
+  else
+    hipLaunchKernelGGL(dy_gate_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, dd, gates,
+                       slot_pos, D, K, ddb, dyb, gp);
+}
+
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const uint16_t* H,
+                                  bool hsplit, const float* gp, int rows, int F, int etype, int act,
+                                  float slope, uint16_t* dgu, float* dgp, hipStream_t s) {
+  // F is a multiple of 32 (the MFMA family's GLU interleave)
+  if (rows > 0)
+    hipLaunchKernelGGL(act_bw_gated_bf16_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, gu, dhr,
+                       H, hsplit, gp, rows, F, etype, act, slope, dgu, dgp);
+}
+
 void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
                             int act, float slope, uint16_t* dgu, hipStream_t s) {
   // F is a multiple of 32 (the MFMA family's GLU interleave), so rows of 8
@@ -673,10 +801,12 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   const bool vec = D % 4 == 0 && al(a.d_delta, 16) &&
                    (a.Yb16 ? al(a.Yb16, 8) : al(a.Y, 16)) &&
                    (a.dyb16 ? al(a.dyb16, 8) : al(a.dy, 16));
-  if (vec)
-    hipLaunchKernelGGL(dgates_dy_kernel<4>, dim3(N), dim3(block_for(D, 4)), 0, s, a);
-  else
-    hipLaunchKernelGGL(dgates_dy_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, a);
+  if (!a.dgp) {  // (else the caller computed the gate gradients and dY)
+    if (vec)
+      hipLaunchKernelGGL(dgates_dy_kernel<4>, dim3(N), dim3(block_for(D, 4)), 0, s, a);
+    else
+      hipLaunchKernelGGL(dgates_dy_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, a);
+  }
   hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
   // dx's router term; fused into the dx sum by the caller when dxr is unset
   if (a.dxr) grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);

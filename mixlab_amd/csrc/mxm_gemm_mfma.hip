@@ -229,7 +229,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   for (int i = 0; i < QA; ++i) {
     const int r = (wave + NW * i) * RPW + lrow;
     const int p = row0 + min(r, rows - 1);  // rows past the segment reload a valid row
-    const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
+    const int src = (MODE == MXM_GEMM_DOWN && !a.gather_a) ? p : a.perm[p];
     aoff[i] = (size_t)src * Kd + lkc * 8;
   }
   const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kb + lkc * 8;

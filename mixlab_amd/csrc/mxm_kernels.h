@@ -162,6 +162,9 @@ struct GemmArgs {
   // wrapping at F) and stores y in fp32 -- the fp32 matmul of the reference
   // to within 2^-16 relative, since bf16 x bf16 products are exact in fp32.
   bool h_split;
+  // MFMA down projections: gather the A rows through perm (as the up
+  // projections do) instead of reading them in slot order
+  bool gather_a;
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
@@ -337,6 +340,8 @@ struct BackwardArgs {
   float d_aux, d_ent;
   // scratch
   float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
+  const float* dgp;          // [N*K] gate gradients by slot position (set: the caller computed
+                             // them; dgates is then not used)
   float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D] (dxr unset:
                                                           // the caller fuses dx's router term)
   uint16_t* dyb16;           // [N*K, D]: when set, dY is written here in bf16 instead of dy
@@ -376,5 +381,17 @@ void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* sl
 void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
                               const int32_t* slot_pos, int N, int D, int K, float* dx,
                               hipStream_t s);
+// bf16 MFMA backward without the forward's down projection: per token,
+// ddb[n] = bf16(dD[n]) and, per slot s at position p = slot_pos[s],
+// dyb[p] = bf16(gates[s] * dD[n]) and gp[p] = gates[s].
+void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
+                        int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
+// ... then, per routed row p: dH = gp[p] * dhr[p] (dhr = dD W_down^T of the
+// row's token, ungated), dG and dU as mxm_launch_act_bw_bf16, and the gate
+// gradient dgp[p] = <dhr[p], h[p]> (h the forward's hidden H, two planes
+// hi + lo when hsplit).
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const uint16_t* H,
+                                  bool hsplit, const float* gp, int rows, int F, int etype, int act,
+                                  float slope, uint16_t* dgu, float* dgp, hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);
