@@ -326,8 +326,10 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     op.close()
     glu = cfg.expert_type != 2
     nkdf = cfg.N * cfg.K * cfg.D * cfg.F
-    # algorithmic work: forward (3 or 2 products) + dH + dX + weight gradients,
-    # plus the router's forward and backward; recomputation is not counted
+    # algorithmic work of a forward + backward as autodiff forms it: forward
+    # (3 or 2 products) + dH + dX + weight gradients, plus the router's
+    # forward and backward.  (The bf16 MFMA path skips the forward's down
+    # product: the gate gradients come from the dH product itself.)
     fl = 2 * nkdf * ((3 if glu else 2) + 1 + (2 if glu else 1)
                      + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
     tf = fl / (ms * 1e-3) / 1e12
