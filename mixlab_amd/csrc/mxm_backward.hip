@@ -593,47 +593,54 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
   const int NC = glu ? 2 * F : F;
   const float gate = gp[p];
   float dot = 0.0f;
-  for (int f = lane * 8; f < F; f += 512) {
-    const size_t e0 = (size_t)p * F + f;
-    const uint4 hv = *reinterpret_cast<const uint4*>(dhr + e0);
-    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    const size_t cu = (size_t)p * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
-    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
-    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    uint32_t gw[4] = {0u, 0u, 0u, 0u};
-    if (glu) {
-      const uint4 gv = *reinterpret_cast<const uint4*>(gu + cu - 32);
-      gw[0] = gv.x; gw[1] = gv.y; gw[2] = gv.z; gw[3] = gv.w;
-    }
-    const size_t hrow = (size_t)p * (hsplit ? 2 * F : F) + f;
-    const uint4 xv = *reinterpret_cast<const uint4*>(H + hrow);
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-    uint32_t lw[4] = {0u, 0u, 0u, 0u};
-    if (hsplit) {
-      const uint4 lv = *reinterpret_cast<const uint4*>(H + hrow + F);
-      lw[0] = lv.x; lw[1] = lv.y; lw[2] = lv.z; lw[3] = lv.w;
-    }
-    uint32_t og[4], ou[4];
+  const size_t hstride = hsplit ? 2 * (size_t)F : (size_t)F;
+  // U steps of 8 hidden units per lane: their loads go out together
+  constexpr int U = 4;
+  for (int f0 = lane * 8; f0 < F; f0 += 512 * U) {
+    uint4 hv[U], uv[U], gv[U], xv[U], lv[U];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float r0 = mxm_u2f(hw[q] << 16), r1 = mxm_u2f(hw[q] & 0xffff0000u);
-      float h0 = mxm_u2f(xw[q] << 16), h1 = mxm_u2f(xw[q] & 0xffff0000u);
-      if (hsplit) {
-        h0 = h0 + mxm_u2f(lw[q] << 16);
-        h1 = h1 + mxm_u2f(lw[q] & 0xffff0000u);
-      }
-      dot = __builtin_fmaf(r0, h0, dot);
-      dot = __builtin_fmaf(r1, h1, dot);
-      float dg0, du0, dg1, du1;
-      act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0, dg0,
-                 du0);
-      act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
-                 gate * r1, dg1, du1);
-      og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
-      ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
+    for (int j = 0; j < U; ++j) {
+      const int f = min(f0 + 512 * j, F - 8);  // (steps past F reload the last group)
+      const size_t cu = (size_t)p * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
+      hv[j] = *reinterpret_cast<const uint4*>(dhr + (size_t)p * F + f);
+      uv[j] = *reinterpret_cast<const uint4*>(gu + cu);
+      gv[j] = glu ? *reinterpret_cast<const uint4*>(gu + cu - 32) : make_uint4(0u, 0u, 0u, 0u);
+      xv[j] = *reinterpret_cast<const uint4*>(H + (size_t)p * hstride + f);
+      lv[j] = hsplit ? *reinterpret_cast<const uint4*>(H + (size_t)p * hstride + F + f)
+                     : make_uint4(0u, 0u, 0u, 0u);
     }
-    *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
-    if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int f = f0 + 512 * j;
+      if (f >= F) break;
+      const size_t cu = (size_t)p * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
+      const uint32_t hw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+      const uint32_t uw[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+      const uint32_t gw[4] = {gv[j].x, gv[j].y, gv[j].z, gv[j].w};
+      const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+      const uint32_t lw[4] = {lv[j].x, lv[j].y, lv[j].z, lv[j].w};
+      uint32_t og[4], ou[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float r0 = mxm_u2f(hw[q] << 16), r1 = mxm_u2f(hw[q] & 0xffff0000u);
+        float h0 = mxm_u2f(xw[q] << 16), h1 = mxm_u2f(xw[q] & 0xffff0000u);
+        if (hsplit) {
+          h0 = h0 + mxm_u2f(lw[q] << 16);
+          h1 = h1 + mxm_u2f(lw[q] & 0xffff0000u);
+        }
+        dot = __builtin_fmaf(r0, h0, dot);
+        dot = __builtin_fmaf(r1, h1, dot);
+        float dg0, du0, dg1, du1;
+        act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0,
+                   dg0, du0);
+        act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
+                   gate * r1, dg1, du1);
+        og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
+        ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
+      }
+      *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+      if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
+    }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) dot = dot + mxm_xor_lane_f(dot, m);
