@@ -9,8 +9,8 @@ expert hidden 1024, 65,536 tokens, bf16; `roofline` is its grouped GEMM
 and C3 (the near-uniform and the Zipf-ragged MFMA-bound configurations,
 under "configs"), C5, the decode shape with int8 expert weights (64 tokens;
 HBM-bound, under "decode_int8"), the backward on the C2 shape (fp32 and
-bf16) and on the Zipf-ragged C3 shape (bf16), and the CPU baseline.  Prints
-one JSON line.
+bf16), on the Zipf-ragged C3 shape and on the headline shape (bf16), and the
+CPU baseline.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
 """
@@ -278,7 +278,7 @@ def copy_calibration(mib: int, reps: int = 5) -> int:
     return 0
 
 
-def run_backward(cfg, steps: int, warmup: int) -> dict:
+def run_backward(cfg, steps: int, warmup: int, w=None) -> dict:
     """Backward of op 74 (mxm_moe_backward: a forward with the routing kept,
     then the gradients of x, the router and every routed expert) on the
     configuration's compute dtype.  fp32: the routing of the forward, then
@@ -290,7 +290,8 @@ def run_backward(cfg, steps: int, warmup: int) -> dict:
     from mixlab_amd.workloads import make_workload
 
     bf16 = cfg.dtype == "bf16"
-    w = make_workload(cfg)
+    if w is None:
+        w = make_workload(cfg)
     op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype)
     op.set_input(1, w.router_upload() if bf16 else np.ascontiguousarray(w.router_w, np.float32))
     idx = 2
@@ -405,6 +406,10 @@ def main() -> int:
         log("timing the CPU baseline")
         cpu = cpu_baseline(w, cfg, args.cpu_seconds)
         log(f"cpu baseline {cpu}")
+    # the backward at the headline shape, on the same generated workload
+    backward_bf16_main = None
+    if not args.no_backward and cfg.dtype == "bf16" and not cfg.int8_weights:
+        backward_bf16_main = run_backward(cfg, 3, 2, w=w)
     del w
 
     decode = None
@@ -493,6 +498,7 @@ def main() -> int:
         "backward_fp32": backward,
         "backward_bf16": backward_bf16,
         "backward_bf16_c3": backward_bf16_c3,
+        f"backward_bf16_{cfg.name.lower()}": backward_bf16_main,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
