@@ -120,44 +120,77 @@ __global__ __launch_bounds__(256) void dgates_dy_kernel(BackwardArgs a) {
   }
 }
 
-// one thread per token: renorm, aux / entropy and softmax backward
-__global__ void router_bw_kernel(BackwardArgs a) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= a.N) return;
+// One wave per token (4 tokens per workgroup): renorm, aux / entropy and
+// softmax backward.  The token's K slot gate gradients dg_k and selected
+// probabilities go to LDS; lane k computes d(tp_k), which lands at its
+// expert sel[k] (the K experts are distinct); lane e then forms
+// dp_e = aux term - entropy term + d(tp) of e, and dlogits_e =
+// p_e (dp_e - sum_e' p_e' dp_e') with the sum reduced over the wave.
+__global__ __launch_bounds__(256) void router_bw_kernel(BackwardArgs a) {
+  __shared__ float dgs[4][MXM_MAX_EXPERTS], tps[4][MXM_MAX_EXPERTS], add[4][MXM_MAX_EXPERTS];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + wave;
+  if (n >= a.N) return;  // (the whole wave; no workgroup barrier below)
   const int K = a.K, E = a.E;
   const float* p = a.probs + (size_t)n * E;
   const int32_t* sel = a.top_idx + (size_t)n * K;
-  // gate gradient of the token's slot k (by slot position when the caller
-  // computed them there)
-  const float* dgs = a.dgates + (size_t)n * K;
   const int32_t* sp = a.slot_pos + (size_t)n * K;
-  auto dg = [&](int k) { return a.dgp ? a.dgp[sp[k]] : dgs[k]; };
+  // gate gradient of slot k (by slot position when the caller computed them there)
+  for (int k = lane; k < K; k += 64) {
+    dgs[wave][k] = a.dgp ? a.dgp[sp[k]] : a.dgates[(size_t)n * K + k];
+    tps[wave][k] = p[sel[k]];
+  }
+  for (int e = lane; e < E; e += 64) add[wave][e] = 0.0f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float S = 0.0f;
-  for (int k = 0; k < K; ++k) S = S + p[sel[k]];
+  for (int k = 0; k < K; ++k) S = S + tps[wave][k];
   const float Sc = fmaxf(S, 1e-12f);
   const bool renorm = S > 1e-12f;
   // d(tp_k) = dg_k / S - sum_j dg_j tp_j / S^2 = sum_j tp_j (dg_k - dg_j) / S^2,
   // the second form free of the cancellation of the first (exactly 0 at K = 1)
-  auto dtp_of = [&](int k) {
-    if (!renorm) return dg(k) / Sc;
-    float t = 0.0f;
-    for (int j = 0; j < K; ++j) t = t + p[sel[j]] * (dg(k) - dg(j));
-    return t / (Sc * Sc);
-  };
+  for (int k = lane; k < K; k += 64) {
+    const float dgk = dgs[wave][k];
+    float d;
+    if (!renorm) {
+      d = dgk / Sc;
+    } else {
+      float t = 0.0f;
+      for (int j = 0; j < K; ++j) t = t + tps[wave][j] * (dgk - dgs[wave][j]);
+      d = t / (Sc * Sc);
+    }
+    add[wave][sel[k]] = d;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const float inv_n = 1.0f / (float)a.N;
   const float aux_c = a.d_aux * (float)E * inv_n / ((float)K * (float)a.N);
-  auto dp_of = [&](int e) {
-    const float pe = p[e];
-    float v = aux_c * (float)a.counts[e];
-    v = v - a.d_ent * inv_n * (logf(fmaxf(pe, 1e-12f)) + (pe > 1e-12f ? 1.0f : 0.0f));
-    for (int k = 0; k < K; ++k)
-      if (sel[k] == e) v = v + dtp_of(k);
-    return v;
-  };
-  float s = 0.0f;
-  for (int e = 0; e < E; ++e) s = s + p[e] * dp_of(e);
+  constexpr int EL = MXM_MAX_EXPERTS / 64;  // experts per lane
+  float dp[EL], pe[EL];
+  float ps = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EL; ++i) {
+    const int e = lane + 64 * i;
+    dp[i] = 0.0f;
+    pe[i] = 0.0f;
+    if (e < E) {
+      pe[i] = p[e];
+      float v = aux_c * (float)a.counts[e];
+      v = v - a.d_ent * inv_n * (logf(fmaxf(pe[i], 1e-12f)) + (pe[i] > 1e-12f ? 1.0f : 0.0f));
+      dp[i] = v + add[wave][e];
+      ps = __builtin_fmaf(pe[i], dp[i], ps);
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ps = ps + mxm_xor_lane_f(ps, m);
   float* out = a.dlogits + (size_t)n * E;
-  for (int e = 0; e < E; ++e) out[e] = p[e] * (dp_of(e) - s);
+#pragma unroll
+  for (int i = 0; i < EL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) out[e] = pe[i] * (dp[i] - ps);
+  }
 }
 
 __device__ __forceinline__ float gelu_t(float v, float& deriv) {
@@ -814,7 +847,7 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
     else
       hipLaunchKernelGGL(dgates_dy_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, a);
   }
-  hipLaunchKernelGGL(router_bw_kernel, dim3((N + 127) / 128), dim3(128), 0, s, a);
+  hipLaunchKernelGGL(router_bw_kernel, dim3((N + 3) / 4), dim3(256), 0, s, a);
   // dx's router term; fused into the dx sum by the caller when dxr is unset
   if (a.dxr) grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
   // router: d router_w = x^T dlogits over all N rows -- a D x E output, so
