@@ -789,10 +789,15 @@ void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int row
 void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
                               const int32_t* slot_pos, int N, int D, int K, float* dx,
                               hipStream_t s) {
-  constexpr int TT = 4;
-  if (N > 0)
-    hipLaunchKernelGGL(dx_fused_bf16_kernel<TT>, dim3((N + TT - 1) / TT), dim3(block_for(D, 4)),
-                       0, s, dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
+  // tokens per workgroup: each float4 of Wr^T is read once per workgroup
+  // from L2, so wide routers want more tokens to share it
+  if (N <= 0) return;
+  if (E > 16)
+    hipLaunchKernelGGL(dx_fused_bf16_kernel<16>, dim3((N + 15) / 16), dim3(block_for(D, 4)), 0, s,
+                       dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
+  else
+    hipLaunchKernelGGL(dx_fused_bf16_kernel<4>, dim3((N + 3) / 4), dim3(block_for(D, 4)), 0, s,
+                       dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
 }
 
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
