@@ -156,7 +156,7 @@ struct MoeOp {
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
   bool bw_wbf_ready = false;
-  DevBuf bw_dyb, bw_xpb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
+  DevBuf bw_dyb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
       bw_ddb, bw_gp, bw_dgp;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
@@ -1082,8 +1082,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   const bool glu = o.wpe == 3;
   const int D = o.D, F = o.F, E = o.E, NC = glu ? 2 * F : F;
   const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
-  if (!o.bw_xpb.p) {
-    o.bw_xpb.alloc(NK * D * 2);
+  if (!o.bw_dhb.p) {
     o.bw_dhb.alloc(NK * F * 2);
     o.bw_dgub.alloc(NK * NC * 2);
     o.bw_dxeb.alloc(NK * D * 2);
@@ -1110,15 +1109,13 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     HIPCK(hipGetLastError());
     o.bw_wbf_ready = true;
   }
-  uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *xpb = o.bw_xpb.as<uint16_t>(),
-           *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
+  uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
            *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>(),
            *ddb = o.bw_ddb.as<uint16_t>();
   // dD in bf16 per token, dY = gate * dD per slot (for dW_down), the gates by
   // slot position
   mxm_launch_dy_gate(b.d_delta, b.gates, b.slot_pos, o.N, D, o.K, ddb, dyb, o.bw_gp.as<float>(),
                      st);
-  mxm_launch_gather_rows_bf16(static_cast<const uint16_t*>(xb), b.perm, (int)NK, D, xpb, st);
   // families as the forward picks them for the same output width (dX has
   // the down projection's, D)
   auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols,
@@ -1178,7 +1175,9 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   wa.scratch = o.bw_wscr.p;
   wa.E = E;
   wa.out_estride = stride;
-  wa.a = xpb;
+  // dW1's A rows are the tokens' x rows, read in place through perm
+  wa.a = static_cast<const uint16_t*>(xb);
+  wa.a_rows = b.perm;
   wa.lda = D;
   wa.planes = 1;
   wa.b = dgub;
@@ -1191,6 +1190,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   mxm_launch_wgrad(wa, st);
   HIPCK(hipGetLastError());
   wa.a = static_cast<const uint16_t*>(o.ws.H);
+  wa.a_rows = nullptr;
   wa.lda = o.hsplit ? 2 * F : F;
   wa.aplane = F;
   wa.planes = o.hsplit ? 2 : 1;

@@ -459,27 +459,6 @@ void grouped(const float* A, const float* B, float* out, int Kd, int NC, const i
 
 // ---- bf16 flow on the MFMA family --------------------------------------------
 
-// out[s] = x[perm[s]] (bf16 rows, permuted order).  VEC: one wave per row,
-// 16-byte pieces (D % 8 == 0 and 16-byte aligned rows).
-template <bool VEC>
-__global__ __launch_bounds__(256) void gather_rows_bf16_kernel(const uint16_t* __restrict__ x,
-                                                               const int32_t* __restrict__ perm,
-                                                               int rows, int D,
-                                                               uint16_t* __restrict__ out) {
-  if constexpr (VEC) {
-    const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (s >= rows) return;
-    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)perm[s] * D);
-    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)s * D);
-    for (int i = threadIdx.x & 63; i < D / 8; i += 64) dst[i] = src[i];
-  } else {
-    const int s = blockIdx.x;
-    const uint16_t* src = x + (size_t)perm[s] * D;
-    uint16_t* dst = out + (size_t)s * D;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
-  }
-}
-
 // dx[n] = dlogits[n] . Wr^T + sum_k dXe[slot_pos(n, k)], k ascending: the
 // router's input gradient (e ascending, fmaf) fused with the sum over the
 // token's slots.  A workgroup takes TT tokens; a thread 4 consecutive d of
@@ -528,11 +507,8 @@ __global__ __launch_bounds__(256) void dx_fused_bf16_kernel(const float* __restr
   }
 }
 
-// Activation backward on the forward's bf16 projections gu [N*K, NC] (GLU:
-// NC = 2F, gate and up columns interleaved in groups of 32 as the MFMA
-// family's W1 rows; MLP: NC = F, up only) and dH [N*K, F]: writes dG and dU
-// into dgu at the columns of g and u, rounded to bf16.  One thread takes 8
-// consecutive hidden units (16-byte loads and stores; F is a multiple of 32).
+// dG and dU of one hidden unit from its gate and up projections g, u and dH
+// (fp32; GLU: dG and dU, MLP: dU only).
 __device__ __forceinline__ void act_bw_one(int etype, int act, float slope, float g, float u,
                                            float dh, float& dg, float& du) {
   if (etype == MXM_EXPERT_MLP) {
@@ -611,8 +587,10 @@ __global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ 
 
 // One wave per routed row p (4 rows per workgroup), 8 hidden units per lane
 // and step: dH = gp[p] * dhr (dhr = dD W_down^T for the row's token, not yet
-// gated), dG and dU from dH and the forward's raw projections gu exactly as
-// act_bw_bf16_kernel, and the gate gradient dgp[p] = <dhr[p], h[p]> with h
+// gated); dG and dU from dH and the forward's raw bf16 projections gu
+// [N*K, NC] (GLU: NC = 2F, gate and up columns interleaved in groups of 32 as
+// the MFMA family's W1 rows; MLP: NC = F, up only), written to dgu at the
+// columns of g and u in bf16; and the gate gradient dgp[p] = <dhr[p], h[p]> with h
 // the forward's hidden (two bf16 planes hi + lo for a split hidden), summed
 // per lane in f order and then over the wave by a fixed butterfly.
 __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
@@ -680,45 +658,6 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
   if (lane == 0) dgp[p] = dot;
 }
 
-__global__ void act_bw_bf16_kernel(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dh,
-                                   int F, int etype, int act, float slope, size_t total8,
-                                   uint16_t* __restrict__ dgu) {
-  const bool glu = etype != MXM_EXPERT_MLP;
-  const int NC = glu ? 2 * F : F;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total8;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const size_t e0 = i * 8;  // first element of [N*K, F]
-    const size_t r = e0 / F;
-    const int f = (int)(e0 % F);
-    const uint4 hv = *reinterpret_cast<const uint4*>(dh + e0);
-    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    const size_t cu = r * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
-    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
-    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    uint32_t gw[4] = {0u, 0u, 0u, 0u};
-    if (glu) {
-      const uint4 gv = *reinterpret_cast<const uint4*>(gu + cu - 32);
-      gw[0] = gv.x;
-      gw[1] = gv.y;
-      gw[2] = gv.z;
-      gw[3] = gv.w;
-    }
-    uint32_t og[4], ou[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float dg0, du0, dg1, du1;
-      act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16),
-                 mxm_u2f(hw[q] << 16), dg0, du0);
-      act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
-                 mxm_u2f(hw[q] & 0xffff0000u), dg1, du1);
-      og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
-      ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
-    }
-    *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
-    if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
-  }
-}
-
 // dx[n] = dxr[n] + sum_k dxe[slot_pos(n, k)] (bf16 rows), k ascending
 __global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __restrict__ dxe,
                                const int32_t* __restrict__ slot_pos, int D, int K,
@@ -773,19 +712,6 @@ void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstar
   hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, counts, E, bm, mstart);
 }
 
-void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
-                                 uint16_t* out, hipStream_t s) {
-  if (rows <= 0) return;
-  const bool vec = D % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
-  if (vec)
-    hipLaunchKernelGGL(gather_rows_bf16_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, s, x,
-                       perm, rows, D, out);
-  else
-    hipLaunchKernelGGL(gather_rows_bf16_kernel<false>, dim3(rows), dim3(256), 0, s, x, perm, rows,
-                       D, out);
-}
-
 void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
                               const int32_t* slot_pos, int N, int D, int K, float* dx,
                               hipStream_t s) {
@@ -819,16 +745,6 @@ void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const
   if (rows > 0)
     hipLaunchKernelGGL(act_bw_gated_bf16_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, gu, dhr,
                        H, hsplit, gp, rows, F, etype, act, slope, dgu, dgp);
-}
-
-void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
-                            int act, float slope, uint16_t* dgu, hipStream_t s) {
-  // F is a multiple of 32 (the MFMA family's GLU interleave), so rows of 8
-  // hidden units never straddle an interleave group or a row
-  const size_t total8 = (size_t)rows * F / 8;
-  if (total8 > 0)
-    hipLaunchKernelGGL(act_bw_bf16_kernel, dim3(grid_of(total8)), dim3(256), 0, s, gu, dh, F, etype,
-                       act, slope, total8, dgu);
 }
 
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,

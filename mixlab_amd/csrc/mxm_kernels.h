@@ -197,6 +197,7 @@ struct WgradArgs {
   size_t out_slot;          // floats from the gate matrix to the up matrix (GLU)
   int glu_f;                // F for GLU de-interleaving, else 0
   void* scratch;            // mxm_wgrad_scratch_bytes(M, C): the schedule and split partials
+  const int32_t* a_rows;    // if set: A's row for reduction row j is a_rows[j] (else j)
 };
 // M and C multiples of 128.
 bool mxm_wgrad_fits(int M, int C);
@@ -368,12 +369,7 @@ void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s);
 void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
 // bf16 flow on the MFMA family (products by the MFMA grouped GEMM, weight
-// gradients by mxm_launch_wgrad): gathered bf16 rows, activation backward on
-// the forward's bf16 projections, dx from bf16 expert input gradients.
-void mxm_launch_gather_rows_bf16(const uint16_t* x, const int32_t* perm, int rows, int D,
-                                 uint16_t* out, hipStream_t s);
-void mxm_launch_act_bw_bf16(const uint16_t* gu, const uint16_t* dh, int rows, int F, int etype,
-                            int act, float slope, uint16_t* dgu, hipStream_t s);
+// gradients by mxm_launch_wgrad): dx from bf16 expert input gradients.
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
                         int D, int K, float* dx, hipStream_t s);
 // dx = dlogits . Wr^T (wrt = Wr^T [E][D]) + the bf16 expert input gradients
@@ -387,7 +383,8 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
 // ... then, per routed row p: dH = gp[p] * dhr[p] (dhr = dD W_down^T of the
-// row's token, ungated), dG and dU as mxm_launch_act_bw_bf16, and the gate
+// row's token, ungated), dG and dU (the activation backward on the forward's
+// bf16 projections gu), and the gate
 // gradient dgp[p] = <dhr[p], h[p]> (h the forward's hidden H, two planes
 // hi + lo when hsplit).
 void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const uint16_t* H,

@@ -4,10 +4,11 @@
 //
 // over expert e's rows k = offsets[e] .. offsets[e+1]-1 (the forward's
 // permuted slot order) and the planes p of A (two for a hidden stored as
-// bf16 hi and lo planes, else one).  This is dW1 = Xp^T dG|dU (A = the
-// gathered x rows, B = the activation backward's output) and dW_down = H^T dY
-// (A = the forward's hidden, B = the routed output gradient); the reduction
-// runs over the expert's rows, whose count is only known on the device.
+// bf16 hi and lo planes, else one).  This is dW1 = Xp^T dG|dU (A = x, row k
+// read at the token index a_rows[k] of the slot, B = the activation
+// backward's output) and dW_down = H^T dY (A = the forward's hidden, rows in
+// slot order, B = the routed output gradient); the reduction runs over the
+// expert's rows, whose count is only known on the device.
 //
 // Both operands are k-outer: a row of A or B is one k, its columns are
 // contiguous.  Tiles move global -> LDS in that natural layout with
@@ -283,13 +284,16 @@ __device__ void build_plan(WgPlan& P, const int32_t* __restrict__ offsets, int E
 }
 
 
-template <class TL, int BM, int BN, int WM, int WN, int BK, int NS>
+template <class TL, int BM, int BN, int WM, int WN, int BK, int NS, bool GATHER>
 __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
   constexpr int NW = TL::NW, TM = TL::TM, TN = TL::TN;
   constexpr int QA = TL::QA, LDPS = TL::LDPS;
   constexpr int RPWA = TL::RPWA, RPWB = TL::RPWB;
   constexpr int BUF = TL::BUF, A_BYTES = TL::A_BYTES;
   static_assert(BK == WG_BK, "the plan counts 64-row stages");
+  // the stage barrier waits for every load (vmcnt 0), the gathered row
+  // indices included; a deeper ring would have to count them
+  static_assert(NS == 2 || !GATHER, "gathered rows with a two-stage ring only");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[NS * BUF];
   __shared__ WgPlan P;
 
@@ -349,6 +353,28 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
 
     // direct-to-LDS loads q0 .. q1-1 of the item's stage kt (q < QA: A rows,
     // else B rows); the item's stage kt is stage s_lo + kt of the expert
+    // GATHER: A's row for reduction row j is a_rows[j] (the token of a slot:
+    // x read in place instead of a gathered copy).  The rows of the stage to
+    // be loaded next are fetched once the current stage's loads are out, as
+    // scalar loads (the wave's RPWA rows per wave-load are uniform; the lane
+    // picks its own at the DMA), so that waiting for them waits on lgkmcnt
+    // and never on the direct-to-LDS loads in flight.  Rows past the
+    // expert's end read its last index and are not used.
+    using crow_t = const __attribute__((address_space(4))) int32_t;
+    crow_t* __restrict__ arows = (crow_t*)a.a_rows;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    int srow[QA][RPWA];
+    auto load_arows = [&](int kt) {
+      if constexpr (GATHER) {
+        if (kt >= nk) return;
+        const int kk = ((s_lo + kt) % kpp) * BK;
+#pragma unroll
+        for (int q = 0; q < QA; ++q)
+#pragma unroll
+          for (int i = 0; i < RPWA; ++i)
+            srow[q][i] = arows[row0 + min(kk + (wv + NW * q) * RPWA + i, cnt - 1)];
+      }
+    };
     auto dma_part = [&](int kt, int l0, int l1) {
       unsigned char* st = lds + (kt % NS) * BUF;
       const int s = s_lo + kt;
@@ -359,7 +385,14 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
         if (q < QA) {
           const int r = (wave + NW * q) * RPWA + ra;
           const int k = kk + r;
-          const uint16_t* src = k < cnt ? A + (size_t)(row0 + k) * a.lda + p * a.aplane + m0 + lca * 8
+          int arw = row0 + k;
+          if constexpr (GATHER) {
+            arw = srow[q][0];
+#pragma unroll
+            for (int i = 1; i < RPWA; ++i)
+              if (ra == i) arw = srow[q][i];
+          }
+          const uint16_t* src = k < cnt ? A + (size_t)arw * a.lda + p * a.aplane + m0 + lca * 8
                                         : a.zero + lca * 8;
           wg_dma16(src, st + (wave + NW * q) * 1024);
         } else {
@@ -398,8 +431,11 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
 
     // prologue: stages 0 .. NS-2 in flight
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s)
+    for (int s = 0; s < NS - 1; ++s) {
+      load_arows(s);
       if (s < nk) dma_part(s, 0, LDPS);
+    }
+    load_arows(NS - 1);
     constexpr int KS = BK / 16;
     constexpr int DSTEPS = KS >= 2 ? 2 : 1;  // k steps the next stage's loads are spread over
     bf16x8_t af[2][TM], bfm[2][TN];
@@ -416,6 +452,10 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
       // flight), and after the barrier for every wave; the stage read at
       // kt-1 is free and receives stage kt+NS-1
       const int ahead = min(NS - 2, nk - 1 - kt);
+      // the row indices' scalar loads are retired here (lgkmcnt(0), vmcnt and
+      // expcnt left open), where the compiler sees it: with none outstanding,
+      // its waits for the fragment reads below need not count to zero
+      if constexpr (GATHER) __builtin_amdgcn_s_waitcnt(0xC07F);
       if (NS >= 3 && ahead >= 2) wg_stage_barrier<2 * LDPS>();
       else if (ahead >= 1) wg_stage_barrier<LDPS>();
       else wg_stage_barrier<0>();
@@ -445,7 +485,10 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
             else if (nr >= 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
           }
         }
-        if (more && ks < DSTEPS) dma_part(kt + NS - 1, ks * LDPS / DSTEPS, (ks + 1) * LDPS / DSTEPS);
+        if (more && ks < DSTEPS) {
+          dma_part(kt + NS - 1, ks * LDPS / DSTEPS, (ks + 1) * LDPS / DSTEPS);
+          if (ks == DSTEPS - 1) load_arows(kt + NS);  // all of stage kt+NS-1 is out
+        }
       }
     }
     // every wave is done reading the ring before the next item's prologue
@@ -579,8 +622,12 @@ struct WFamily {
     return WG_HDR_BYTES + (size_t)grid() * WG_SLOTS_PER_WG * BM * BN * sizeof(float);
   }
   static void launch(const WgradArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS>), dim3(grid()), dim3(TL::NT), 0,
-                       s, a);
+    if (a.a_rows)
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, true>), dim3(grid()),
+                         dim3(TL::NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, false>), dim3(grid()),
+                         dim3(TL::NT), 0, s, a);
     hipLaunchKernelGGL((wgrad_reduce_kernel<BM, BN>), dim3(std::max(8, n_cus() * 2)), dim3(256),
                        0, s, a);
   }
