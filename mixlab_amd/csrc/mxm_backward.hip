@@ -463,47 +463,127 @@ void grouped(const float* A, const float* B, float* out, int Kd, int NC, const i
 // router's input gradient (e ascending, fmaf) fused with the sum over the
 // token's slots.  A workgroup takes TT tokens; a thread 4 consecutive d of
 // each 4 * blockDim.x wide block (Wr^T rows [E][D] as float4, shared by the
-// TT tokens).  D % 4 == 0.
-template <int TT>
+// TT tokens).  D % 4 == 0.  The workgroup's dlogits rows are staged in LDS
+// once; Wr^T is read 4 experts at a time, one group ahead; the token's KK
+// slot rows are requested together, token t+1's while token t's are summed,
+// so a thread keeps up to 2 KK row loads in flight.  Every global load here
+// is unconditional (the workgroup's tokens all exist, K = KK, the last
+// group's Wr^T rows are clamped and their FMAs skipped): the compiler's
+// wait counts are then exact instead of draining everything in flight.
+// Tokens n_first + blockIdx.x * TT + (0 .. TT-1).
+template <int TT, int KK>
 __global__ __launch_bounds__(256) void dx_fused_bf16_kernel(const float* __restrict__ dlogits,
                                                             const float* __restrict__ wrt, int E,
                                                             const uint16_t* __restrict__ dxe,
                                                             const int32_t* __restrict__ slot_pos,
-                                                            int N, int D, int K,
+                                                            int n_first, int D,
                                                             float* __restrict__ dx) {
-  const int n0 = blockIdx.x * TT;
+  __shared__ __attribute__((aligned(16))) float sdl[TT * MXM_MAX_EXPERTS];
+  const int n0 = n_first + blockIdx.x * TT;
+  const int E4 = (E + 3) & ~3;  // LDS row stride: 16-byte aligned rows
+  for (int i = threadIdx.x; i < TT * E4; i += blockDim.x) {
+    const int t = i / E4, e = i % E4;
+    sdl[i] = e < E ? dlogits[(size_t)(n0 + t) * E + e] : 0.0f;
+  }
+  __syncthreads();
   for (int d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {
     float acc[TT][4];
 #pragma unroll
     for (int t = 0; t < TT; ++t)
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[t][q] = 0.0f;
-    for (int e = 0; e < E; ++e) {
-      const float4 w = *reinterpret_cast<const float4*>(wrt + (size_t)e * D + d);
+    float4 wa[4], wb[4];
+    auto wload = [&](int e0, float4* w) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = *reinterpret_cast<const float4*>(wrt + (size_t)min(e0 + j, E - 1) * D + d);
+    };
+    auto wfma = [&](int e0, const float4* w, auto full) {
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        const float l = n0 + t < N ? dlogits[(size_t)(n0 + t) * E + e] : 0.0f;
-        acc[t][0] = __builtin_fmaf(l, w.x, acc[t][0]);
-        acc[t][1] = __builtin_fmaf(l, w.y, acc[t][1]);
-        acc[t][2] = __builtin_fmaf(l, w.z, acc[t][2]);
-        acc[t][3] = __builtin_fmaf(l, w.w, acc[t][3]);
+        const float4 l = *reinterpret_cast<const float4*>(sdl + t * E4 + e0);
+        const float lj[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!decltype(full)::value && e0 + j >= E) break;
+          acc[t][0] = __builtin_fmaf(lj[j], w[j].x, acc[t][0]);
+          acc[t][1] = __builtin_fmaf(lj[j], w[j].y, acc[t][1]);
+          acc[t][2] = __builtin_fmaf(lj[j], w[j].z, acc[t][2]);
+          acc[t][3] = __builtin_fmaf(lj[j], w[j].w, acc[t][3]);
+        }
       }
+    };
+    // whole groups of 4 experts, the next group requested before the
+    // current one's FMAs (a clamped group past the end is harmless), then
+    // the E % 4 experts left
+    const std::true_type full;
+    const int EF = E & ~3;
+    if (EF > 0) wload(0, wa);
+    for (int e0 = 0; e0 < EF; e0 += 8) {
+      wload(e0 + 4, wb);
+      __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the FMAs
+      wfma(e0, wa, full);
+      if (e0 + 4 >= EF) break;
+      wload(e0 + 8, wa);
+      __builtin_amdgcn_sched_barrier(0);
+      wfma(e0 + 4, wb, full);
     }
+    if (EF < E) {
+      wload(EF, wa);
+      wfma(EF, wa, std::false_type{});
+    }
+
+    uint2 v[2][KK];
+    auto issue = [&](int t, uint2* vv) {
+      const int32_t* sp = slot_pos + (size_t)(n0 + t) * KK;
+#pragma unroll
+      for (int k = 0; k < KK; ++k)
+        vv[k] = *reinterpret_cast<const uint2*>(dxe + (size_t)sp[k] * D + d);
+    };
+    issue(0, v[0]);
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int n = n0 + t;
-      if (n >= N) break;
-      for (int k = 0; k < K; ++k) {
-        const uint2 v =
-            *reinterpret_cast<const uint2*>(dxe + (size_t)slot_pos[(size_t)n * K + k] * D + d);
-        acc[t][0] = acc[t][0] + mxm_u2f(v.x << 16);
-        acc[t][1] = acc[t][1] + mxm_u2f(v.x & 0xffff0000u);
-        acc[t][2] = acc[t][2] + mxm_u2f(v.y << 16);
-        acc[t][3] = acc[t][3] + mxm_u2f(v.y & 0xffff0000u);
+      if (t + 1 < TT) issue(t + 1, v[(t + 1) & 1]);
+#pragma unroll
+      for (int k = 0; k < KK; ++k) {
+        const uint2 x = v[t & 1][k];
+        acc[t][0] = acc[t][0] + mxm_u2f(x.x << 16);
+        acc[t][1] = acc[t][1] + mxm_u2f(x.x & 0xffff0000u);
+        acc[t][2] = acc[t][2] + mxm_u2f(x.y << 16);
+        acc[t][3] = acc[t][3] + mxm_u2f(x.y & 0xffff0000u);
       }
-      *reinterpret_cast<float4*>(dx + (size_t)n * D + d) =
+      *reinterpret_cast<float4*>(dx + (size_t)(n0 + t) * D + d) =
           float4{acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
     }
+  }
+}
+
+// The same sum, one token per workgroup, any K: the tokens a whole group of
+// TT does not cover, and K > 8.  Tokens n_first + blockIdx.x.
+__global__ __launch_bounds__(256) void dx_fused_one_bf16_kernel(
+    const float* __restrict__ dlogits, const float* __restrict__ wrt, int E,
+    const uint16_t* __restrict__ dxe, const int32_t* __restrict__ slot_pos, int n_first, int D,
+    int K, float* __restrict__ dx) {
+  const int n = n_first + blockIdx.x;
+  for (int d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      const float4 w = *reinterpret_cast<const float4*>(wrt + (size_t)e * D + d);
+      const float l = dlogits[(size_t)n * E + e];
+      a0 = __builtin_fmaf(l, w.x, a0);
+      a1 = __builtin_fmaf(l, w.y, a1);
+      a2 = __builtin_fmaf(l, w.z, a2);
+      a3 = __builtin_fmaf(l, w.w, a3);
+    }
+    for (int k = 0; k < K; ++k) {
+      const uint2 x =
+          *reinterpret_cast<const uint2*>(dxe + (size_t)slot_pos[(size_t)n * K + k] * D + d);
+      a0 = a0 + mxm_u2f(x.x << 16);
+      a1 = a1 + mxm_u2f(x.x & 0xffff0000u);
+      a2 = a2 + mxm_u2f(x.y << 16);
+      a3 = a3 + mxm_u2f(x.y & 0xffff0000u);
+    }
+    *reinterpret_cast<float4*>(dx + (size_t)n * D + d) = float4{a0, a1, a2, a3};
   }
 }
 
@@ -718,12 +798,34 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
   // tokens per workgroup: each float4 of Wr^T is read once per workgroup
   // from L2, so wide routers want more tokens to share it
   if (N <= 0) return;
-  if (E > 16)
-    hipLaunchKernelGGL(dx_fused_bf16_kernel<16>, dim3((N + 15) / 16), dim3(block_for(D, 4)), 0, s,
-                       dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
-  else
-    hipLaunchKernelGGL(dx_fused_bf16_kernel<4>, dim3((N + 3) / 4), dim3(block_for(D, 4)), 0, s,
-                       dlogits, wrt, E, dxe, slot_pos, N, D, K, dx);
+  const dim3 blk(block_for(D, 4));
+  int done = 0;
+  auto groups = [&](auto tt, auto kk) {
+    constexpr int TT = decltype(tt)::value, KK = decltype(kk)::value;
+    const int g = N / TT;
+    if (g > 0)
+      hipLaunchKernelGGL((dx_fused_bf16_kernel<TT, KK>), dim3(g), blk, 0, s, dlogits, wrt, E, dxe,
+                         slot_pos, 0, D, dx);
+    done = g * TT;
+  };
+  auto by_k = [&](auto tt) {
+    switch (K) {
+      case 1: groups(tt, std::integral_constant<int, 1>{}); break;
+      case 2: groups(tt, std::integral_constant<int, 2>{}); break;
+      case 3: groups(tt, std::integral_constant<int, 3>{}); break;
+      case 4: groups(tt, std::integral_constant<int, 4>{}); break;
+      case 5: groups(tt, std::integral_constant<int, 5>{}); break;
+      case 6: groups(tt, std::integral_constant<int, 6>{}); break;
+      case 7: groups(tt, std::integral_constant<int, 7>{}); break;
+      case 8: groups(tt, std::integral_constant<int, 8>{}); break;
+      default: break;  // K > 8: every token below
+    }
+  };
+  if (E > 16) by_k(std::integral_constant<int, 16>{});
+  else by_k(std::integral_constant<int, 4>{});
+  if (done < N)
+    hipLaunchKernelGGL(dx_fused_one_bf16_kernel, dim3(N - done), blk, 0, s, dlogits, wrt, E, dxe,
+                       slot_pos, done, D, K, dx);
 }
 
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,

@@ -653,18 +653,25 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
-def test_backward_bf16_unaligned_dx(gpu_lib):
+@pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 1001, 256, 26, 256, 6),
+                                   (1, 1001, 256, 26, 256, 10)])
+def test_backward_bf16_unaligned_dx(gpu_lib, shape):
     """mxm_moe_backward on device pointers with dx 4 bytes off 16-byte
     alignment: the MFMA backward then computes dx's router term as a separate
     product instead of inside the dx sum.  dx agrees with the aligned call's
     within fp32 rounding of the two summation orders; d router_w and the
     expert gradients, computed the same way in both calls, are bitwise
-    equal."""
+    equal.  The aligned call's fused dx pass takes whole groups of 4 tokens
+    (E <= 16) or 16 (E > 16) for K <= 8 and one token at a time otherwise:
+    the shapes cover 4-token groups with E % 4 != 0, 16-token groups with
+    1001 % 16 = 9 tokens left over, and K = 10 (every token on its own); dx
+    is also held to the float64 restatement within the bf16 bar."""
     import ctypes
 
     from mixlab_amd.op import MoEFeedForward
+    from oracle.backward import backward64
 
-    B, T, D, E, F, K = 2, 96, 256, 6, 256, 2
+    B, T, D, E, F, K = shape
     N = B * T
     x, wr, experts = random_case(83, N, D, E, F, wscale=0.1)
     rng = np.random.default_rng(84)
@@ -694,6 +701,11 @@ def test_backward_bf16_unaligned_dx(gpu_lib):
     assert rel_l2(dx1, dx0) <= 1e-5
     assert np.array_equal(dwr0.view(np.uint32), dwr1.view(np.uint32))
     assert np.array_equal(dw0.view(np.uint32), dw1.view(np.uint32))
+    xr, wrr = round_bf16(x), round_bf16(wr)
+    er = [[round_bf16(w) for w in ws] for ws in experts]
+    want = run_oracle(xr, wrr, er, K=K, bf16=True)
+    rdx = backward64(xr, wrr, er, want["top_idx"].astype(np.int64), dD, 0.3, -0.2, 0, 0, 0.0)[0]
+    assert rel_l2(dx0, rdx) <= BF16_TOL
 
 
 @pytest.mark.parametrize("etype,act,slope,case", [(0, 0, 0.0, "uniform"), (1, 1, 0.0, "uniform"),
