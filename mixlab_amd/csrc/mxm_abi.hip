@@ -9,8 +9,10 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <array>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -146,6 +148,9 @@ struct MoeOp {
   // (router, scan, scatter); the backward computes the experts' products itself
   bool route_only = false;
   bool up_only = false;  // the forward stops after the up projection (MFMA backward)
+  // d router_w in the MFMA backward: on the weight-gradient kernel (1), on
+  // the SIMT kernel (0), or by size (-1); MXM_ROUTER_WGRAD_MFMA at creation
+  int dwr_mode = -1;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
       bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
@@ -157,7 +162,7 @@ struct MoeOp {
   // handle for the weight gradients
   bool bw_wbf_ready = false;
   DevBuf bw_dyb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
-      bw_ddb, bw_gp, bw_dgp;
+      bw_ddb, bw_gp, bw_dgp, bw_dlb, bw_dwr2;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
 
@@ -781,6 +786,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     if (!int_params || n_int_params < 8)
       fail("OP_MOE_FEED_FORWARD requires B,T,D,E,topK,expertType,ffn,activation");
     auto o = std::make_unique<MoeOp>();
+    if (const char* v = std::getenv("MXM_ROUTER_WGRAD_MFMA")) o->dwr_mode = std::atoi(v) != 0;
     o->B = int_params[0];
     o->T = int_params[1];
     o->D = int_params[2];
@@ -1082,6 +1088,13 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   const bool glu = o.wpe == 3;
   const int D = o.D, F = o.F, E = o.E, NC = glu ? 2 * F : F;
   const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
+  // d router_w = x^T dlogits is N*D*E fmaf on the SIMT kernel: from 2^28 of
+  // them on (C3's shape has 2^30, C2's 2^26) the weight-gradient kernel's
+  // product is faster than that VALU work, below it its schedule and
+  // reduction cost more
+  const bool dwr_mfma =
+      o.dwr_mode >= 0 ? o.dwr_mode == 1 : (double)o.N * D * E >= (double)(1 << 28);
+  const int Ep = (E + 63) / 64 * 64;  // that product's hi and lo halves of Ep columns
   if (!o.bw_dhb.p) {
     o.bw_dhb.alloc(NK * F * 2);
     o.bw_dgub.alloc(NK * NC * 2);
@@ -1091,7 +1104,12 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
     // the weight gradients' schedule and split-reduction partials (both
     // launches run in stream order and share it)
-    o.bw_wscr.alloc(std::max(mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(F, D)));
+    o.bw_wscr.alloc(std::max({mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(F, D),
+                              dwr_mfma ? mxm_wgrad_scratch_bytes(D, 2 * Ep) : 0}));
+    if (dwr_mfma) {
+      o.bw_dlb.alloc((size_t)o.N * 2 * Ep * 2);
+      o.bw_dwr2.alloc((size_t)D * 2 * Ep * 4);
+    }
     o.bw_w2o.alloc((size_t)E * DF * 2);
     o.bw_w1u.alloc((size_t)E * D * NC * 2);
     o.bw_ddb.alloc((size_t)o.N * D * 2);
@@ -1153,8 +1171,34 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // the router part from those gate gradients
   BackwardArgs br = b;
   br.dgp = o.bw_dgp.as<float>();
+  br.dwr_by_caller = dwr_mfma;
   mxm_launch_backward_router(br, st);
   HIPCK(hipGetLastError());
+  // d router_w = x^T dlogits on the weight-gradient kernel: one segment of
+  // all N token rows (b.one = {0, N}), B = dlogits as bf16 hi and lo halves,
+  // the two halves' products added at the end
+  if (dwr_mfma && !mxm_wgrad_fits(D, 2 * Ep))
+    fail("OP_MOE_FEED_FORWARD backward: router weight-gradient tiles need D a multiple of 128 "
+         "(D=%d)", D);
+  if (dwr_mfma) {
+    mxm_launch_dl_split_bf16(b.dlogits, o.N, E, Ep, o.bw_dlb.as<uint16_t>(), st);
+    WgradArgs ra{};
+    ra.a = static_cast<const uint16_t*>(xb);
+    ra.lda = D;
+    ra.planes = 1;
+    ra.b = o.bw_dlb.as<uint16_t>();
+    ra.ldb = 2 * Ep;
+    ra.offsets = b.one;
+    ra.zero = o.bw_zero.as<uint16_t>();
+    ra.E = 1;
+    ra.M = D;
+    ra.C = 2 * Ep;
+    ra.out = o.bw_dwr2.as<float>();
+    ra.scratch = o.bw_wscr.p;
+    mxm_launch_wgrad(ra, st);
+    mxm_launch_dwr_halves(o.bw_dwr2.as<float>(), D, E, Ep, b.dwr, st);
+    HIPCK(hipGetLastError());
+  }
   product(2, dgub, o.bw_w1u.p, dxeb, NC, D, o.fam2, false);
   if (b.dxr)
     mxm_launch_dx_bf16(b.dxr, dxeb, b.slot_pos, o.N, D, o.K, dx, st);

@@ -459,6 +459,47 @@ void grouped(const float* A, const float* B, float* out, int Kd, int NC, const i
 
 // ---- bf16 flow on the MFMA family --------------------------------------------
 
+// One thread per 8 columns of a row of out [N][2 Ep]: hi = bf16(dl) at
+// columns e, lo = bf16(dl - hi) at Ep + e (dl - hi is exact in fp32), zeros
+// past E.  hi + lo carries dl to about 2^-16 relative.
+__global__ void dl_split_kernel(const float* __restrict__ dl, int E, int Ep,
+                                uint16_t* __restrict__ out, size_t total) {
+  const int nb = Ep / 8;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t n = i / nb;
+    const int e0 = (int)(i % nb) * 8;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float h2[2], l2[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = e0 + 2 * q + r;
+        const float v = e < E ? dl[n * E + e] : 0.0f;
+        h2[r] = mxm_rbf_fast(v);
+        l2[r] = v - h2[r];
+      }
+      hw[q] = mxm_pack_bf2_fast(h2[0], h2[1]);
+      lw[q] = mxm_pack_bf2_fast(l2[0], l2[1]);
+    }
+    uint16_t* row = out + n * 2 * Ep;
+    *reinterpret_cast<uint4*>(row + e0) = uint4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<uint4*>(row + Ep + e0) = uint4{lw[0], lw[1], lw[2], lw[3]};
+  }
+}
+
+// dwr[d][e] = t[d][e] + t[d][Ep + e]: x^T hi plus x^T lo.
+__global__ void dwr_halves_kernel(const float* __restrict__ t, int E, int Ep,
+                                  float* __restrict__ dwr, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t d = i / E;
+    const int e = (int)(i % E);
+    dwr[i] = t[d * 2 * Ep + e] + t[d * 2 * Ep + Ep + e];
+  }
+}
+
 // dx[n] = dlogits[n] . Wr^T + sum_k dXe[slot_pos(n, k)], k ascending: the
 // router's input gradient (e ascending, fmaf) fused with the sum over the
 // token's slots.  A workgroup takes TT tokens; a thread 4 consecutive d of
@@ -828,6 +869,20 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
                        slot_pos, done, D, K, dx);
 }
 
+void mxm_launch_dl_split_bf16(const float* dl, int N, int E, int Ep, uint16_t* out, hipStream_t s) {
+  const size_t total = (size_t)N * (Ep / 8);
+  if (total > 0)
+    hipLaunchKernelGGL(dl_split_kernel, dim3(grid_of(total)), dim3(256), 0, s, dl, E, Ep, out,
+                       total);
+}
+
+void mxm_launch_dwr_halves(const float* t, int D, int E, int Ep, float* dwr, hipStream_t s) {
+  const size_t total = (size_t)D * E;
+  if (total > 0)
+    hipLaunchKernelGGL(dwr_halves_kernel, dim3(grid_of(total)), dim3(256), 0, s, t, E, Ep, dwr,
+                       total);
+}
+
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s) {
   if (N <= 0) return;
@@ -873,6 +928,7 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(router_bw_kernel, dim3((N + 3) / 4), dim3(256), 0, s, a);
   // dx's router term; fused into the dx sum by the caller when dxr is unset
   if (a.dxr) grouped(a.dlogits, a.wrt, a.dxr, E, D, a.one, a.one + 2, 1, (N + 63) / 64, s);
+  if (a.dwr_by_caller) return;
   // router: d router_w = x^T dlogits over all N rows -- a D x E output, so
   // the rows are split in chunks (fixed chunk order, rows ascending within a
   // chunk) to spread the reduction over the GPU

@@ -349,6 +349,7 @@ struct BackwardArgs {
   float* wrt;                                             // router_w transposed [E][D]
   int32_t* one;                                           // [4]: offsets/mstart of one segment
   float* wr_part;            // [wgrad_router_chunks(N, D, E)][D][E]: row-chunk partials of d router_w
+  bool dwr_by_caller;        // set: the caller computes d router_w (wr_part is not used)
   // outputs
   float* dx;                 // [N, D]
   float* dwr;                // [D, E]
@@ -380,6 +381,13 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
 // bf16 MFMA backward without the forward's down projection: per token,
 // ddb[n] = bf16(dD[n]) and, per slot s at position p = slot_pos[s],
 // dyb[p] = bf16(gates[s] * dD[n]) and gp[p] = gates[s].
+// d router_w on the weight-gradient kernel: dlogits [N][E] as bf16 halves
+// hi = bf16(dl), lo = bf16(dl - hi) in out [N][2 Ep] (hi at column e, lo at
+// Ep + e, zeros for e >= E; Ep = E rounded up to 64), so that x^T out holds
+// x^T hi and x^T lo side by side ...
+void mxm_launch_dl_split_bf16(const float* dl, int N, int E, int Ep, uint16_t* out, hipStream_t s);
+// ... and dwr[d][e] = t[d][e] + t[d][Ep + e] from that product t [D][2 Ep].
+void mxm_launch_dwr_halves(const float* t, int D, int E, int Ep, float* dwr, hipStream_t s);
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
 // ... then, per routed row p: dH = gp[p] * dhr[p] (dhr = dD W_down^T of the

@@ -653,6 +653,52 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
+@pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 2048, 256, 64, 256, 8),
+                                   (1, 1000, 384, 72, 128, 4)])
+def test_backward_bf16_router_wgrad_paths(gpu_lib, monkeypatch, shape):
+    """d router_w = x^T dlogits in the MFMA backward on either kernel: the
+    SIMT one (fmaf over rows in fixed chunks) or the weight-gradient kernel's
+    product with dlogits as bf16 hi and lo halves (E rounded up to 64 columns
+    each), chosen by size unless MXM_ROUTER_WGRAD_MFMA sets it when the op is
+    created.  On the same inputs the two d router_w agree within 1e-5
+    relative L2 (the halves carry dlogits to about 2^-16; without the lo half
+    the error would be about 2e-3), dx and the expert gradients are bitwise
+    equal, and d router_w matches the float64 restatement within the bf16
+    bar.  The shapes pad 6 experts to 64 columns, take the headline's 64,
+    and 72 (two column groups per half) with 1000 rows, not a multiple of
+    the 64-row stage, on the 128-wide tiles (D = 384)."""
+    from mixlab_amd.op import MoEFeedForward
+    from oracle.backward import backward64
+
+    B, T, D, E, F, K = shape
+    N = B * T
+    x, wr, experts = random_case(85, N, D, E, F, wscale=0.1)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(w) for w in ws] for ws in experts]
+    dD = np.random.default_rng(86).standard_normal((N, D), dtype=np.float32)
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MXM_ROUTER_WGRAD_MFMA", mode)
+        with MoEFeedForward([B, T, D, E, K, 0, F, 0], [0.0], compute_dtype="bf16") as op:
+            op.set_weights(bf16_bits(wr), [[bf16_bits(w) for w in ws] for ws in experts])
+            assert op.info()["mfma"]
+            outs[mode] = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
+    (dx1, dwr1, dexp1), (dx0, dwr0, dexp0) = outs["1"], outs["0"]
+    err = rel_l2(dwr1, dwr0)
+    assert 0.0 < err <= 1e-5, err
+    assert np.array_equal(dx1.view(np.uint32), dx0.view(np.uint32))
+    for e in range(E):
+        for m in range(len(experts[0])):
+            assert np.array_equal(np.asarray(dexp1[e][m]).view(np.uint32),
+                                  np.asarray(dexp0[e][m]).view(np.uint32)), (e, m)
+    want = run_oracle(x, wr, experts, K=K, bf16=True)
+    rdwr = backward64(x, wr, experts, want["top_idx"].astype(np.int64), dD, 0.3, -0.2, 0, 0,
+                      0.0)[1]
+    assert rel_l2(dwr1, rdwr) <= BF16_TOL
+    print(f"{shape}: d router_w, product vs SIMT kernel {err:.2e}, vs float64 "
+          f"{rel_l2(dwr1, rdwr):.2e}")
+
+
 @pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 1001, 256, 26, 256, 6),
                                    (1, 1001, 256, 26, 256, 10)])
 def test_backward_bf16_unaligned_dx(gpu_lib, shape):
