@@ -66,6 +66,16 @@ __device__ __forceinline__ void wg_dma16(const void* g, const void* lds) {
                : "memory", "m0");
 }
 
+// The same load from a uniform 64-bit base in SGPRs plus the lane's 32-bit
+// byte offset (the SGPR-base form: no 64-bit address arithmetic per load).
+__device__ __forceinline__ void wg_dma16s(const void* base, unsigned off_bytes, const void* lds) {
+  const unsigned lb = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off_bytes), "s"(base), "s"(lb)
+               : "memory", "m0");
+}
+
 template <int N>
 __device__ __forceinline__ void wg_stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
@@ -351,8 +361,28 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     const int lca = (lane % (BM / 8)) ^ (((wave * RPWA + ra) & 3) << 2);
     const int lcb = (lane % (BN / 8)) ^ (((wave * RPWB + rb) & 3) << 2);
 
-    // direct-to-LDS loads q0 .. q1-1 of the item's stage kt (q < QA: A rows,
-    // else B rows); the item's stage kt is stage s_lo + kt of the expert
+    // The item's stages are loaded in order; (dp, dkk) is the plane and the
+    // first reduction row (within the expert) of the next stage to load,
+    // advanced one stage at a time (no division in the loop).
+    int dp = s_lo / kpp, dkk = (s_lo % kpp) * BK;
+    const int kend = kpp * BK;
+    auto next_stage = [&]() {
+      dkk += BK;
+      if (dkk >= kend) {
+        dkk = 0;
+        ++dp;
+      }
+    };
+    // element offsets of this lane's loads within a whole stage, fixed for
+    // the item: the stage adds a uniform base (rows row0 + dkk, plane dp)
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    int a_lane[QA], b_lane[LDPS - QA];
+#pragma unroll
+    for (int q = 0; q < QA; ++q) a_lane[q] = ((wv + NW * q) * RPWA + ra) * a.lda + m0 + lca * 8;
+#pragma unroll
+    for (int q = 0; q < LDPS - QA; ++q)
+      b_lane[q] = ((wv + NW * q) * RPWB + rb) * a.ldb + c0 + lcb * 8;
+
     // GATHER: A's row for reduction row j is a_rows[j] (the token of a slot:
     // x read in place instead of a gathered copy).  The rows of the stage to
     // be loaded next are fetched once the current stage's loads are out, as
@@ -362,46 +392,68 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     // expert's end read its last index and are not used.
     using crow_t = const __attribute__((address_space(4))) int32_t;
     crow_t* __restrict__ arows = (crow_t*)a.a_rows;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
     int srow[QA][RPWA];
-    auto load_arows = [&](int kt) {
+    auto load_arows = [&](int kt) {  // rows of the next stage to load (dkk)
       if constexpr (GATHER) {
         if (kt >= nk) return;
-        const int kk = ((s_lo + kt) % kpp) * BK;
 #pragma unroll
         for (int q = 0; q < QA; ++q)
 #pragma unroll
           for (int i = 0; i < RPWA; ++i)
-            srow[q][i] = arows[row0 + min(kk + (wv + NW * q) * RPWA + i, cnt - 1)];
+            srow[q][i] = arows[row0 + min(dkk + (wv + NW * q) * RPWA + i, cnt - 1)];
       }
     };
+    // direct-to-LDS loads q0 .. q1-1 (q < QA: A rows, else B rows) of the
+    // next stage to load, into ring slot kt % NS
     auto dma_part = [&](int kt, int l0, int l1) {
       unsigned char* st = lds + (kt % NS) * BUF;
-      const int s = s_lo + kt;
-      const int p = s / kpp, kk = (s % kpp) * BK;
+      const int p = dp, kk = dkk;
+      if (kk + BK <= cnt) {
+        // a whole stage of rows
+        const uint16_t* as = A + (size_t)(row0 + kk) * a.lda + (size_t)p * a.aplane;
+        const uint16_t* bs = B + (size_t)(row0 + kk) * a.ldb;
 #pragma unroll
-      for (int q = 0; q < LDPS; ++q) {
-        if (q < l0 || q >= l1) continue;
-        if (q < QA) {
-          const int r = (wave + NW * q) * RPWA + ra;
-          const int k = kk + r;
-          int arw = row0 + k;
-          if constexpr (GATHER) {
-            arw = srow[q][0];
+        for (int q = 0; q < LDPS; ++q) {
+          if (q < l0 || q >= l1) continue;
+          if (q < QA) {
+            if constexpr (GATHER) {
+              int arw = srow[q][0];
 #pragma unroll
-            for (int i = 1; i < RPWA; ++i)
-              if (ra == i) arw = srow[q][i];
+              for (int i = 1; i < RPWA; ++i)
+                if (ra == i) arw = srow[q][i];
+              wg_dma16(A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8,
+                       st + (wv + NW * q) * 1024);
+            } else {
+              wg_dma16s(as, 2u * (unsigned)a_lane[q], st + (wv + NW * q) * 1024);
+            }
+          } else {
+            wg_dma16s(bs, 2u * (unsigned)b_lane[q - QA], st + A_BYTES + (wv + NW * (q - QA)) * 1024);
           }
-          const uint16_t* src = k < cnt ? A + (size_t)arw * a.lda + p * a.aplane + m0 + lca * 8
-                                        : a.zero + lca * 8;
-          wg_dma16(src, st + (wave + NW * q) * 1024);
-        } else {
-          const int qb = q - QA;
-          const int r = (wave + NW * qb) * RPWB + rb;
-          const int k = kk + r;
-          const uint16_t* src =
-              k < cnt ? B + (size_t)(row0 + k) * a.ldb + c0 + lcb * 8 : a.zero + lcb * 8;
-          wg_dma16(src, st + A_BYTES + (wave + NW * qb) * 1024);
+        }
+      } else {
+        // the expert's last, partial stage: rows past its end load the zero row
+#pragma unroll
+        for (int q = 0; q < LDPS; ++q) {
+          if (q < l0 || q >= l1) continue;
+          if (q < QA) {
+            const int k = kk + (wv + NW * q) * RPWA + ra;
+            int arw = row0 + k;
+            if constexpr (GATHER) {
+              arw = srow[q][0];
+#pragma unroll
+              for (int i = 1; i < RPWA; ++i)
+                if (ra == i) arw = srow[q][i];
+            }
+            const uint16_t* src = k < cnt ? A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8
+                                          : a.zero + lca * 8;
+            wg_dma16(src, st + (wv + NW * q) * 1024);
+          } else {
+            const int qb = q - QA;
+            const int k = kk + (wv + NW * qb) * RPWB + rb;
+            const uint16_t* src =
+                k < cnt ? B + (size_t)(row0 + k) * a.ldb + c0 + lcb * 8 : a.zero + lcb * 8;
+            wg_dma16(src, st + A_BYTES + (wv + NW * qb) * 1024);
+          }
         }
       }
     };
@@ -434,6 +486,7 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     for (int s = 0; s < NS - 1; ++s) {
       load_arows(s);
       if (s < nk) dma_part(s, 0, LDPS);
+      next_stage();
     }
     load_arows(NS - 1);
     constexpr int KS = BK / 16;
@@ -487,7 +540,10 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
         }
         if (more && ks < DSTEPS) {
           dma_part(kt + NS - 1, ks * LDPS / DSTEPS, (ks + 1) * LDPS / DSTEPS);
-          if (ks == DSTEPS - 1) load_arows(kt + NS);  // all of stage kt+NS-1 is out
+          if (ks == DSTEPS - 1) {  // all of stage kt+NS-1 is out
+            next_stage();
+            load_arows(kt + NS);
+          }
         }
       }
     }
