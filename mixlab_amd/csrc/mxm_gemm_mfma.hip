@@ -131,6 +131,16 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
                : "memory", "m0");
 }
 
+// The same load from a uniform 64-bit base in SGPRs plus the lane's 32-bit
+// byte offset (the SGPR-base form: no 64-bit address arithmetic per load).
+__device__ __forceinline__ void dma16s(const void* base, unsigned off_bytes, const void* lds) {
+  const unsigned lb = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off_bytes), "s"(base), "s"(lb)
+               : "memory", "m0");
+}
+
 // Wait until at most N of this thread's direct-to-LDS loads are in flight and
 // its LDS reads are done, then the workgroup barrier.
 template <int N>
@@ -232,8 +242,13 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
     const int src = (MODE == MXM_GEMM_DOWN && !a.gather_a) ? p : a.perm[p];
     aoff[i] = (size_t)src * Kd + lkc * 8;
   }
-  const uint16_t* bsrc = B + (size_t)(n0 + wave * RPW + lrow) * Kb + lkc * 8;
   const size_t bstep = (size_t)(NW * RPW) * Kb;
+  // the B loads as 32-bit byte offsets from the expert's matrix (one expert's
+  // Ncols x Kb bf16 stays far below 4 GiB); the wave index in an SGPR keeps
+  // every load's LDS destination scalar
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const unsigned boff = (unsigned)(2 * ((size_t)(n0 + wv * RPW + lrow) * Kb + lkc * 8));
+  const unsigned bstep_b = (unsigned)(2 * bstep);
 
 // Direct-to-LDS loads Q0 .. Q1-1 of one stage (load q < QA fills A rows,
 // the rest B rows).
@@ -241,10 +256,10 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   do {                                                                                        \
     _Pragma("unroll") for (int q_ = (Q0); q_ < (Q1); ++q_) {                                  \
       if (q_ < QA) {                                                                          \
-        dma16(A + aoff[q_] + (K0), STAGE + (wave + NW * q_) * 64);                            \
+        dma16(A + aoff[q_] + (K0), STAGE + (wv + NW * q_) * 64);                              \
       } else {                                                                                \
-        dma16(bsrc + (q_ - QA) * bstep + (DOWN_SPLIT && (K0) >= Kb ? (K0) - Kb : (K0)),     \
-              STAGE + A_CH + (wave + NW * (q_ - QA)) * 64);                                   \
+        dma16s(B + (DOWN_SPLIT && (K0) >= Kb ? (K0) - Kb : (K0)), boff + (q_ - QA) * bstep_b, \
+               STAGE + A_CH + (wv + NW * (q_ - QA)) * 64);                                    \
       }                                                                                       \
     }                                                                                         \
   } while (0)
@@ -683,6 +698,8 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
 
 int mxm_mfma_tile_rows(int Ncols, int Kd, int family) {
   if (Kd % 64 != 0) return 0;
+  // B loads address one expert's matrix with 32-bit byte offsets
+  if ((size_t)Ncols * Kd * 2 >= ((size_t)1 << 32)) return 0;
   const bool f256 = Ncols % 256 == 0, f128 = Ncols % 128 == 0;
   switch (family) {
     case MXM_TILE_256x128:
