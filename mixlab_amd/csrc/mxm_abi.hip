@@ -1222,6 +1222,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // dW1's A rows are the tokens' x rows, read in place through perm
   wa.a = static_cast<const uint16_t*>(xb);
   wa.a_rows = b.perm;
+  wa.a_rows32 = (size_t)o.N * D * 2 < ((size_t)1 << 32);
   wa.lda = D;
   wa.planes = 1;
   wa.b = dgub;

@@ -198,6 +198,7 @@ struct WgradArgs {
   int glu_f;                // F for GLU de-interleaving, else 0
   void* scratch;            // mxm_wgrad_scratch_bytes(M, C): the schedule and split partials
   const int32_t* a_rows;    // if set: A's row for reduction row j is a_rows[j] (else j)
+  bool a_rows32;            // with a_rows: all of A lies within 4 GiB of a (32-bit offsets)
 };
 // M and C multiples of 128.
 bool mxm_wgrad_fits(int M, int C);

@@ -382,6 +382,11 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
 #pragma unroll
     for (int q = 0; q < LDPS - QA; ++q)
       b_lane[q] = ((wv + NW * q) * RPWB + rb) * a.ldb + c0 + lcb * 8;
+    // GATHER with A below 4 GiB: the lane's column part in bytes and A's row
+    // pitch in bytes (rows are added per stage from the scalar row indices)
+    const unsigned a_colb = 2u * (unsigned)(m0 + lca * 8);
+    const unsigned a_pitch = 2u * (unsigned)a.lda;
+    const bool a32 = GATHER && a.a_rows32;
 
     // GATHER: A's row for reduction row j is a_rows[j] (the token of a slot:
     // x read in place instead of a gathered copy).  The rows of the stage to
@@ -412,24 +417,39 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
         // a whole stage of rows
         const uint16_t* as = A + (size_t)(row0 + kk) * a.lda + (size_t)p * a.aplane;
         const uint16_t* bs = B + (size_t)(row0 + kk) * a.ldb;
+        auto whole = [&](auto off32) {
 #pragma unroll
-        for (int q = 0; q < LDPS; ++q) {
-          if (q < l0 || q >= l1) continue;
-          if (q < QA) {
-            if constexpr (GATHER) {
-              int arw = srow[q][0];
+          for (int q = 0; q < LDPS; ++q) {
+            if (q < l0 || q >= l1) continue;
+            if (q < QA) {
+              if constexpr (GATHER && decltype(off32)::value) {
+                // each candidate row's byte offset (scalar) plus the lane's
+                // column; the lane takes its own row's
+                unsigned off = (unsigned)srow[q][0] * a_pitch + a_colb;
 #pragma unroll
-              for (int i = 1; i < RPWA; ++i)
-                if (ra == i) arw = srow[q][i];
-              wg_dma16(A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8,
-                       st + (wv + NW * q) * 1024);
+                for (int i = 1; i < RPWA; ++i) {
+                  const unsigned oi = (unsigned)srow[q][i] * a_pitch + a_colb;
+                  if (ra == i) off = oi;
+                }
+                wg_dma16s(A + (size_t)p * a.aplane, off, st + (wv + NW * q) * 1024);
+              } else if constexpr (GATHER) {
+                int arw = srow[q][0];
+#pragma unroll
+                for (int i = 1; i < RPWA; ++i)
+                  if (ra == i) arw = srow[q][i];
+                wg_dma16(A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8,
+                         st + (wv + NW * q) * 1024);
+              } else {
+                wg_dma16s(as, 2u * (unsigned)a_lane[q], st + (wv + NW * q) * 1024);
+              }
             } else {
-              wg_dma16s(as, 2u * (unsigned)a_lane[q], st + (wv + NW * q) * 1024);
+              wg_dma16s(bs, 2u * (unsigned)b_lane[q - QA],
+                        st + A_BYTES + (wv + NW * (q - QA)) * 1024);
             }
-          } else {
-            wg_dma16s(bs, 2u * (unsigned)b_lane[q - QA], st + A_BYTES + (wv + NW * (q - QA)) * 1024);
           }
-        }
+        };
+        if (a32) whole(std::true_type{});
+        else whole(std::false_type{});
       } else {
         // the expert's last, partial stage: rows past its end load the zero row
 #pragma unroll
