@@ -174,6 +174,10 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
                                                                             int nblocks) {
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // A = [hi | lo] planes, y in fp32
+  // 32-bit A offsets (when A fits) for the forward's up projections only:
+  // measured faster there, slower for the down projection and for the
+  // raw-keeping variant, whose extra registers spill
+  constexpr bool A_OFF32 = MODE != MXM_GEMM_DOWN && !Epi<EPI>::KEEP_RAW;
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // H stored as [hi | lo] planes
   constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN;
   constexpr int A_CH = TL::A_CH, BUF = TL::BUF;
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
     const int r = (wave + NW * i) * RPW + lrow;
     const int p = row0 + min(r, rows - 1);  // rows past the segment reload a valid row
     const int src = (MODE == MXM_GEMM_DOWN && !a.gather_a) ? p : a.perm[p];
-    aoff[i] = (size_t)src * Kd + lkc * 8;
+    aoff[i] = 2 * ((size_t)src * Kd + lkc * 8);  // bytes
   }
   const size_t bstep = (size_t)(NW * RPW) * Kb;
   // the B loads as 32-bit byte offsets from the expert's matrix (one expert's
@@ -252,15 +256,24 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 
 // Direct-to-LDS loads Q0 .. Q1-1 of one stage (load q < QA fills A rows,
 // the rest B rows).
+#define MXM_DMA_LOOP(STAGE, K0, Q0, Q1, ALOAD)                                                \
+  _Pragma("unroll") for (int q_ = (Q0); q_ < (Q1); ++q_) {                                    \
+    if (q_ < QA) {                                                                            \
+      ALOAD;                                                                                  \
+    } else {                                                                                  \
+      dma16s(B + (DOWN_SPLIT && (K0) >= Kb ? (K0) - Kb : (K0)), boff + (q_ - QA) * bstep_b,   \
+             STAGE + A_CH + (wv + NW * (q_ - QA)) * 64);                                      \
+    }                                                                                         \
+  }
 #define MXM_DMA_PART(STAGE, K0, Q0, Q1)                                                       \
   do {                                                                                        \
-    _Pragma("unroll") for (int q_ = (Q0); q_ < (Q1); ++q_) {                                  \
-      if (q_ < QA) {                                                                          \
-        dma16(A + aoff[q_] + (K0), STAGE + (wv + NW * q_) * 64);                              \
-      } else {                                                                                \
-        dma16s(B + (DOWN_SPLIT && (K0) >= Kb ? (K0) - Kb : (K0)), boff + (q_ - QA) * bstep_b, \
-               STAGE + A_CH + (wv + NW * (q_ - QA)) * 64);                                    \
-      }                                                                                       \
+    if (A_OFF32 && a.a_off32) {                                                               \
+      MXM_DMA_LOOP(STAGE, K0, Q0, Q1,                                                         \
+                   dma16s(A + (K0), (unsigned)aoff[q_], STAGE + (wv + NW * q_) * 64))         \
+    } else {                                                                                  \
+      MXM_DMA_LOOP(STAGE, K0, Q0, Q1,                                                         \
+                   dma16(reinterpret_cast<const char*>(A + (K0)) + aoff[q_],                  \
+                         STAGE + (wv + NW * q_) * 64))                                        \
     }                                                                                         \
   } while (0)
 #define MXM_DMA(STAGE, K0) MXM_DMA_PART(STAGE, K0, 0, LDPS)
@@ -719,8 +732,10 @@ static int resolve_family(const GemmArgs& a) {
   return a.Ncols % 256 == 0 ? MXM_TILE_256x256 : MXM_TILE_128x128;
 }
 
-void mxm_launch_gemm_mfma(const GemmArgs& a, hipStream_t s) {
-  if (a.max_mtiles <= 0) return;
+void mxm_launch_gemm_mfma(const GemmArgs& args, hipStream_t s) {
+  if (args.max_mtiles <= 0) return;
+  GemmArgs a = args;
+  a.a_off32 = (size_t)a.rows_total * a.Kd * 2 < ((size_t)1 << 32);
   switch (resolve_family(a)) {
     case MXM_TILE_256x128:
       launch_family<256, 128, 2, 2, 2, 3, 32>(a, s);
