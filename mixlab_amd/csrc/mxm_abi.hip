@@ -1164,7 +1164,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // gate gradients <dD, Y> = <dH', h>, and dH = gate * dH'
   product(0, ddb, o.bw_w2o.p, dhb, D, F, o.fam_dh, true);
   // gub holds G|U from the forward (run_forward's pre_out)
-  mxm_launch_act_bw_gated_bf16(gub, dhb, static_cast<const uint16_t*>(o.ws.H), o.hsplit,
+  mxm_launch_act_bw_gated_bf16(gub, dhb, static_cast<uint16_t*>(o.ws.H), o.hsplit,
                                o.bw_gp.as<float>(), (int)NK, F, o.etype, o.act, o.slope, dgub,
                                o.bw_dgp.as<float>(), st);
   HIPCK(hipGetLastError());

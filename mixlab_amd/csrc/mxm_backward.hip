@@ -707,16 +707,18 @@ __global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ 
 }
 
 // One wave per routed row p (4 rows per workgroup), 8 hidden units per lane
-// and step: dH = gp[p] * dhr (dhr = dD W_down^T for the row's token, not yet
-// gated); dG and dU from dH and the forward's raw bf16 projections gu
-// [N*K, NC] (GLU: NC = 2F, gate and up columns interleaved in groups of 32 as
-// the MFMA family's W1 rows; MLP: NC = F, up only), written to dgu at the
-// columns of g and u in bf16; and the gate gradient dgp[p] = <dhr[p], h[p]> with h
-// the forward's hidden (two bf16 planes hi + lo for a split hidden), summed
-// per lane in f order and then over the wave by a fixed butterfly.
+// and step, from the forward's raw bf16 projections gu [N*K, NC] (GLU: NC =
+// 2F, gate and up columns interleaved in groups of 32 as the MFMA family's W1
+// rows; MLP: NC = F, up only): the hidden h = mxm_hidden_fast of them, as the
+// up GEMM's epilogue computes it, stored to H in bf16 (two planes hi and lo =
+// bf16(h - hi) for a split hidden); dH = gp[p] * dhr (dhr = dD W_down^T for
+// the row's token, not yet gated); dG and dU from dH, written to dgu at the
+// columns of g and u in bf16; and the gate gradient dgp[p] = <dhr[p], h[p]>
+// with h as stored (hi + lo when split), summed per lane in f order and then
+// over the wave by a fixed butterfly.
 __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
     const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dhr,
-    const uint16_t* __restrict__ H, bool hsplit, const float* __restrict__ gp, int rows, int F,
+    uint16_t* __restrict__ H, bool hsplit, const float* __restrict__ gp, int rows, int F,
     int etype, int act, float slope, uint16_t* __restrict__ dgu, float* __restrict__ dgp) {
   const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -729,7 +731,7 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
   // U steps of 8 hidden units per lane: their loads go out together
   constexpr int U = 4;
   for (int f0 = lane * 8; f0 < F; f0 += 512 * U) {
-    uint4 hv[U], uv[U], gv[U], xv[U], lv[U];
+    uint4 hv[U], uv[U], gv[U];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       const int f = min(f0 + 512 * j, F - 8);  // (steps past F reload the last group)
@@ -737,9 +739,6 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
       hv[j] = *reinterpret_cast<const uint4*>(dhr + (size_t)p * F + f);
       uv[j] = *reinterpret_cast<const uint4*>(gu + cu);
       gv[j] = glu ? *reinterpret_cast<const uint4*>(gu + cu - 32) : make_uint4(0u, 0u, 0u, 0u);
-      xv[j] = *reinterpret_cast<const uint4*>(H + (size_t)p * hstride + f);
-      lv[j] = hsplit ? *reinterpret_cast<const uint4*>(H + (size_t)p * hstride + F + f)
-                     : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int j = 0; j < U; ++j) {
@@ -749,14 +748,23 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
       const uint32_t hw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
       const uint32_t uw[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
       const uint32_t gw[4] = {gv[j].x, gv[j].y, gv[j].z, gv[j].w};
-      const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-      const uint32_t lw[4] = {lv[j].x, lv[j].y, lv[j].z, lv[j].w};
-      uint32_t og[4], ou[4];
+      uint32_t og[4], ou[4], xw[4], lw[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float r0 = mxm_u2f(hw[q] << 16), r1 = mxm_u2f(hw[q] & 0xffff0000u);
+        // the hidden as the up epilogue computes it (mxm_hidden_fast on the
+        // bf16 projections), then as stored
+        float h[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const float gg = glu ? mxm_u2f(t ? gw[q] & 0xffff0000u : gw[q] << 16) : 0.0f;
+          const float uu = mxm_u2f(t ? uw[q] & 0xffff0000u : uw[q] << 16);
+          h[t] = mxm_hidden_fast<true>(glu ? etype : MXM_EXPERT_MLP, act, slope, gg, uu);
+        }
+        xw[q] = mxm_pack_bf2_fast(h[0], h[1]);
         float h0 = mxm_u2f(xw[q] << 16), h1 = mxm_u2f(xw[q] & 0xffff0000u);
         if (hsplit) {
+          lw[q] = mxm_pack_bf2_fast(h[0] - h0, h[1] - h1);
           h0 = h0 + mxm_u2f(lw[q] << 16);
           h1 = h1 + mxm_u2f(lw[q] & 0xffff0000u);
         }
@@ -772,6 +780,10 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
       }
       *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
       if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
+      *reinterpret_cast<uint4*>(H + (size_t)p * hstride + f) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+      if (hsplit)
+        *reinterpret_cast<uint4*>(H + (size_t)p * hstride + F + f) =
+            make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
   }
 #pragma unroll
@@ -895,7 +907,7 @@ void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot
                        slot_pos, D, K, ddb, dyb, gp);
 }
 
-void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const uint16_t* H,
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* H,
                                   bool hsplit, const float* gp, int rows, int F, int etype, int act,
                                   float slope, uint16_t* dgu, float* dgp, hipStream_t s) {
   // F is a multiple of 32 (the MFMA family's GLU interleave)

@@ -516,9 +516,9 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
       if (grow + 1 < rows)
         *reinterpret_cast<u32x4_t*>(rout + (size_t)(row0 + grow + 1) * a.Ncols + c0r) = hi;
     }
-    // every wave's staging reads are done before the hidden's staging writes
-    // (the hidden's per-wave regions are laid out at another stride)
+    // every wave's staging reads are done before the next tile's loads
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    continue;  // no hidden: the backward's activation pass derives it
   }
   // kinds whose hidden is fp32 store it as two bf16 planes (hi, then lo =
   // bf16(h - hi)) through the same staging, one plane after the other

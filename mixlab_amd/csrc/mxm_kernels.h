@@ -214,8 +214,9 @@ int mxm_simt_bm();
 enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN,
        EPI_DOWN_F32 };
 
-// EPI_KEEP + an up-projection kind: the same epilogue, which first also
-// stores the raw projections to GemmArgs::out2.
+// EPI_KEEP + an up-projection kind: the raw bf16 projections to
+// GemmArgs::out2 instead of the hidden (the MFMA backward derives H from
+// them in its activation pass).
 constexpr int EPI_KEEP = 16;
 
 template <int EPI_>
@@ -382,9 +383,6 @@ void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* sl
 void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, const uint16_t* dxe,
                               const int32_t* slot_pos, int N, int D, int K, float* dx,
                               hipStream_t s);
-// bf16 MFMA backward without the forward's down projection: per token,
-// ddb[n] = bf16(dD[n]) and, per slot s at position p = slot_pos[s],
-// dyb[p] = bf16(gates[s] * dD[n]) and gp[p] = gates[s].
 // d router_w on the weight-gradient kernel: dlogits [N][E] as bf16 halves
 // hi = bf16(dl), lo = bf16(dl - hi) in out [N][2 Ep] (hi at column e, lo at
 // Ep + e, zeros for e >= E; Ep = E rounded up to 64), so that x^T out holds
@@ -392,14 +390,18 @@ void mxm_launch_dx_fused_bf16(const float* dlogits, const float* wrt, int E, con
 void mxm_launch_dl_split_bf16(const float* dl, int N, int E, int Ep, uint16_t* out, hipStream_t s);
 // ... and dwr[d][e] = t[d][e] + t[d][Ep + e] from that product t [D][2 Ep].
 void mxm_launch_dwr_halves(const float* t, int D, int E, int Ep, float* dwr, hipStream_t s);
+// bf16 MFMA backward without the forward's down projection: per token,
+// ddb[n] = bf16(dD[n]) and, per slot s at position p = slot_pos[s],
+// dyb[p] = bf16(gates[s] * dD[n]) and gp[p] = gates[s].
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
-// ... then, per routed row p: dH = gp[p] * dhr[p] (dhr = dD W_down^T of the
-// row's token, ungated), dG and dU (the activation backward on the forward's
-// bf16 projections gu), and the gate
-// gradient dgp[p] = <dhr[p], h[p]> (h the forward's hidden H, two planes
-// hi + lo when hsplit).
-void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, const uint16_t* H,
+// ... then, per routed row p: the hidden h from the forward's raw bf16
+// projections gu with the up epilogue's own activation code (bit for bit the
+// forward's), written to H (hi, and lo = bf16(h - hi) after F columns when
+// hsplit); dH = gp[p] * dhr[p] (dhr = dD W_down^T of the row's token,
+// ungated), dG and dU (the activation backward); and the gate gradient
+// dgp[p] = <dhr[p], h[p]> with h as stored (hi + lo when hsplit).
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* H,
                                   bool hsplit, const float* gp, int rows, int F, int etype, int act,
                                   float slope, uint16_t* dgu, float* dgp, hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
