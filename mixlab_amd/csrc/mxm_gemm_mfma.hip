@@ -175,8 +175,8 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // A = [hi | lo] planes, y in fp32
   // 32-bit A offsets (when A fits) for the forward's up projections only:
-  // measured faster there, slower for the down projection and for the
-  // raw-keeping variant, whose extra registers spill
+  // measured faster there, slower for the down projection and no faster
+  // for the raw-keeping variant
   constexpr bool A_OFF32 = MODE != MXM_GEMM_DOWN && !Epi<EPI>::KEEP_RAW;
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // H stored as [hi | lo] planes
   constexpr int NT = TL::NT, TM = TL::TM, TN = TL::TN;
