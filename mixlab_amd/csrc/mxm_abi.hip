@@ -161,7 +161,7 @@ struct MoeOp {
   // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
   // handle for the weight gradients
   bool bw_wbf_ready = false;
-  DevBuf bw_dyb, bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
+  DevBuf bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
       bw_ddb, bw_gp, bw_dgp, bw_dlb, bw_dwr2;
   rocblas_handle bw_blas = nullptr;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
@@ -1072,17 +1072,20 @@ void check_blas(rocblas_status st, const char* what) {
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
 // permuted order throughout (expert e owns rows offsets[e] ..).  The forward
 // stops after its up projection: Y is never formed.
-//   G|U = Xp W1, H             kept by the forward (its gate+up GEMM stores
-//                              the raw projections beside H, GemmArgs::out2)
+//   G|U = Xp W1                kept by the forward (its gate+up GEMM stores
+//                              only the raw projections, GemmArgs::out2)
 //   dH' = dD[token] W_down^T   MFMA grouped GEMM on the bf16 dD rows gathered
 //                              through perm, W_down kept as [F][D] bf16; not
 //                              yet gated
-//   dgates = <dH', h>          (= <dD, Y>), dH = gate * dH', dG|dU: one pass
+//   dgates = <dH', h>          (= <dD, Y>), dH = gate * dH', dG|dU and the
+//                              gated hidden Hg = gate * h, h from G|U as the
+//                              forward's epilogue computes it: one pass
 //                              (act_bw_gated_bf16), then the router part
 //   dXe = dG|dU W1^T           MFMA grouped GEMM, W1 kept as [D][NC] bf16
 //   dx  = dlogits Wr^T + sum_k dXe   (dx_fused_bf16; with a dx that is not
 //                              16-byte aligned: dxr + sum_k dXe, dx_bf16)
-//   dW1 = Xp^T dG|dU, dW_down = H^T dY   MFMA weight-gradient kernel (fp32 out)
+//   dW1 = Xp^T dG|dU, dW_down = Hg^T dD[token]   MFMA weight-gradient kernel
+//                              (fp32 out; x and dD rows read through perm)
 void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* dx, float* dw) {
   hipStream_t st = o.stream;
   const bool glu = o.wpe == 3;
@@ -1127,13 +1130,13 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     HIPCK(hipGetLastError());
     o.bw_wbf_ready = true;
   }
-  uint16_t *dyb = o.bw_dyb.as<uint16_t>(), *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
+  uint16_t *dhb = o.bw_dhb.as<uint16_t>(), *gub = o.bw_gub.as<uint16_t>(),
            *dgub = o.bw_dgub.as<uint16_t>(), *dxeb = o.bw_dxeb.as<uint16_t>(),
            *ddb = o.bw_ddb.as<uint16_t>();
-  // dD in bf16 per token, dY = gate * dD per slot (for dW_down), the gates by
-  // slot position
-  mxm_launch_dy_gate(b.d_delta, b.gates, b.slot_pos, o.N, D, o.K, ddb, dyb, o.bw_gp.as<float>(),
-                     st);
+  // dD in bf16 per token and the gates by slot position (dW_down takes the
+  // gate on its left operand, so no per-slot dY = gate * dD is written)
+  mxm_launch_dy_gate(b.d_delta, b.gates, b.slot_pos, o.N, D, o.K, ddb, nullptr,
+                     o.bw_gp.as<float>(), st);
   // families as the forward picks them for the same output width (dX has
   // the down projection's, D)
   auto product = [&](int which, const uint16_t* A, const void* W, uint16_t* out, int Kd, int Ncols,
@@ -1209,7 +1212,8 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // weight gradients on MFMA, each reduced over its expert's rows (ragged,
   // from the device-side offsets): dW1 = Xp^T dG|dU, its GLU columns landing
   // de-interleaved in the gate and up matrices (x.W layout), and
-  // dW_down = H^T dY over the hidden's planes (hi and lo for a split hidden)
+  // dW_down = Hg^T dD[token] over the gated hidden's planes (hi and lo for a
+  // split hidden)
   if (!mxm_wgrad_fits(D, NC) || !mxm_wgrad_fits(F, D))
     fail("OP_MOE_FEED_FORWARD backward: weight-gradient tiles need D, F multiples of 128 "
          "(D=%d F=%d)", D, F);
@@ -1234,12 +1238,16 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   wa.glu_f = glu ? F : 0;
   mxm_launch_wgrad(wa, st);
   HIPCK(hipGetLastError());
+  // dW_down = sum over slots of (gate h)^T dD[token]: A = the gated hidden
+  // the activation pass wrote, B = bf16(dD) rows read in place through perm
   wa.a = static_cast<const uint16_t*>(o.ws.H);
   wa.a_rows = nullptr;
   wa.lda = o.hsplit ? 2 * F : F;
   wa.aplane = F;
   wa.planes = o.hsplit ? 2 : 1;
-  wa.b = dyb;
+  wa.b = ddb;
+  wa.b_rows = b.perm;
+  wa.b_rows32 = (size_t)o.N * D * 2 < ((size_t)1 << 32);
   wa.ldb = D;
   wa.M = F;
   wa.C = D;
@@ -1364,10 +1372,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   if (!o.bw_probs.p) o.bw_probs.alloc(N * E * 4);
   if (!o.bw_ready) {
     o.bw_delta.alloc(N * D * 4);
-    if (mfma_bw)
-      o.bw_dyb.alloc(NK * D * 2);  // dY straight in bf16
-    else
-      o.bw_dy.alloc(NK * D * 4);
+    if (!mfma_bw) o.bw_dy.alloc(NK * D * 4);  // (the MFMA backward keeps no dY)
     o.bw_dgates.alloc(NK * 4);
     o.bw_dlogits.alloc(N * E * 4);
     o.bw_wrt.alloc(D * E * 4);
@@ -1488,7 +1493,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.d_aux = d_aux;
   b.d_ent = d_ent;
   b.dy = o.bw_dy.as<float>();
-  if (mfma_bw) b.dyb16 = o.bw_dyb.as<uint16_t>();
   b.dgates = o.bw_dgates.as<float>();
   b.dlogits = o.bw_dlogits.as<float>();
   // the MFMA path fuses dx's router term dlogits . Wr^T into the dx sum

@@ -668,9 +668,9 @@ __device__ __forceinline__ void act_bw_one(int etype, int act, float slope, floa
 }
 
 // One workgroup per token n: ddb[n] = bf16(dD[n]); for each slot s = n*K + k
-// at position p = slot_pos[s]: dyb[p] = bf16(gates[s] * dD[n]), gp[p] =
-// gates[s].  V = 4: 4 consecutive d per thread (16-byte dD loads, 8-byte
-// stores).
+// at position p = slot_pos[s]: gp[p] = gates[s] and, if dyb is set, dyb[p] =
+// bf16(gates[s] * dD[n]).  V = 4: 4 consecutive d per thread (16-byte dD
+// loads, 8-byte stores).
 template <int V>
 __global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ dd,
                                                       const float* __restrict__ gates,
@@ -693,7 +693,7 @@ __global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ 
       v[0] = src[d];
       ddb[(size_t)n * D + d] = mxm_f2bf(v[0]);
     }
-    for (int k = 0; k < K; ++k) {
+    for (int k = 0; k < K && dyb; ++k) {
       const float g = gates[(size_t)n * K + k];
       uint16_t* o = dyb + (size_t)slot_pos[(size_t)n * K + k] * D + d;
       if constexpr (V == 4)
@@ -710,15 +710,16 @@ __global__ __launch_bounds__(256) void dy_gate_kernel(const float* __restrict__ 
 // and step, from the forward's raw bf16 projections gu [N*K, NC] (GLU: NC =
 // 2F, gate and up columns interleaved in groups of 32 as the MFMA family's W1
 // rows; MLP: NC = F, up only): the hidden h = mxm_hidden_fast of them, as the
-// up GEMM's epilogue computes it, stored to H in bf16 (two planes hi and lo =
-// bf16(h - hi) for a split hidden); dH = gp[p] * dhr (dhr = dD W_down^T for
-// the row's token, not yet gated); dG and dU from dH, written to dgu at the
-// columns of g and u in bf16; and the gate gradient dgp[p] = <dhr[p], h[p]>
-// with h as stored (hi + lo when split), summed per lane in f order and then
-// over the wave by a fixed butterfly.
+// up GEMM's epilogue computes it; the gated hidden gp[p] * h stored to Hg in
+// bf16 (two planes hi and lo = bf16(v - hi) for a split hidden), dW_down's
+// left operand; dH = gp[p] * dhr (dhr = dD W_down^T for the row's token, not
+// yet gated); dG and dU from dH, written to dgu at the columns of g and u in
+// bf16; and the gate gradient dgp[p] = <dhr[p], h[p]> with h as the forward
+// stores it (bf16, or hi + lo when split), summed per lane in f order and
+// then over the wave by a fixed butterfly.
 __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
     const uint16_t* __restrict__ gu, const uint16_t* __restrict__ dhr,
-    uint16_t* __restrict__ H, bool hsplit, const float* __restrict__ gp, int rows, int F,
+    uint16_t* __restrict__ Hg, bool hsplit, const float* __restrict__ gp, int rows, int F,
     int etype, int act, float slope, uint16_t* __restrict__ dgu, float* __restrict__ dgp) {
   const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -761,15 +762,19 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
           const float uu = mxm_u2f(t ? uw[q] & 0xffff0000u : uw[q] << 16);
           h[t] = mxm_hidden_fast<true>(glu ? etype : MXM_EXPERT_MLP, act, slope, gg, uu);
         }
-        xw[q] = mxm_pack_bf2_fast(h[0], h[1]);
-        float h0 = mxm_u2f(xw[q] << 16), h1 = mxm_u2f(xw[q] & 0xffff0000u);
+        // h as the forward stores it, for the gate gradient
+        float h0 = mxm_rbf_fast(h[0]), h1 = mxm_rbf_fast(h[1]);
         if (hsplit) {
-          lw[q] = mxm_pack_bf2_fast(h[0] - h0, h[1] - h1);
-          h0 = h0 + mxm_u2f(lw[q] << 16);
-          h1 = h1 + mxm_u2f(lw[q] & 0xffff0000u);
+          h0 = h0 + mxm_rbf_fast(h[0] - h0);
+          h1 = h1 + mxm_rbf_fast(h[1] - h1);
         }
         dot = __builtin_fmaf(r0, h0, dot);
         dot = __builtin_fmaf(r1, h1, dot);
+        // the gated hidden
+        const float v0 = gate * h[0], v1 = gate * h[1];
+        xw[q] = mxm_pack_bf2_fast(v0, v1);
+        if (hsplit)
+          lw[q] = mxm_pack_bf2_fast(v0 - mxm_u2f(xw[q] << 16), v1 - mxm_u2f(xw[q] & 0xffff0000u));
         float dg0, du0, dg1, du1;
         act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0,
                    dg0, du0);
@@ -780,9 +785,9 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
       }
       *reinterpret_cast<uint4*>(dgu + cu) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
       if (glu) *reinterpret_cast<uint4*>(dgu + cu - 32) = make_uint4(og[0], og[1], og[2], og[3]);
-      *reinterpret_cast<uint4*>(H + (size_t)p * hstride + f) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+      *reinterpret_cast<uint4*>(Hg + (size_t)p * hstride + f) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
       if (hsplit)
-        *reinterpret_cast<uint4*>(H + (size_t)p * hstride + F + f) =
+        *reinterpret_cast<uint4*>(Hg + (size_t)p * hstride + F + f) =
             make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
   }
@@ -907,13 +912,13 @@ void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot
                        slot_pos, D, K, ddb, dyb, gp);
 }
 
-void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* H,
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* Hg,
                                   bool hsplit, const float* gp, int rows, int F, int etype, int act,
                                   float slope, uint16_t* dgu, float* dgp, hipStream_t s) {
   // F is a multiple of 32 (the MFMA family's GLU interleave)
   if (rows > 0)
     hipLaunchKernelGGL(act_bw_gated_bf16_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, gu, dhr,
-                       H, hsplit, gp, rows, F, etype, act, slope, dgu, dgp);
+                       Hg, hsplit, gp, rows, F, etype, act, slope, dgu, dgp);
 }
 
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,

@@ -202,6 +202,8 @@ struct WgradArgs {
   void* scratch;            // mxm_wgrad_scratch_bytes(M, C): the schedule and split partials
   const int32_t* a_rows;    // if set: A's row for reduction row j is a_rows[j] (else j)
   bool a_rows32;            // with a_rows: all of A lies within 4 GiB of a (32-bit offsets)
+  const int32_t* b_rows;    // the same for B (at most one of a_rows, b_rows)
+  bool b_rows32;
 };
 // M and C multiples of 128.
 bool mxm_wgrad_fits(int M, int C);
@@ -392,16 +394,18 @@ void mxm_launch_dl_split_bf16(const float* dl, int N, int E, int Ep, uint16_t* o
 void mxm_launch_dwr_halves(const float* t, int D, int E, int Ep, float* dwr, hipStream_t s);
 // bf16 MFMA backward without the forward's down projection: per token,
 // ddb[n] = bf16(dD[n]) and, per slot s at position p = slot_pos[s],
-// dyb[p] = bf16(gates[s] * dD[n]) and gp[p] = gates[s].
+// gp[p] = gates[s] and (if dyb is set) dyb[p] = bf16(gates[s] * dD[n]).
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
 // ... then, per routed row p: the hidden h from the forward's raw bf16
 // projections gu with the up epilogue's own activation code (bit for bit the
-// forward's), written to H (hi, and lo = bf16(h - hi) after F columns when
-// hsplit); dH = gp[p] * dhr[p] (dhr = dD W_down^T of the row's token,
+// forward's); the gated hidden gp[p] * h written to Hg (hi, and lo =
+// bf16(v - hi) after F columns when hsplit) for dW_down = Hg^T dD over the
+// slots' tokens; dH = gp[p] * dhr[p] (dhr = dD W_down^T of the row's token,
 // ungated), dG and dU (the activation backward); and the gate gradient
-// dgp[p] = <dhr[p], h[p]> with h as stored (hi + lo when hsplit).
-void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* H,
+// dgp[p] = <dhr[p], h[p]> with h as the forward stores it (hi + lo when
+// hsplit).
+void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* Hg,
                                   bool hsplit, const float* gp, int rows, int F, int etype, int act,
                                   float slope, uint16_t* dgu, float* dgp, hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).

@@ -6,9 +6,10 @@
 // permuted slot order) and the planes p of A (two for a hidden stored as
 // bf16 hi and lo planes, else one).  This is dW1 = Xp^T dG|dU (A = x, row k
 // read at the token index a_rows[k] of the slot, B = the activation
-// backward's output) and dW_down = H^T dY (A = the forward's hidden, rows in
-// slot order, B = the routed output gradient); the reduction runs over the
-// expert's rows, whose count is only known on the device.
+// backward's output) and dW_down = Hg^T dD (A = the gated hidden gate * h,
+// rows in slot order, B = the upstream gradient's bf16 row of the slot's
+// token, read through b_rows); the reduction runs over the expert's rows,
+// whose count is only known on the device.
 //
 // Both operands are k-outer: a row of A or B is one k, its columns are
 // contiguous.  Tiles move global -> LDS in that natural layout with
@@ -294,10 +295,13 @@ __device__ void build_plan(WgPlan& P, const int32_t* __restrict__ offsets, int E
 }
 
 
-template <class TL, int BM, int BN, int WM, int WN, int BK, int NS, bool GATHER>
+// GATHER: bit 1 = A's rows gathered through a_rows, bit 2 = B's through b_rows.
+template <class TL, int BM, int BN, int WM, int WN, int BK, int NS, int GATHER>
 __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
   constexpr int NW = TL::NW, TM = TL::TM, TN = TL::TN;
-  constexpr int QA = TL::QA, LDPS = TL::LDPS;
+  constexpr int QA = TL::QA, LDPS = TL::LDPS, QB = LDPS - QA;
+  constexpr bool GA = (GATHER & 1) != 0, GB = (GATHER & 2) != 0;
+  static_assert(!(GA && GB), "one gathered operand");
   constexpr int RPWA = TL::RPWA, RPWB = TL::RPWB;
   constexpr int BUF = TL::BUF, A_BYTES = TL::A_BYTES;
   static_assert(BK == WG_BK, "the plan counts 64-row stages");
@@ -382,32 +386,62 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
 #pragma unroll
     for (int q = 0; q < LDPS - QA; ++q)
       b_lane[q] = ((wv + NW * q) * RPWB + rb) * a.ldb + c0 + lcb * 8;
-    // GATHER with A below 4 GiB: the lane's column part in bytes and A's row
-    // pitch in bytes (rows are added per stage from the scalar row indices)
+    // a gathered operand below 4 GiB: the lane's column part in bytes and the
+    // row pitch in bytes (rows are added per stage from the scalar row indices)
     const unsigned a_colb = 2u * (unsigned)(m0 + lca * 8);
     const unsigned a_pitch = 2u * (unsigned)a.lda;
-    const bool a32 = GATHER && a.a_rows32;
+    const unsigned b_colb = 2u * (unsigned)(c0 + lcb * 8);
+    const unsigned b_pitch = 2u * (unsigned)a.ldb;
+    const bool g32 = (GA && a.a_rows32) || (GB && a.b_rows32);
 
-    // GATHER: A's row for reduction row j is a_rows[j] (the token of a slot:
-    // x read in place instead of a gathered copy).  The rows of the stage to
-    // be loaded next are fetched once the current stage's loads are out, as
-    // scalar loads (the wave's RPWA rows per wave-load are uniform; the lane
-    // picks its own at the DMA), so that waiting for them waits on lgkmcnt
-    // and never on the direct-to-LDS loads in flight.  Rows past the
-    // expert's end read its last index and are not used.
+    // Gathered rows: A's (B's) row for reduction row j is a_rows[j] (b_rows[j])
+    // -- the token of a slot, so x (or a per-token gradient) is read in place
+    // instead of a gathered copy.  The rows of the stage to be loaded next
+    // are fetched once the current stage's loads are out, as scalar loads
+    // (the wave's rows per wave-load are uniform; the lane picks its own at
+    // the DMA), so that waiting for them waits on lgkmcnt and never on the
+    // direct-to-LDS loads in flight.  Rows past the expert's end read its
+    // last index and are not used.
     using crow_t = const __attribute__((address_space(4))) int32_t;
     crow_t* __restrict__ arows = (crow_t*)a.a_rows;
-    int srow[QA][RPWA];
+    crow_t* __restrict__ brows = (crow_t*)a.b_rows;
+    int srow[QA][RPWA], srowb[QB][RPWB];
     auto load_arows = [&](int kt) {  // rows of the next stage to load (dkk)
-      if constexpr (GATHER) {
-        if (kt >= nk) return;
+      if (kt >= nk) return;
+      if constexpr (GA) {
 #pragma unroll
         for (int q = 0; q < QA; ++q)
 #pragma unroll
           for (int i = 0; i < RPWA; ++i)
             srow[q][i] = arows[row0 + min(dkk + (wv + NW * q) * RPWA + i, cnt - 1)];
       }
+      if constexpr (GB) {
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
+#pragma unroll
+          for (int i = 0; i < RPWB; ++i)
+            srowb[q][i] = brows[row0 + min(dkk + (wv + NW * q) * RPWB + i, cnt - 1)];
+      }
     };
+    // the lane's own row among a wave-load's gathered rows
+    auto pick = [](const int* rowsq, int rl, auto rpw) {
+      int r = rowsq[0];
+#pragma unroll
+      for (int i = 1; i < decltype(rpw)::value; ++i)
+        if (rl == i) r = rowsq[i];
+      return r;
+    };
+    auto pick_off = [](const int* rowsq, int rl, auto rpw, unsigned pitch, unsigned colb) {
+      unsigned off = (unsigned)rowsq[0] * pitch + colb;
+#pragma unroll
+      for (int i = 1; i < decltype(rpw)::value; ++i) {
+        const unsigned oi = (unsigned)rowsq[i] * pitch + colb;
+        if (rl == i) off = oi;
+      }
+      return off;
+    };
+    const std::integral_constant<int, RPWA> rpwa;
+    const std::integral_constant<int, RPWB> rpwb;
     // direct-to-LDS loads q0 .. q1-1 (q < QA: A rows, else B rows) of the
     // next stage to load, into ring slot kt % NS
     auto dma_part = [&](int kt, int l0, int l1) {
@@ -422,33 +456,33 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
           for (int q = 0; q < LDPS; ++q) {
             if (q < l0 || q >= l1) continue;
             if (q < QA) {
-              if constexpr (GATHER && decltype(off32)::value) {
-                // each candidate row's byte offset (scalar) plus the lane's
-                // column; the lane takes its own row's
-                unsigned off = (unsigned)srow[q][0] * a_pitch + a_colb;
-#pragma unroll
-                for (int i = 1; i < RPWA; ++i) {
-                  const unsigned oi = (unsigned)srow[q][i] * a_pitch + a_colb;
-                  if (ra == i) off = oi;
-                }
-                wg_dma16s(A + (size_t)p * a.aplane, off, st + (wv + NW * q) * 1024);
-              } else if constexpr (GATHER) {
-                int arw = srow[q][0];
-#pragma unroll
-                for (int i = 1; i < RPWA; ++i)
-                  if (ra == i) arw = srow[q][i];
-                wg_dma16(A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8,
+              // gathered rows: each candidate row's byte offset (scalar) plus
+              // the lane's column, the lane taking its own row's
+              if constexpr (GA && decltype(off32)::value) {
+                wg_dma16s(A + (size_t)p * a.aplane, pick_off(srow[q], ra, rpwa, a_pitch, a_colb),
+                          st + (wv + NW * q) * 1024);
+              } else if constexpr (GA) {
+                wg_dma16(A + (size_t)pick(srow[q], ra, rpwa) * a.lda + (size_t)p * a.aplane + m0 +
+                             lca * 8,
                          st + (wv + NW * q) * 1024);
               } else {
                 wg_dma16s(as, 2u * (unsigned)a_lane[q], st + (wv + NW * q) * 1024);
               }
             } else {
-              wg_dma16s(bs, 2u * (unsigned)b_lane[q - QA],
-                        st + A_BYTES + (wv + NW * (q - QA)) * 1024);
+              const int qb = q - QA;
+              if constexpr (GB && decltype(off32)::value) {
+                wg_dma16s(B, pick_off(srowb[qb], rb, rpwb, b_pitch, b_colb),
+                          st + A_BYTES + (wv + NW * qb) * 1024);
+              } else if constexpr (GB) {
+                wg_dma16(B + (size_t)pick(srowb[qb], rb, rpwb) * a.ldb + c0 + lcb * 8,
+                         st + A_BYTES + (wv + NW * qb) * 1024);
+              } else {
+                wg_dma16s(bs, 2u * (unsigned)b_lane[qb], st + A_BYTES + (wv + NW * qb) * 1024);
+              }
             }
           }
         };
-        if (a32) whole(std::true_type{});
+        if (g32) whole(std::true_type{});
         else whole(std::false_type{});
       } else {
         // the expert's last, partial stage: rows past its end load the zero row
@@ -458,20 +492,17 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
           if (q < QA) {
             const int k = kk + (wv + NW * q) * RPWA + ra;
             int arw = row0 + k;
-            if constexpr (GATHER) {
-              arw = srow[q][0];
-#pragma unroll
-              for (int i = 1; i < RPWA; ++i)
-                if (ra == i) arw = srow[q][i];
-            }
+            if constexpr (GA) arw = pick(srow[q], ra, rpwa);
             const uint16_t* src = k < cnt ? A + (size_t)arw * a.lda + (size_t)p * a.aplane + m0 + lca * 8
                                           : a.zero + lca * 8;
             wg_dma16(src, st + (wv + NW * q) * 1024);
           } else {
             const int qb = q - QA;
             const int k = kk + (wv + NW * qb) * RPWB + rb;
+            int brw = row0 + k;
+            if constexpr (GB) brw = pick(srowb[qb], rb, rpwb);
             const uint16_t* src =
-                k < cnt ? B + (size_t)(row0 + k) * a.ldb + c0 + lcb * 8 : a.zero + lcb * 8;
+                k < cnt ? B + (size_t)brw * a.ldb + c0 + lcb * 8 : a.zero + lcb * 8;
             wg_dma16(src, st + A_BYTES + (wv + NW * qb) * 1024);
           }
         }
@@ -699,10 +730,13 @@ struct WFamily {
   }
   static void launch(const WgradArgs& a, hipStream_t s) {
     if (a.a_rows)
-      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, true>), dim3(grid()),
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 1>), dim3(grid()),
+                         dim3(TL::NT), 0, s, a);
+    else if (a.b_rows)
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 2>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
     else
-      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, false>), dim3(grid()),
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 0>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
     hipLaunchKernelGGL((wgrad_reduce_kernel<BM, BN>), dim3(std::max(8, n_cus() * 2)), dim3(256),
                        0, s, a);
