@@ -755,12 +755,19 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
         const float r0 = mxm_u2f(hw[q] << 16), r1 = mxm_u2f(hw[q] & 0xffff0000u);
         // the hidden as the up epilogue computes it (mxm_hidden_fast on the
         // bf16 projections), then as stored
-        float h[2];
+        // (sigmoid-GLU: the one fast sigmoid serves h and the derivative)
+        const bool sw = etype == MXM_EXPERT_SWIGLU;
+        float h[2], sg[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const float gg = glu ? mxm_u2f(t ? gw[q] & 0xffff0000u : gw[q] << 16) : 0.0f;
           const float uu = mxm_u2f(t ? uw[q] & 0xffff0000u : uw[q] << 16);
-          h[t] = mxm_hidden_fast<true>(glu ? etype : MXM_EXPERT_MLP, act, slope, gg, uu);
+          if (sw) {
+            sg[t] = mxm_sigmoid_fast(gg);
+            h[t] = mxm_rbf_fast(mxm_rbf_fast(sg[t]) * uu);  // as mxm_hidden_fast
+          } else {
+            h[t] = mxm_hidden_fast<true>(glu ? etype : MXM_EXPERT_MLP, act, slope, gg, uu);
+          }
         }
         // h as the forward stores it, for the gate gradient
         float h0 = mxm_rbf_fast(h[0]), h1 = mxm_rbf_fast(h[1]);
@@ -776,10 +783,19 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
         if (hsplit)
           lw[q] = mxm_pack_bf2_fast(v0 - mxm_u2f(xw[q] << 16), v1 - mxm_u2f(xw[q] & 0xffff0000u));
         float dg0, du0, dg1, du1;
-        act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0,
-                   dg0, du0);
-        act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u), mxm_u2f(uw[q] & 0xffff0000u),
-                   gate * r1, dg1, du1);
+        if (sw) {
+          const float u0 = mxm_u2f(uw[q] << 16), u1 = mxm_u2f(uw[q] & 0xffff0000u);
+          const float d0 = gate * r0, d1 = gate * r1;
+          dg0 = d0 * u0 * (sg[0] * (1.0f - sg[0]));
+          du0 = d0 * sg[0];
+          dg1 = d1 * u1 * (sg[1] * (1.0f - sg[1]));
+          du1 = d1 * sg[1];
+        } else {
+          act_bw_one(etype, act, slope, mxm_u2f(gw[q] << 16), mxm_u2f(uw[q] << 16), gate * r0,
+                     dg0, du0);
+          act_bw_one(etype, act, slope, mxm_u2f(gw[q] & 0xffff0000u),
+                     mxm_u2f(uw[q] & 0xffff0000u), gate * r1, dg1, du1);
+        }
         og[q] = (uint32_t)mxm_f2bf(dg0) | ((uint32_t)mxm_f2bf(dg1) << 16);
         ou[q] = (uint32_t)mxm_f2bf(du0) | ((uint32_t)mxm_f2bf(du1) << 16);
       }
