@@ -151,6 +151,10 @@ struct MoeOp {
   // d router_w in the MFMA backward: on the weight-gradient kernel (1), on
   // the SIMT kernel (0), or by size (-1); MXM_ROUTER_WGRAD_MFMA at creation
   int dwr_mode = -1;
+  // 64-bit addressing where 32-bit byte offsets would do (operands below
+  // 4 GiB): MXM_FORCE_64BIT_OFFSETS at creation, so that the paths larger
+  // operands take can be checked on small ones
+  bool force64 = false;
   DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
       bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
@@ -451,6 +455,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   if (o.route_only) return;
   const bool glu = o.etype != MXM_EXPERT_MLP;
   GemmArgs g1{};
+  g1.no_off32 = o.force64;
   g1.mode = glu ? MXM_GEMM_GLU : MXM_GEMM_MLP;
   g1.a = xin;
   g1.perm = sc.perm;
@@ -488,6 +493,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
 
   mark(4);
   GemmArgs g2{};
+  g2.no_off32 = o.force64;
   g2.mode = MXM_GEMM_DOWN;
   g2.a = w.H;
   g2.b0 = o.w2.p;
@@ -787,6 +793,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
       fail("OP_MOE_FEED_FORWARD requires B,T,D,E,topK,expertType,ffn,activation");
     auto o = std::make_unique<MoeOp>();
     if (const char* v = std::getenv("MXM_ROUTER_WGRAD_MFMA")) o->dwr_mode = std::atoi(v) != 0;
+    if (const char* v = std::getenv("MXM_FORCE_64BIT_OFFSETS")) o->force64 = std::atoi(v) != 0;
     o->B = int_params[0];
     o->T = int_params[1];
     o->D = int_params[2];
@@ -1145,6 +1152,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     int32_t* ms = o.bw_ms.as<int32_t>() + (size_t)which * (E + 1);
     mxm_launch_tile_prefix(b.counts, E, bm, ms, st);
     GemmArgs g{};
+    g.no_off32 = o.force64;
     g.mode = MXM_GEMM_DOWN;
     g.a = A;
     g.b0 = W;
@@ -1226,7 +1234,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // dW1's A rows are the tokens' x rows, read in place through perm
   wa.a = static_cast<const uint16_t*>(xb);
   wa.a_rows = b.perm;
-  wa.a_rows32 = (size_t)o.N * D * 2 < ((size_t)1 << 32);
+  wa.a_rows32 = !o.force64 && (size_t)o.N * D * 2 < ((size_t)1 << 32);
   wa.lda = D;
   wa.planes = 1;
   wa.b = dgub;
@@ -1247,7 +1255,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   wa.planes = o.hsplit ? 2 : 1;
   wa.b = ddb;
   wa.b_rows = b.perm;
-  wa.b_rows32 = (size_t)o.N * D * 2 < ((size_t)1 << 32);
+  wa.b_rows32 = !o.force64 && (size_t)o.N * D * 2 < ((size_t)1 << 32);
   wa.ldb = D;
   wa.M = F;
   wa.C = D;

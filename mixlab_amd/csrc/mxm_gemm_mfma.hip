@@ -735,7 +735,7 @@ static int resolve_family(const GemmArgs& a) {
 void mxm_launch_gemm_mfma(const GemmArgs& args, hipStream_t s) {
   if (args.max_mtiles <= 0) return;
   GemmArgs a = args;
-  a.a_off32 = (size_t)a.rows_total * a.Kd * 2 < ((size_t)1 << 32);
+  a.a_off32 = !a.no_off32 && (size_t)a.rows_total * a.Kd * 2 < ((size_t)1 << 32);
   switch (resolve_family(a)) {
     case MXM_TILE_256x128:
       launch_family<256, 128, 2, 2, 2, 3, 32>(a, s);

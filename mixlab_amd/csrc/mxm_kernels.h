@@ -166,8 +166,10 @@ struct GemmArgs {
   // projections do) instead of reading them in slot order
   bool gather_a;
   // set by the MFMA launcher: every A row lies within 4 GiB of a (rows_total
-  // * Kd bf16 bound it), so A loads take 32-bit byte offsets
+  // * Kd bf16 bound it), so A loads take 32-bit byte offsets ...
   bool a_off32;
+  // ... unless the caller forbids it (64-bit addressing throughout)
+  bool no_off32;
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.

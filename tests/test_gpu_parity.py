@@ -653,6 +653,39 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
+@pytest.mark.parametrize("shape", [(1, 2048, 256, 64, 256, 8), (1, 1000, 384, 24, 128, 4),
+                                   (1, 1000, 384, 24, 128, 10)])
+def test_64bit_offset_paths(gpu_lib, monkeypatch, shape):
+    """The MFMA kernels address operands below 4 GiB with 32-bit byte offsets
+    (the grouped GEMM's gathered A rows, the weight gradients' gathered x and
+    dD rows) and keep 64-bit addressing for larger ones.
+    MXM_FORCE_64BIT_OFFSETS=1 at op creation takes the 64-bit paths on these
+    small shapes: the forward and the whole backward must come out bit for
+    bit the same.  The shapes cover the 256-wide tiles (64 experts, top-8)
+    and the 128-wide ones (D = 384) with 1000 rows, so that experts end in
+    partial 64-row stages, at K = 4 and K = 10."""
+    from mixlab_amd.op import MoEFeedForward
+
+    B, T, D, E, F, K = shape
+    N = B * T
+    x, wr, experts = random_case(87, N, D, E, F, wscale=0.1)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(w) for w in ws] for ws in experts]
+    dD = np.random.default_rng(88).standard_normal((N, D), dtype=np.float32)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("MXM_FORCE_64BIT_OFFSETS", mode)
+        with MoEFeedForward([B, T, D, E, K, 0, F, 0], [0.0], compute_dtype="bf16") as op:
+            op.set_weights(bf16_bits(wr), [[bf16_bits(w) for w in ws] for ws in experts])
+            assert op.info()["mfma"]
+            delta = op.forward_host(x)[0]
+            dx, dwr, dexp = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
+            outs[mode] = [delta, dx, dwr] + [np.asarray(w) for ws in dexp for w in ws]
+    for i, (a, b) in enumerate(zip(outs["0"], outs["1"])):
+        assert np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                              np.asarray(b, np.float32).view(np.uint32)), i
+
+
 @pytest.mark.parametrize("shape", [(2, 96, 256, 6, 256, 2), (1, 2048, 256, 64, 256, 8),
                                    (1, 1000, 384, 72, 128, 4)])
 def test_backward_bf16_router_wgrad_paths(gpu_lib, monkeypatch, shape):
