@@ -278,13 +278,16 @@ def copy_calibration(mib: int, reps: int = 5) -> int:
     return 0
 
 
-def run_backward(cfg, steps: int, warmup: int, w=None) -> dict:
+def run_backward(cfg, steps: int, warmup: int, w=None, train: bool = False) -> dict:
     """Backward of op 74 (mxm_moe_backward: a forward with the routing kept,
     then the gradients of x, the router and every routed expert) on the
     configuration's compute dtype.  fp32: the routing of the forward, then
     every expert product as a per-expert rocBLAS fp32 GEMM (fp32 matrix
     cores); bf16 (MFMA weight family): every product on MFMA, the weight
-    gradients on the ragged grouped weight-gradient kernel (fp32 out)."""
+    gradients on the ragged grouped weight-gradient kernel (fp32 out).
+    train: a training step instead -- mxm_moe_forward on an op created with
+    MXM_FLAG_KEEP_FOR_BACKWARD, then mxm_moe_backward on the same x, which
+    reuses the forward's routing and projections."""
     from mixlab_amd import _lib
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import make_workload
@@ -292,7 +295,8 @@ def run_backward(cfg, steps: int, warmup: int, w=None) -> dict:
     bf16 = cfg.dtype == "bf16"
     if w is None:
         w = make_workload(cfg)
-    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype)
+    op = MoEFeedForward(cfg.int_params, [cfg.leaky_slope], compute_dtype=cfg.dtype,
+                        flags=_lib.MXM_FLAG_KEEP_FOR_BACKWARD if train else 0)
     op.set_input(1, w.router_upload() if bf16 else np.ascontiguousarray(w.router_w, np.float32))
     idx = 2
     for e in range(cfg.E):
@@ -311,7 +315,11 @@ def run_backward(cfg, steps: int, warmup: int, w=None) -> dict:
     lib = _lib.init()
     mfma = op.info()["mfma"]
 
+    delta = _lib.DeviceBuffer(cfg.N * cfg.D * 4) if train else None
+
     def step():
+        if train:
+            op.forward(xdev.value, xcode, cfg.N, delta.value)
         _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, xcode, cfg.N,
                                         dd.value, 0.01, 0.0, dx.value, dwr.value, dw.value),
                    "mxm_moe_backward")
@@ -334,10 +342,11 @@ def run_backward(cfg, steps: int, warmup: int, w=None) -> dict:
     fl = 2 * nkdf * ((3 if glu else 2) + 1 + (2 if glu else 1)
                      + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
     tf = fl / (ms * 1e-3) / 1e12
-    log(f"backward {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+    log(f"{'training step' if train else 'backward'} {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, "
+        f"{tf:.1f} TFLOP/s")
     if bf16 and mfma:
-        roof = {"bound": "mfma", "kernel": "whole backward (MFMA grouped products and "
-                "weight gradients)", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+        roof = {"bound": "mfma", "kernel": ("forward + backward" if train else "whole backward")
+                + " (MFMA grouped products and weight gradients)", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": tf / PEAK_BF16_TFLOPS, "traffic": None}
     else:
         roof = {"bound": "mfma", "kernel": "whole backward (per-expert rocBLAS fp32 GEMMs)",
@@ -407,9 +416,10 @@ def main() -> int:
         cpu = cpu_baseline(w, cfg, args.cpu_seconds)
         log(f"cpu baseline {cpu}")
     # the backward at the headline shape, on the same generated workload
-    backward_bf16_main = None
+    backward_bf16_main = train_bf16_main = None
     if not args.no_backward and cfg.dtype == "bf16" and not cfg.int8_weights:
         backward_bf16_main = run_backward(cfg, 3, 2, w=w)
+        train_bf16_main = run_backward(cfg, 3, 2, w=w, train=True)
     del w
 
     decode = None
@@ -499,6 +509,7 @@ def main() -> int:
         "backward_bf16": backward_bf16,
         "backward_bf16_c3": backward_bf16_c3,
         f"backward_bf16_{cfg.name.lower()}": backward_bf16_main,
+        f"train_step_bf16_{cfg.name.lower()}": train_bf16_main,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -57,6 +57,14 @@ extern "C" {
 #define MXM_FLAG_MFMA_TILE_MASK 12
 #define MXM_FLAG_INT8_WEIGHTS 16 /* expert weights are int8 + per-output-channel scales
                                     (mxm_moe_set_input_q8); bf16 compute */
+/* bf16 compute on the MFMA family: each mxm_moe_forward also keeps its
+ * routing, router probabilities and raw up projections, and the next
+ * mxm_moe_backward on the same x (same device pointer, dtype and rows, x
+ * unchanged in between) uses them instead of running the forward again, as
+ * the reference's autodiff keeps the forward's values for its backward.
+ * Any other forward on the op drops them.  No counterpart flag in the
+ * reference (its graph keeps them implicitly). */
+#define MXM_FLAG_KEEP_FOR_BACKWARD 32
 
 /* Stages timed by mxm_moe_stage_times, in launch order. */
 #define MXM_STAGE_ROUTER 0

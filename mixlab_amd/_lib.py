@@ -24,6 +24,7 @@ MXM_FLAG_MFMA_TILE128 = 4
 MXM_FLAG_MFMA_TILE256x128 = 8
 MXM_FLAG_MFMA_TILE256x256 = 12
 MXM_FLAG_INT8_WEIGHTS = 16
+MXM_FLAG_KEEP_FOR_BACKWARD = 32
 MXM_NUM_STAGES = 6
 MXM_NOALLOC_MAX_BYTES = 64 << 20
 STAGE_NAMES = ("router", "scan", "scatter", "gemm_up", "gemm_down", "combine")

@@ -148,6 +148,11 @@ struct MoeOp {
   // (router, scan, scatter); the backward computes the experts' products itself
   bool route_only = false;
   bool up_only = false;  // the forward stops after the up projection (MFMA backward)
+  // MXM_FLAG_KEEP_FOR_BACKWARD: the last mxm_moe_forward kept its routing,
+  // probabilities and raw up projections for a backward on the same x
+  bool train = false, kept = false;
+  const void* kept_x = nullptr;
+  int kept_dtype = -1;
   // d router_w in the MFMA backward: on the weight-gradient kernel (1), on
   // the SIMT kernel (0), or by size (-1); MXM_ROUTER_WGRAD_MFMA at creation
   int dwr_mode = -1;
@@ -333,6 +338,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   hipStream_t st = o.stream;
   o.last = w;
   o.have_last = true;
+  o.kept = false;  // every forward overwrites what a kept one left
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
     mxm_launch_to_bf16(x, MXM_DTYPE_F32, static_cast<uint16_t*>(w.xcast), (int64_t)o.N * o.D, st);
@@ -481,9 +487,12 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     require_operands(g1, glu, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
   } else if (o.mfma) {
-    g1.out2 = pre_out;  // the backward keeps the raw projections too
+    g1.out2 = pre_out;  // the backward keeps the raw projections (and no hidden)
     require_operands(g1, false, false);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
+    if (pre_out && !o.up_only)  // a kept forward: the hidden from them, as the epilogue would
+      mxm_launch_hidden_from_raw_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope, o.hsplit,
+                                      static_cast<uint16_t*>(w.H), st);
   } else {
     require_operands(g1, glu, false);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_simt(g1, o.bf16, st);
@@ -831,6 +840,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
                 mxm_mfma_tile_rows(o->D, o->F, f) > 0;
     }
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
+    o->train = (flags & MXM_FLAG_KEEP_FOR_BACKWARD) != 0;
     o->q8 = (flags & MXM_FLAG_INT8_WEIGHTS) != 0;
     if (o->q8) {
       if (!o->bf16) fail("OP_MOE_FEED_FORWARD int8 weights need bf16 compute");
@@ -913,6 +923,9 @@ int mxm_moe_set_input_q8(int64_t h, int input_index, const int8_t* q, const floa
   });
 }
 
+bool mfma_backward_fits(const MoeOp& o);
+static uint16_t* bw_gu_buffer(MoeOp& o);
+
 int mxm_moe_forward(int64_t h, const void* x, int x_dtype, int64_t rows, float* delta, float* aux,
                     float* entropy) {
   OP_OR_RETURN(h);
@@ -920,7 +933,25 @@ int mxm_moe_forward(int64_t h, const void* x, int x_dtype, int64_t rows, float* 
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
     if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
     if (!op->ws_ready) alloc_workspace(*op);
-    run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy);
+    if (op->train && mfma_backward_fits(*op)) {
+      // keep what the backward's own forward would recompute
+      op->keep_probs = true;
+      try {
+        run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy, nullptr, bw_gu_buffer(*op));
+      } catch (...) {
+        op->keep_probs = false;
+        throw;
+      }
+      op->keep_probs = false;
+      if (op->debug_probs)  // (mxm_moe_probs reads the workspace's copy)
+        HIPCK(hipMemcpyAsync(op->ws.probs, op->bw_probs.p, (size_t)op->N * op->E * 4,
+                             hipMemcpyDeviceToDevice, op->stream));
+      op->kept = true;
+      op->kept_x = x;
+      op->kept_dtype = x_dtype;
+    } else {
+      run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy);
+    }
     return MXM_OK;
   });
 }
@@ -1368,8 +1399,16 @@ void run_backward_blas32(MoeOp& o, BackwardArgs& b, bool own_forward) {
   HIPCK(hipGetLastError());
 }
 
+static uint16_t* bw_gu_buffer(MoeOp& o) {
+  if (!o.bw_probs.p) o.bw_probs.alloc((size_t)o.N * o.E * 4);
+  if (!o.bw_gub.p) o.bw_gub.alloc((size_t)o.N * o.K * (size_t)(o.wpe == 3 ? 2 * o.F : o.F) * 2);
+  return o.bw_gub.as<uint16_t>();
+}
+
+// allow_kept: a forward kept for the same x may stand in for the backward's
+// own (device calls only: a host call's staging copy is a new buffer)
 void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
-                  float d_ent, float* dx, float* dwr, float* dw) {
+                  float d_ent, float* dx, float* dwr, float* dw, bool allow_kept = false) {
   if (o.q8) fail("OP_MOE_FEED_FORWARD backward is not available for int8 expert weights");
   if (x_dtype != MXM_DTYPE_F32 && !(o.bf16 && x_dtype == MXM_DTYPE_BF16))
     fail("OP_MOE_FEED_FORWARD backward takes fp32 x (or bf16 x under bf16 compute)");
@@ -1439,26 +1478,28 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     }
   }
   // the MFMA backward's G|U (pre-activation products) come from the forward
-  uint16_t* gu = nullptr;
-  if (mfma_bw) {
-    if (!o.bw_gub.p) o.bw_gub.alloc(NK * (size_t)(o.wpe == 3 ? 2 * F : F) * 2);
-    gu = o.bw_gub.as<uint16_t>();
-  }
+  uint16_t* gu = mfma_bw ? bw_gu_buffer(o) : nullptr;
+  // a forward kept for this x (MXM_FLAG_KEEP_FOR_BACKWARD) left the routing,
+  // the probabilities and the raw projections where this forward puts them
+  const bool reuse = mfma_bw && allow_kept && o.kept && x == o.kept_x && x_dtype == o.kept_dtype;
   // fp32 compute: the forward's routing only; the experts' forward products
   // are computed by run_backward_blas32 (and kept for the backward)
   const bool own_forward = !o.bf16;
-  o.keep_probs = true;
-  o.route_only = own_forward;
-  // the MFMA backward needs the routing, H and G|U only: its gate gradients
-  // come from dD W_down^T (the product that also gives dH), not from Y
-  o.up_only = mfma_bw;
-  try {
-    run_forward(o, o.ws, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
-  } catch (...) {
+  if (!reuse) {
+    o.keep_probs = true;
+    o.route_only = own_forward;
+    // the MFMA backward needs the routing and G|U only: its gate gradients
+    // come from dD W_down^T (the product that also gives dH), not from Y
+    o.up_only = mfma_bw;
+    try {
+      run_forward(o, o.ws, x, x_dtype, o.bw_delta.as<float>(), nullptr, nullptr, nullptr, gu);
+    } catch (...) {
+      o.keep_probs = o.route_only = o.up_only = false;
+      throw;
+    }
     o.keep_probs = o.route_only = o.up_only = false;
-    throw;
   }
-  o.keep_probs = o.route_only = o.up_only = false;
+  o.kept = false;  // (the backward overwrites the hidden)
   // x as the forward saw it (rounded to bf16 when given in fp32)
   const void* xb = (o.bf16 && x_dtype == MXM_DTYPE_BF16) ? x : o.ws.xcast;
   // The MFMA backward's router part reads x and a bf16 Y as they are; the
@@ -1538,7 +1579,7 @@ int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const 
   OP_OR_RETURN(h);
   return fenced([&] {
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
-    run_backward(*op, x, x_dtype, d_delta, d_aux, d_entropy, dx, d_router_w, d_experts);
+    run_backward(*op, x, x_dtype, d_delta, d_aux, d_entropy, dx, d_router_w, d_experts, true);
     return MXM_OK;
   });
 }

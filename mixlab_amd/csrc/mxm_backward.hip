@@ -812,6 +812,42 @@ __global__ __launch_bounds__(256) void act_bw_gated_bf16_kernel(
   if (lane == 0) dgp[p] = dot;
 }
 
+// One thread per 8 hidden units of a routed row: h = mxm_hidden_fast of the
+// raw bf16 projections (GLU: gate and up columns interleaved in groups of
+// 32), stored as the up GEMM's epilogue stores it.
+__global__ void hidden_from_raw_bf16_kernel(const uint16_t* __restrict__ gu, int F, int etype,
+                                            int act, float slope, bool hsplit,
+                                            uint16_t* __restrict__ H, size_t total) {
+  const bool glu = etype != MXM_EXPERT_MLP;
+  const int NC = glu ? 2 * F : F, nb = F / 8;
+  const size_t hstride = hsplit ? 2 * (size_t)F : (size_t)F;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t p = i / nb;
+    const int f = (int)(i % nb) * 8;
+    const size_t cu = p * NC + (glu ? (size_t)(f >> 5) * 64 + 32 + (f & 31) : (size_t)f);
+    const uint4 uv = *reinterpret_cast<const uint4*>(gu + cu);
+    const uint4 gv = glu ? *reinterpret_cast<const uint4*>(gu + cu - 32) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float h[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float gg = glu ? mxm_u2f(t ? gw[q] & 0xffff0000u : gw[q] << 16) : 0.0f;
+        const float uu = mxm_u2f(t ? uw[q] & 0xffff0000u : uw[q] << 16);
+        h[t] = mxm_hidden_fast<true>(glu ? etype : MXM_EXPERT_MLP, act, slope, gg, uu);
+      }
+      hw[q] = mxm_pack_bf2_fast(h[0], h[1]);
+      lw[q] = mxm_pack_bf2_fast(h[0] - mxm_u2f(hw[q] << 16), h[1] - mxm_u2f(hw[q] & 0xffff0000u));
+    }
+    *reinterpret_cast<uint4*>(H + p * hstride + f) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    if (hsplit)
+      *reinterpret_cast<uint4*>(H + p * hstride + F + f) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+}
+
 // dx[n] = dxr[n] + sum_k dxe[slot_pos(n, k)] (bf16 rows), k ascending
 __global__ void dx_bf16_kernel(const float* __restrict__ dxr, const uint16_t* __restrict__ dxe,
                                const int32_t* __restrict__ slot_pos, int D, int K,
@@ -926,6 +962,14 @@ void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot
   else
     hipLaunchKernelGGL(dy_gate_kernel<1>, dim3(N), dim3(block_for(D, 1)), 0, s, dd, gates,
                        slot_pos, D, K, ddb, dyb, gp);
+}
+
+void mxm_launch_hidden_from_raw_bf16(const uint16_t* gu, int rows, int F, int etype, int act,
+                                     float slope, bool hsplit, uint16_t* H, hipStream_t s) {
+  const size_t total = (size_t)rows * (F / 8);
+  if (total > 0)
+    hipLaunchKernelGGL(hidden_from_raw_bf16_kernel, dim3(grid_of(total)), dim3(256), 0, s, gu, F,
+                       etype, act, slope, hsplit, H, total);
 }
 
 void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint16_t* Hg,

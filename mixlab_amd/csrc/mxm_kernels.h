@@ -399,6 +399,11 @@ void mxm_launch_dwr_halves(const float* t, int D, int E, int Ep, float* dwr, hip
 // gp[p] = gates[s] and (if dyb is set) dyb[p] = bf16(gates[s] * dD[n]).
 void mxm_launch_dy_gate(const float* dd, const float* gates, const int32_t* slot_pos, int N, int D,
                         int K, uint16_t* ddb, uint16_t* dyb, float* gp, hipStream_t s);
+// The hidden H [rows][F] (hi, and lo = bf16(h - hi) after F columns when
+// hsplit) from raw bf16 up projections gu [rows][NC] with the up epilogue's
+// own activation code: bit for bit what the epilogue would store.
+void mxm_launch_hidden_from_raw_bf16(const uint16_t* gu, int rows, int F, int etype, int act,
+                                     float slope, bool hsplit, uint16_t* H, hipStream_t s);
 // ... then, per routed row p: the hidden h from the forward's raw bf16
 // projections gu with the up epilogue's own activation code (bit for bit the
 // forward's); the gated hidden gp[p] * h written to Hg (hi, and lo =

@@ -653,6 +653,59 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
+@pytest.mark.parametrize("shape,etype,act", [((1, 2048, 256, 64, 256, 8), 0, 0),
+                                             ((1, 1000, 384, 24, 128, 4), 1, 1)])
+def test_backward_kept_forward(gpu_lib, shape, etype, act):
+    """MXM_FLAG_KEEP_FOR_BACKWARD: a device forward keeps its routing,
+    probabilities and raw up projections (and derives the hidden from them
+    for its down projection), and the next device backward on the same x
+    buffer uses them instead of its own forward.  Against an op without the
+    flag on the same inputs: the forward's delta and the backward's dx,
+    d router_w and expert gradients are bit for bit the same; a backward on
+    another buffer holding the same x runs its own forward and gives them
+    too.  The second case has a split (fp32) hidden: geglu."""
+    import ctypes
+
+    from mixlab_amd.op import MoEFeedForward
+
+    B, T, D, E, F, K = shape
+    N = B * T
+    x, wr, experts = random_case(89, N, D, E, F, expert_type=etype, wscale=0.1)
+    dD = np.random.default_rng(90).standard_normal((N, D), dtype=np.float32)
+    lib = _lib.init()
+    xb = bf16_bits(round_bf16(x))
+    xdev = _lib.DeviceBuffer.from_array(xb)
+    xdev2 = _lib.DeviceBuffer.from_array(xb)
+    ddev = _lib.DeviceBuffer.from_array(dD)
+    nw = 2 if etype == 2 else 3
+
+    def run(flags, backward_x):
+        with MoEFeedForward([B, T, D, E, K, etype, F, act], [0.0], compute_dtype="bf16",
+                            flags=flags) as op:
+            op.set_weights(bf16_bits(round_bf16(wr)),
+                           [[bf16_bits(round_bf16(w)) for w in ws] for ws in experts])
+            assert op.info()["mfma"]
+            delta = _lib.DeviceBuffer(N * D * 4)
+            aux, ent = _lib.DeviceBuffer(4), _lib.DeviceBuffer(4)
+            op.forward(xdev.value, _lib.MXM_DTYPE_BF16, N, delta.value, aux.value, ent.value)
+            dx = _lib.DeviceBuffer(N * D * 4)
+            dwr = _lib.DeviceBuffer(D * E * 4)
+            dw = _lib.DeviceBuffer(E * nw * D * F * 4)
+            _lib.check(lib.mxm_moe_backward(op.handle, backward_x.value, _lib.MXM_DTYPE_BF16, N,
+                                            ddev.value, 0.3, -0.2, dx.value, dwr.value,
+                                            dw.value), "mxm_moe_backward")
+            op.synchronize()
+            return [delta.download(np.float32, (N * D,)), aux.download(np.float32, (1,)),
+                    dx.download(np.float32, (N * D,)), dwr.download(np.float32, (D * E,)),
+                    dw.download(np.float32, (E * nw * D * F,))]
+
+    want = run(0, xdev)
+    for got in (run(_lib.MXM_FLAG_KEEP_FOR_BACKWARD, xdev),
+                run(_lib.MXM_FLAG_KEEP_FOR_BACKWARD, xdev2)):
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+
+
 @pytest.mark.parametrize("shape", [(1, 2048, 256, 64, 256, 8), (1, 1000, 384, 24, 128, 4),
                                    (1, 1000, 384, 24, 128, 10)])
 def test_64bit_offset_paths(gpu_lib, monkeypatch, shape):
