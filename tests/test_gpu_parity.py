@@ -654,7 +654,8 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
 
 
 @pytest.mark.parametrize("shape,etype,act", [((1, 2048, 256, 64, 256, 8), 0, 0),
-                                             ((1, 1000, 384, 24, 128, 4), 1, 1)])
+                                             ((1, 1000, 384, 24, 128, 4), 1, 1),
+                                             ((1, 1000, 384, 24, 128, 4), 2, 0)])
 def test_backward_kept_forward(gpu_lib, shape, etype, act):
     """MXM_FLAG_KEEP_FOR_BACKWARD: a device forward keeps its routing,
     probabilities and raw up projections (and derives the hidden from them
@@ -663,7 +664,8 @@ def test_backward_kept_forward(gpu_lib, shape, etype, act):
     flag on the same inputs: the forward's delta and the backward's dx,
     d router_w and expert gradients are bit for bit the same; a backward on
     another buffer holding the same x runs its own forward and gives them
-    too.  The second case has a split (fp32) hidden: geglu."""
+    too.  The second case has a split (fp32) hidden (geglu), the third is a
+    plain MLP expert (silu, bf16 hidden)."""
     import ctypes
 
     from mixlab_amd.op import MoEFeedForward
