@@ -286,8 +286,8 @@ def run_backward(cfg, steps: int, warmup: int, w=None, train: bool = False) -> d
     cores); bf16 (MFMA weight family): every product on MFMA, the weight
     gradients on the ragged grouped weight-gradient kernel (fp32 out).
     train: a training step instead -- mxm_moe_forward on an op created with
-    MXM_FLAG_KEEP_FOR_BACKWARD, then mxm_moe_backward on the same x, which
-    reuses the forward's routing and projections."""
+    MXM_FLAG_KEEP_FOR_BACKWARD, then mxm_moe_backward_kept, which starts
+    from the routing and projections that forward kept."""
     from mixlab_amd import _lib
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import make_workload
@@ -320,9 +320,12 @@ def run_backward(cfg, steps: int, warmup: int, w=None, train: bool = False) -> d
     def step():
         if train:
             op.forward(xdev.value, xcode, cfg.N, delta.value)
-        _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, xcode, cfg.N,
-                                        dd.value, 0.01, 0.0, dx.value, dwr.value, dw.value),
-                   "mxm_moe_backward")
+            _lib.check(lib.mxm_moe_backward_kept(op.handle, dd.value, 0.01, 0.0, dx.value,
+                                                 dwr.value, dw.value), "mxm_moe_backward_kept")
+        else:
+            _lib.check(lib.mxm_moe_backward(op.handle, xdev.value, xcode, cfg.N,
+                                            dd.value, 0.01, 0.0, dx.value, dwr.value, dw.value),
+                       "mxm_moe_backward")
 
     for _ in range(warmup):
         step()
@@ -335,12 +338,18 @@ def run_backward(cfg, steps: int, warmup: int, w=None, train: bool = False) -> d
     op.close()
     glu = cfg.expert_type != 2
     nkdf = cfg.N * cfg.K * cfg.D * cfg.F
-    # algorithmic work of a forward + backward as autodiff forms it: forward
-    # (3 or 2 products) + dH + dX + weight gradients, plus the router's
-    # forward and backward.  (The bf16 MFMA path skips the forward's down
-    # product: the gate gradients come from the dH product itself.)
-    fl = 2 * nkdf * ((3 if glu else 2) + 1 + (2 if glu else 1)
-                     + (3 if glu else 2)) + 6 * cfg.N * cfg.D * cfg.E
+    # The products the call runs, each 2*N*K*D*F FLOP (one D x F product over
+    # all routed rows), plus the router's 2*N*D*E forward and 4*N*D*E
+    # backward.  The backward call of the bf16 MFMA path runs its forward's
+    # up projections (2 or 1) but not the down product (its gate gradients
+    # come from dH' = dD W_down^T), then dH', dX (2 or 1) and the weight
+    # gradients (3 or 2): 8 or 5.  A training step runs the whole forward (3
+    # or 2) and that backward without the forward: 9 or 6.  The fp32 path's
+    # backward call runs the whole forward before its backward: 9 or 6.
+    fwd = 3 if glu else 2
+    bwd = 1 + (2 if glu else 1) + (3 if glu else 2)
+    units = fwd + bwd if (train or not (bf16 and mfma)) else fwd - 1 + bwd
+    fl = 2 * nkdf * units + 6 * cfg.N * cfg.D * cfg.E
     tf = fl / (ms * 1e-3) / 1e12
     log(f"{'training step' if train else 'backward'} {cfg.name} {cfg.dtype}: {ms:.3f} ms/step, "
         f"{tf:.1f} TFLOP/s")
@@ -353,7 +362,8 @@ def run_backward(cfg, steps: int, warmup: int, w=None, train: bool = False) -> d
                 "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": tf / PEAK_FP32_TFLOPS, "traffic": None}
     return {"workload": f"{cfg.name} shape, {cfg.dtype} compute", "tokens": cfg.N,
-            "ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3), "roofline": roof}
+            "ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3),
+            "expert_products_counted": units, "flop_per_step": fl, "roofline": roof}
 
 
 def main() -> int:

@@ -15,8 +15,11 @@
  *   Outputs     = [delta [B*T, D] fp32, aux [1] fp32, entropy [1] fp32]
  *
  * Conventions follow gpu/mlx_bridge.h: opaque int64 handles with 0 meaning
- * failure (gpu/mlx_bridge.h:70-83), int status codes with 0 = OK and -1 =
- * failure (gpu/mlx_bridge.cpp:814-823), and no C++ exception ever crosses the
+ * failure (gpu/mlx_bridge.h:70-83), int status codes (gpu/mlx_bridge.cpp:
+ * 814-823): 0 = OK, -10 = an argument the call cannot accept (shape, dtype,
+ * index, size limit, NULL pointer), -11 = the HIP runtime or device could not
+ * be initialised, -12 = not a live op handle, -1 = any other failure (a HIP
+ * error, a call out of sequence); no C++ exception ever crosses the
  * boundary (gpu/mlx_bridge.cpp:64-82): the message of the last failure on the
  * calling thread is available from mxm_last_error.  Tensor dtype codes extend
  * mlx_tensor_input's (0 = int32, 1 = float32; gpu/mlx_bridge.h:92-99).
@@ -34,10 +37,10 @@ extern "C" {
 #endif
 
 #define MXM_OK 0
-#define MXM_ERR -1
-#define MXM_ERR_ARGS -10 /* gpu/mlx_bridge.cpp:814-823: argument error */
-#define MXM_ERR_INIT -11 /* runtime / device not initialised */
-#define MXM_ERR_OP -12   /* bad op handle */
+#define MXM_ERR -1       /* HIP error, call out of sequence */
+#define MXM_ERR_ARGS -10 /* gpu/mlx_bridge.cpp:814-815: argument error */
+#define MXM_ERR_INIT -11 /* gpu/mlx_bridge.cpp:818-819: runtime / device not initialised */
+#define MXM_ERR_OP -12   /* gpu/mlx_bridge.cpp:821-822: bad op handle */
 
 #define MXM_DTYPE_INT32 0 /* gpu/mlx_bridge.h:94 */
 #define MXM_DTYPE_F32 1   /* gpu/mlx_bridge.h:94 */
@@ -57,12 +60,11 @@ extern "C" {
 #define MXM_FLAG_MFMA_TILE_MASK 12
 #define MXM_FLAG_INT8_WEIGHTS 16 /* expert weights are int8 + per-output-channel scales
                                     (mxm_moe_set_input_q8); bf16 compute */
-/* bf16 compute on the MFMA family: each mxm_moe_forward also keeps its
- * routing, router probabilities and raw up projections, and the next
- * mxm_moe_backward on the same x (same device pointer, dtype and rows, x
- * unchanged in between) uses them instead of running the forward again, as
- * the reference's autodiff keeps the forward's values for its backward.
- * Any other forward on the op drops them.  No counterpart flag in the
+/* Each mxm_moe_forward keeps the op's own copy of x and, under bf16 compute
+ * on the MFMA family, its routing, router probabilities and raw up
+ * projections, for mxm_moe_backward_kept: the backward of that forward,
+ * which then does not run the forward again, as the reference's autodiff
+ * keeps the forward's values for its backward.  No counterpart flag in the
  * reference (its graph keeps them implicitly). */
 #define MXM_FLAG_KEEP_FOR_BACKWARD 32
 
@@ -76,7 +78,7 @@ extern "C" {
 #define MXM_NUM_STAGES 6
 
 /* Initialise the HIP runtime on the current device.  Replaces mlx_init
- * (gpu/mlx_bridge.h:15).  0 on success, -1 on failure. */
+ * (gpu/mlx_bridge.h:15).  0 on success, MXM_ERR_INIT on failure. */
 int mxm_init(void);
 
 /* Device name ("AMD Instinct MI355X ..."); replaces mlx_device_name
@@ -210,6 +212,19 @@ int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t r
  * holds the weight gradients' split-reduction partials). */
 int mxm_moe_backward(int64_t op, const void* x, int x_dtype, int64_t rows, const float* d_delta,
                      float d_aux, float d_entropy, float* dx, float* d_router_w, float* d_experts);
+
+/* The backward of the op's last call, which must be an mxm_moe_forward on
+ * an op created with MXM_FLAG_KEEP_FOR_BACKWARD: the gradients at the x that
+ * forward read (the op kept its own copy, so the caller's buffer may have
+ * changed since), from the routing and projections it kept.  Outputs as
+ * mxm_moe_backward's.  Any other call that runs the op -- another forward
+ * (plain, host, no-allocation or block), a backward -- or a weight update
+ * with mxm_moe_set_input[_q8] drops the kept forward; without one this
+ * returns MXM_ERR.  Replaces the backward half of the trainer's
+ * value_and_grad over the graph (gpu/ir_trainer.cpp:2790-2816), which
+ * differentiates the forward it just ran. */
+int mxm_moe_backward_kept(int64_t op, const float* d_delta, float d_aux, float d_entropy, float* dx,
+                          float* d_router_w, float* d_experts);
 
 /* Same with host buffers; synchronous. */
 int mxm_moe_backward_host(int64_t op, const void* x, int x_dtype, int64_t rows,

@@ -14,6 +14,10 @@ import numpy as np
 LIB_PATH = Path(__file__).resolve().parent / "libmixmoe.so"
 
 MXM_OK = 0
+MXM_ERR = -1
+MXM_ERR_ARGS = -10
+MXM_ERR_INIT = -11
+MXM_ERR_OP = -12
 MXM_DTYPE_INT32 = 0
 MXM_DTYPE_F32 = 1
 MXM_DTYPE_BF16 = 2
@@ -67,6 +71,8 @@ SIGNATURES = {
                                         ctypes.c_float, ctypes.c_float, _VP, _VP, _VP]),
     "mxm_moe_backward_host": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_int, ctypes.c_int64,
                                              _VP, ctypes.c_float, ctypes.c_float, _VP, _VP, _VP]),
+    "mxm_moe_backward_kept": (ctypes.c_int, [ctypes.c_int64, _VP, ctypes.c_float, ctypes.c_float,
+                                             _VP, _VP, _VP]),
     "mxm_moe_synchronize": (ctypes.c_int, [ctypes.c_int64]),
     "mxm_moe_routing": (ctypes.c_int, [ctypes.c_int64, _VP, _VP, _VP, _VP, _VP, ctypes.c_int]),
     "mxm_moe_probs": (ctypes.c_int, [ctypes.c_int64, _VP]),

@@ -33,19 +33,48 @@ std::map<int64_t, std::unique_ptr<struct MoeOp>> g_ops;
 int64_t g_next_handle = 1;
 std::string g_device_name = "uninitialised";
 
-[[noreturn]] void fail(const char* fmt, ...) {
+// Failure classes of the bridge's status codes (gpu/mlx_bridge.cpp:814-823):
+// an argument the call cannot accept (MXM_ERR_ARGS), a runtime that is not
+// initialised (MXM_ERR_INIT); every other failure -- a HIP error, a call out
+// of sequence -- is MXM_ERR.
+struct ArgError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct InitError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+template <class Ex>
+[[noreturn]] void vthrow(const char* fmt, va_list ap) {
   char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
   vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  throw std::runtime_error(buf);
+  throw Ex(buf);
 }
 
-#define HIPCK(expr)                                                                    \
-  do {                                                                                 \
-    hipError_t _e = (expr);                                                            \
-    if (_e != hipSuccess) fail("HIP error %s at %s:%d", hipGetErrorString(_e), __FILE__, __LINE__); \
+// An argument error (shape, dtype, index, size limit, NULL pointer).
+[[noreturn]] void fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vthrow<ArgError>(fmt, ap);
+}
+// A runtime failure or a call out of sequence.
+[[noreturn]] void fail_rt(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vthrow<std::runtime_error>(fmt, ap);
+}
+// The HIP runtime or the device is not (or cannot be) initialised.
+[[noreturn]] void fail_init(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vthrow<InitError>(fmt, ap);
+}
+
+#define HIPCK(expr)                                                                       \
+  do {                                                                                    \
+    hipError_t _e = (expr);                                                               \
+    if (_e != hipSuccess)                                                                 \
+      fail_rt("HIP error %s at %s:%d", hipGetErrorString(_e), __FILE__, __LINE__);       \
   } while (0)
 
 struct DevBuf {
@@ -148,10 +177,11 @@ struct MoeOp {
   // (router, scan, scatter); the backward computes the experts' products itself
   bool route_only = false;
   bool up_only = false;  // the forward stops after the up projection (MFMA backward)
-  // MXM_FLAG_KEEP_FOR_BACKWARD: the last mxm_moe_forward kept its routing,
-  // probabilities and raw up projections for a backward on the same x
+  // MXM_FLAG_KEEP_FOR_BACKWARD: the last call was an mxm_moe_forward, which
+  // kept its own copy of x and (MFMA backward family) its routing,
+  // probabilities and raw up projections for mxm_moe_backward_kept
   bool train = false, kept = false;
-  const void* kept_x = nullptr;
+  DevBuf kept_xbuf;
   int kept_dtype = -1;
   // d router_w in the MFMA backward: on the weight-gradient kernel (1), on
   // the SIMT kernel (0), or by size (-1); MXM_ROUTER_WGRAD_MFMA at creation
@@ -204,6 +234,12 @@ template <typename F>
 int fenced(F&& f) {
   try {
     return f();
+  } catch (const ArgError& e) {
+    g_last_error = e.what();
+    return MXM_ERR_ARGS;
+  } catch (const InitError& e) {
+    g_last_error = e.what();
+    return MXM_ERR_INIT;
   } catch (const std::exception& e) {
     g_last_error = e.what();
     return MXM_ERR;
@@ -310,7 +346,7 @@ void require_operands(const GemmArgs& g, bool second_matrix, bool scaled) {
   if (!g.a || !g.b0 || !g.out || !g.offsets || !g.mstart || (second_matrix && !g.b1) ||
       (scaled && (!g.scale0 || (second_matrix && !g.scale1))) ||
       (g.mode != MXM_GEMM_DOWN && !g.perm))
-    fail("OP_MOE_FEED_FORWARD internal error: expert GEMM operand not allocated (mode %d)", g.mode);
+    fail_rt("OP_MOE_FEED_FORWARD internal error: expert GEMM operand not allocated (mode %d)", g.mode);
 }
 
 // Block-level extras of a forward (arch/moe.go:152-213): the rows before
@@ -334,7 +370,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
                  float* ent, const BlockIO* blk = nullptr, uint16_t* pre_out = nullptr,
                  bool events = true) {
   for (int i = 1; i < o.n_inputs; ++i)
-    if (!o.have[i]) fail("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
+    if (!o.have[i]) fail_rt("OP_MOE_FEED_FORWARD input w%d (Op.Inputs[%d]) is not set", i - 1, i);
   hipStream_t st = o.stream;
   o.last = w;
   o.have_last = true;
@@ -635,6 +671,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
   o.have[idx] = 1;
   o.bw_w32_ready = false;
   o.bw_wbf_ready = false;
+  o.kept = false;  // a kept forward ran on the weights this call replaced
 }
 
 void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, const int64_t* shape,
@@ -669,6 +706,7 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   o.have[idx] = 1;
   o.bw_w32_ready = false;
   o.bw_wbf_ready = false;
+  o.kept = false;  // a kept forward ran on the weights this call replaced
 }
 
 // ---- device scratch of the no-allocation forward ----
@@ -694,20 +732,20 @@ char* g_scratch[kMaxDevices] = {};
 char* device_scratch(hipStream_t capturing) {
   int dev = 0;
   HIPCK(hipGetDevice(&dev));
-  if (dev < 0 || dev >= kMaxDevices) fail("OP_MOE_FEED_FORWARD device %d out of range", dev);
+  if (dev < 0 || dev >= kMaxDevices) fail_rt("OP_MOE_FEED_FORWARD device %d out of range", dev);
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch[dev]) {
     if (capturing) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
       HIPCK(hipStreamIsCapturing(capturing, &cs));
       if (cs != hipStreamCaptureStatusNone)
-        fail("OP_MOE_FEED_FORWARD no-allocation forward: call mxm_init on device %d before "
+        fail_init("OP_MOE_FEED_FORWARD no-allocation forward: call mxm_init on device %d before "
              "capturing",
              dev);
     }
     void* p = nullptr;
     HIPCK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    if (!p) fail("OP_MOE_FEED_FORWARD device scratch has no address on device %d", dev);
+    if (!p) fail_rt("OP_MOE_FEED_FORWARD device scratch has no address on device %d", dev);
     hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, nullptr, static_cast<int32_t*>(p),
                        64);
     HIPCK(hipGetLastError());
@@ -723,19 +761,24 @@ extern "C" {
 
 int mxm_init(void) {
   return fenced([&] {
-    int n = 0;
-    HIPCK(hipGetDeviceCount(&n));
-    if (n <= 0) fail("no HIP device");
-    int dev = 0;
-    HIPCK(hipGetDevice(&dev));
-    hipDeviceProp_t prop;
-    HIPCK(hipGetDeviceProperties(&prop, dev));
-    {
-      std::lock_guard<std::mutex> lk(g_mu);
-      g_device_name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
-                      std::to_string(prop.multiProcessorCount) + " CUs)";
+    // every failure here is an initialisation failure (MXM_ERR_INIT)
+    try {
+      int n = 0;
+      HIPCK(hipGetDeviceCount(&n));
+      if (n <= 0) fail_init("no HIP device");
+      int dev = 0;
+      HIPCK(hipGetDevice(&dev));
+      hipDeviceProp_t prop;
+      HIPCK(hipGetDeviceProperties(&prop, dev));
+      {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_device_name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
+                        std::to_string(prop.multiProcessorCount) + " CUs)";
+      }
+      device_scratch(nullptr);  // the no-allocation forward's scratch on this device
+    } catch (const std::exception& e) {
+      throw InitError(e.what());
     }
-    device_scratch(nullptr);  // the no-allocation forward's scratch on this device
     return MXM_OK;
   });
 }
@@ -933,21 +976,34 @@ int mxm_moe_forward(int64_t h, const void* x, int x_dtype, int64_t rows, float* 
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
     if (!x || !delta) fail("OP_MOE_FEED_FORWARD x and delta must be non-NULL");
     if (!op->ws_ready) alloc_workspace(*op);
-    if (op->train && mfma_backward_fits(*op)) {
-      // keep what the backward's own forward would recompute
-      op->keep_probs = true;
-      try {
-        run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy, nullptr, bw_gu_buffer(*op));
-      } catch (...) {
+    if (op->train) {
+      // the forward runs on the op's own copy of x, so that the kept backward
+      // differentiates at the x this forward saw whatever the caller's
+      // buffer holds by then
+      if (x_dtype != MXM_DTYPE_F32 && x_dtype != MXM_DTYPE_BF16)
+        fail("OP_MOE_FEED_FORWARD unsupported x dtype %d for this compute dtype", x_dtype);
+      const size_t xbytes = (size_t)op->N * op->D * (x_dtype == MXM_DTYPE_BF16 ? 2 : 4);
+      if (op->kept_xbuf.bytes < xbytes) op->kept_xbuf.alloc(xbytes);
+      op->kept = false;
+      HIPCK(hipMemcpyAsync(op->kept_xbuf.p, x, xbytes, hipMemcpyDeviceToDevice, op->stream));
+      const void* xk = op->kept_xbuf.p;
+      if (mfma_backward_fits(*op)) {
+        // keep what the backward's own forward would recompute
+        op->keep_probs = true;
+        try {
+          run_forward(*op, op->ws, xk, x_dtype, delta, aux, entropy, nullptr, bw_gu_buffer(*op));
+        } catch (...) {
+          op->keep_probs = false;
+          throw;
+        }
         op->keep_probs = false;
-        throw;
+        if (op->debug_probs)  // (mxm_moe_probs reads the workspace's copy)
+          HIPCK(hipMemcpyAsync(op->ws.probs, op->bw_probs.p, (size_t)op->N * op->E * 4,
+                               hipMemcpyDeviceToDevice, op->stream));
+      } else {
+        run_forward(*op, op->ws, xk, x_dtype, delta, aux, entropy);
       }
-      op->keep_probs = false;
-      if (op->debug_probs)  // (mxm_moe_probs reads the workspace's copy)
-        HIPCK(hipMemcpyAsync(op->ws.probs, op->bw_probs.p, (size_t)op->N * op->E * 4,
-                             hipMemcpyDeviceToDevice, op->stream));
       op->kept = true;
-      op->kept_x = x;
       op->kept_dtype = x_dtype;
     } else {
       run_forward(*op, op->ws, x, x_dtype, delta, aux, entropy);
@@ -1104,7 +1160,7 @@ bool mfma_backward_fits(const MoeOp& o) {
 
 void check_blas(rocblas_status st, const char* what) {
   if (st != rocblas_status_success)
-    fail("OP_MOE_FEED_FORWARD backward: %s failed (rocBLAS status %d)", what, (int)st);
+    fail_rt("OP_MOE_FEED_FORWARD backward: %s failed (rocBLAS status %d)", what, (int)st);
 }
 
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
@@ -1405,8 +1461,8 @@ static uint16_t* bw_gu_buffer(MoeOp& o) {
   return o.bw_gub.as<uint16_t>();
 }
 
-// allow_kept: a forward kept for the same x may stand in for the backward's
-// own (device calls only: a host call's staging copy is a new buffer)
+// allow_kept (mxm_moe_backward_kept, x = the kept forward's copy): the kept
+// routing and projections stand in for the backward's own forward
 void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, float d_aux,
                   float d_ent, float* dx, float* dwr, float* dw, bool allow_kept = false) {
   if (o.q8) fail("OP_MOE_FEED_FORWARD backward is not available for int8 expert weights");
@@ -1479,9 +1535,9 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   }
   // the MFMA backward's G|U (pre-activation products) come from the forward
   uint16_t* gu = mfma_bw ? bw_gu_buffer(o) : nullptr;
-  // a forward kept for this x (MXM_FLAG_KEEP_FOR_BACKWARD) left the routing,
-  // the probabilities and the raw projections where this forward puts them
-  const bool reuse = mfma_bw && allow_kept && o.kept && x == o.kept_x && x_dtype == o.kept_dtype;
+  // the kept forward (MXM_FLAG_KEEP_FOR_BACKWARD) left the routing, the
+  // probabilities and the raw projections where this forward puts them
+  const bool reuse = mfma_bw && allow_kept && o.kept;
   // fp32 compute: the forward's routing only; the experts' forward products
   // are computed by run_backward_blas32 (and kept for the backward)
   const bool own_forward = !o.bf16;
@@ -1579,7 +1635,23 @@ int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const 
   OP_OR_RETURN(h);
   return fenced([&] {
     if (rows != op->N) fail("OP_MOE_FEED_FORWARD expects x shape [B*T,D]");
-    run_backward(*op, x, x_dtype, d_delta, d_aux, d_entropy, dx, d_router_w, d_experts, true);
+    run_backward(*op, x, x_dtype, d_delta, d_aux, d_entropy, dx, d_router_w, d_experts);
+    return MXM_OK;
+  });
+}
+
+int mxm_moe_backward_kept(int64_t h, const float* d_delta, float d_aux, float d_entropy, float* dx,
+                          float* d_router_w, float* d_experts) {
+  OP_OR_RETURN(h);
+  return fenced([&] {
+    if (!op->train)
+      fail("OP_MOE_FEED_FORWARD backward_kept needs an op created with "
+           "MXM_FLAG_KEEP_FOR_BACKWARD");
+    if (!op->kept)
+      fail_rt("OP_MOE_FEED_FORWARD backward_kept: no kept forward (the op's last call must be "
+              "mxm_moe_forward; another forward, a backward or a weight update drops it)");
+    run_backward(*op, op->kept_xbuf.p, op->kept_dtype, d_delta, d_aux, d_entropy, dx, d_router_w,
+                 d_experts, true);
     return MXM_OK;
   });
 }
@@ -1628,7 +1700,7 @@ int mxm_moe_routing(int64_t h, int32_t* top_idx, float* gates, int32_t* counts, 
                     int32_t* perm, int to_host) {
   OP_OR_RETURN(h);
   return fenced([&] {
-    if (!op->have_last) fail("OP_MOE_FEED_FORWARD routing requested before any forward");
+    if (!op->have_last) fail_rt("OP_MOE_FEED_FORWARD routing requested before any forward");
     const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
     const size_t NK = (size_t)op->N * op->K;
     const Workspace& w = op->last;
@@ -1649,7 +1721,7 @@ int mxm_moe_probs(int64_t h, float* probs) {
   OP_OR_RETURN(h);
   return fenced([&] {
     if (!op->debug_probs) fail("OP_MOE_FEED_FORWARD probabilities need MXM_FLAG_DEBUG_PROBS");
-    if (!op->have_last) fail("OP_MOE_FEED_FORWARD probabilities requested before any forward");
+    if (!op->have_last) fail_rt("OP_MOE_FEED_FORWARD probabilities requested before any forward");
     HIPCK(hipMemcpyAsync(probs, op->last.probs, (size_t)op->N * op->E * 4, hipMemcpyDeviceToHost,
                          op->stream));
     HIPCK(hipStreamSynchronize(op->stream));
@@ -1672,7 +1744,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
   OP_OR_RETURN(h);
   int count = 0;
   const int rc = fenced([&] {
-    if (op->ev_used == 0) fail("OP_MOE_FEED_FORWARD no profiled forward yet");
+    if (op->ev_used == 0) fail_rt("OP_MOE_FEED_FORWARD no profiled forward yet");
     for (int i = 0; i < n; ++i) ms[i] = 0.0f;
     for (size_t f = 0; f < op->ev_used; ++f) {
       auto& set = op->ev_sets[f];

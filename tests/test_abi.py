@@ -47,12 +47,15 @@ def test_library_exports_every_declared_symbol():
 
 def test_header_constants_match_binding():
     d = _defines()
-    for name in ("MXM_OK", "MXM_DTYPE_INT32", "MXM_DTYPE_F32", "MXM_DTYPE_BF16", "MXM_DTYPE_I8",
+    for name in ("MXM_OK", "MXM_ERR", "MXM_ERR_ARGS", "MXM_ERR_INIT", "MXM_ERR_OP",
+                 "MXM_DTYPE_INT32", "MXM_DTYPE_F32", "MXM_DTYPE_BF16", "MXM_DTYPE_I8",
                  "MXM_FLAG_FORCE_SIMT", "MXM_FLAG_DEBUG_PROBS", "MXM_FLAG_MFMA_TILE128",
                  "MXM_FLAG_MFMA_TILE256x128", "MXM_FLAG_MFMA_TILE256x256",
-                 "MXM_FLAG_INT8_WEIGHTS", "MXM_NUM_STAGES"):
+                 "MXM_FLAG_INT8_WEIGHTS", "MXM_FLAG_KEEP_FOR_BACKWARD", "MXM_NUM_STAGES"):
         assert d[name] == getattr(_lib, name), name
     assert d["MXM_OP_MOE_FEED_FORWARD"] == 74
+    m = re.search(r"^#define\s+MXM_NOALLOC_MAX_BYTES\s+\((\d+)ll << (\d+)\)", HEADER, flags=re.M)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.MXM_NOALLOC_MAX_BYTES
     stage_defs = sorted((v, k) for k, v in d.items() if k.startswith("MXM_STAGE_"))
     assert [k[len("MXM_STAGE_"):].lower() for _, k in stage_defs] == list(_lib.STAGE_NAMES)
 
@@ -85,6 +88,19 @@ def test_create_rejects_bad_parameters(int_params, n_inputs, dtype, flags, want)
     assert handle == 0
     msg = _lib.last_error()
     assert msg.startswith("OP_MOE_FEED_FORWARD") and want in msg, msg
+
+
+def test_status_code_classes():
+    """gpu/mlx_bridge.cpp:814-823: -10 for an argument the call cannot take,
+    -11 when the runtime cannot be initialised, -12 for a handle that is not
+    live.  An argument error is reported before any device call."""
+    lib = _lib.load()
+    assert lib.mxm_malloc(None, 16) == _lib.MXM_ERR_ARGS
+    assert "bad arguments" in _lib.last_error()
+    assert lib.mxm_moe_backward_kept(987654321, None, 0.0, 0.0, None, None, None) == _lib.MXM_ERR_OP
+    if not Path("/dev/kfd").exists():  # no GPU here: initialisation must fail as such
+        assert lib.mxm_init() == _lib.MXM_ERR_INIT
+        assert "device" in _lib.last_error()
 
 
 def test_bad_handle_and_error_truncation():

@@ -653,59 +653,139 @@ def test_backward_bf16(gpu_lib, etype, act, slope, flow, shape):
               f"worst expert matrix vs the SIMT backward {worst:.2e}")
 
 
-@pytest.mark.parametrize("shape,etype,act", [((1, 2048, 256, 64, 256, 8), 0, 0),
-                                             ((1, 1000, 384, 24, 128, 4), 1, 1),
-                                             ((1, 1000, 384, 24, 128, 4), 2, 0)])
-def test_backward_kept_forward(gpu_lib, shape, etype, act):
-    """MXM_FLAG_KEEP_FOR_BACKWARD: a device forward keeps its routing,
-    probabilities and raw up projections (and derives the hidden from them
-    for its down projection), and the next device backward on the same x
-    buffer uses them instead of its own forward.  Against an op without the
-    flag on the same inputs: the forward's delta and the backward's dx,
-    d router_w and expert gradients are bit for bit the same; a backward on
-    another buffer holding the same x runs its own forward and gives them
-    too.  The second case has a split (fp32) hidden (geglu), the third is a
-    plain MLP expert (silu, bf16 hidden)."""
-    import ctypes
-
+@pytest.mark.parametrize("shape,etype,act,dtype", [
+    ((1, 2048, 256, 64, 256, 8), 0, 0, "bf16"),
+    ((1, 1000, 384, 24, 128, 4), 1, 1, "bf16"),
+    ((1, 1000, 384, 24, 128, 4), 2, 0, "bf16"),
+    ((1, 1000, 384, 24, 128, 4), 0, 0, "fp32x"),
+    ((1, 600, 128, 8, 96, 2), 0, 0, "fp32")])
+def test_backward_kept_forward(gpu_lib, shape, etype, act, dtype):
+    """MXM_FLAG_KEEP_FOR_BACKWARD + mxm_moe_backward_kept: the backward of the
+    op's last forward, from the routing, probabilities and raw up projections
+    that forward kept and from the op's own copy of x.  Against an op without
+    the flag on the same inputs, bit for bit (forward delta, dx, d router_w,
+    expert gradients):
+    * forward on x, backward_kept;
+    * forward on a buffer holding x, the buffer then rewritten with other
+      rows, backward_kept: still the gradients at x (the forward's input),
+      while mxm_moe_backward on the rewritten buffer gives the new rows';
+    * a weight update (mxm_moe_set_input), another forward (no-allocation,
+      block) or a backward between them drops the kept forward:
+      backward_kept then fails with MXM_ERR.
+    The second case has a split (fp32) hidden (geglu), the third is a plain
+    MLP expert; "fp32x" feeds fp32 x to a bf16 op (the forward keeps the
+    rounded copy), "fp32" is the fp32 flow (nothing is kept but x: the kept
+    backward runs its own forward on the copy)."""
     from mixlab_amd.op import MoEFeedForward
 
     B, T, D, E, F, K = shape
     N = B * T
+    bf16 = dtype != "fp32"
     x, wr, experts = random_case(89, N, D, E, F, expert_type=etype, wscale=0.1)
+    x2 = np.random.default_rng(91).standard_normal((N, D), dtype=np.float32)
     dD = np.random.default_rng(90).standard_normal((N, D), dtype=np.float32)
     lib = _lib.init()
-    xb = bf16_bits(round_bf16(x))
-    xdev = _lib.DeviceBuffer.from_array(xb)
-    xdev2 = _lib.DeviceBuffer.from_array(xb)
+    if dtype == "bf16":
+        xcode, up = _lib.MXM_DTYPE_BF16, lambda a: bf16_bits(round_bf16(a))
+    else:
+        xcode, up = _lib.MXM_DTYPE_F32, lambda a: np.ascontiguousarray(a, np.float32)
+    wup = (lambda a: bf16_bits(round_bf16(a))) if bf16 else up
+    xdev = _lib.DeviceBuffer.from_array(up(x))
     ddev = _lib.DeviceBuffer.from_array(dD)
     nw = 2 if etype == 2 else 3
+    outs = lambda: (_lib.DeviceBuffer(N * D * 4), _lib.DeviceBuffer(D * E * 4),  # noqa: E731
+                    _lib.DeviceBuffer(E * nw * D * F * 4))
 
-    def run(flags, backward_x):
-        with MoEFeedForward([B, T, D, E, K, etype, F, act], [0.0], compute_dtype="bf16",
-                            flags=flags) as op:
-            op.set_weights(bf16_bits(round_bf16(wr)),
-                           [[bf16_bits(round_bf16(w)) for w in ws] for ws in experts])
-            assert op.info()["mfma"]
-            delta = _lib.DeviceBuffer(N * D * 4)
-            aux, ent = _lib.DeviceBuffer(4), _lib.DeviceBuffer(4)
-            op.forward(xdev.value, _lib.MXM_DTYPE_BF16, N, delta.value, aux.value, ent.value)
-            dx = _lib.DeviceBuffer(N * D * 4)
-            dwr = _lib.DeviceBuffer(D * E * 4)
-            dw = _lib.DeviceBuffer(E * nw * D * F * 4)
-            _lib.check(lib.mxm_moe_backward(op.handle, backward_x.value, _lib.MXM_DTYPE_BF16, N,
-                                            ddev.value, 0.3, -0.2, dx.value, dwr.value,
-                                            dw.value), "mxm_moe_backward")
-            op.synchronize()
-            return [delta.download(np.float32, (N * D,)), aux.download(np.float32, (1,)),
-                    dx.download(np.float32, (N * D,)), dwr.download(np.float32, (D * E,)),
-                    dw.download(np.float32, (E * nw * D * F,))]
+    def grads(bufs):
+        dx, dwr, dw = bufs
+        return [dx.download(np.float32, (N * D,)), dwr.download(np.float32, (D * E,)),
+                dw.download(np.float32, (E * nw * D * F,))]
 
-    want = run(0, xdev)
-    for got in (run(_lib.MXM_FLAG_KEEP_FOR_BACKWARD, xdev),
-                run(_lib.MXM_FLAG_KEEP_FOR_BACKWARD, xdev2)):
+    def make(flags):
+        op = MoEFeedForward([B, T, D, E, K, etype, F, act], [0.0],
+                            compute_dtype="bf16" if bf16 else "fp32", flags=flags)
+        op.set_weights(wup(wr), [[wup(w) for w in ws] for ws in experts])
+        assert op.info()["mfma"] == bf16
+        return op
+
+    def forward(op, xbuf):
+        delta = _lib.DeviceBuffer(N * D * 4)
+        aux = _lib.DeviceBuffer(4)
+        op.forward(xbuf.value, xcode, N, delta.value, aux.value, None)
+        op.synchronize()  # (the op's stream does not wait for, nor is waited by, other streams)
+        return [delta.download(np.float32, (N * D,)), aux.download(np.float32, (1,))]
+
+    def backward(op, xbuf):
+        bufs = outs()
+        _lib.check(lib.mxm_moe_backward(op.handle, xbuf.value, xcode, N, ddev.value, 0.3, -0.2,
+                                        *[b.value for b in bufs]), "mxm_moe_backward")
+        op.synchronize()
+        return grads(bufs)
+
+    def backward_kept(op):
+        bufs = outs()
+        rc = lib.mxm_moe_backward_kept(op.handle, ddev.value, 0.3, -0.2, *[b.value for b in bufs])
+        op.synchronize()
+        return rc, (grads(bufs) if rc == 0 else None)
+
+    def same(got, want):
         for i, (a, b) in enumerate(zip(got, want)):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+
+    with make(0) as ref:
+        want_fwd = forward(ref, xdev)
+        want = backward(ref, xdev)
+        x2dev = _lib.DeviceBuffer.from_array(up(x2))
+        want2 = backward(ref, x2dev)
+        rc, _ = backward_kept(ref)
+        assert rc == _lib.MXM_ERR_ARGS and "MXM_FLAG_KEEP_FOR_BACKWARD" in _lib.last_error()
+
+    with make(_lib.MXM_FLAG_KEEP_FOR_BACKWARD) as op:
+        same(forward(op, xdev), want_fwd)
+        rc, got = backward_kept(op)
+        assert rc == 0, _lib.last_error()
+        same(got, want)
+        # one backward per kept forward
+        rc, _ = backward_kept(op)
+        assert rc == _lib.MXM_ERR and "no kept forward" in _lib.last_error()
+        # the caller's buffer rewritten between forward and backward
+        xbuf = _lib.DeviceBuffer.from_array(up(x))
+        same(forward(op, xbuf), want_fwd)
+        xbuf.upload(up(x2))
+        rc, got = backward_kept(op)
+        assert rc == 0, _lib.last_error()
+        same(got, want)
+        same(backward(op, xbuf), want2)
+        # a weight update drops the kept forward; the plain backward still runs
+        forward(op, xdev)
+        op.set_input(1, wup(wr))
+        rc, _ = backward_kept(op)
+        assert rc == _lib.MXM_ERR and "no kept forward" in _lib.last_error()
+        same(backward(op, xdev), want)
+        # so do the other forwards
+        forward(op, xdev)
+        delta = _lib.DeviceBuffer(N * D * 4)
+        _lib.check(lib.mxm_moe_forward_noalloc(op.handle, xdev.value, xcode, N, delta.value, None,
+                                               None), "mxm_moe_forward_noalloc")
+        op.synchronize()
+        rc, _ = backward_kept(op)
+        assert rc == _lib.MXM_ERR
+        forward(op, xdev)
+        scale = _lib.DeviceBuffer.from_array(np.ones(D, np.float32))
+        op.block_forward(xdev.value, xcode, N, scale.value, 0, _lib.MXM_DTYPE_F32, 1e-5, 0.01,
+                         delta.value, 0, 0)
+        op.synchronize()
+        rc, _ = backward_kept(op)
+        assert rc == _lib.MXM_ERR
+        forward(op, xdev)
+        backward(op, xdev)
+        rc, _ = backward_kept(op)
+        assert rc == _lib.MXM_ERR
+        # and the next forward keeps again
+        same(forward(op, xdev), want_fwd)
+        rc, got = backward_kept(op)
+        assert rc == 0, _lib.last_error()
+        same(got, want)
 
 
 @pytest.mark.parametrize("shape", [(1, 2048, 256, 64, 256, 8), (1, 1000, 384, 24, 128, 4),
