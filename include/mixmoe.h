@@ -131,7 +131,8 @@ int mxm_moe_set_input(int64_t op, int input_index, int dtype, const int64_t* sha
  * ops created with MXM_FLAG_INT8_WEIGHTS.  This has no counterpart in the
  * reference, whose bridge takes fp32 weights only (gpu/mlx_bridge.cpp:210-217);
  * it serves decode-shaped serving, where the expert weights are the traffic.
- * D and ffn must be multiples of 64 and at most 2048. */
+ * Any D and ffn (widths that are not multiples of 64 are padded with zero
+ * weights inside the library; one expert's matrix below 2^31 entries). */
 int mxm_moe_set_input_q8(int64_t op, int input_index, const int8_t* q, const float* scales,
                          const int64_t* shape, int ndim, int on_device);
 
@@ -259,9 +260,13 @@ int mxm_moe_set_profiling(int64_t op, int enable);
 int mxm_moe_stage_times(int64_t op, float* ms, int n);
 
 /* Executor facts: info[0] = expert kernel family (0 SIMT, 1 bf16 MFMA, 2 int8
- * weights), info[1] =
- * workspace bytes, info[2] = row-tile height of the grouped GEMM, info[3] =
- * number of router tiles.  Returns the number of entries written. */
+ * weights), info[1] = workspace bytes, info[2] = row-tile height of the
+ * grouped GEMM, info[3] = number of router tiles, info[4] = the expert width
+ * the kernels run at (ffn, or ffn rounded up to the tiles: 128 for MFMA, 64
+ * for int8, with zero weights in the padding), info[5] = the down
+ * projection's output width (D, or D rounded up to 128 / 16), info[6] = the
+ * up projection's reduction length (D, or D rounded up to 64).  Returns the
+ * number of entries written (at most n, at most 7). */
 int mxm_moe_info(int64_t op, int64_t* info, int n);
 
 #ifdef __cplusplus

@@ -124,8 +124,9 @@ struct Workspace {
   float* ent = nullptr;            // [1]
   int32_t* expert_count = nullptr; // [E]
   float* expert_pmean = nullptr;   // [E]
-  void* H = nullptr;               // [N*K, F] (split hidden: [N*K, 2F])
-  void* Y = nullptr;               // [N*K, D]
+  void* xpad = nullptr;            // [N, Kx] bf16 x padded to the up projection's reduction
+  void* H = nullptr;               // [N*K, Fk] (split hidden: [N*K, 2Fk])
+  void* Y = nullptr;               // [N*K, Dk]
   float* probs = nullptr;          // [N, E] (MXM_FLAG_DEBUG_PROBS)
   float* small_probs = nullptr;    // [N, E] one-launch router's probabilities
   float* tok_ent = nullptr;        // [N]
@@ -137,6 +138,17 @@ struct MoeOp {
   int B = 0, T = 0, D = 0, E = 0, K = 0, etype = 0, F = 0, act = 0;
   float slope = 0.0f;
   int N = 0, wpe = 0, n_inputs = 0;
+  // Widths the expert kernels run at (set at create; equal to F and D on the
+  // SIMT family).  The MFMA tiles want the expert width a multiple of 128
+  // and the model width a multiple of 128 (down projection's columns) and
+  // 64 (up projection's reduction); the int8 kernels want 64 and 16.  Other
+  // widths are padded with zero weights: Fk is F rounded up (zero gate / up
+  // columns, zero W_down rows: the hidden of a zero projection is 0 for every
+  // kind, so y is unchanged), Dk is the down projection's output width (zero
+  // W_down columns; y and the combine read D of Dk columns), Kx the up
+  // projection's reduction length (D, or Dk when D is not a multiple of 64:
+  // x's rows are then copied with zero columns).
+  int Fk = 0, Dk = 0, Kx = 0;
   bool bf16 = false, mfma = false, debug_probs = false, q8 = false;
   // MFMA / int8 families with a kind whose hidden is fp32 in the bf16 flow:
   // H holds two bf16 planes [N*K][2F] and Y is fp32 (GemmArgs::h_split)
@@ -275,12 +287,12 @@ void set_schedule(MoeOp& o) {
       const int64_t tiles = ((int64_t)NK + 255) / 256 * (ncols / 256);
       return tiles < 2 * (int64_t)o.n_cu ? (int)MXM_TILE_128x128 : (int)MXM_TILE_256x256;
     };
-    const int nc1 = glu ? 2 * o.F : o.F;
+    const int nc1 = glu ? 2 * o.Fk : o.Fk;
     o.fam1 = pick(nc1);
-    o.fam2 = pick(o.D);
-    o.fam_dh = pick(o.F);
-    o.bm1 = mxm_mfma_tile_rows(nc1, o.D, o.fam1);
-    o.bm2 = mxm_mfma_tile_rows(o.D, o.hsplit ? 2 * o.F : o.F, o.fam2);
+    o.fam2 = pick(o.Dk);
+    o.fam_dh = pick(o.Fk);
+    o.bm1 = mxm_mfma_tile_rows(nc1, o.Kx, o.fam1);
+    o.bm2 = mxm_mfma_tile_rows(o.Dk, o.hsplit ? 2 * o.Fk : o.Fk, o.fam2);
   } else {
     o.bm1 = o.bm2 = mxm_simt_bm();
   }
@@ -321,8 +333,9 @@ Workspace layout_workspace(const MoeOp& o, char* base) {
   w.expert_count = reinterpret_cast<int32_t*>(take(E * 4));
   w.expert_pmean = reinterpret_cast<float*>(take(E * 4));
   const size_t esz = (o.mfma || o.q8) ? 2 : 4;
-  w.H = take(NK * (size_t)o.F * esz * (o.hsplit ? 2 : 1));
-  w.Y = take(NK * (size_t)o.D * (o.hsplit ? 4 : esz));
+  if ((o.mfma || o.q8) && o.Kx != o.D) w.xpad = take(N * (size_t)o.Kx * 2);
+  w.H = take(NK * (size_t)o.Fk * esz * (o.hsplit ? 2 : 1));
+  w.Y = take(NK * (size_t)o.Dk * (o.hsplit ? 4 : esz));
   if (o.debug_probs) w.probs = reinterpret_cast<float*>(take(N * E * 4));
   if (o.small_route) {
     w.small_probs = reinterpret_cast<float*>(take(N * E * 4));
@@ -496,10 +509,19 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   mark(3);
   if (o.route_only) return;
   const bool glu = o.etype != MXM_EXPERT_MLP;
+  // the up projection reads x's rows Kx long: a zero-padded copy when D is
+  // not a multiple of 64
+  const void* xg = xin;
+  if (w.xpad) {
+    for (int rep = 0; rep < reps; ++rep)
+      mxm_launch_pad_rows_bf16(static_cast<const uint16_t*>(xin), o.N, o.D, o.Kx,
+                               static_cast<uint16_t*>(w.xpad), st);
+    xg = w.xpad;
+  }
   GemmArgs g1{};
   g1.no_off32 = o.force64;
   g1.mode = glu ? MXM_GEMM_GLU : MXM_GEMM_MLP;
-  g1.a = xin;
+  g1.a = xg;
   g1.perm = sc.perm;
   g1.b0 = o.w1.p;
   g1.b1 = o.w1b.p;
@@ -507,8 +529,8 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.offsets = sa.offsets;
   g1.mstart = sa.mstart1;
   g1.E = o.E;
-  g1.Kd = o.D;
-  g1.Ncols = (o.mfma && glu) ? 2 * o.F : o.F;
+  g1.Kd = o.Kx;
+  g1.Ncols = (o.mfma && glu) ? 2 * o.Fk : o.Fk;
   g1.max_mtiles = o.max_mtiles1;
   g1.family = o.fam1;
   g1.expert_type = o.etype;
@@ -527,7 +549,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     require_operands(g1, false, false);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
     if (pre_out && !o.up_only)  // a kept forward: the hidden from them, as the epilogue would
-      mxm_launch_hidden_from_raw_bf16(pre_out, o.N * o.K, o.F, o.etype, o.act, o.slope, o.hsplit,
+      mxm_launch_hidden_from_raw_bf16(pre_out, o.N * o.K, o.Fk, o.etype, o.act, o.slope, o.hsplit,
                                       static_cast<uint16_t*>(w.H), st);
   } else {
     require_operands(g1, glu, false);
@@ -547,9 +569,9 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.mstart = sa.mstart2;
   g2.E = o.E;
   // the split MFMA down projection reduces over both planes of H
-  g2.Kd = (o.hsplit && o.mfma) ? 2 * o.F : o.F;
+  g2.Kd = (o.hsplit && o.mfma) ? 2 * o.Fk : o.Fk;
   g2.h_split = o.hsplit;
-  g2.Ncols = o.D;
+  g2.Ncols = o.Dk;
   g2.max_mtiles = o.max_mtiles2;
   g2.family = o.fam2;
   g2.expert_type = o.etype;
@@ -579,6 +601,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   ca.slot_pos = sc.slot_pos;
   ca.N = o.N;
   ca.D = o.D;
+  ca.ldy = o.Dk;
   ca.K = o.K;
   ca.delta = delta;
   if (blk) {
@@ -637,14 +660,16 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
     if (o.small_route)
       mxm_launch_router_t(o.router.p, o.bf16, o.D, o.E, o.ldw, o.router_t.p, st);
   } else if (o.mfma) {
+    // rows of Fk (W_down [Dk][Fk]) and of Kx (W1 [NC][Kx]); the padding stays
+    // zero from the allocation
     const bool glu = o.wpe == 3;
     if (j == o.wpe - 1) {
-      uint16_t* dst = o.w2.as<uint16_t>() + (size_t)e * o.D * o.F;
-      mxm_launch_transpose_bf16(src, dtype, o.F, o.D, -1, dst, st);
+      uint16_t* dst = o.w2.as<uint16_t>() + (size_t)e * o.Dk * o.Fk;
+      mxm_launch_transpose_bf16(src, dtype, o.F, o.D, -1, dst, st, o.Fk);
     } else {
-      const size_t ncols1 = glu ? 2 * (size_t)o.F : (size_t)o.F;
-      uint16_t* dst = o.w1.as<uint16_t>() + (size_t)e * ncols1 * o.D;
-      mxm_launch_transpose_bf16(src, dtype, o.D, o.F, glu ? j : -1, dst, st);
+      const size_t ncols1 = glu ? 2 * (size_t)o.Fk : (size_t)o.Fk;
+      uint16_t* dst = o.w1.as<uint16_t>() + (size_t)e * ncols1 * o.Kx;
+      mxm_launch_transpose_bf16(src, dtype, o.D, o.F, glu ? j : -1, dst, st, o.Kx);
     }
   } else {
     // SIMT family keeps the reference layout in fp32 storage, values rounded
@@ -698,8 +723,12 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   }
   DevBuf* qdst = down ? &o.q2 : (o.wpe == 3 && j == 1) ? &o.q1b : &o.q1;
   DevBuf* sdst = down ? &o.s2 : (o.wpe == 3 && j == 1) ? &o.s1b : &o.s1;
-  mxm_launch_shuffle_q8(src, rows, cols, qdst->as<uint8_t>() + (size_t)e * n, st);
-  HIPCK(hipMemcpyAsync(sdst->as<float>() + (size_t)e * cols, scales, (size_t)cols * 4,
+  // padded to [Kx][Fk] (up) or [Fk][Dk] (down) with zero weights; the
+  // padded columns' scales stay zero from the allocation
+  const int rows_k = down ? o.Fk : o.Kx, cols_k = down ? o.Dk : o.Fk;
+  mxm_launch_shuffle_q8(src, rows, cols, rows_k, cols_k,
+                        qdst->as<uint8_t>() + (size_t)e * rows_k * cols_k, st);
+  HIPCK(hipMemcpyAsync(sdst->as<float>() + (size_t)e * cols_k, scales, (size_t)cols * 4,
                        on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
   HIPCK(hipGetLastError());
   HIPCK(hipStreamSynchronize(st));
@@ -876,21 +905,38 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->N = o->B * o->T;
     o->n_inputs = n_inputs;
     o->bf16 = compute_dtype == MXM_DTYPE_BF16;
+    auto round_up = [](int v, int m) { return (v + m - 1) / m * m; };
+    o->Fk = o->F;
+    o->Dk = o->Kx = o->D;
     {
+      // MFMA tiles on the padded widths (see MoeOp::Fk) once both widths span
+      // at least one 128-wide tile; smaller ops keep the exact-order SIMT
+      // kernels
       const int f = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
-      const int n1 = o->etype == MXM_EXPERT_MLP ? o->F : 2 * o->F;
-      o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && mxm_mfma_tile_rows(n1, o->D, f) > 0 &&
-                mxm_mfma_tile_rows(o->D, o->F, f) > 0;
+      const int Fk = round_up(o->F, 128), Dk = round_up(o->D, 128), Kx = round_up(o->D, 64);
+      const int n1 = o->etype == MXM_EXPERT_MLP ? Fk : 2 * Fk;
+      o->mfma = o->bf16 && !(flags & MXM_FLAG_FORCE_SIMT) && o->D >= 128 && o->F >= 128 &&
+                mxm_mfma_tile_rows(n1, Kx, f) > 0 && mxm_mfma_tile_rows(Dk, Fk, f) > 0;
+      if (o->mfma) {
+        o->Fk = Fk;
+        o->Dk = Dk;
+        o->Kx = Kx;
+      }
     }
     o->debug_probs = (flags & MXM_FLAG_DEBUG_PROBS) != 0;
     o->train = (flags & MXM_FLAG_KEEP_FOR_BACKWARD) != 0;
     o->q8 = (flags & MXM_FLAG_INT8_WEIGHTS) != 0;
     if (o->q8) {
       if (!o->bf16) fail("OP_MOE_FEED_FORWARD int8 weights need bf16 compute");
-      if (o->D % 64 || o->F % 64 || o->D > mxm_q8_max_kd() || o->F > mxm_q8_max_kd())
-        fail("OP_MOE_FEED_FORWARD int8 weights need D and ffn multiples of 64 and at most %d",
-             mxm_q8_max_kd());
+      // the int8 kernels: reduction lengths multiples of 64, output columns
+      // multiples of 16; one expert's matrix addressed with 32-bit offsets
       o->mfma = false;
+      o->Fk = round_up(o->F, 64);
+      o->Dk = round_up(o->D, 16);
+      o->Kx = round_up(o->D, 64);
+      if ((int64_t)o->Kx * o->Fk >= ((int64_t)1 << 31) || (int64_t)o->Fk * o->Dk >= ((int64_t)1 << 31))
+        fail("OP_MOE_FEED_FORWARD int8 weights: one expert's matrix must hold fewer than 2^31 "
+             "entries (D=%d ffn=%d)", o->D, o->F);
     }
     o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
     o->hsplit = (o->mfma || o->q8) && !mxm_hidden_is_bf16(o->etype, o->act);
@@ -899,6 +945,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     HIPCK(hipDeviceGetAttribute(&o->n_cu, hipDeviceAttributeMultiprocessorCount, o->device));
     HIPCK(hipStreamCreateWithFlags(&o->stream, hipStreamNonBlocking));
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
+    const size_t F1 = (size_t)o->Kx * o->Fk, F2 = (size_t)o->Fk * o->Dk;  // padded matrices
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
@@ -907,15 +954,28 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
       o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * (o->bf16 ? 2 : 4));
     }
     if (o->q8) {
-      o->q1.alloc(EE * DF);
-      if (o->wpe == 3) o->q1b.alloc(EE * DF);
-      o->q2.alloc(EE * DF);
-      o->s1.alloc(EE * o->F * 4);
-      if (o->wpe == 3) o->s1b.alloc(EE * o->F * 4);
-      o->s2.alloc(EE * o->D * 4);
+      o->q1.alloc(EE * F1);
+      if (o->wpe == 3) o->q1b.alloc(EE * F1);
+      o->q2.alloc(EE * F2);
+      // padded output channels keep a zero scale
+      o->s1.alloc(EE * o->Fk * 4);
+      HIPCK(hipMemsetAsync(o->s1.p, 0, o->s1.bytes, o->stream));
+      if (o->wpe == 3) {
+        o->s1b.alloc(EE * o->Fk * 4);
+        HIPCK(hipMemsetAsync(o->s1b.p, 0, o->s1b.bytes, o->stream));
+      }
+      o->s2.alloc(EE * o->Dk * 4);
+      HIPCK(hipMemsetAsync(o->s2.p, 0, o->s2.bytes, o->stream));
+      HIPCK(hipStreamSynchronize(o->stream));
     } else if (o->mfma) {
-      o->w1.alloc(EE * DF * 2 * (o->wpe == 3 ? 2 : 1));
-      o->w2.alloc(EE * DF * 2);
+      // the padded rows and columns stay zero: uploads write only the real ones
+      o->w1.alloc(EE * F1 * 2 * (o->wpe == 3 ? 2 : 1));
+      o->w2.alloc(EE * F2 * 2);
+      if (F1 != DF || F2 != DF) {
+        HIPCK(hipMemsetAsync(o->w1.p, 0, o->w1.bytes, o->stream));
+        HIPCK(hipMemsetAsync(o->w2.p, 0, o->w2.bytes, o->stream));
+        HIPCK(hipStreamSynchronize(o->stream));
+      }
     } else {
       o->w1.alloc(EE * DF * 4);
       if (o->wpe == 3) o->w1b.alloc(EE * DF * 4);
@@ -1149,12 +1209,16 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
 // Op.Inputs order (per expert gate, up, down -- or up, down -- in x.W layout).
 
 // Shapes of the MFMA backward's three grouped products: dH = dY W_down^T
-// (F columns, reduction D), the forward's kept projections (NC, D) and
-// dX = dGU W1^T (D, NC), NC = 2F (GLU) or F; the activation backward takes
-// hidden units 8 at a time within groups of 32 (F % 32 == 0).
+// (Fk columns, reduction D), the forward's kept projections (NC, D) and
+// dX = dGU W1^T (D, NC), NC = 2Fk (GLU) or Fk; the activation backward takes
+// hidden units 8 at a time within groups of 32 (Fk % 32 == 0).  The expert
+// width may be padded (Fk > F: the padded units' gradients are zero and not
+// stored), the model width not (D a multiple of 128: x, dD and dx are the
+// caller's rows as they are).
 bool mfma_backward_fits(const MoeOp& o) {
-  const int NC = o.wpe == 3 ? 2 * o.F : o.F;
-  return o.mfma && o.F % 32 == 0 && mxm_mfma_tile_rows(o.F, o.D, o.family) > 0 &&
+  const int NC = o.wpe == 3 ? 2 * o.Fk : o.Fk;
+  return o.mfma && o.Dk == o.D && o.Kx == o.D && o.Fk % 32 == 0 &&
+         mxm_mfma_tile_rows(o.Fk, o.D, o.family) > 0 &&
          mxm_mfma_tile_rows(NC, o.D, o.family) > 0 && mxm_mfma_tile_rows(o.D, NC, o.family) > 0;
 }
 
@@ -1183,8 +1247,11 @@ void check_blas(rocblas_status st, const char* what) {
 void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* dx, float* dw) {
   hipStream_t st = o.stream;
   const bool glu = o.wpe == 3;
-  const int D = o.D, F = o.F, E = o.E, NC = glu ? 2 * F : F;
-  const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
+  // F: the op's expert width (the layout of the gradients written to dw);
+  // Fk: the kernels' (padded) width, NC its up-projection columns
+  const int D = o.D, F = o.F, Fk = o.Fk, E = o.E, NC = glu ? 2 * Fk : Fk;
+  const size_t NK = (size_t)o.N * o.K, DF = (size_t)D * F, DFk = (size_t)D * Fk,
+               stride = (size_t)o.wpe * DF;
   // d router_w = x^T dlogits is N*D*E fmaf on the SIMT kernel: from 2^28 of
   // them on (C3's shape has 2^30, C2's 2^26) the weight-gradient kernel's
   // product is faster than that VALU work, below it its schedule and
@@ -1193,7 +1260,7 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
       o.dwr_mode >= 0 ? o.dwr_mode == 1 : (double)o.N * D * E >= (double)(1 << 28);
   const int Ep = (E + 63) / 64 * 64;  // that product's hi and lo halves of Ep columns
   if (!o.bw_dhb.p) {
-    o.bw_dhb.alloc(NK * F * 2);
+    o.bw_dhb.alloc(NK * Fk * 2);
     o.bw_dgub.alloc(NK * NC * 2);
     o.bw_dxeb.alloc(NK * D * 2);
     o.bw_zero.alloc(512);  // 256 zero bf16: the weight gradients' rows past an expert's end
@@ -1201,13 +1268,13 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
     o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
     // the weight gradients' schedule and split-reduction partials (both
     // launches run in stream order and share it)
-    o.bw_wscr.alloc(std::max({mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(F, D),
+    o.bw_wscr.alloc(std::max({mxm_wgrad_scratch_bytes(D, NC), mxm_wgrad_scratch_bytes(Fk, D),
                               dwr_mfma ? mxm_wgrad_scratch_bytes(D, 2 * Ep) : 0}));
     if (dwr_mfma) {
       o.bw_dlb.alloc((size_t)o.N * 2 * Ep * 2);
       o.bw_dwr2.alloc((size_t)D * 2 * Ep * 4);
     }
-    o.bw_w2o.alloc((size_t)E * DF * 2);
+    o.bw_w2o.alloc((size_t)E * DFk * 2);
     o.bw_w1u.alloc((size_t)E * D * NC * 2);
     o.bw_ddb.alloc((size_t)o.N * D * 2);
     o.bw_gp.alloc(NK * 4);
@@ -1215,9 +1282,9 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   }
   if (!o.bw_wbf_ready) {
     for (int e = 0; e < E; ++e) {
-      // W_down: forward [D][F] -> [F][D]; W1: forward [NC][D] -> [D][NC]
-      mxm_launch_transpose_bf16(o.w2.as<uint16_t>() + (size_t)e * DF, MXM_DTYPE_BF16, D, F, -1,
-                                o.bw_w2o.as<uint16_t>() + (size_t)e * DF, st);
+      // W_down: forward [D][Fk] -> [Fk][D]; W1: forward [NC][D] -> [D][NC]
+      mxm_launch_transpose_bf16(o.w2.as<uint16_t>() + (size_t)e * DFk, MXM_DTYPE_BF16, D, Fk, -1,
+                                o.bw_w2o.as<uint16_t>() + (size_t)e * DFk, st);
       mxm_launch_transpose_bf16(o.w1.as<uint16_t>() + (size_t)e * NC * D, MXM_DTYPE_BF16, NC, D, -1,
                                 o.bw_w1u.as<uint16_t>() + (size_t)e * D * NC, st);
     }
@@ -1260,10 +1327,10 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   };
   // dH' = dD W_down^T for each slot's token, ungated: with H it gives the
   // gate gradients <dD, Y> = <dH', h>, and dH = gate * dH'
-  product(0, ddb, o.bw_w2o.p, dhb, D, F, o.fam_dh, true);
+  product(0, ddb, o.bw_w2o.p, dhb, D, Fk, o.fam_dh, true);
   // gub holds G|U from the forward (run_forward's pre_out)
   mxm_launch_act_bw_gated_bf16(gub, dhb, static_cast<uint16_t*>(o.ws.H), o.hsplit,
-                               o.bw_gp.as<float>(), (int)NK, F, o.etype, o.act, o.slope, dgub,
+                               o.bw_gp.as<float>(), (int)NK, Fk, o.etype, o.act, o.slope, dgub,
                                o.bw_dgp.as<float>(), st);
   HIPCK(hipGetLastError());
   // the router part from those gate gradients
@@ -1309,9 +1376,9 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   // de-interleaved in the gate and up matrices (x.W layout), and
   // dW_down = Hg^T dD[token] over the gated hidden's planes (hi and lo for a
   // split hidden)
-  if (!mxm_wgrad_fits(D, NC) || !mxm_wgrad_fits(F, D))
+  if (!mxm_wgrad_fits(D, NC) || !mxm_wgrad_fits(Fk, D))
     fail("OP_MOE_FEED_FORWARD backward: weight-gradient tiles need D, F multiples of 128 "
-         "(D=%d F=%d)", D, F);
+         "(D=%d F=%d)", D, Fk);
   WgradArgs wa{};
   wa.offsets = b.offsets;
   wa.zero = o.bw_zero.as<uint16_t>();
@@ -1330,22 +1397,26 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   wa.C = NC;
   wa.out = dw;
   wa.out_slot = DF;
+  // the gradients land in the op's [D][F] layout; padded units are not stored
   wa.glu_f = glu ? F : 0;
+  wa.c_store = (!glu && Fk != F) ? F : 0;
   mxm_launch_wgrad(wa, st);
   HIPCK(hipGetLastError());
   // dW_down = sum over slots of (gate h)^T dD[token]: A = the gated hidden
   // the activation pass wrote, B = bf16(dD) rows read in place through perm
   wa.a = static_cast<const uint16_t*>(o.ws.H);
   wa.a_rows = nullptr;
-  wa.lda = o.hsplit ? 2 * F : F;
-  wa.aplane = F;
+  wa.lda = o.hsplit ? 2 * Fk : Fk;
+  wa.aplane = Fk;
   wa.planes = o.hsplit ? 2 : 1;
   wa.b = ddb;
   wa.b_rows = b.perm;
   wa.b_rows32 = !o.force64 && (size_t)o.N * D * 2 < ((size_t)1 << 32);
   wa.ldb = D;
-  wa.M = F;
+  wa.M = Fk;
+  wa.m_store = Fk != F ? F : 0;
   wa.C = D;
+  wa.c_store = 0;
   wa.out = dw + (glu ? 2 : 1) * DF;
   wa.out_slot = 0;
   wa.glu_f = 0;
@@ -1457,7 +1528,7 @@ void run_backward_blas32(MoeOp& o, BackwardArgs& b, bool own_forward) {
 
 static uint16_t* bw_gu_buffer(MoeOp& o) {
   if (!o.bw_probs.p) o.bw_probs.alloc((size_t)o.N * o.E * 4);
-  if (!o.bw_gub.p) o.bw_gub.alloc((size_t)o.N * o.K * (size_t)(o.wpe == 3 ? 2 * o.F : o.F) * 2);
+  if (!o.bw_gub.p) o.bw_gub.alloc((size_t)o.N * o.K * (size_t)(o.wpe == 3 ? 2 * o.Fk : o.Fk) * 2);
   return o.bw_gub.as<uint16_t>();
 }
 
@@ -1515,9 +1586,12 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
         if (glu && !o.bw_w1b_32.p) o.bw_w1b_32.alloc(E * DF * 4);
         if (!o.bw_w2_32.p) o.bw_w2_32.alloc(E * DF * 4);
         const uint16_t* m1 = o.w1.as<uint16_t>();
-        mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, glu ? 0 : -1, o.bw_w1_32.as<float>(), o.stream);
-        if (glu) mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, 1, o.bw_w1b_32.as<float>(), o.stream);
-        mxm_launch_w2_to_xw(o.w2.as<uint16_t>(), o.E, o.D, o.F, o.bw_w2_32.as<float>(), o.stream);
+        mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, o.Kx, o.Fk, glu ? 0 : -1, o.bw_w1_32.as<float>(),
+                            o.stream);
+        if (glu)
+          mxm_launch_w1_to_xw(m1, o.E, o.D, o.F, o.Kx, o.Fk, 1, o.bw_w1b_32.as<float>(), o.stream);
+        mxm_launch_w2_to_xw(o.w2.as<uint16_t>(), o.E, o.D, o.F, o.Dk, o.Fk, o.bw_w2_32.as<float>(),
+                            o.stream);
       }
       HIPCK(hipGetLastError());
       o.bw_w32_ready = true;
@@ -1563,9 +1637,12 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   const bool read_bf16 = o.bf16 && mfma_bw;
   if (o.bf16 && !read_bf16) {
     mxm_launch_to_f32(xb, MXM_DTYPE_BF16, o.bw_x32.as<float>(), (int64_t)(N * D), o.stream);
-    if (o.mfma && !o.hsplit) {  // (a split hidden's y is fp32 already)
+    // y in fp32 [NK][D] (a split hidden's y is fp32 already; a padded down
+    // projection's rows are Dk long)
+    if (o.mfma && (!o.hsplit || o.Dk != o.D)) {
       if (!o.bw_y32.p) o.bw_y32.alloc(NK * D * 4);
-      mxm_launch_to_f32(o.ws.Y, MXM_DTYPE_BF16, o.bw_y32.as<float>(), (int64_t)(NK * D), o.stream);
+      mxm_launch_rows_to_f32(o.ws.Y, o.hsplit ? MXM_DTYPE_F32 : MXM_DTYPE_BF16, (int64_t)NK,
+                             (int)D, o.Dk, o.bw_y32.as<float>(), o.stream);
       y32 = o.bw_y32.as<float>();
     }
     HIPCK(hipGetLastError());
@@ -1765,11 +1842,12 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t vals[4] = {op->q8 ? 2 : op->mfma ? 1 : 0,
+  const int64_t vals[7] = {op->q8 ? 2 : op->mfma ? 1 : 0,
                            (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
-                           (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM)};
+                           (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM),
+                           (int64_t)op->Fk, (int64_t)op->Dk, (int64_t)op->Kx};
   int w = 0;
-  for (; w < n && w < 4; ++w) info[w] = vals[w];
+  for (; w < n && w < 7; ++w) info[w] = vals[w];
   return w;
 }
 

@@ -55,7 +55,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int NW = 8;          // waves (column blocks) per workgroup
-constexpr int MAX_KD = 2048;   // A staging: 16 rows x Kd bf16 in LDS (64 KB)
+constexpr int MAX_KD = 2048;   // A staging: 16 rows x up to 2048 k bf16 per chunk in LDS (64 KB)
 
 // Eight offset-binary bytes (two dwords) -> eight bf16 of their value, exact.
 __device__ __forceinline__ bf16x8_t u8x8_to_bf16(unsigned lo, unsigned hi) {
@@ -83,6 +83,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 16 : 16 * RG;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
   constexpr int ASZ = MAX_KD / 64 * 2 * 64;  // pieces of one row group
+  constexpr int CH = MAX_KD / 64 / P * P;    // k blocks per staged chunk
   // A rows of the current pass, per row group: [kb][half][lane] 16-byte
   // pieces; lane 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
   __shared__ u32x4_t ash[RG * ASZ];
@@ -97,7 +98,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   const int Kd = a.Kd, NC = a.Ncols;  // NC: output columns per matrix
   const int kblocks = Kd / 64;
   const size_t kstride = (size_t)NC * 64;  // bytes between k blocks of one column block
-  const int pieces = Kd / 8;          // 16-byte pieces per row
+  // rows are staged in chunks: all of Kd when it fits the LDS, else chunks of
+  // CH k blocks (a multiple of the ring depth, so every chunk starts on ring
+  // slot 0); the weight ring runs on across chunk boundaries
+  const int chunk = kblocks <= MAX_KD / 64 ? kblocks : CH;
   const int cb = grp * NW + wave;
   const bool active = cb < NC / 16;   // wave-uniform
   const int g = lane >> 4, m = lane & 15;
@@ -131,12 +135,25 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   if (active) prologue();
 
   for (int rc = 0; rc < count; rc += ROWS_PER_PASS) {
-    __syncthreads();  // the previous pass has finished reading ash
+    if (active && rc > 0) prologue();
+
+    f32x4_t acc[RG][NMAT], rs[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      rs[rg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) acc[rg][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int k0 = 0; k0 < kblocks; k0 += chunk) {
+    const int k1 = min(k0 + chunk, kblocks);
+    const int pieces = (k1 - k0) * 8;  // 16-byte pieces of a row's chunk
+    __syncthreads();  // every wave has finished reading ash
     for (int i = tid; i < 16 * RG * pieces; i += NW * 64) {
       const int r = i / pieces, c8 = i - r * pieces;
       // staged row r: row group r / 16 (the plane, when split), row r % 16
       const int rr = DOWN_SPLIT ? (r & 15) : r;
-      const int col0 = DOWN_SPLIT ? (r >> 4) * Kd : 0;
+      const int col0 = (DOWN_SPLIT ? (r >> 4) * Kd : 0) + 64 * k0;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
       if (rc + rr < count) {
         const int p = row_begin + rc + rr;
@@ -147,15 +164,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     }
     __syncthreads();
     if (!active) continue;
-    if (rc > 0) prologue();
-
-    f32x4_t acc[RG][NMAT], rs[RG];
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-      rs[rg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) acc[rg][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
 
 #define MXM_Q8_STEP(s, kbi)                                                                  \
   {                                                                                          \
@@ -176,20 +184,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     }                                                                                        \
   }
 
-    int kb = 0;
-    for (; kb + P < kblocks; kb += P) {
+    int kb = k0;
+    for (; kb + P < k1; kb += P) {
 #pragma unroll
       for (int s = 0; s < P; ++s) {
-        MXM_Q8_STEP(s, kb + s);
+        MXM_Q8_STEP(s, kb + s - k0);
         const int nk = clamp_kb(kb + P + s, kblocks);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt)
           wb[s][mt] = MXM_WLD(W[mt] + (size_t)nk * kstride);
       }
     }
+    // the chunk's last group; its slots take the next chunk's first blocks
 #pragma unroll
     for (int s = 0; s < P; ++s)
-      if (kb + s < kblocks) MXM_Q8_STEP(s, kb + s);
+      if (kb + s < k1) {
+        MXM_Q8_STEP(s, kb + s - k0);
+        if (k1 < kblocks) {
+          const int nk = clamp_kb(kb + P + s, kblocks);
+#pragma unroll
+          for (int mt = 0; mt < NMAT; ++mt)
+            wb[s][mt] = MXM_WLD(W[mt] + (size_t)nk * kstride);
+        }
+      }
+    }  // k chunks
+    if (!active) continue;
 #undef MXM_Q8_STEP
 
     // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
@@ -255,26 +274,28 @@ void launch_epi(const GemmArgs& a, hipStream_t s) {
     launch_q8<EPI, P, 1>(a, s);
 }
 
-// Reorder one int8 matrix src [Kd][C] into the 1 KB block layout.
-__global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
+// Reorder one int8 matrix src [Kd][C] into the 1 KB block layout of a
+// [Kdp][Cp] matrix; entries past the source's rows or columns are 0 (byte
+// 0x80 in offset binary).
+__global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C, int Kdp, int Cp,
                                   uint8_t* __restrict__ dst) {
-  const size_t total = (size_t)Kd * C;
+  const size_t total = (size_t)Kdp * Cp;
   for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
        o += (size_t)gridDim.x * blockDim.x) {
     const size_t blk = o >> 10;
     const int within = (int)(o & 1023);
     const int l = within >> 4, i = within & 15;
-    const int ncb = C / 16;
+    const int ncb = Cp / 16;
     const int kb = (int)(blk / ncb), cb = (int)(blk % ncb);
     const int k = 64 * kb + 16 * (l >> 4) + i;
     const int c = 16 * cb + (l & 15);
-    dst[o] = (uint8_t)((uint8_t)src[(size_t)k * C + c] ^ 0x80u);
+    const int8_t q = (k < Kd && c < C) ? src[(size_t)k * C + c] : (int8_t)0;
+    dst[o] = (uint8_t)((uint8_t)q ^ 0x80u);
   }
 }
 
 }  // namespace
 
-int mxm_q8_max_kd() { return MAX_KD; }
 
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
   if (a.mode == MXM_GEMM_DOWN) {
@@ -306,9 +327,11 @@ void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s) {
-  const size_t total = (size_t)Kd * C;
+void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, int Kdp, int Cp, uint8_t* dst,
+                           hipStream_t s) {
+  const size_t total = (size_t)Kdp * Cp;
   int blocks = (int)((total + 255) / 256);
   if (blocks > 65536) blocks = 65536;
-  if (blocks > 0) hipLaunchKernelGGL(shuffle_q8_kernel, dim3(blocks), dim3(256), 0, s, src, Kd, C, dst);
+  if (blocks > 0)
+    hipLaunchKernelGGL(shuffle_q8_kernel, dim3(blocks), dim3(256), 0, s, src, Kd, C, Kdp, Cp, dst);
 }

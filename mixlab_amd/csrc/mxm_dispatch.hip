@@ -196,6 +196,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   }
   __syncthreads();
   const TY* y = static_cast<const TY*>(a.y);
+  const size_t ldy = a.ldy > 0 ? (size_t)a.ldy : (size_t)a.D;
   for (int d = tid * VEC; d < a.D; d += 256 * VEC) {
     float acc[VEC];
 #pragma unroll
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         for (int u = 0; u < KC; ++u)
           if (u < kn)
             r[u] = __builtin_nontemporal_load(
-                reinterpret_cast<const raw_t*>(y + (size_t)sp[k0 + u] * a.D + d));
+                reinterpret_cast<const raw_t*>(y + (size_t)sp[k0 + u] * ldy + d));
 #pragma unroll
         for (int u = 0; u < KC; ++u) {
           if (u < kn) {
@@ -235,7 +236,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
       }
     } else {
       for (int k = 0; k < K; ++k) {
-        const TY* src = y + (size_t)sp[k] * a.D + d;
+        const TY* src = y + (size_t)sp[k] * ldy + d;
         float f[VEC];
 #pragma unroll
         for (int q = 0; q < VEC; ++q) {
@@ -295,8 +296,9 @@ void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s) {
 
 void mxm_launch_combine(const CombineArgs& a, bool y_bf16, hipStream_t s) {
   if (a.N <= 0) return;
+  const int ldy = a.ldy > 0 ? a.ldy : a.D;
   const bool aligned = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(a.delta) % 16 == 0);
+                       (reinterpret_cast<uintptr_t>(a.delta) % 16 == 0) && ldy % 8 == 0;
   if (y_bf16) {
     if (aligned && a.D % 8 == 0)
       hipLaunchKernelGGL((combine_kernel<uint16_t, 8>), dim3(a.N), dim3(256), 0, s, a);

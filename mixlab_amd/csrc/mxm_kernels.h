@@ -206,6 +206,12 @@ struct WgradArgs {
   bool a_rows32;            // with a_rows: all of A lies within 4 GiB of a (32-bit offsets)
   const int32_t* b_rows;    // the same for B (at most one of a_rows, b_rows)
   bool b_rows32;
+  // Operands padded past the output's shape (an expert width rounded up to
+  // the tiles): only rows m < m_store are stored (0: all M), and without the
+  // GLU interleave only columns c < c_store, at row stride c_store instead
+  // of C (0: all).  With the interleave, glu_f is the real width: hidden
+  // units f >= glu_f are not stored.
+  int m_store, c_store;
 };
 // M and C multiples of 128.
 bool mxm_wgrad_fits(int M, int C);
@@ -266,6 +272,7 @@ struct CombineArgs {
   const float* gates;     // [N, K]
   const int32_t* slot_pos;
   int N, D, K;
+  int ldy;                // y's row stride (0: D; a padded down projection's width)
   float* delta;           // [N, D]
   // Block level (null resid: plain op output): delta[n, d] = resid[n, d] +
   // combined * rscale[d] (or + combined when rscale is null), in fp32.
@@ -296,28 +303,42 @@ void mxm_launch_rmsnorm(const RmsNormArgs& a, hipStream_t s);
 
 // Weight preparation (run once at upload).
 void mxm_launch_to_f32(const void* src, int src_dtype, float* dst, int64_t n, hipStream_t s);
+// dst [rows][cols] fp32 = the first cols of each row of src [rows][ld]
+// (fp32 or bf16 bits), e.g. a padded down projection's outputs.
+void mxm_launch_rows_to_f32(const void* src, int src_dtype, int64_t rows, int cols, int ld,
+                            float* dst, hipStream_t s);
+// dst [rows][ldd] bf16 = src [rows][cols] (bf16 bits) with columns cols ..
+// ldd-1 zero: the rows of x padded to the up projection's reduction length.
+void mxm_launch_pad_rows_bf16(const uint16_t* src, int64_t rows, int cols, int ldd, uint16_t* dst,
+                              hipStream_t s);
 void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n, hipStream_t s);
 // Transposed bf16 copy of one weight matrix src [Kd, C] (x.W layout):
-// dst[q, k] = bf16(src[k, c]) with q = c (slot < 0), or, for the GLU
-// interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up.
+// dst[q * ldd + k] = bf16(src[k, c]) with q = c (slot < 0), or, for the GLU
+// interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up;
+// ldd = Kd by default (a larger ldd leaves each row's padded tail as it is).
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
-                               uint16_t* dst, hipStream_t s);
+                               uint16_t* dst, hipStream_t s, int ldd = 0);
 // The decode router's copy of router_w [D, E] (stored in the flow's dtype:
 // bf16 when bf16, else fp32), in RouteSmallArgs::wr_t's layout.
 void mxm_launch_router_t(const void* src, bool bf16, int D, int E, int ldw, void* dst,
                          hipStream_t s);
-// MFMA-family expert weights back to fp32 x.W layout (backward of bf16 ops).
-void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int slot, float* dst,
+// MFMA-family expert weights (padded to Dk x Fk) back to fp32 x.W layout
+// [E][D][F] / [E][F][D] (backward of bf16 ops).
+void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int Dk, int Fk, int slot,
+                         float* dst, hipStream_t s);
+void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, int Dk, int Fk, float* dst,
                          hipStream_t s);
-void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, float* dst, hipStream_t s);
 
 // int8-weight family (decode shapes): weights in the 1 KB block layout of
 // mxm_launch_shuffle_q8, fp32 scale per output channel (scale0/scale1),
-// H and Y bf16.  Reduction length Kd must be a multiple of 64 and at most
-// mxm_q8_max_kd(); output columns a multiple of 16.
+// H and Y bf16.  Reduction length Kd must be a multiple of 64 (rows are
+// staged in chunks of at most 2048); output columns a multiple of 16.
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s);
-void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, uint8_t* dst, hipStream_t s);
-int mxm_q8_max_kd();
+// src [Kd][C] int8 -> dst in the 1 KB block layout of a [Kdp][Cp] matrix
+// (Kdp a multiple of 64, Cp of 16, both at least the source's): entries
+// past the source's rows or columns are 0.
+void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, int Kdp, int Cp, uint8_t* dst,
+                           hipStream_t s);
 
 // Backward of op 74 (fp32 flow).  Uses the routing and probabilities of a
 // forward on the same x and the expert outputs Y (the forward's, or under

@@ -23,9 +23,10 @@ __global__ void to_bf16_kernel(const void* src, int dtype, uint16_t* dst, int64_
 
 // 32x32 LDS transpose: block (32, 8) covers source cols c0..c0+31 and
 // k0..k0+31; the 32 destination rows of an aligned group of 32 source
-// columns are consecutive in both layouts.
+// columns are consecutive in both layouts.  Destination rows are ldd
+// elements apart (ldd >= Kd: a padded row's tail is not written).
 __global__ void transpose_kernel(const void* src, int dtype, int Kd, int C, int slot,
-                                 uint16_t* dst) {
+                                 uint16_t* dst, int ldd) {
   __shared__ uint16_t tile[32][33];
   const int c0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
   for (int yy = threadIdx.y; yy < 32; yy += 8) {
@@ -37,7 +38,7 @@ __global__ void transpose_kernel(const void* src, int dtype, int Kd, int C, int 
     const int c = c0 + yy, k = k0 + threadIdx.x;
     if (c < C && k < Kd) {
       const int q = slot < 0 ? c : (c >> 5) * 64 + slot * 32 + (c & 31);
-      dst[(size_t)q * Kd + k] = tile[threadIdx.x][yy];
+      dst[(size_t)q * ldd + k] = tile[threadIdx.x][yy];
     }
   }
 }
@@ -58,10 +59,53 @@ void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n
   if (n > 0) hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, dst, n);
 }
 
+namespace {
+
+__global__ void rows_to_f32_kernel(const void* src, int dtype, int64_t rows, int cols, int ld,
+                                   float* dst) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols;
+    const int c = (int)(i - r * cols);
+    dst[i] = src_at(src, dtype, (size_t)r * ld + c);
+  }
+}
+
+__global__ void pad_rows_bf16_kernel(const uint16_t* src, int64_t rows, int cols, int ldd,
+                                     uint16_t* dst) {
+  const int64_t n = rows * ldd;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / ldd;
+    const int c = (int)(i - r * ldd);
+    dst[i] = c < cols ? src[(size_t)r * cols + c] : (uint16_t)0;
+  }
+}
+
+}  // namespace
+
+void mxm_launch_rows_to_f32(const void* src, int src_dtype, int64_t rows, int cols, int ld,
+                            float* dst, hipStream_t s) {
+  const int64_t n = rows * cols;
+  if (n > 0)
+    hipLaunchKernelGGL(rows_to_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, src_dtype, rows,
+                       cols, ld, dst);
+}
+
+void mxm_launch_pad_rows_bf16(const uint16_t* src, int64_t rows, int cols, int ldd, uint16_t* dst,
+                              hipStream_t s) {
+  const int64_t n = rows * ldd;
+  if (n > 0)
+    hipLaunchKernelGGL(pad_rows_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, rows, cols,
+                       ldd, dst);
+}
+
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
-                               uint16_t* dst, hipStream_t s) {
+                               uint16_t* dst, hipStream_t s, int ldd) {
   const dim3 grid((C + 31) / 32, (Kd + 31) / 32);
-  hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, s, src, src_dtype, Kd, C, slot, dst);
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, s, src, src_dtype, Kd, C, slot, dst,
+                     ldd > 0 ? ldd : Kd);
 }
 
 namespace {
@@ -103,11 +147,13 @@ void mxm_launch_router_t(const void* src, bool bf16, int D, int E, int ldw, void
 namespace {
 
 // MFMA-family expert weights back to fp32 in x.W layout, for the backward of
-// bf16 ops.  w1 holds per expert [NC][D] bf16 (NC = 2F, gate and up rows
-// interleaved in groups of 32, or F for one matrix); slot picks the matrix
-// (0 gate, 1 up, -1 not interleaved).  dst[e][d][f] = w1[e][q(f)][d].
-__global__ void w1_to_xw_kernel(const uint16_t* w1, int E, int D, int F, int slot, float* dst) {
-  const int NC = slot < 0 ? F : 2 * F;
+// bf16 ops.  w1 holds per expert [NC][Dk] bf16 (NC = 2Fk, gate and up rows
+// interleaved in groups of 32, or Fk for one matrix; Fk >= F and Dk >= D the
+// padded widths); slot picks the matrix (0 gate, 1 up, -1 not interleaved).
+// dst[e][d][f] = w1[e][q(f)][d].
+__global__ void w1_to_xw_kernel(const uint16_t* w1, int E, int D, int F, int Dk, int Fk, int slot,
+                                float* dst) {
+  const int NC = slot < 0 ? Fk : 2 * Fk;
   const int64_t n = (int64_t)E * D * F;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -115,33 +161,37 @@ __global__ void w1_to_xw_kernel(const uint16_t* w1, int E, int D, int F, int slo
     const int64_t ed = i / F;
     const int d = (int)(ed % D), e = (int)(ed / D);
     const int q = slot < 0 ? f : (f >> 5) * 64 + slot * 32 + (f & 31);
-    dst[i] = mxm_bf2f(w1[((size_t)e * NC + q) * D + d]);
+    dst[i] = mxm_bf2f(w1[((size_t)e * NC + q) * Dk + d]);
   }
 }
 
-// w2 [E][D][F] bf16 (the down projection, k = F contiguous) -> dst [E][F][D].
-__global__ void w2_to_xw_kernel(const uint16_t* w2, int E, int D, int F, float* dst) {
+// w2 [E][Dk][Fk] bf16 (the down projection, k = F contiguous) -> dst [E][F][D].
+__global__ void w2_to_xw_kernel(const uint16_t* w2, int E, int D, int F, int Dk, int Fk,
+                                float* dst) {
   const int64_t n = (int64_t)E * D * F;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int d = (int)(i % D);
     const int64_t ef = i / D;
     const int f = (int)(ef % F), e = (int)(ef / F);
-    dst[i] = mxm_bf2f(w2[((size_t)e * D + d) * F + f]);
+    dst[i] = mxm_bf2f(w2[((size_t)e * Dk + d) * Fk + f]);
   }
 }
 
 }  // namespace
 
-void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int slot, float* dst,
+void mxm_launch_w1_to_xw(const uint16_t* w1, int E, int D, int F, int Dk, int Fk, int slot,
+                         float* dst, hipStream_t s) {
+  const int64_t n = (int64_t)E * D * F;
+  if (n > 0)
+    hipLaunchKernelGGL(w1_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w1, E, D, F, Dk, Fk,
+                       slot, dst);
+}
+
+void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, int Dk, int Fk, float* dst,
                          hipStream_t s) {
   const int64_t n = (int64_t)E * D * F;
   if (n > 0)
-    hipLaunchKernelGGL(w1_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w1, E, D, F, slot, dst);
-}
-
-void mxm_launch_w2_to_xw(const uint16_t* w2, int E, int D, int F, float* dst, hipStream_t s) {
-  const int64_t n = (int64_t)E * D * F;
-  if (n > 0)
-    hipLaunchKernelGGL(w2_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w2, E, D, F, dst);
+    hipLaunchKernelGGL(w2_to_xw_kernel, dim3(grid_for(n)), dim3(256), 0, s, w2, E, D, F, Dk, Fk,
+                       dst);
 }

@@ -608,9 +608,14 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     // BM x BN fp32 row-major partial into their scratch slot.
     float* __restrict__ base;
     int ldr;
+    // the stored region (padded operands: see WgradArgs::m_store); partials
+    // in scratch are whole tiles
+    int mlim = BM, cvalid = 1 << 30;
     if (j == 0) {
-      base = a.out + (size_t)e * a.out_estride + (size_t)m0 * (a.glu_f > 0 ? a.glu_f : a.C);
-      ldr = a.glu_f > 0 ? a.glu_f : a.C;
+      ldr = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
+      base = a.out + (size_t)e * a.out_estride + (size_t)m0 * ldr;
+      if (a.m_store > 0) mlim = min(BM, a.m_store - m0);
+      cvalid = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
     } else {
       const int slot = __builtin_amdgcn_readfirstlane(P.slot0[e]) + (j - 1) * per_e + tile;
       base = slots + (size_t)slot * (BM * BN);
@@ -620,16 +625,19 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     for (int jj = 0; jj < TN; ++jj) {
       const int cl = wn * TN * 32 + jj * 32 + (lane & 31);
       const int c = c0 + cl;
+      // output column (GLU: the hidden unit) this lane stores
+      const int cu = j > 0 ? 0 : a.glu_f > 0 ? (c >> 6) * 32 + (c & 31) : c;
       const size_t cofs =
           j > 0 ? (size_t)cl
-                : a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)((c >> 6) * 32 + (c & 31))
-                              : (size_t)c;
+                : a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)cu : (size_t)c;
+      const bool cok = cu < cvalid;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = wm * TM * 32 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          __builtin_nontemporal_store(acc[i][jj][r], base + (size_t)m * ldr + cofs);
+          if (cok && m < mlim)
+            __builtin_nontemporal_store(acc[i][jj][r], base + (size_t)m * ldr + cofs);
         }
     }
   }
@@ -639,7 +647,9 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
 // Work units are 16-row slices of the (split expert, tile) pairs; a thread
 // takes 4 float4 of a slice (4 consecutive columns stay inside one GLU group
 // of 32) and keeps their loads in flight together.
-template <int BM, int BN>
+// VEC: whole float4 of the output (16-byte aligned rows, nothing past the
+// stored region); else element by element within the stored region.
+template <int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
   constexpr int SR = 16;                       // rows per unit
   constexpr int V = SR * BN / 4 / 256;         // float4 per thread per unit
@@ -665,7 +675,8 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
   const int units = ppre[a.E] * (BM / SR);
   const float* __restrict__ slots =
       reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.scratch) + WG_HDR_BYTES);
-  const int ld = a.glu_f > 0 ? a.glu_f : a.C;
+  const int ld = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
+  const int mst = a.m_store > 0 ? a.m_store : a.M;
   int e = 0;
   for (int k = blockIdx.x; k < units; k += gridDim.x) {
     const int pair = k / (BM / SR), r0 = (k % (BM / SR)) * SR;
@@ -673,6 +684,29 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
     const int tile = pair - ppre[e];
     const int m0 = (tile % ntm) * BM, c0 = (tile / ntm) * BN;
     float* __restrict__ out = a.out + (size_t)e * a.out_estride;
+    if constexpr (!VEC) {
+      // element by element: the four columns of a float4 of the partial, each
+      // stored only inside the output's shape
+      for (int q = 0; q < V; ++q) {
+        const int i = tid + 256 * q;
+        const int m = r0 + i / (BN / 4), cb = c0 + (i % (BN / 4)) * 4;
+        if (m0 + m >= mst) continue;
+        for (int t = 0; t < 4; ++t) {
+          const int c = cb + t;
+          const int cu = a.glu_f > 0 ? (c >> 6) * 32 + (c & 31) : c;
+          if (cu >= ld) continue;
+          const size_t cofs = a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)cu
+                                          : (size_t)c;
+          float* po = out + (size_t)(m0 + m) * ld + cofs;
+          float v = *po;
+          for (int jc = 1; jc < nch[e]; ++jc)
+            v = v + slots[(size_t)(slot0[e] + (jc - 1) * per_e + tile) * (BM * BN) +
+                          (size_t)r0 * BN + 4 * i + t];
+          *po = v;
+        }
+      }
+      continue;
+    }
     float4* o[V];
     float4 v[V];
 #pragma unroll
@@ -738,8 +772,19 @@ struct WFamily {
     else
       hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 0>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
-    hipLaunchKernelGGL((wgrad_reduce_kernel<BM, BN>), dim3(std::max(8, n_cus() * 2)), dim3(256),
-                       0, s, a);
+    // whole float4 when the output rows are 16-byte aligned and every column
+    // of the padded operands is stored
+    const int ld = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
+    const bool vec = ld % 4 == 0 && (a.m_store <= 0 || a.m_store == a.M) &&
+                     (a.glu_f > 0 ? 2 * a.glu_f == a.C : (a.c_store <= 0 || a.c_store == a.C)) &&
+                     reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && a.out_estride % 4 == 0 &&
+                     a.out_slot % 4 == 0;
+    if (vec)
+      hipLaunchKernelGGL((wgrad_reduce_kernel<BM, BN, true>), dim3(std::max(8, n_cus() * 2)),
+                         dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((wgrad_reduce_kernel<BM, BN, false>), dim3(std::max(8, n_cus() * 2)),
+                         dim3(256), 0, s, a);
   }
 };
 using WBig = WFamily<256, 256, 2, 4, 64, 2>;

@@ -79,7 +79,7 @@ def _create(int_params, n_inputs, dtype=_lib.MXM_DTYPE_F32, flags=0, floats=(0.0
     ([1, 4, 3, 3, 2, 2, 4, 0], 11, 1, 0, "unexpected expert weight input count"),
     ([1, 4, 3, 300, 2, 2, 4, 0], 602, 1, 0, "at most 256 experts"),
     ([1, 4, 64, 3, 2, 0, 64, 0], 11, 1, 16, "int8 weights need bf16 compute"),
-    ([1, 4, 96, 3, 2, 0, 64, 0], 11, 2, 16, "multiples of 64"),
+    ([1, 4, 65536, 3, 2, 0, 65536, 0], 11, 2, 16, "fewer than 2^31 entries"),
     ([1, 4, 3, 3, 2, 0, 4, 0], 11, 7, 0, "compute dtype"),
     ([32768, 32768, 3, 3, 2, 0, 4, 0], 11, 1, 0, "routed slots exceeds 2147483647"),
 ])
