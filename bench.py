@@ -212,11 +212,12 @@ def run_config(cfg, steps: int, warmup: int, flags: int = 0, stage_repeats: int 
     stages = op.stage_times()
     op.set_profiling(False)
     counts = op.routing()["counts"]
+    info = op.info()
     op.close()
     ms = elapsed * 1e3 / steps
     log(f"{cfg.name}: {steps} steps, {ms:.4f} ms/step; stages {stages}")
     return w, {"ms_per_step": ms, "tokens_per_s": cfg.N / (ms * 1e-3), "stages": stages,
-               "counts": counts}
+               "counts": counts, "info": info}
 
 
 def vendor_gemm(cfg) -> dict:
@@ -460,10 +461,12 @@ def main() -> int:
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
 
-    # the other MFMA-bound configurations: near-uniform C2 and Zipf-ragged C3
+    # the other MFMA-bound configurations: near-uniform C2, Zipf-ragged C3 and
+    # C4 at the reference's default expert width (F = 5468, padded to 5504
+    # by the library; the figures count the op's own F)
     extra = {}
     if not args.no_configs:
-        for name in ("C2", "C3"):
+        for name in ("C2", "C3", "C4F"):
             if name == cfg.name:
                 continue
             c = CONFIGS[name]
@@ -475,7 +478,8 @@ def main() -> int:
                            "grouped_gemm": grouped_gemm_summary(c, rc["stages"]),
                            "stages_ms": {k: v for k, v in rc["stages"].items() if k != "forwards"},
                            "expert_rows": {"max": int(counts.max()), "min": int(counts.min()),
-                                           "mean": float(counts.mean())}}
+                                           "mean": float(counts.mean())},
+                           "executor": rc["info"]}
 
     vendor = vendor_gemm(cfg) if args.vendor_gemm else None
 

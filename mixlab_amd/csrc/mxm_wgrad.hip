@@ -296,7 +296,10 @@ __device__ void build_plan(WgPlan& P, const int32_t* __restrict__ offsets, int E
 
 
 // GATHER: bit 1 = A's rows gathered through a_rows, bit 2 = B's through b_rows.
-template <class TL, int BM, int BN, int WM, int WN, int BK, int NS, int GATHER>
+// PAD: the output is smaller than the padded operands' M x C (WgradArgs::
+// m_store): stores are masked (a variant of its own: the masks' registers
+// would otherwise spill in every launch).
+template <class TL, int BM, int BN, int WM, int WN, int BK, int NS, int GATHER, bool PAD>
 __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
   constexpr int NW = TL::NW, TM = TL::TM, TN = TL::TN;
   constexpr int QA = TL::QA, LDPS = TL::LDPS, QB = LDPS - QA;
@@ -608,37 +611,71 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
     // BM x BN fp32 row-major partial into their scratch slot.
     float* __restrict__ base;
     int ldr;
-    // the stored region (padded operands: see WgradArgs::m_store); partials
-    // in scratch are whole tiles
-    int mlim = BM, cvalid = 1 << 30;
-    if (j == 0) {
-      ldr = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
-      base = a.out + (size_t)e * a.out_estride + (size_t)m0 * ldr;
-      if (a.m_store > 0) mlim = min(BM, a.m_store - m0);
-      cvalid = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
-    } else {
-      const int slot = __builtin_amdgcn_readfirstlane(P.slot0[e]) + (j - 1) * per_e + tile;
-      base = slots + (size_t)slot * (BM * BN);
-      ldr = BN;
+    // with padded operands, only the tiles that reach past the output's shape
+    // take the masked stores (a uniform branch)
+    bool whole = true;
+    if constexpr (PAD) {
+      const int cend = a.glu_f > 0 ? ((c0 + BN - 1) >> 6) * 32 + 32 : c0 + BN;
+      const int cst = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
+      whole = j > 0 || ((a.m_store <= 0 || m0 + BM <= a.m_store) && cend <= cst);
     }
+    if (!PAD || whole) {
+      if (j == 0) {
+        ldr = a.glu_f > 0 ? a.glu_f : (PAD && a.c_store > 0) ? a.c_store : a.C;
+        base = a.out + (size_t)e * a.out_estride + (size_t)m0 * ldr;
+      } else {
+        const int slot = __builtin_amdgcn_readfirstlane(P.slot0[e]) + (j - 1) * per_e + tile;
+        base = slots + (size_t)slot * (BM * BN);
+        ldr = BN;
+      }
 #pragma unroll
-    for (int jj = 0; jj < TN; ++jj) {
-      const int cl = wn * TN * 32 + jj * 32 + (lane & 31);
-      const int c = c0 + cl;
-      // output column (GLU: the hidden unit) this lane stores
-      const int cu = j > 0 ? 0 : a.glu_f > 0 ? (c >> 6) * 32 + (c & 31) : c;
-      const size_t cofs =
-          j > 0 ? (size_t)cl
-                : a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)cu : (size_t)c;
-      const bool cok = cu < cvalid;
+      for (int jj = 0; jj < TN; ++jj) {
+        const int cl = wn * TN * 32 + jj * 32 + (lane & 31);
+        const int c = c0 + cl;
+        const size_t cofs =
+            j > 0 ? (size_t)cl
+                  : a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)((c >> 6) * 32 + (c & 31))
+                                : (size_t)c;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = wm * TM * 32 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          if (cok && m < mlim)
+          for (int r = 0; r < 16; ++r) {
+            const int m = wm * TM * 32 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
             __builtin_nontemporal_store(acc[i][jj][r], base + (size_t)m * ldr + cofs);
-        }
+          }
+      }
+    } else {
+      // the stored region only (partials in scratch are whole tiles)
+      int mlim = BM, cvalid = 1 << 30;
+      if (j == 0) {
+        ldr = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;
+        base = a.out + (size_t)e * a.out_estride + (size_t)m0 * ldr;
+        if (a.m_store > 0) mlim = min(BM, a.m_store - m0);
+        cvalid = ldr;
+      } else {
+        const int slot = __builtin_amdgcn_readfirstlane(P.slot0[e]) + (j - 1) * per_e + tile;
+        base = slots + (size_t)slot * (BM * BN);
+        ldr = BN;
+      }
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj) {
+        const int cl = wn * TN * 32 + jj * 32 + (lane & 31);
+        const int c = c0 + cl;
+        // output column (GLU: the hidden unit) this lane stores
+        const int cu = j > 0 ? 0 : a.glu_f > 0 ? (c >> 6) * 32 + (c & 31) : c;
+        const size_t cofs =
+            j > 0 ? (size_t)cl
+                  : a.glu_f > 0 ? (size_t)((c >> 5) & 1) * a.out_slot + (size_t)cu : (size_t)c;
+        const bool cok = cu < cvalid;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = wm * TM * 32 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (cok && m < mlim)
+              __builtin_nontemporal_store(acc[i][jj][r], base + (size_t)m * ldr + cofs);
+          }
+      }
     }
   }
 }
@@ -762,16 +799,25 @@ struct WFamily {
   static size_t scratch_bytes() {
     return WG_HDR_BYTES + (size_t)grid() * WG_SLOTS_PER_WG * BM * BN * sizeof(float);
   }
-  static void launch(const WgradArgs& a, hipStream_t s) {
+  template <bool PAD>
+  static void launch_main(const WgradArgs& a, hipStream_t s) {
     if (a.a_rows)
-      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 1>), dim3(grid()),
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 1, PAD>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
     else if (a.b_rows)
-      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 2>), dim3(grid()),
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 2, PAD>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
     else
-      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 0>), dim3(grid()),
+      hipLaunchKernelGGL((wgrad_kernel<TL, BM, BN, WM, WN, BK, NS, 0, PAD>), dim3(grid()),
                          dim3(TL::NT), 0, s, a);
+  }
+  static void launch(const WgradArgs& a, hipStream_t s) {
+    const bool pad = (a.m_store > 0 && a.m_store != a.M) ||
+                     (a.glu_f > 0 ? 2 * a.glu_f != a.C : (a.c_store > 0 && a.c_store != a.C));
+    if (pad)
+      launch_main<true>(a, s);
+    else
+      launch_main<false>(a, s);
     // whole float4 when the output rows are 16-byte aligned and every column
     // of the padded operands is stored
     const int ld = a.glu_f > 0 ? a.glu_f : a.c_store > 0 ? a.c_store : a.C;

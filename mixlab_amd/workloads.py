@@ -71,6 +71,12 @@ CONFIGS = {
                     note="bf16 d=2048, 64 experts top-8, F=1024 gated, 65536 tokens"),
     "C5": MoEConfig("C5", 1, 64, 2048, 64, 8, 1408, "bf16", seed=5, int8_weights=True,
                     note="decode: 64 tokens, d=2048, 64 experts top-8, F=1408, int8 weights"),
+    # not a benchmark-plan configuration: C4 at the reference's default expert
+    # width ffnDim(2048, 2.67) = 5468 (arch/weight_shapes.go:11,56-65), which
+    # the MFMA kernels run at 5504 with zero weights in the padding
+    "C4F": MoEConfig("C4F", 32, 2048, 2048, 64, 8, 5468, "bf16", seed=6,
+                     note="bf16 d=2048, 64 experts top-8, F=5468 (default mlp_mult 2.67) "
+                          "gated, 65536 tokens"),
 }
 
 

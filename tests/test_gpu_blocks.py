@@ -66,22 +66,25 @@ def test_moe_tiny_blocks(gpu_lib, flow):
         x = out  # the next block's input, as the stream carries it
 
 
-@pytest.mark.parametrize("mode", ["int8", "int6"])
-def test_int8_block_from_quantized_checkpoint(gpu_lib, tmp_path, mode):
+@pytest.mark.parametrize("mode,D,mult", [("int8", 256, 2.0), ("int6", 256, 2.0),
+                                         ("int8", 512, 2.67)])
+def test_int8_block_from_quantized_checkpoint(gpu_lib, tmp_path, mode, D, mult):
     """An MoE block written by the reference's quantized export (per-row
     int8 / int6 matrices, F32 norm and moe_scale), read back and run on the
     int8 expert kernels.  Routing is bit-exact against the restatement fed
     the router as the file dequantises it; the delta is checked against the
     restatement fed the executor's per-channel weights and against the one
     fed the file's own per-row dequantised weights (what the reference would
-    compute from this file), both within the bf16 bar."""
+    compute from this file), both within the bf16 bar.  The third case is a
+    block at the reference's default expert width (mlp_mult 2.67: F =
+    ffnDim(512, 2.67) = 1367, which the int8 kernels run at 1408)."""
     from mixlab_amd.op import MoEBlock
     from mixlab_amd.weights import (QuantizedWeight, export_safetensors_quantized,
                                     load_quantized_weights)
 
     spec = moe.BlockSpec.from_json('{"type":"moe","num_experts":6,"top_k":2,'
                                    '"residual_scale_init":0.5}')
-    B, T, D, mult = 1, 64, 256, 2.0
+    B, T = 1, 64
     rng = np.random.default_rng(77)
     with MoEBlock(spec, B, T, D, mlp_mult=mult, block_scales=True, compute_dtype="bf16",
                   flags=_lib.MXM_FLAG_INT8_WEIGHTS) as blk:
@@ -91,7 +94,8 @@ def test_int8_block_from_quantized_checkpoint(gpu_lib, tmp_path, mode):
         path = str(tmp_path / "q.safetensors")
         export_safetensors_quantized(path, blk.metas, ws, mode, first_index=3)
         blk.load_quantized(path, first_index=3)
-        assert blk.op.info()["int8"]
+        info = blk.op.info()
+        assert info["int8"] and info["ffn_kernel"] == (moe.ffn_dim(D, mult) + 63) // 64 * 64
         x = round_bf16(rng.standard_normal((B * T, D), dtype=np.float32))
         out, aux, ent = blk.forward_host(bf16_bits(x))
         routing = blk.op.routing()
