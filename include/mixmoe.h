@@ -204,13 +204,13 @@ int mxm_moe_block_forward_host(int64_t op, const void* x, int x_dtype, int64_t r
  * indices carry no gradient) and writes dx [rows, D], d_router_w [D, E] and
  * d_experts: the expert weight gradients in Op.Inputs order (per expert
  * w_gate, w_up, w_down -- or w_up, w_down -- each in x.W layout, as
- * mxm_moe_set_input takes them).  Device pointers.  Under bf16 compute on
- * the MFMA weight family the call is asynchronous on the op's stream (the
- * weight gradients are reduced over each expert's rows on the device); the
- * other flows wait once for the op's stream (the per-expert row counts size
- * their per-expert GEMMs) and leave the rest of their work queued on it.  The
- * first call allocates the backward's workspace (on MI355X, 128 MiB of it
- * holds the weight gradients' split-reduction partials). */
+ * mxm_moe_set_input takes them).  Device pointers; the call is asynchronous
+ * on the op's stream (every expert product is a ragged grouped product whose
+ * row ranges come from the device-side routing).  Under fp32 compute each
+ * expert product runs as a bf16 MFMA product over the operands' hi / lo
+ * planes (hi = bf16(v), lo = bf16(v - hi); about 2^-16 relative).  The first
+ * call allocates the backward's workspace (on MI355X, 128 MiB of it holds the
+ * weight gradients' split-reduction partials). */
 int mxm_moe_backward(int64_t op, const void* x, int x_dtype, int64_t rows, const float* d_delta,
                      float d_aux, float d_entropy, float* dx, float* d_router_w, float* d_experts);
 

@@ -1,5 +1,5 @@
 """Build libmixmoe.so (gfx950) in-tree with hipcc (linked against the HIP
-runtime and rocBLAS).
+runtime only).
 
 Every HIP source is compiled with -ffp-contract=off (the routing arithmetic
 must match the CPU restatement operation for operation) and with packed-fp32
@@ -71,9 +71,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
     tmp = LIB.with_suffix(".so.tmp")
-    # rocBLAS: the fp32 flow's backward products (per-expert fp32 GEMMs)
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-lrocblas"]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

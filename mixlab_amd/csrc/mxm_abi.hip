@@ -7,7 +7,6 @@
 // point (gpu/mlx_bridge.cpp:64-82) that turns failures into status codes and
 // a per-thread message.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <array>
@@ -202,7 +201,7 @@ struct MoeOp {
   // 4 GiB): MXM_FORCE_64BIT_OFFSETS at creation, so that the paths larger
   // operands take can be checked on small ones
   bool force64 = false;
-  DevBuf bw_delta, bw_xp, bw_g, bw_u, bw_h, bw_dy, bw_dh, bw_dg, bw_du, bw_dxg, bw_dxu, bw_dgates,
+  DevBuf bw_delta, bw_dy, bw_dgates,
       bw_dlogits, bw_dxr, bw_wrt, bw_one, bw_wr_part;
   // bf16 ops: fp32 copies of the (bf16-valued) weights in x.W layout, of x
   // and of the forward's expert outputs, for the fp32 backward kernels
@@ -214,7 +213,11 @@ struct MoeOp {
   bool bw_wbf_ready = false;
   DevBuf bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
       bw_ddb, bw_gp, bw_dgp, bw_dlb, bw_dwr2;
-  rocblas_handle bw_blas = nullptr;
+  // the fp32 backward's products (run_backward_x3): bf16 planes of the
+  // operands at the padded widths Dq x Fq, fp32 products
+  bool bx_w_ready = false;
+  int bx_Dq = 0, bx_Fq = 0;
+  DevBuf bx_w1p, bx_w1t, bx_w2p, bx_w2t, bx_x3, bx_gu, bx_h3, bx_y, bx_dy3, bx_dh, bx_dgu3, bx_dxe;
   int32_t bw_one_host[4] = {0, 0, 0, 0};
 
   // profiling: one set of MXM_NUM_STAGES+1 events per profiled forward
@@ -231,7 +234,6 @@ struct MoeOp {
     for (auto& set : ev_sets)
       for (auto& e : set)
         if (e) (void)hipEventDestroy(e);
-    if (bw_blas) (void)rocblas_destroy_handle(bw_blas);
   }
 };
 
@@ -696,6 +698,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
   o.have[idx] = 1;
   o.bw_w32_ready = false;
   o.bw_wbf_ready = false;
+  o.bx_w_ready = false;
   o.kept = false;  // a kept forward ran on the weights this call replaced
 }
 
@@ -735,6 +738,7 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
   o.have[idx] = 1;
   o.bw_w32_ready = false;
   o.bw_wbf_ready = false;
+  o.bx_w_ready = false;
   o.kept = false;  // a kept forward ran on the weights this call replaced
 }
 
@@ -1222,10 +1226,6 @@ bool mfma_backward_fits(const MoeOp& o) {
          mxm_mfma_tile_rows(NC, o.D, o.family) > 0 && mxm_mfma_tile_rows(o.D, NC, o.family) > 0;
 }
 
-void check_blas(rocblas_status st, const char* what) {
-  if (st != rocblas_status_success)
-    fail_rt("OP_MOE_FEED_FORWARD backward: %s failed (rocBLAS status %d)", what, (int)st);
-}
 
 // The experts' products of the bf16 flow on MFMA.  Rows are in the forward's
 // permuted order throughout (expert e owns rows offsets[e] ..).  The forward
@@ -1424,105 +1424,172 @@ void run_backward_mfma(MoeOp& o, const void* xb, const BackwardArgs& b, float* d
   HIPCK(hipGetLastError());
 }
 
+// MFMA tile family for a product with Ncols output columns over `rows`
+// rows: 256 x 256 where the columns allow and there are at least two tiles
+// per CU, else 128 x 128 (as the forward's schedule picks them).
+int product_family(const MoeOp& o, int ncols, size_t rows) {
+  if (ncols % 256 != 0) return MXM_TILE_128x128;
+  const int64_t tiles = ((int64_t)rows + 255) / 256 * (ncols / 256);
+  return tiles < 2 * (int64_t)o.n_cu ? (int)MXM_TILE_128x128 : (int)MXM_TILE_256x256;
+}
+
 // The fp32 backward after the routing (fp32 compute, or the bf16 flow on
-// fp32 copies where the MFMA tiles do not apply).  Rows are in the forward's
-// permuted order (expert e owns rows offsets[e] ..); per expert, with r rows,
-// all matrices row-major and the weights in the reference's x.W layout:
-//   G = Xp W_gate, U = Xp W_up          (the forward projections)
-//   own_forward (fp32 compute): H elementwise, Y = H W_down (the forward's
-//                                expert outputs, which dgates reads)
-//   the router part (mxm_launch_backward_router: dgates .. dY, d router_w)
-//   dH = dY W_down^T
-//   dG, dU, H                           elementwise (mxm_launch_backward_act)
-//   dX = dG W_gate^T + dU W_up^T        (summed per token by mxm_launch_backward_dx)
-//   dW_gate = Xp^T dG, dW_up = Xp^T dU, dW_down = H^T dY
-// each a rocBLAS fp32 GEMM (column-major, so each is issued as its
-// transpose).  The per-expert row counts are read back once.  Without
-// own_forward (the bf16 flow) Y comes from the op's forward.
-void run_backward_blas32(MoeOp& o, BackwardArgs& b, bool own_forward) {
+// fp32 copies where the MFMA backward does not apply).  Every product of the
+// experts runs on the library's bf16 MFMA kernels as the product of the
+// operands' bf16 planes (hi = bf16(v), lo = bf16(v - hi), concatenated along
+// k so that one product sums hi.hi + hi.lo + lo.hi; mxm_launch_planes3):
+// about 2^-16 relative per term, accumulated in fp32.  Operands are padded
+// with zeros to Dq x Fq (multiples of 128); rows are in the forward's
+// permuted order and every grouped product takes its experts' row ranges
+// from the device-side offsets, so nothing waits for the host.
+//   G|U = Xp W1                 grouped product, A = x's planes through perm
+//   H = act(G, U)               planes of H
+//   Y = H W_down                (own_forward: fp32 compute; else the op's
+//                                forward's expert outputs)
+//   the router part             (mxm_launch_backward_router: dgates .. dY,
+//                                dx's router term, d router_w)
+//   dH = dY W_down^T            grouped product on dY's planes
+//   dG, dU                      the activation backward, as planes
+//   dXe = dGU W1^T, dx = dxr + sum_k dXe
+//   dW1 = Xp^T dGU, dW_down = H^T dY   the weight-gradient kernel, three
+//                                plane pairs each, the gradients stored in
+//                                the op's [D][F] / [F][D] layout
+void run_backward_x3(MoeOp& o, BackwardArgs& b, bool own_forward) {
   hipStream_t st = o.stream;
   const bool glu = o.wpe == 3;
   const int D = o.D, F = o.F, E = o.E;
-  const size_t DF = (size_t)D * F, stride = (size_t)o.wpe * DF;
-  mxm_launch_backward_gather(b, st);
-  HIPCK(hipGetLastError());
-  std::vector<int32_t> cnt(E);
-  HIPCK(hipMemcpyAsync(cnt.data(), b.counts, (size_t)E * 4, hipMemcpyDeviceToHost, st));
-  HIPCK(hipStreamSynchronize(st));
-  if (!o.bw_blas) check_blas(rocblas_create_handle(&o.bw_blas), "rocblas_create_handle");
-  check_blas(rocblas_set_stream(o.bw_blas, st), "rocblas_set_stream");
-  const float one = 1.0f, zero = 0.0f;
-  auto mm = [&](rocblas_operation ta, rocblas_operation tb, int m, int n, int k, const float* A,
-                int lda, const float* B, int ldb, float* C, int ldc) {
-    check_blas(rocblas_sgemm(o.bw_blas, ta, tb, m, n, k, &one, A, lda, B, ldb, &zero, C, ldc),
-               "fp32 backward GEMM");
-  };
-  constexpr rocblas_operation NO = rocblas_operation_none, TR = rocblas_operation_transpose;
-  size_t off = 0;
-  for (int e = 0; e < E; ++e) {
-    const int r = cnt[e];
-    if (r > 0) {
-      const float* xp = b.xp + off * D;
-      const float* w1 = b.w1 + (size_t)e * DF;
-      if (glu) {
-        mm(NO, NO, F, r, D, w1, F, xp, D, b.g + off * F, F);
-        mm(NO, NO, F, r, D, b.w1b + (size_t)e * DF, F, xp, D, b.u + off * F, F);
-      } else {
-        mm(NO, NO, F, r, D, w1, F, xp, D, b.u + off * F, F);
-      }
+  const int Dq = (D + 127) / 128 * 128, Fq = (F + 127) / 128 * 128, NCq = glu ? 2 * Fq : Fq;
+  const size_t N = o.N, NK = (size_t)o.N * o.K, DF = (size_t)D * F;
+  if (o.bx_Dq != Dq || o.bx_Fq != Fq || !o.bx_x3.p) {
+    o.bx_Dq = Dq;
+    o.bx_Fq = Fq;
+    o.bx_w1p.alloc((size_t)E * NCq * 3 * Dq * 2);
+    o.bx_w1t.alloc((size_t)E * Dq * 3 * NCq * 2);
+    o.bx_w2p.alloc((size_t)E * Dq * 3 * Fq * 2);
+    o.bx_w2t.alloc((size_t)E * Fq * 3 * Dq * 2);
+    o.bx_x3.alloc(N * 3 * Dq * 2);
+    o.bx_gu.alloc(NK * NCq * 4);
+    o.bx_h3.alloc(NK * 3 * Fq * 2);
+    if (Dq != D) o.bx_y.alloc(NK * Dq * 4);
+    o.bx_dy3.alloc(NK * 3 * Dq * 2);
+    o.bx_dh.alloc(NK * Fq * 4);
+    o.bx_dgu3.alloc(NK * 3 * NCq * 2);
+    o.bx_dxe.alloc(NK * Dq * 4);
+    if (!o.bw_zero.p) {
+      o.bw_zero.alloc(512);  // 256 zero bf16: the weight gradients' rows past an expert's end
+      HIPCK(hipMemsetAsync(o.bw_zero.p, 0, 512, st));
     }
-    off += (size_t)(r > 0 ? r : 0);
+    if (!o.bw_ms.p) o.bw_ms.alloc(3 * ((size_t)E + 1) * 4);
+    o.bw_wscr.alloc(std::max(mxm_wgrad_scratch_bytes(Dq, NCq), mxm_wgrad_scratch_bytes(Fq, Dq)));
+    o.bx_w_ready = false;
   }
-  if (own_forward) {
-    mxm_launch_backward_hidden(b, st);
+  if (!o.bx_w_ready) {
+    mxm_launch_planes3_weights(b.w1, glu ? b.w1b : nullptr, b.w2, E, D, F, Dq, Fq, glu,
+                               o.bx_w1p.as<uint16_t>(), o.bx_w1t.as<uint16_t>(),
+                               o.bx_w2p.as<uint16_t>(), o.bx_w2t.as<uint16_t>(), st);
     HIPCK(hipGetLastError());
-    off = 0;
-    for (int e = 0; e < E; ++e) {
-      const int r = cnt[e];
-      if (r > 0)
-        mm(NO, NO, D, r, F, b.w2 + (size_t)e * DF, D, b.h + off * F, F,
-           static_cast<float*>(o.ws.Y) + off * D, D);
-      off += (size_t)(r > 0 ? r : 0);
-    }
+    o.bx_w_ready = true;
+  }
+  uint16_t *x3 = o.bx_x3.as<uint16_t>(), *h3 = o.bx_h3.as<uint16_t>(),
+           *dy3 = o.bx_dy3.as<uint16_t>(), *dgu3 = o.bx_dgu3.as<uint16_t>();
+  float *gu = o.bx_gu.as<float>(), *dh = o.bx_dh.as<float>(), *dxe = o.bx_dxe.as<float>();
+  // grouped product out [NK][Ncols] fp32 = A [NK][Kd] (rows through perm when
+  // gather) . B_e^T (B_e [Ncols][Kd] per expert)
+  auto product = [&](int which, const uint16_t* A, const uint16_t* W, float* out, int Kd,
+                     int Ncols, bool gather) {
+    const int family = product_family(o, Ncols, NK);
+    const int bm = mxm_mfma_tile_rows(Ncols, Kd, family);
+    if (bm <= 0)
+      fail("OP_MOE_FEED_FORWARD backward: a %d x %d expert product exceeds the MFMA tiles' "
+           "addressing", Ncols, Kd);
+    int32_t* ms = o.bw_ms.as<int32_t>() + (size_t)which * (E + 1);
+    mxm_launch_tile_prefix(b.counts, E, bm, ms, st);
+    GemmArgs g{};
+    g.no_off32 = o.force64;
+    g.mode = MXM_GEMM_DOWN;
+    g.f32_out = true;
+    g.a = A;
+    g.b0 = W;
+    g.out = out;
+    g.offsets = b.offsets;
+    g.mstart = ms;
+    g.E = E;
+    g.Kd = Kd;
+    g.Ncols = Ncols;
+    g.max_mtiles = (int)((NK + bm - 1) / bm) + E;
+    g.family = family;
+    g.gather_a = gather;
+    g.perm = b.perm;
+    g.rows_total = (int)NK;
+    require_operands(g, false, false);
+    mxm_launch_gemm_mfma(g, st);
+    HIPCK(hipGetLastError());
+  };
+  // x's planes (one row per token; the products gather them through perm)
+  mxm_launch_planes3(b.x, (int64_t)N, D, D, Dq, false, x3, st);
+  // G|U = Xp W1 (fp32, W1's interleaved column order), H's planes
+  product(0, x3, o.bx_w1p.as<uint16_t>(), gu, 3 * Dq, NCq, true);
+  mxm_launch_hidden_planes3(gu, (int64_t)NK, Fq, o.etype, o.act, o.slope, h3, st);
+  HIPCK(hipGetLastError());
+  if (own_forward) {
+    // the expert outputs Y = H W_down, which the gate gradients read
+    float* y = static_cast<float*>(o.ws.Y);
+    product(1, h3, o.bx_w2p.as<uint16_t>(), Dq == D ? y : o.bx_y.as<float>(), 3 * Fq, Dq, false);
+    if (Dq != D) mxm_launch_rows_to_f32(o.bx_y.p, MXM_DTYPE_F32, (int64_t)NK, D, Dq, y, st);
+    HIPCK(hipGetLastError());
   }
   mxm_launch_backward_router(b, st);
   HIPCK(hipGetLastError());
-  off = 0;
-  for (int e = 0; e < E; ++e) {
-    const int r = cnt[e];
-    if (r > 0)
-      mm(TR, NO, F, r, D, b.w2 + (size_t)e * DF, D, b.dy + off * D, D, b.dh + off * F, F);
-    off += (size_t)(r > 0 ? r : 0);
-  }
-  mxm_launch_backward_act(b, st);
+  // dH = dY W_down^T, the activation backward, dXe = dGU W1^T, dx
+  mxm_launch_planes3(b.dy, (int64_t)NK, D, D, Dq, true, dy3, st);
+  product(1, dy3, o.bx_w2t.as<uint16_t>(), dh, 3 * Dq, Fq, false);
+  mxm_launch_act_bw_planes3(gu, dh, (int64_t)NK, Fq, o.etype, o.act, o.slope, dgu3, st);
   HIPCK(hipGetLastError());
-  off = 0;
-  for (int e = 0; e < E; ++e) {
-    const int r = cnt[e];
-    float* dwe = b.dw + (size_t)e * stride;
-    if (r <= 0) {
-      HIPCK(hipMemsetAsync(dwe, 0, stride * 4, st));
-      continue;
-    }
-    const float* xp = b.xp + off * D;
-    const float* dy = b.dy + off * D;
-    const float* w1 = b.w1 + (size_t)e * DF;
-    const float* dg = b.dg + off * F;
-    const float* du = b.du + off * F;
-    if (glu) {
-      mm(TR, NO, D, r, F, w1, F, dg, F, b.dxg + off * D, D);
-      mm(TR, NO, D, r, F, b.w1b + (size_t)e * DF, F, du, F, b.dxu + off * D, D);
-      mm(NO, TR, F, D, r, dg, F, xp, D, dwe, F);                          // gate [D][F]
-      mm(NO, TR, F, D, r, du, F, xp, D, dwe + DF, F);                     // up [D][F]
-      mm(NO, TR, D, F, r, dy, D, b.h + off * F, F, dwe + 2 * DF, D);      // down [F][D]
-    } else {
-      mm(TR, NO, D, r, F, w1, F, du, F, b.dxu + off * D, D);
-      mm(NO, TR, F, D, r, du, F, xp, D, dwe, F);                          // up [D][F]
-      mm(NO, TR, D, F, r, dy, D, b.h + off * F, F, dwe + DF, D);          // down [F][D]
-    }
-    off += (size_t)r;
-  }
-  mxm_launch_backward_dx(b, st);
+  product(2, dgu3, o.bx_w1t.as<uint16_t>(), dxe, 3 * NCq, Dq, false);
+  mxm_launch_dx_sum(b.dxr, dxe, Dq, b.slot_pos, o.N, D, o.K, b.dx, st);
+  HIPCK(hipGetLastError());
+  // weight gradients: dW1 = Xp^T dGU over the plane pairs (x hi, dGU hi),
+  // (x hi, dGU lo), (x lo, dGU hi); dW_down = H^T dY likewise
+  WgradArgs wa{};
+  wa.offsets = b.offsets;
+  wa.zero = o.bw_zero.as<uint16_t>();
+  wa.scratch = o.bw_wscr.p;
+  wa.E = E;
+  wa.out_estride = (size_t)o.wpe * DF;
+  wa.planes = 3;
+  wa.a = x3;
+  wa.a_rows = b.perm;
+  wa.a_rows32 = !o.force64 && N * 3 * Dq * 2 < ((size_t)1 << 32);
+  wa.lda = 3 * Dq;
+  wa.aplane = Dq;
+  wa.b = dgu3;
+  wa.ldb = 3 * NCq;
+  wa.bplane = NCq;
+  wa.M = Dq;
+  wa.m_store = Dq != D ? D : 0;
+  wa.C = NCq;
+  wa.c_store = (!glu && Fq != F) ? F : 0;
+  wa.out = b.dw;
+  wa.out_slot = DF;
+  wa.glu_f = glu ? F : 0;
+  mxm_launch_wgrad(wa, st);
+  HIPCK(hipGetLastError());
+  wa.a = h3;
+  wa.a_rows = nullptr;
+  wa.a_rows32 = false;
+  wa.lda = 3 * Fq;
+  wa.aplane = Fq;
+  wa.b = dy3;
+  wa.ldb = 3 * Dq;
+  wa.bplane = Dq;
+  wa.M = Fq;
+  wa.m_store = Fq != F ? F : 0;
+  wa.C = Dq;
+  wa.c_store = Dq != D ? D : 0;
+  wa.out = b.dw + (glu ? 2 : 1) * DF;
+  wa.out_slot = 0;
+  wa.glu_f = 0;
+  mxm_launch_wgrad(wa, st);
   HIPCK(hipGetLastError());
 }
 
@@ -1555,17 +1622,6 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
     o.bw_one_host[1] = o.N;
     o.bw_one_host[3] = (o.N + 63) / 64;
     HIPCK(hipMemcpyAsync(o.bw_one.p, o.bw_one_host, 16, hipMemcpyHostToDevice, o.stream));
-    if (!mfma_bw) {
-      o.bw_xp.alloc(NK * D * 4);
-      o.bw_dxg.alloc(NK * D * 4);
-      o.bw_dxu.alloc(NK * D * 4);
-      o.bw_g.alloc(NK * F * 4);
-      o.bw_u.alloc(NK * F * 4);
-      o.bw_h.alloc(NK * F * 4);
-      o.bw_dh.alloc(NK * F * 4);
-      o.bw_dg.alloc(NK * F * 4);
-      o.bw_du.alloc(NK * F * 4);
-    }
     o.bw_ready = true;
   }
   const float *w1 = o.w1.as<float>(), *w1b = o.w1b.as<float>(), *w2 = o.w2.as<float>();
@@ -1613,7 +1669,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   // probabilities and the raw projections where this forward puts them
   const bool reuse = mfma_bw && allow_kept && o.kept;
   // fp32 compute: the forward's routing only; the experts' forward products
-  // are computed by run_backward_blas32 (and kept for the backward)
+  // are computed by run_backward_x3
   const bool own_forward = !o.bf16;
   if (!reuse) {
     o.keep_probs = true;
@@ -1695,16 +1751,7 @@ void run_backward(MoeOp& o, const void* x, int x_dtype, const float* d_delta, fl
   b.w1 = w1;
   b.w1b = w1b;
   b.w2 = w2;
-  b.xp = o.bw_xp.as<float>();
-  b.g = o.bw_g.as<float>();
-  b.u = o.bw_u.as<float>();
-  b.h = o.bw_h.as<float>();
-  b.dh = o.bw_dh.as<float>();
-  b.dg = o.bw_dg.as<float>();
-  b.du = o.bw_du.as<float>();
-  b.dxg = o.bw_dxg.as<float>();
-  b.dxu = o.bw_dxu.as<float>();
-  run_backward_blas32(o, b, own_forward);
+  run_backward_x3(o, b, own_forward);
 }
 
 int mxm_moe_backward(int64_t h, const void* x, int x_dtype, int64_t rows, const float* d_delta,

@@ -18,10 +18,11 @@
 //                   dW_gate = X^T dG, dW_up = X^T dU.
 // The router part runs here (dgates, router_bw, dy, the router's input and
 // weight gradients; the weight gradient reduces over row chunks in a fixed
-// order).  The experts' fp32 products are one rocBLAS GEMM per expert and
-// product, issued by the library's host code; the elementwise parts (the
-// gathered rows, the activation derivative, dx) are the launchers at the end.
-// Every result is deterministic.
+// order).  The experts' products run on the MFMA grouped GEMM and weight-
+// gradient kernels (bf16, or fp32 values as bf16 planes), issued by the
+// library's host code; the elementwise parts around them (activation
+// derivatives, planes, dx sums) are the kernels here.  Every result is
+// deterministic.
 #include <algorithm>
 
 #include "mxm_kernels.h"
@@ -31,13 +32,6 @@ namespace {
 __device__ __forceinline__ float ld_x(const float* p) { return *p; }
 __device__ __forceinline__ float ld_x(const uint16_t* p) { return mxm_bf2f(*p); }
 
-__global__ void gather_rows_kernel(const float* __restrict__ x, const int32_t* __restrict__ perm,
-                                   int D, float* __restrict__ out) {
-  const int s = blockIdx.x;
-  const float* src = x + (size_t)perm[s] * D;
-  float* dst = out + (size_t)s * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[d] = src[d];
-}
 
 // dst[b][c][r] = src[b][r][c]
 __global__ void transpose_f32_kernel(const float* __restrict__ src, int R, int C,
@@ -244,31 +238,7 @@ __device__ __forceinline__ void act_eval(int etype, int act, float slope, float 
   }
 }
 
-// activation backward per element of [N*K, F]; recomputes H
-__global__ void act_bw_kernel(BackwardArgs a, size_t total) {
-  const bool glu = a.etype != MXM_EXPERT_MLP;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const float dh = a.dh[i];
-    float h, cg, cu;
-    act_eval(a.etype, a.act, a.slope, glu ? a.g[i] : 0.0f, a.u[i], h, cg, cu);
-    a.h[i] = h;
-    if (glu) a.dg[i] = dh * cg;
-    a.du[i] = dh * cu;
-  }
-}
 
-// H per element of [N*K, F] from the projections (the forward's hidden
-// units, for the backward's own expert forward)
-__global__ void hidden_kernel(BackwardArgs a, size_t total) {
-  const bool glu = a.etype != MXM_EXPERT_MLP;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (size_t)gridDim.x * blockDim.x) {
-    float h, cg, cu;
-    act_eval(a.etype, a.act, a.slope, glu ? a.g[i] : 0.0f, a.u[i], h, cg, cu);
-    a.h[i] = h;
-  }
-}
 
 // d router_w = x^T dlogits, a D x E output reduced over all N rows.  Row
 // group c (one workgroup) produces part[c][d][e]; its 4 waves take 4
@@ -419,20 +389,6 @@ __global__ __launch_bounds__(256) void wgrad_sum_kernel(const float* __restrict_
   if (g == 0 && q < n) out[q] = ((sg[0][l] + sg[1][l]) + sg[2][l]) + sg[3][l];
 }
 
-// dx[n] = dxr[n] + sum_k (dxg + dxu)[slot_pos(n, k)], k ascending
-__global__ void dx_kernel(BackwardArgs a) {
-  const int n = blockIdx.x;
-  const bool glu = a.etype != MXM_EXPERT_MLP;
-  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
-    float acc = a.dxr[(size_t)n * a.D + d];
-    for (int k = 0; k < a.K; ++k) {
-      const size_t p = (size_t)a.slot_pos[(size_t)n * a.K + k] * a.D + d;
-      const float v = glu ? a.dxg[p] + a.dxu[p] : a.dxu[p];
-      acc = acc + v;
-    }
-    a.dx[(size_t)n * a.D + d] = acc;
-  }
-}
 
 void transpose_batch(const float* src, int batch, int R, int C, float* dst, hipStream_t s) {
   if (batch <= 0 || R <= 0 || C <= 0) return;
@@ -894,6 +850,158 @@ __global__ void tile_prefix_kernel(const int32_t* counts, int E, int bm, int32_t
   mstart[E] = m;
 }
 
+
+// ---- the fp32 backward's products on the bf16 MFMA kernels ----
+// An fp32 value v is carried as two bf16 planes, hi = bf16(v) and lo =
+// bf16(v - hi) (|v - hi - lo| <= 2^-18 |v|), and an fp32 product A . B as
+// the bf16 product of the k-concatenated planes [a0 | a1 | a2] . [b0 | b1 |
+// b2] with (a, b) = (hi, hi), (hi, lo), (lo, hi): A . B to within about
+// 3 * 2^-18 relative per term (the lo . lo term, below 2^-18, is dropped),
+// accumulated in fp32 by the MFMA.  Operands that pair with A-side planes
+// are laid out HHL = [hi | hi | lo], those on the B side HLH = [hi | lo | hi].
+
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+  hi = mxm_f2bf(v);
+  lo = mxm_f2bf(v - mxm_bf2f(hi));
+}
+
+// dst[r][p * ldq + c] = plane p (order hlh: HLH, else HHL) of src[r][c] for
+// c < cols, 0 for cols <= c < ldq.
+__global__ void planes3_kernel(const float* __restrict__ src, int64_t rows, int cols, int lds,
+                               int ldq, int hlh, uint16_t* __restrict__ dst) {
+  const int64_t n = rows * ldq;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / ldq;
+    const int c = (int)(i - r * ldq);
+    uint16_t hi = 0, lo = 0;
+    if (c < cols) split_bf16(src[(size_t)r * lds + c], hi, lo);
+    uint16_t* d = dst + (size_t)r * 3 * ldq + c;
+    d[0] = hi;
+    d[ldq] = hlh ? lo : hi;
+    d[2 * ldq] = hlh ? hi : lo;
+  }
+}
+
+// One fp32 expert matrix of the x.W layout in the planes of an MFMA B
+// operand [R][3 Kq] bf16 per expert: dst[e][r][p * Kq + k] = plane p of the
+// source value at (r, k), 0 past the real extent.  For the up projections
+// (gate, up: src0, src1 [D][F]) or the down one (src0 [F][D]); the row or the
+// k index may be a GLU-interleaved column (groups of 32 gate then 32 up).
+struct Planes3W {
+  const float* src0;
+  const float* src1;    // the up matrix of a GLU pair (interleaved index), else null
+  int E, R, Kq;         // rows and padded k per expert
+  int r_lim, k_lim;     // real extent of the decoded row and k indices
+  int glu_r, glu_k;     // the row / k index is GLU-interleaved
+  int64_t sr, sk;       // source strides of the decoded row and k indices
+  int64_t es;           // source stride between experts
+  int hlh;
+  uint16_t* dst;
+};
+
+__global__ void planes3_w_kernel(Planes3W a) {
+  const int64_t per = (int64_t)a.R * a.Kq;
+  const int64_t n = (int64_t)a.E * per;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i / per);
+    const int64_t rk = i - (int64_t)e * per;
+    const int r = (int)(rk / a.Kq), k = (int)(rk - (int64_t)r * a.Kq);
+    int slot = 0, rr = r, kk = k;
+    if (a.glu_r) {
+      slot = (r >> 5) & 1;
+      rr = (r >> 6) * 32 + (r & 31);
+    }
+    if (a.glu_k) {
+      slot = (k >> 5) & 1;
+      kk = (k >> 6) * 32 + (k & 31);
+    }
+    uint16_t hi = 0, lo = 0;
+    if (rr < a.r_lim && kk < a.k_lim) {
+      const float* src = slot ? a.src1 : a.src0;
+      split_bf16(src[(size_t)e * a.es + (size_t)rr * a.sr + (size_t)kk * a.sk], hi, lo);
+    }
+    uint16_t* d = a.dst + ((size_t)e * a.R + r) * 3 * a.Kq + k;
+    d[0] = hi;
+    d[a.Kq] = a.hlh ? lo : hi;
+    d[2 * (size_t)a.Kq] = a.hlh ? hi : lo;
+  }
+}
+
+// The hidden units of the raw projections gu [rows][NC] fp32 (GLU: gate and
+// up interleaved in groups of 32; NC = 2 Fq, else Fq), as the HHL planes of
+// H [rows][3 Fq].
+__global__ void hidden_planes3_kernel(const float* __restrict__ gu, int64_t rows, int Fq, int etype,
+                                      int act, float slope, uint16_t* __restrict__ h3) {
+  const bool glu = etype != MXM_EXPERT_MLP;
+  const int NC = glu ? 2 * Fq : Fq;
+  const int64_t n = rows * Fq;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / Fq;
+    const int f = (int)(i - r * Fq);
+    const float* row = gu + (size_t)r * NC;
+    const int qg = (f >> 5) * 64 + (f & 31);
+    const float g = glu ? row[qg] : 0.0f, u = glu ? row[qg + 32] : row[f];
+    float h, cg, cu;
+    act_eval(etype, act, slope, g, u, h, cg, cu);
+    uint16_t hi, lo;
+    split_bf16(h, hi, lo);
+    uint16_t* d = h3 + (size_t)r * 3 * Fq + f;
+    d[0] = hi;
+    d[Fq] = hi;
+    d[2 * (size_t)Fq] = lo;
+  }
+}
+
+// The activation backward: from gu (as above) and dh [rows][Fq] fp32, dG and
+// dU as the HLH planes of dGU [rows][3 NC] in gu's column order.
+__global__ void act_bw_planes3_kernel(const float* __restrict__ gu, const float* __restrict__ dh,
+                                      int64_t rows, int Fq, int etype, int act, float slope,
+                                      uint16_t* __restrict__ dgu3) {
+  const bool glu = etype != MXM_EXPERT_MLP;
+  const int NC = glu ? 2 * Fq : Fq;
+  const int64_t n = rows * Fq;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / Fq;
+    const int f = (int)(i - r * Fq);
+    const float* row = gu + (size_t)r * NC;
+    const int qg = (f >> 5) * 64 + (f & 31);
+    const float g = glu ? row[qg] : 0.0f, u = glu ? row[qg + 32] : row[f];
+    float h, cg, cu;
+    act_eval(etype, act, slope, g, u, h, cg, cu);
+    const float d = dh[(size_t)r * Fq + f];
+    uint16_t* base = dgu3 + (size_t)r * 3 * NC;
+    auto put = [&](int q, float v) {
+      uint16_t hi, lo;
+      split_bf16(v, hi, lo);
+      base[q] = hi;
+      base[NC + q] = lo;
+      base[2 * NC + q] = hi;
+    };
+    if (glu) {
+      put(qg, d * cg);
+      put(qg + 32, d * cu);
+    } else {
+      put(f, d * cu);
+    }
+  }
+}
+
+// dx[n] = dxr[n] + sum_k dxe[slot_pos[n, k]] (k ascending; dxe rows ld apart).
+__global__ void dx_sum_kernel(const float* __restrict__ dxr, const float* __restrict__ dxe, int ld,
+                              const int32_t* __restrict__ slot_pos, int D, int K,
+                              float* __restrict__ dx) {
+  const int n = blockIdx.x;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float acc = dxr[(size_t)n * D + d];
+    for (int k = 0; k < K; ++k) acc = acc + dxe[(size_t)slot_pos[(size_t)n * K + k] * ld + d];
+    dx[(size_t)n * D + d] = acc;
+  }
+}
+
 }  // namespace
 
 int wgrad_router_chunks(int N, int D, int E) { return wgrad_router_chunks_impl(N, D, E); }
@@ -1037,23 +1145,51 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
 
 // The fp32 experts' elementwise parts; their products are per-expert rocBLAS
 // GEMMs issued by the library's host code.
-void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s) {
-  const int NK = a.N * a.K;
-  if (NK > 0) hipLaunchKernelGGL(gather_rows_kernel, dim3(NK), dim3(256), 0, s, a.x, a.perm, a.D, a.xp);
+void mxm_launch_planes3(const float* src, int64_t rows, int cols, int lds, int ldq, bool hlh,
+                        uint16_t* dst, hipStream_t s) {
+  const int64_t n = rows * ldq;
+  if (n > 0)
+    hipLaunchKernelGGL(planes3_kernel, dim3(grid_of((size_t)n)), dim3(256), 0, s, src, rows, cols,
+                       lds, ldq, hlh ? 1 : 0, dst);
 }
 
-void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s) {
-  const size_t total = (size_t)a.N * a.K * a.F;
-  if (total > 0)
-    hipLaunchKernelGGL(act_bw_kernel, dim3(grid_of(total)), dim3(256), 0, s, a, total);
+void mxm_launch_planes3_weights(const float* w1, const float* w1b, const float* w2, int E, int D,
+                                int F, int Dq, int Fq, bool glu, uint16_t* w1p, uint16_t* w1t,
+                                uint16_t* w2p, uint16_t* w2t, hipStream_t s) {
+  const int NCq = glu ? 2 * Fq : Fq;
+  const int64_t DF = (int64_t)D * F;
+  auto go = [&](Planes3W a) {
+    const int64_t n = (int64_t)a.E * a.R * a.Kq;
+    if (n > 0) hipLaunchKernelGGL(planes3_w_kernel, dim3(grid_of((size_t)n)), dim3(256), 0, s, a);
+  };
+  // up projections: B of G|U = X W1 is [NCq][3 Dq] HLH (row = column of W1)
+  go(Planes3W{w1, glu ? w1b : nullptr, E, NCq, Dq, F, D, glu ? 1 : 0, 0, 1, F, DF, 1, w1p});
+  // B of dX = dGU W1^T is [Dq][3 NCq] HHL (row = d, k = column of W1)
+  go(Planes3W{w1, glu ? w1b : nullptr, E, Dq, NCq, D, F, 0, glu ? 1 : 0, F, 1, DF, 0, w1t});
+  // down projection W2 [F][D]: B of Y = H W2 is [Dq][3 Fq] HLH (row = d, k = f)
+  go(Planes3W{w2, nullptr, E, Dq, Fq, D, F, 0, 0, 1, D, DF, 1, w2p});
+  // B of dH = dY W2^T is [Fq][3 Dq] HHL (row = f, k = d)
+  go(Planes3W{w2, nullptr, E, Fq, Dq, F, D, 0, 0, D, 1, DF, 0, w2t});
 }
 
-void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s) {
-  const size_t total = (size_t)a.N * a.K * a.F;
-  if (total > 0)
-    hipLaunchKernelGGL(hidden_kernel, dim3(grid_of(total)), dim3(256), 0, s, a, total);
+void mxm_launch_hidden_planes3(const float* gu, int64_t rows, int Fq, int etype, int act,
+                               float slope, uint16_t* h3, hipStream_t s) {
+  const int64_t n = rows * Fq;
+  if (n > 0)
+    hipLaunchKernelGGL(hidden_planes3_kernel, dim3(grid_of((size_t)n)), dim3(256), 0, s, gu, rows,
+                       Fq, etype, act, slope, h3);
 }
 
-void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s) {
-  if (a.N > 0) hipLaunchKernelGGL(dx_kernel, dim3(a.N), dim3(256), 0, s, a);
+void mxm_launch_act_bw_planes3(const float* gu, const float* dh, int64_t rows, int Fq, int etype,
+                               int act, float slope, uint16_t* dgu3, hipStream_t s) {
+  const int64_t n = rows * Fq;
+  if (n > 0)
+    hipLaunchKernelGGL(act_bw_planes3_kernel, dim3(grid_of((size_t)n)), dim3(256), 0, s, gu, dh,
+                       rows, Fq, etype, act, slope, dgu3);
+}
+
+void mxm_launch_dx_sum(const float* dxr, const float* dxe, int ld, const int32_t* slot_pos, int N,
+                       int D, int K, float* dx, hipStream_t s) {
+  if (N > 0)
+    hipLaunchKernelGGL(dx_sum_kernel, dim3(N), dim3(256), 0, s, dxr, dxe, ld, slot_pos, D, K, dx);
 }

@@ -420,7 +420,7 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #undef MXM_COMPUTE
 #undef MXM_KSTEP
 
-  if constexpr (DOWN_SPLIT) {
+  if constexpr (Epi<EPI>::Y_F32) {
     // y in fp32, straight from the accumulators: register r of lane l holds
     // C[(r/4)*8 + (l/32)*4 + r%4][l%32], so each store instruction writes
     // 32 consecutive floats of two rows
@@ -681,6 +681,8 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
   if (a.mode == MXM_GEMM_DOWN) {
     if (a.h_split)
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN_F32>(a, s, blocks, ngroups);
+    else if (a.f32_out)
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_F32>(a, s, blocks, ngroups);
     else
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN>(a, s, blocks, ngroups);
     return;

@@ -170,6 +170,10 @@ struct GemmArgs {
   bool a_off32;
   // ... unless the caller forbids it (64-bit addressing throughout)
   bool no_off32;
+  // MFMA mode 2 (MXM_GEMM_DOWN): store the fp32 accumulators as they are,
+  // out [rows][Ncols] fp32 (the products of the fp32 backward, each an
+  // A . B^T over bf16 planes concatenated along k)
+  bool f32_out;
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
@@ -184,7 +188,7 @@ enum { MXM_TILE_AUTO = 0, MXM_TILE_128x128 = 1, MXM_TILE_256x128 = 2, MXM_TILE_2
 int mxm_mfma_tile_rows(int Ncols, int Kd, int family);
 
 // Weight gradients on MFMA (mxm_wgrad.hip): per expert e,
-//   out[e][m][c] = sum_p sum_k A[k][p * aplane + m] * B[k][c]   (fp32)
+//   out[e][m][c] = sum_p sum_k A[k][p * aplane + m] * B[k][p * bplane + c]   (fp32)
 // over rows k = offsets[e] .. offsets[e+1]-1 and planes p < planes.  With
 // glu_f > 0 the C columns are GLU-interleaved in groups of 32 (gate, up) and
 // land de-interleaved: column c -> out[e] + ((c/32) % 2) * out_slot +
@@ -194,6 +198,7 @@ struct WgradArgs {
   int lda, aplane, planes;
   const uint16_t* b;        // bf16 [rows][ldb]
   int ldb;
+  int bplane;               // B's columns of plane p start at p * bplane (0: B is shared)
   const int32_t* offsets;   // [E + 1]
   const uint16_t* zero;     // 256 zero bf16 (rows past an expert's end)
   int E, M, C;
@@ -222,7 +227,7 @@ int mxm_simt_bm();
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
 // projections, or the plain bf16 store of the down projection.
 enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_LEAKY, EPI_DOWN,
-       EPI_DOWN_F32 };
+       EPI_DOWN_F32, EPI_F32 };
 
 // EPI_KEEP + an up-projection kind: the raw bf16 projections to
 // GemmArgs::out2 instead of the hidden (the MFMA backward derives H from
@@ -233,13 +238,17 @@ template <int EPI_>
 struct Epi {
   static constexpr int EPI = EPI_ % EPI_KEEP;
   static constexpr bool KEEP_RAW = EPI_ >= EPI_KEEP;
-  static constexpr int MODE = EPI <= EPI_GEGLU                         ? MXM_GEMM_GLU
-                              : (EPI == EPI_DOWN || EPI == EPI_DOWN_F32) ? MXM_GEMM_DOWN
-                                                                        : MXM_GEMM_MLP;
+  static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
+                              : (EPI == EPI_DOWN || EPI == EPI_DOWN_F32 || EPI == EPI_F32)
+                                  ? MXM_GEMM_DOWN
+                                  : MXM_GEMM_MLP;
   // up projections whose hidden is fp32 in the bf16 flow: H in two planes
   static constexpr bool H_SPLIT = EPI == EPI_GEGLU || EPI == EPI_MLP_GELU || EPI == EPI_MLP_LEAKY;
   // down projection over the two planes, y stored in fp32
   static constexpr bool DOWN_SPLIT = EPI == EPI_DOWN_F32;
+  // the accumulators stored in fp32 (the split down projection's y, or a
+  // plain product: GemmArgs::f32_out)
+  static constexpr bool Y_F32 = EPI == EPI_DOWN_F32 || EPI == EPI_F32;
   static constexpr int ETYPE = EPI == EPI_SWIGLU ? MXM_EXPERT_SWIGLU
                                : EPI == EPI_GEGLU ? MXM_EXPERT_GEGLU
                                                   : MXM_EXPERT_MLP;
@@ -370,7 +379,7 @@ struct BackwardArgs {
   const float* d_delta;      // [N, D]
   float d_aux, d_ent;
   // scratch
-  float *xp, *g, *u, *h, *dy, *dh, *dg, *du, *dxg, *dxu;  // [N*K, D or F]
+  float* dy;                 // [N*K, D]: dY = gate * dD by slot position
   const float* dgp;          // [N*K] gate gradients by slot position (set: the caller computed
                              // them; dgates is then not used)
   float *dgates, *dlogits, *dxr;                          // [N*K], [N, E], [N, D] (dxr unset:
@@ -390,15 +399,6 @@ struct BackwardArgs {
 int wgrad_router_chunks(int N, int D, int E);
 // The router part: gate/router gradients, dY, dx's router term and d router_w.
 void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s);
-// The fp32 experts' elementwise parts around their products (which the host
-// issues as per-expert GEMMs): xp = x gathered by perm; dg, du and h from
-// g, u, dh (the activation's derivative, h recomputed); dx = dxr + the
-// experts' input gradients summed over each token's slots, k ascending.
-void mxm_launch_backward_gather(const BackwardArgs& a, hipStream_t s);
-void mxm_launch_backward_act(const BackwardArgs& a, hipStream_t s);
-// h from g, u alone (the expert forward of an fp32 backward)
-void mxm_launch_backward_hidden(const BackwardArgs& a, hipStream_t s);
-void mxm_launch_backward_dx(const BackwardArgs& a, hipStream_t s);
 // bf16 flow on the MFMA family (products by the MFMA grouped GEMM, weight
 // gradients by mxm_launch_wgrad): dx from bf16 expert input gradients.
 void mxm_launch_dx_bf16(const float* dxr, const uint16_t* dxe, const int32_t* slot_pos, int N,
@@ -438,3 +438,29 @@ void mxm_launch_act_bw_gated_bf16(const uint16_t* gu, const uint16_t* dhr, uint1
                                   float slope, uint16_t* dgu, float* dgp, hipStream_t s);
 // Row-tile prefix of counts for tile height bm (mstart[0..E]).
 void mxm_launch_tile_prefix(const int32_t* counts, int E, int bm, int32_t* mstart, hipStream_t s);
+
+// fp32 products on the bf16 MFMA kernels (the fp32 backward): fp32 values
+// as bf16 planes hi = bf16(v), lo = bf16(v - hi), concatenated along k as
+// HHL = [hi | hi | lo] (A side) or HLH = [hi | lo | hi] (B side), so that one
+// bf16 product gives hi.hi + hi.lo + lo.hi.
+// dst [rows][3 ldq]: the planes of src [rows][cols] (row stride lds), zero
+// for cols <= c < ldq.
+void mxm_launch_planes3(const float* src, int64_t rows, int cols, int lds, int ldq, bool hlh,
+                        uint16_t* dst, hipStream_t s);
+// The four B operands of the experts' products from fp32 x.W weights (w1 /
+// w1b [E][D][F], w2 [E][F][D]), padded to Dq x Fq (NCq = 2 Fq for GLU, GLU
+// columns interleaved in groups of 32): w1p [E][NCq][3 Dq] (HLH) for
+// G|U = X W1, w1t [E][Dq][3 NCq] (HHL) for dX = dGU W1^T, w2p [E][Dq][3 Fq]
+// (HLH) for Y = H W2, w2t [E][Fq][3 Dq] (HHL) for dH = dY W2^T.
+void mxm_launch_planes3_weights(const float* w1, const float* w1b, const float* w2, int E, int D,
+                                int F, int Dq, int Fq, bool glu, uint16_t* w1p, uint16_t* w1t,
+                                uint16_t* w2p, uint16_t* w2t, hipStream_t s);
+// H [rows][3 Fq] (HHL) from the raw fp32 projections gu [rows][NC].
+void mxm_launch_hidden_planes3(const float* gu, int64_t rows, int Fq, int etype, int act,
+                               float slope, uint16_t* h3, hipStream_t s);
+// dGU [rows][3 NC] (HLH) from gu and dH [rows][Fq] fp32.
+void mxm_launch_act_bw_planes3(const float* gu, const float* dh, int64_t rows, int Fq, int etype,
+                               int act, float slope, uint16_t* dgu3, hipStream_t s);
+// dx[n] = dxr[n] + sum_k dxe[slot_pos[n, k]] (dxe rows ld apart).
+void mxm_launch_dx_sum(const float* dxr, const float* dxe, int ld, const int32_t* slot_pos, int N,
+                       int D, int K, float* dx, hipStream_t s);

@@ -453,7 +453,7 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
       if (kk + BK <= cnt) {
         // a whole stage of rows
         const uint16_t* as = A + (size_t)(row0 + kk) * a.lda + (size_t)p * a.aplane;
-        const uint16_t* bs = B + (size_t)(row0 + kk) * a.ldb;
+        const uint16_t* bs = B + (size_t)(row0 + kk) * a.ldb + (size_t)p * a.bplane;
         auto whole = [&](auto off32) {
 #pragma unroll
           for (int q = 0; q < LDPS; ++q) {
@@ -474,10 +474,11 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
             } else {
               const int qb = q - QA;
               if constexpr (GB && decltype(off32)::value) {
-                wg_dma16s(B, pick_off(srowb[qb], rb, rpwb, b_pitch, b_colb),
+                wg_dma16s(B + (size_t)p * a.bplane, pick_off(srowb[qb], rb, rpwb, b_pitch, b_colb),
                           st + A_BYTES + (wv + NW * qb) * 1024);
               } else if constexpr (GB) {
-                wg_dma16(B + (size_t)pick(srowb[qb], rb, rpwb) * a.ldb + c0 + lcb * 8,
+                wg_dma16(B + (size_t)pick(srowb[qb], rb, rpwb) * a.ldb + (size_t)p * a.bplane + c0 +
+                             lcb * 8,
                          st + A_BYTES + (wv + NW * qb) * 1024);
               } else {
                 wg_dma16s(bs, 2u * (unsigned)b_lane[qb], st + A_BYTES + (wv + NW * qb) * 1024);
@@ -504,8 +505,9 @@ __global__ __launch_bounds__(TL::NT, 1) void wgrad_kernel(WgradArgs a) {
             const int k = kk + (wv + NW * qb) * RPWB + rb;
             int brw = row0 + k;
             if constexpr (GB) brw = pick(srowb[qb], rb, rpwb);
-            const uint16_t* src =
-                k < cnt ? B + (size_t)brw * a.ldb + c0 + lcb * 8 : a.zero + lcb * 8;
+            const uint16_t* src = k < cnt ? B + (size_t)brw * a.ldb + (size_t)p * a.bplane + c0 +
+                                                lcb * 8
+                                          : a.zero + lcb * 8;
             wg_dma16(src, st + A_BYTES + (wv + NW * qb) * 1024);
           }
         }
