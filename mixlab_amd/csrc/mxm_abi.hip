@@ -180,6 +180,14 @@ struct MoeOp {
   bool ws_ready = false, have_last = false;
   DevBuf wsbuf;
   Workspace ws, last;
+  // the last forward took the int8 decode flow: its dispatch (counts,
+  // offsets, perm, slot_pos) is computed when the routing is queried, from
+  // its per-token results and the probabilities at last_probs
+  bool last_decode = false;
+  float* last_probs = nullptr;
+  // the int8 decode flow (1, default) or the dispatch of the one-launch
+  // router (0): MXM_DECODE_FLOW at creation, for measurements of the two
+  bool decode_flow = true;
   DevBuf xn, blk_scales;  // block level: normalised rows; host-call copies of the scales
   DevBuf bw_probs;        // the backward's forward keeps its probabilities here
   // backward (fp32 flow): the experts' projections, gradients and scratch
@@ -390,6 +398,13 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   o.last = w;
   o.have_last = true;
   o.kept = false;  // every forward overwrites what a kept one left
+  // int8 weights at decode sizes: the router writes only the per-token
+  // results; the expert kernels find their rows from the top-k picks, the
+  // down projection stores y token-major and the combine computes aux and
+  // entropy, so no launch waits for a dispatch (mxm_moe_routing computes it
+  // on demand)
+  const bool decode_flow = o.q8 && o.small_route && o.decode_flow;
+  o.last_decode = decode_flow;
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
     mxm_launch_to_bf16(x, MXM_DTYPE_F32, static_cast<uint16_t*>(w.xcast), (int64_t)o.N * o.D, st);
@@ -453,6 +468,8 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     rs.aux_weight = blk ? blk->aux_weight : 1.0f;
     rs.aux_scaled = blk ? blk->aux_scaled : nullptr;
     rs.ticket = w.ticket;
+    rs.dispatch = !decode_flow;
+    o.last_probs = rs.probs;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_route_small(rs, o.bf16, st);
     HIPCK(hipGetLastError());
     mark(1);
@@ -544,6 +561,25 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     g1.b1 = o.q1b.p;
     g1.scale0 = o.s1.as<float>();
     g1.scale1 = o.s1b.as<float>();
+    if (decode_flow) {
+      g1.top_idx = w.top_idx;
+      g1.topk = o.K;
+      g1.tk_offsets = w.offsets;
+      g1.tk_counts = w.counts;
+      g1.tk_ypos = w.slot_rank;
+      // aux and entropy in one more workgroup of this launch
+      g1.daux.top_idx = w.top_idx;
+      g1.daux.probs = o.last_probs;
+      g1.daux.tok_ent = w.tok_ent;
+      g1.daux.N = o.N;
+      g1.daux.E = o.E;
+      g1.daux.K = o.K;
+      g1.daux.bf16 = o.bf16;
+      g1.daux.aux = aux_p;
+      g1.daux.entropy = ent_p;
+      g1.daux.aux_weight = blk ? blk->aux_weight : 1.0f;
+      g1.daux.aux_scaled = blk ? blk->aux_scaled : nullptr;
+    }
     require_operands(g1, glu, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
   } else if (o.mfma) {
@@ -584,6 +620,13 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   if (o.q8) {
     g2.b0 = o.q2.p;
     g2.scale0 = o.s2.as<float>();
+    if (decode_flow) {
+      // the rows the up projection handed on (offsets, counts, y rows)
+      g2.top_idx = w.top_idx;
+      g2.topk = o.K;
+      g2.tk_counts = w.counts;
+      g2.tk_ypos = w.slot_rank;
+    }
     require_operands(g2, false, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g2, st);
   } else if (o.mfma) {
@@ -612,7 +655,12 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     ca.rscale = blk->moe_scale;
     ca.rscale_bf16 = blk->scale_bf16;
   }
-  for (int rep = 0; rep < reps; ++rep) mxm_launch_combine(ca, (o.mfma || o.q8) && !o.hsplit, st);
+  if (decode_flow) {
+    for (int rep = 0; rep < reps; ++rep) mxm_launch_combine_tm(ca, !o.hsplit, st);
+  } else {
+    for (int rep = 0; rep < reps; ++rep)
+      mxm_launch_combine(ca, (o.mfma || o.q8) && !o.hsplit, st);
+  }
   HIPCK(hipGetLastError());
   mark(6);
 }
@@ -879,6 +927,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     auto o = std::make_unique<MoeOp>();
     if (const char* v = std::getenv("MXM_ROUTER_WGRAD_MFMA")) o->dwr_mode = std::atoi(v) != 0;
     if (const char* v = std::getenv("MXM_FORCE_64BIT_OFFSETS")) o->force64 = std::atoi(v) != 0;
+    if (const char* v = std::getenv("MXM_DECODE_FLOW")) o->decode_flow = std::atoi(v) != 0;
     o->B = int_params[0];
     o->T = int_params[1];
     o->D = int_params[2];
@@ -1828,6 +1877,33 @@ int mxm_moe_routing(int64_t h, int32_t* top_idx, float* gates, int32_t* counts, 
     const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
     const size_t NK = (size_t)op->N * op->K;
     const Workspace& w = op->last;
+    if (op->last_decode) {
+      // the decode flow's dispatch, from the last forward's per-token results
+      // (its aux and entropy go to the workspace's own slots)
+      RouteSmallArgs rs{};
+      rs.N = op->N;
+      rs.D = op->D;
+      rs.E = op->E;
+      rs.K = op->K;
+      rs.bm1 = op->bm1;
+      rs.bm2 = op->bm2;
+      rs.top_idx = w.top_idx;
+      rs.gates = w.gates;
+      rs.probs = op->last_probs;
+      rs.tok_ent = w.tok_ent;
+      rs.counts = w.counts;
+      rs.offsets = w.offsets;
+      rs.mstart1 = w.mstart1;
+      rs.mstart2 = w.mstart2;
+      rs.perm = w.perm;
+      rs.slot_pos = w.slot_pos;
+      rs.aux = w.aux;
+      rs.entropy = w.ent;
+      rs.aux_weight = 1.0f;
+      rs.dispatch = true;
+      mxm_launch_route_dispatch(rs, op->bf16, op->stream);
+      HIPCK(hipGetLastError());
+    }
     auto cp = [&](void* dst, const void* src, size_t bytes) {
       if (dst) HIPCK(hipMemcpyAsync(dst, src, bytes, kind, op->stream));
     };

@@ -72,9 +72,63 @@ __device__ __forceinline__ int clamp_kb(int kb, int kblocks) {
   return kb < kblocks ? kb : kblocks - 1;
 }
 
+// aux and entropy of a decode batch from its per-token results, in the
+// order of the one-launch router's dispatch: the probabilities of expert e
+// summed in 16 strided token subsets (t = w, w + 16, ...), the subsets then
+// added in order; aux over the experts lane-wise, then an xor butterfly; the
+// entropy terms lane-strided, then a butterfly.  NW waves; `scratch` holds
+// at least (MXM_MAX_EXPERTS * 17) words of LDS.
+__device__ void decode_aux(const DecodeAux& a, void* scratch) {
+  constexpr int SUBSETS = 16;
+  int* cnt = static_cast<int*>(scratch);
+  float* part = reinterpret_cast<float*>(cnt + MXM_MAX_EXPERTS);  // [SUBSETS][MXM_MAX_EXPERTS]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = a.N, E = a.E, K = a.K, NK = N * K;
+  for (int e = tid; e < E; e += NW * 64) cnt[e] = 0;
+  __syncthreads();
+  for (int sl = tid; sl < NK; sl += NW * 64) atomicAdd(&cnt[a.top_idx[sl]], 1);
+  for (int w = wave; w < SUBSETS; w += NW) {
+    for (int e = lane; e < E; e += 64) {
+      float ps = 0.0f;
+      for (int t = w; t < N; t += SUBSETS) ps = ps + a.probs[(size_t)t * E + e];
+      part[w * MXM_MAX_EXPERTS + e] = ps;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float aux = 0.0f;
+    for (int e = lane; e < E; e += 64) {
+      float pm = 0.0f;
+      for (int w = 0; w < SUBSETS; ++w) pm = pm + part[w * MXM_MAX_EXPERTS + e];
+      const float mean = pm / (float)N;
+      const float frac = ((float)cnt[e] / (float)K) / (float)N;
+      aux = aux + (a.bf16 ? mxm_rbf(mean) : mean) * frac;
+    }
+    for (int s = 32; s >= 1; s >>= 1) aux = aux + __shfl_xor(aux, s, 64);
+    if (lane == 0) {
+      const float raw = aux * (float)E;
+      a.aux[0] = raw;
+      if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
+    }
+  } else if (wave == 1) {
+    float es = 0.0f;
+    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
+    for (int s = 32; s >= 1; s >>= 1) es = es + __shfl_xor(es, s, 64);
+    if (lane == 0) a.entropy[0] = -(es / (float)N);
+  }
+}
+
 // P: weight blocks in flight per matrix per wave.  RG: groups of 16 rows per
 // pass (each weight block, converted once, feeds RG MFMA row groups).
-template <int EPI, int P, int RG>
+// TOPK (decode batches, GemmArgs::top_idx): the up projection's workgroups
+// find their expert's rows themselves from the top-k picks -- the slots on
+// the expert, tokens ascending (the stable permutation's order), at offset =
+// the number of slots on lower experts -- so they do not wait for a
+// dispatch; the expert's first workgroup hands the offset, the count and
+// each row's token-major y row (n * K + j, j the expert's place among the
+// token's experts in ascending order) to the down projection, which reads
+// them as the dispatch's offsets would be read and stores y token-major.
+template <int EPI, int P, int RG, bool TOPK>
 __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // up: store H as hi | lo planes
@@ -87,14 +141,35 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   // A rows of the current pass, per row group: [kb][half][lane] 16-byte
   // pieces; lane 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
   __shared__ u32x4_t ash[RG * ASZ];
+  // TOPK: the expert's rows (their tokens) and, for the down projection,
+  // each row's token-major y row
+  constexpr bool SCAN = TOPK && MODE != MXM_GEMM_DOWN;  // rows from the picks
+  __shared__ int s_tok[SCAN ? MXM_SMALL_BATCH : 1];
+  __shared__ int s_ypos[TOPK ? MXM_SMALL_BATCH : 1];
+  __shared__ int s_wc[NW], s_wl[NW];
+  static_assert((int)sizeof(ash) >= MXM_MAX_EXPERTS * 17 * 4, "decode_aux scratch");
 
+  if (TOPK && a.daux.aux && (int)blockIdx.x == a.E * groups_per_expert) {
+    decode_aux(a.daux, ash);  // the launch's extra workgroup
+    return;
+  }
   const int e = blockIdx.x / groups_per_expert;
   const int grp = blockIdx.x % groups_per_expert;
-  const int row_begin = a.offsets[e];
-  const int count = a.offsets[e + 1] - row_begin;
-  if (count <= 0) return;
-
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int row_begin = 0, count = 0;
+  int tk0 = -1;  // SCAN: this thread's first slot, requested before the weights
+  if constexpr (SCAN) {
+    if (tid < a.rows_total) tk0 = a.top_idx[tid];
+  } else if constexpr (TOPK) {
+    // the up projection's handoff
+    row_begin = a.offsets[e];
+    count = a.tk_counts[e];
+    if (count <= 0) return;
+  } else {
+    row_begin = a.offsets[e];
+    count = a.offsets[e + 1] - row_begin;
+    if (count <= 0) return;
+  }
   const int Kd = a.Kd, NC = a.Ncols;  // NC: output columns per matrix
   const int kblocks = Kd / 64;
   const size_t kstride = (size_t)NC * 64;  // bytes between k blocks of one column block
@@ -131,8 +206,78 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         wb[s][mt] = MXM_WLD(W[mt] + (size_t)clamp_kb(s, kblocks) * kstride);
   };
   // the first blocks of the weight stream are requested before the rows are
-  // staged, so HBM is busy from the workgroup's start
-  if (active) prologue();
+  // staged, so HBM is busy from the workgroup's start (TOPK: when most experts
+  // have rows, i.e. at least two slots per expert on average; else after the
+  // expert's row count is known, so that experts without rows read nothing)
+  const bool early = !SCAN || a.rows_total >= 2 * a.E;
+  if (early && active) prologue();
+  if constexpr (TOPK && !SCAN) {
+    for (int i = tid; i < count; i += NW * 64) s_ypos[i] = a.tk_ypos[row_begin + i];
+    // (ordered before the epilogue by the staging barriers)
+  }
+  if constexpr (SCAN) {
+    // the slots on expert e, in slot order (= tokens ascending: a token's
+    // picks are distinct), by wave ballots; `less` counts the slots on lower
+    // experts
+    const int NK = a.rows_total, Kt = a.topk;
+    int less = 0, base = 0;
+    for (int c0 = 0; c0 < NK; c0 += NW * 64) {
+      const int sl = c0 + tid;
+      const int ex = c0 == 0 ? tk0 : (sl < NK ? a.top_idx[sl] : -1);
+      const bool lower = ex >= 0 && ex < e;
+      less += lower ? 1 : 0;
+      const bool hit = ex == e;
+      const unsigned long long bal = __ballot(hit);
+      // the down projection's y row n * K + j, j = the token's picks below e:
+      // when K divides 64 a token's K slots are lanes of one wave
+      const unsigned long long low = __ballot(lower);
+      if (lane == 0) s_wc[wave] = __popcll(bal);
+      __syncthreads();
+      int before = 0, tot = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int v = s_wc[w];
+        before += w < wave ? v : 0;
+        tot += v;
+      }
+      if (hit) {
+        const int r = base + before + __popcll(bal & ((1ull << lane) - 1ull));
+        const int n = sl / Kt;
+        s_tok[r] = n;
+        if (grp == 0) {  // (the expert's first workgroup hands the y rows on)
+          int j = 0;
+          if (64 % Kt == 0) {
+            const int l0 = lane - sl % Kt;  // the token's first slot's lane
+            const unsigned long long tm = Kt == 64 ? ~0ull : ((1ull << Kt) - 1ull) << l0;
+            j = __popcll(low & tm);
+          } else {
+            for (int k = 0; k < Kt; ++k) j += a.top_idx[(size_t)n * Kt + k] < e ? 1 : 0;
+          }
+          s_ypos[r] = n * Kt + j;
+        }
+      }
+      base += tot;
+      __syncthreads();  // s_wc is reused
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) less += __shfl_xor(less, sh, 64);
+    if (lane == 0) s_wl[wave] = less;
+    __syncthreads();
+    row_begin = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) row_begin += s_wl[w];
+    count = base;
+    if (grp == 0) {
+      // the handoff to the down projection (read after this launch ends)
+      if (tid == 0) {
+        a.tk_offsets[e] = row_begin;
+        a.tk_counts[e] = count;
+      }
+      for (int i = tid; i < count; i += NW * 64) a.tk_ypos[row_begin + i] = s_ypos[i];
+    }
+    if (count <= 0) return;
+    if (!early && active) prologue();
+  }
 
   for (int rc = 0; rc < count; rc += ROWS_PER_PASS) {
     if (active && rc > 0) prologue();
@@ -157,7 +302,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
       if (rc + rr < count) {
         const int p = row_begin + rc + rr;
-        const int src = (MODE == MXM_GEMM_DOWN) ? p : a.perm[p];
+        const int src = (MODE == MXM_GEMM_DOWN) ? p : TOPK ? s_tok[rc + rr] : a.perm[p];
         v = *reinterpret_cast<const u32x4_t*>(X + (size_t)src * ldx + col0 + 8 * c8);
       }
       ash[(r >> 4) * ASZ + ((c8 >> 3) * 2 + (c8 & 1)) * 64 + ((c8 >> 1) & 3) * 16 + (r & 15)] = v;
@@ -219,7 +364,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         if (r >= count) continue;
         const float hi = acc[0][0][i] - 128.0f * rs[0][i];
         const float lo = acc[1][0][i] - 128.0f * rs[1][i];
-        static_cast<float*>(a.out)[(size_t)(row_begin + r) * NC + c] = (hi + lo) * sc[0];
+        const int yr = TOPK ? s_ypos[r] : row_begin + r;
+        static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0];
       }
       continue;
     }
@@ -248,7 +394,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         H[o] = mxm_f2bf_fast(hi);
         H[o + NC] = mxm_f2bf_fast(out - hi);
       } else {
-        H[(size_t)(row_begin + r) * NC + c] = mxm_f2bf_fast(out);
+        // (the down projection's y: token-major rows in the TOPK flow)
+        const int yr = (TOPK && MODE == MXM_GEMM_DOWN) ? s_ypos[r] : row_begin + r;
+        H[(size_t)yr * NC + c] = mxm_f2bf_fast(out);
       }
     }
   }
@@ -258,9 +406,13 @@ template <int EPI, int P, int RG>
 void launch_q8(const GemmArgs& a, hipStream_t s) {
   const int ncb = a.Ncols / 16;
   const int gpe = (ncb + NW - 1) / NW;
-  hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG>), dim3(a.E * gpe), dim3(NW * 64), 0, s, a, gpe);
+  if (a.top_idx)
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, true>), dim3(a.E * gpe + (a.daux.aux ? 1 : 0)),
+                       dim3(NW * 64), 0, s, a, gpe);
+  else
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, false>), dim3(a.E * gpe), dim3(NW * 64), 0, s,
+                       a, gpe);
 }
-
 template <int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s) {
   constexpr bool two = Epi<EPI>::MODE == MXM_GEMM_GLU;

@@ -279,6 +279,129 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   }
 }
 
+
+// The int8 decode flow's combine: y token-major, so a token's rows are known
+// before its picks are read -- the first KC rows of each thread's first
+// columns are requested first, then the gates are sorted into ascending
+// expert order, then the sum runs multiply then add in fp32 in that order
+// (the reference's e-loop, as combine_kernel).
+template <typename TY, int VEC>
+__global__ __launch_bounds__(256) void combine_tm_kernel(CombineArgs a) {
+  __shared__ int sk[MXM_MAX_EXPERTS];
+  __shared__ float sg[MXM_MAX_EXPERTS];
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int K = a.K;
+  const TY* y = static_cast<const TY*>(a.y);
+  const size_t ldy = a.ldy > 0 ? (size_t)a.ldy : (size_t)a.D;
+  const size_t row0 = (size_t)n * K;
+  constexpr bool WIDE = (sizeof(TY) == 2 && VEC == 8) || (sizeof(TY) == 4 && VEC == 4);
+  typedef typename std::conditional<sizeof(TY) == 2, vu4, vf4>::type raw_t;
+  constexpr int KC = 8;
+  const int d0 = tid * VEC;
+  raw_t pre[KC];
+  if constexpr (WIDE) {
+    if (d0 < a.D) {
+#pragma unroll
+      for (int u = 0; u < KC; ++u)
+        if (u < K) pre[u] = __builtin_nontemporal_load(
+                       reinterpret_cast<const raw_t*>(y + (row0 + u) * ldy + d0));
+    }
+  }
+  int e = 0;
+  float g = 0.0f;
+  if (tid < K) {
+    e = a.top_idx[row0 + tid];
+    g = a.gates[row0 + tid];
+    sk[tid] = e;
+  }
+  __syncthreads();
+  if (tid < K) {
+    int r = 0;
+    for (int j = 0; j < K; ++j) r += sk[j] < e;
+    sg[r] = g;
+  }
+  __syncthreads();
+  auto add_raw = [&](float (&acc)[VEC], const raw_t& v, float gg) {
+    float f[VEC];
+    if constexpr (sizeof(TY) == 2) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = mxm_u2f(v[q] << 16);
+        f[2 * q + 1] = mxm_u2f(v[q] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) f[q] = v[q];
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], gg));
+  };
+  for (int d = d0; d < a.D; d += 256 * VEC) {
+    float acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = 0.0f;
+    if constexpr (WIDE) {
+      for (int k0 = 0; k0 < K; k0 += KC) {
+        const int kn = min(KC, K - k0);
+        raw_t r[KC];
+        if (d == d0 && k0 == 0) {
+#pragma unroll
+          for (int u = 0; u < KC; ++u) r[u] = pre[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < KC; ++u)
+            if (u < kn) r[u] = __builtin_nontemporal_load(
+                            reinterpret_cast<const raw_t*>(y + (row0 + k0 + u) * ldy + d));
+        }
+#pragma unroll
+        for (int u = 0; u < KC; ++u)
+          if (u < kn) add_raw(acc, r[u], sg[k0 + u]);
+      }
+    } else {
+      for (int k = 0; k < K; ++k) {
+        const TY* src = y + (row0 + k) * ldy + d;
+        float f[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          if constexpr (sizeof(TY) == 2)
+            f[q] = mxm_bf2f(reinterpret_cast<const uint16_t*>(src)[q]);
+          else
+            f[q] = reinterpret_cast<const float*>(src)[q];
+        }
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(f[q], sg[k]));
+      }
+    }
+    if (a.resid) {
+      // block level: x + delta (* moe_scale), fp32
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        const size_t i = (size_t)n * a.D + d + q;
+        const float xr = a.resid_bf16 ? mxm_bf2f(static_cast<const uint16_t*>(a.resid)[i])
+                                      : static_cast<const float*>(a.resid)[i];
+        float v = acc[q];
+        if (a.rscale) {
+          const float sc = a.rscale_bf16 ? mxm_bf2f(static_cast<const uint16_t*>(a.rscale)[d + q])
+                                         : static_cast<const float*>(a.rscale)[d + q];
+          v = __fmul_rn(v, sc);
+        }
+        acc[q] = __fadd_rn(xr, v);
+      }
+    }
+    float* dst = a.delta + (size_t)n * a.D + d;
+    if constexpr (VEC == 4 || VEC == 8) {
+#pragma unroll
+      for (int q = 0; q < VEC; q += 4)
+        __builtin_nontemporal_store(vf4{acc[q], acc[q + 1], acc[q + 2], acc[q + 3]},
+                                    reinterpret_cast<vf4*>(dst + q));
+    } else {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) dst[q] = acc[q];
+    }
+  }
+}
+
 }  // namespace
 
 void mxm_launch_scan(const ScanArgs& a, bool bf16, hipStream_t s) {
@@ -309,5 +432,24 @@ void mxm_launch_combine(const CombineArgs& a, bool y_bf16, hipStream_t s) {
       hipLaunchKernelGGL((combine_kernel<float, 4>), dim3(a.N), dim3(256), 0, s, a);
     else
       hipLaunchKernelGGL((combine_kernel<float, 1>), dim3(a.N), dim3(256), 0, s, a);
+  }
+}
+
+void mxm_launch_combine_tm(const CombineArgs& a, bool y_bf16, hipStream_t s) {
+  if (a.N <= 0) return;
+  const int ldy = a.ldy > 0 ? a.ldy : a.D;
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(a.delta) % 16 == 0) && ldy % 8 == 0;
+  const dim3 grid(a.N);
+  if (y_bf16) {
+    if (aligned && a.D % 8 == 0)
+      hipLaunchKernelGGL((combine_tm_kernel<uint16_t, 8>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((combine_tm_kernel<uint16_t, 1>), grid, dim3(256), 0, s, a);
+  } else {
+    if (aligned && a.D % 4 == 0)
+      hipLaunchKernelGGL((combine_tm_kernel<float, 4>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((combine_tm_kernel<float, 1>), grid, dim3(256), 0, s, a);
   }
 }

@@ -94,9 +94,16 @@ struct RouteSmallArgs {
   float aux_weight;
   float* aux_scaled;   // [1] or null
   int32_t* ticket;     // [1], zero between calls (the last workgroup resets it)
+  // false: only the per-token results (top_idx, gates, probs, tok_ent); the
+  // dispatch (counts .. slot_pos, aux, entropy) is left to
+  // mxm_launch_route_dispatch and the int8 decode flow's own kernels
+  bool dispatch;
 };
 bool mxm_route_small_fits(int N, int D, int E, int K);
 void mxm_launch_route_small(const RouteSmallArgs& a, bool bf16, hipStream_t s);
+// The dispatch of route_small_kernel's last workgroup as a launch of its own
+// (one workgroup) from the per-token results already written.
+void mxm_launch_route_dispatch(const RouteSmallArgs& a, bool bf16, hipStream_t s);
 
 struct ScanArgs {
   const int32_t* tile_counts;  // [E, ntiles]
@@ -129,6 +136,20 @@ struct ScatterArgs {
   int32_t* slot_pos;  // [N*K] slot (n, k) -> permuted position
 };
 void mxm_launch_scatter(const ScatterArgs& a, hipStream_t s);
+
+// aux and entropy of a decode batch from its per-token results (the int8
+// decode flow computes them in one more workgroup of its gate+up launch).
+struct DecodeAux {
+  const int32_t* top_idx;  // [N, K]
+  const float* probs;      // [N, E]
+  const float* tok_ent;    // [N] sum_e p log max(p, 1e-12) per token
+  int N, E, K;
+  bool bf16;               // the bf16 flow (the mean probabilities rounded to bf16)
+  float* aux;              // [1]; null: not computed
+  float* entropy;          // [1]
+  float aux_weight;
+  float* aux_scaled;       // [1] or null
+};
 
 // Grouped expert FFN.  mode: 0 = gate+up with GLU epilogue, 1 = up with MLP
 // activation, 2 = down projection.
@@ -174,6 +195,22 @@ struct GemmArgs {
   // out [rows][Ncols] fp32 (the products of the fp32 backward, each an
   // A . B^T over bf16 planes concatenated along k)
   bool f32_out;
+  // int8 family, decode batches (N <= MXM_SMALL_BATCH): if set, the kernels
+  // take each expert's rows from the top-k picks [rows_total = N * topk]
+  // instead of offsets / perm (H at the same offsets as the dispatch's), and
+  // the down projection stores y token-major, row n * topk + j for the j-th
+  // smallest of token n's experts
+  const int32_t* top_idx;
+  int topk;
+  // the up projection's handoff to the down projection in that flow: each
+  // expert's first row (tk_offsets, the down projection reads it as
+  // `offsets`), row count and the token-major y row of each of its rows
+  int32_t* tk_offsets;  // [E]
+  int32_t* tk_counts;   // [E]
+  int32_t* tk_ypos;     // [N * topk]
+  // ... and with daux.aux set, the up projection's launch has one more
+  // workgroup that computes aux and entropy
+  DecodeAux daux;
 };
 // SIMT family: weights in the reference layout (x . W, [in, out]) per expert,
 // fp32 storage; H and Y are fp32.  Accumulation is fmaf in ascending k.
@@ -291,6 +328,9 @@ struct CombineArgs {
   bool rscale_bf16;
 };
 void mxm_launch_combine(const CombineArgs& a, bool y_bf16, hipStream_t s);
+// The int8 decode flow's combine: y token-major (token n's rows n*K ..
+// n*K+K-1 in ascending expert id; slot_pos unused).
+void mxm_launch_combine_tm(const CombineArgs& a, bool y_bf16, hipStream_t s);
 
 // RMSNorm of gpu/ir.cpp:4949-4960 with a fixed summation order: one wave
 // per row; lane l sums x[d]^2 (product rounded, then added) over

@@ -466,6 +466,156 @@ __device__ __forceinline__ float rs_wave_sum(float v) {
   return v;
 }
 
+// The batch's dispatch from its per-token results (top_idx, probs,
+// tok_ent): per-expert counts, offsets and row-tile prefixes, aux and
+// entropy, and the stable permutation.  One workgroup of RS_NT threads; cnt,
+// runc and msk zeroed before the call (ordered by a barrier); sidx holds
+// N * K ints of LDS.
+template <bool BF16, int NJ>
+__device__ __forceinline__ void route_dispatch_body(const RouteSmallArgs& a, int* sidx,
+                                                    float* rs_part, int* cnt, int* offs,
+                                                    int* runc, uint32_t (*msk)[2]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = a.N, E = a.E, K = a.K;
+  // ---- dispatch, aux, entropy (one workgroup) -----------------------------
+  // One round trip reads the batch's results back: each thread's first slots
+  // (top_idx), its wave's tokens' probabilities and, on the last wave, the
+  // entropy terms are loaded together.  Slots go to LDS and straight into the
+  // per-expert counts and, for the first 64 tokens, the expert masks of the
+  // stable permutation.  Probabilities are summed per wave over a fixed token
+  // subset, then over the waves in wave order.
+  const int NK = N * K;
+  constexpr int SV = 4;  // slots per thread loaded in the first pass
+  int sv[SV];
+#pragma unroll
+  for (int q = 0; q < SV; ++q) {
+    const int sl = q * RS_NT + tid;
+    sv[q] = sl < NK ? a.top_idx[sl] : 0;
+  }
+  float ps[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) ps[j] = 0.0f;
+#pragma unroll 4
+  for (int t = wave; t < N; t += RS_WAVES) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) ps[j] = ps[j] + a.probs[(size_t)t * E + e];
+    }
+  }
+  constexpr int ENT_WAVE = RS_WAVES - 1;
+  if (wave == ENT_WAVE) {
+    float es = 0.0f;
+    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
+    es = rs_wave_sum(es);
+    if (lane == 0) a.entropy[0] = -(es / (float)N);
+  }
+  auto take_slot = [&](int sl, int e) {
+    sidx[sl] = e;
+    atomicAdd(&cnt[e], 1);
+    const int t = sl / K;
+    if (t < 64) atomicOr(&msk[e][t >> 5], 1u << (t & 31));
+  };
+#pragma unroll
+  for (int q = 0; q < SV; ++q) {
+    const int sl = q * RS_NT + tid;
+    if (sl < NK) take_slot(sl, sv[q]);
+  }
+  for (int sl = SV * RS_NT + tid; sl < NK; sl += RS_NT) take_slot(sl, a.top_idx[sl]);
+  static_assert(RS_WAVES * MXM_MAX_EXPERTS <= RS_PART_FLOATS, "per-wave probability sums");
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) rs_part[wave * MXM_MAX_EXPERTS + e] = ps[j];
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    // expert e = lane + 64 j: exclusive prefixes of the counts and of the row
+    // tiles of both GEMM families (one wave scan per j), the mean
+    // probabilities and the aux terms
+    int run0 = 0, run1 = 0, run2 = 0;
+    float aux = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + 64 * j;
+      const int c = e < E ? cnt[e] : 0;
+      const int u1 = (c + a.bm1 - 1) / a.bm1, u2 = (c + a.bm2 - 1) / a.bm2;
+      int i0 = c, i1 = u1, i2 = u2;
+#pragma unroll
+      for (int sh = 1; sh < 64; sh <<= 1) {
+        const int v0 = __shfl_up(i0, sh, 64), v1 = __shfl_up(i1, sh, 64), v2 = __shfl_up(i2, sh, 64);
+        if (lane >= sh) {
+          i0 += v0;
+          i1 += v1;
+          i2 += v2;
+        }
+      }
+      if (e < E) {
+        const int o = run0 + i0 - c;
+        offs[e] = o;
+        a.offsets[e] = o;
+        a.counts[e] = c;
+        a.mstart1[e] = run1 + i1 - u1;
+        a.mstart2[e] = run2 + i2 - u2;
+        float pm = 0.0f;
+#pragma unroll
+        for (int w = 0; w < RS_WAVES; ++w) pm = pm + rs_part[w * MXM_MAX_EXPERTS + e];
+        const float mean = pm / (float)N;
+        const float frac = ((float)c / (float)K) / (float)N;
+        aux = aux + (BF16 ? mxm_rbf(mean) : mean) * frac;
+      }
+      run0 += __shfl(i0, 63, 64);
+      run1 += __shfl(i1, 63, 64);
+      run2 += __shfl(i2, 63, 64);
+    }
+    aux = rs_wave_sum(aux);
+    if (lane == 0) {
+      a.offsets[E] = run0;
+      a.mstart1[E] = run1;
+      a.mstart2[E] = run2;
+      const float raw = aux * (float)E;
+      a.aux[0] = raw;
+      if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
+    }
+  }
+  __syncthreads();
+
+  // stable permutation, 64 tokens at a time (chunk 0's masks are built above):
+  // the rank of a slot among the chunk's tokens on its expert from the
+  // expert's 64-bit token mask, plus the running count of earlier chunks
+  for (int c0 = 0; c0 < N; c0 += 64) {
+    const int ct = min(64, N - c0);
+    if (c0 > 0) {
+      for (int e = tid; e < E; e += RS_NT) {
+        msk[e][0] = 0u;
+        msk[e][1] = 0u;
+      }
+      __syncthreads();
+      for (int i = tid; i < ct * K; i += RS_NT) {
+        const int t = i / K;
+        atomicOr(&msk[sidx[c0 * K + i]][t >> 5], 1u << (t & 31));
+      }
+      __syncthreads();
+    }
+    for (int i = tid; i < ct * K; i += RS_NT) {
+      const int t = i / K, sl = c0 * K + i;
+      const int e = sidx[sl];
+      const uint32_t lo = msk[e][0], hi = msk[e][1];
+      const int r = t < 32 ? __popc(lo & ((1u << t) - 1u))
+                           : __popc(lo) + __popc(hi & ((1u << (t - 32)) - 1u));
+      const int pos = offs[e] + runc[e] + r;
+      a.perm[pos] = c0 + t;
+      a.slot_pos[sl] = pos;
+    }
+    if (c0 + 64 < N) {
+      __syncthreads();
+      for (int e = tid; e < E; e += RS_NT) runc[e] += __popc(msk[e][0]) + __popc(msk[e][1]);
+      __syncthreads();
+    }
+  }
+}
+
 template <typename TX, bool BF16, int NJ, bool VEC>
 __global__ __launch_bounds__(RS_NT, 1) void route_small_kernel(RouteSmallArgs a) {
   extern __shared__ __attribute__((aligned(16))) float rs_dyn[];  // x row, then the slots
@@ -621,6 +771,10 @@ __global__ __launch_bounds__(RS_NT, 1) void route_small_kernel(RouteSmallArgs a)
     if (lane == 0) a.tok_ent[n] = ent;
   }
 
+  // the int8 decode flow reads the per-token results directly; its dispatch
+  // runs on demand (mxm_launch_route_dispatch)
+  if (!a.dispatch) return;
+
   // ---- ticket: the last workgroup continues --------------------------------
   // Wave 0 wrote all of this token's results, so it alone releases them; in
   // the last workgroup wave 0 alone acquires the others' (the caches it
@@ -635,144 +789,7 @@ __global__ __launch_bounds__(RS_NT, 1) void route_small_kernel(RouteSmallArgs a)
   if (wave == 0) __threadfence();
   __syncthreads();
 
-  // ---- dispatch, aux, entropy (one workgroup) -----------------------------
-  // One round trip reads the batch's results back: each thread's first slots
-  // (top_idx), its wave's tokens' probabilities and, on the last wave, the
-  // entropy terms are loaded together.  Slots go to LDS and straight into the
-  // per-expert counts and, for the first 64 tokens, the expert masks of the
-  // stable permutation.  Probabilities are summed per wave over a fixed token
-  // subset, then over the waves in wave order.
-  const int NK = N * K;
-  int* sidx = reinterpret_cast<int*>(rs_dyn);  // the x row is no longer needed
-  constexpr int SV = 4;  // slots per thread loaded in the first pass
-  int sv[SV];
-#pragma unroll
-  for (int q = 0; q < SV; ++q) {
-    const int sl = q * RS_NT + tid;
-    sv[q] = sl < NK ? a.top_idx[sl] : 0;
-  }
-  float ps[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) ps[j] = 0.0f;
-#pragma unroll 4
-  for (int t = wave; t < N; t += RS_WAVES) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E) ps[j] = ps[j] + a.probs[(size_t)t * E + e];
-    }
-  }
-  constexpr int ENT_WAVE = RS_WAVES - 1;
-  if (wave == ENT_WAVE) {
-    float es = 0.0f;
-    for (int t = lane; t < N; t += 64) es = es + a.tok_ent[t];
-    es = rs_wave_sum(es);
-    if (lane == 0) a.entropy[0] = -(es / (float)N);
-  }
-  auto take_slot = [&](int sl, int e) {
-    sidx[sl] = e;
-    atomicAdd(&cnt[e], 1);
-    const int t = sl / K;
-    if (t < 64) atomicOr(&msk[e][t >> 5], 1u << (t & 31));
-  };
-#pragma unroll
-  for (int q = 0; q < SV; ++q) {
-    const int sl = q * RS_NT + tid;
-    if (sl < NK) take_slot(sl, sv[q]);
-  }
-  for (int sl = SV * RS_NT + tid; sl < NK; sl += RS_NT) take_slot(sl, a.top_idx[sl]);
-  static_assert(RS_WAVES * MXM_MAX_EXPERTS <= RS_PART_FLOATS, "per-wave probability sums");
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int e = lane + 64 * j;
-    if (e < E) rs_part[wave * MXM_MAX_EXPERTS + e] = ps[j];
-  }
-  __syncthreads();
-
-  if (wave == 0) {
-    // expert e = lane + 64 j: exclusive prefixes of the counts and of the row
-    // tiles of both GEMM families (one wave scan per j), the mean
-    // probabilities and the aux terms
-    int run0 = 0, run1 = 0, run2 = 0;
-    float aux = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int e = lane + 64 * j;
-      const int c = e < E ? cnt[e] : 0;
-      const int u1 = (c + a.bm1 - 1) / a.bm1, u2 = (c + a.bm2 - 1) / a.bm2;
-      int i0 = c, i1 = u1, i2 = u2;
-#pragma unroll
-      for (int sh = 1; sh < 64; sh <<= 1) {
-        const int v0 = __shfl_up(i0, sh, 64), v1 = __shfl_up(i1, sh, 64), v2 = __shfl_up(i2, sh, 64);
-        if (lane >= sh) {
-          i0 += v0;
-          i1 += v1;
-          i2 += v2;
-        }
-      }
-      if (e < E) {
-        const int o = run0 + i0 - c;
-        offs[e] = o;
-        a.offsets[e] = o;
-        a.counts[e] = c;
-        a.mstart1[e] = run1 + i1 - u1;
-        a.mstart2[e] = run2 + i2 - u2;
-        float pm = 0.0f;
-#pragma unroll
-        for (int w = 0; w < RS_WAVES; ++w) pm = pm + rs_part[w * MXM_MAX_EXPERTS + e];
-        const float mean = pm / (float)N;
-        const float frac = ((float)c / (float)K) / (float)N;
-        aux = aux + (BF16 ? mxm_rbf(mean) : mean) * frac;
-      }
-      run0 += __shfl(i0, 63, 64);
-      run1 += __shfl(i1, 63, 64);
-      run2 += __shfl(i2, 63, 64);
-    }
-    aux = rs_wave_sum(aux);
-    if (lane == 0) {
-      a.offsets[E] = run0;
-      a.mstart1[E] = run1;
-      a.mstart2[E] = run2;
-      const float raw = aux * (float)E;
-      a.aux[0] = raw;
-      if (a.aux_scaled) a.aux_scaled[0] = raw * a.aux_weight;
-    }
-  }
-  __syncthreads();
-
-  // stable permutation, 64 tokens at a time (chunk 0's masks are built above):
-  // the rank of a slot among the chunk's tokens on its expert from the
-  // expert's 64-bit token mask, plus the running count of earlier chunks
-  for (int c0 = 0; c0 < N; c0 += 64) {
-    const int ct = min(64, N - c0);
-    if (c0 > 0) {
-      for (int e = tid; e < E; e += RS_NT) {
-        msk[e][0] = 0u;
-        msk[e][1] = 0u;
-      }
-      __syncthreads();
-      for (int i = tid; i < ct * K; i += RS_NT) {
-        const int t = i / K;
-        atomicOr(&msk[sidx[c0 * K + i]][t >> 5], 1u << (t & 31));
-      }
-      __syncthreads();
-    }
-    for (int i = tid; i < ct * K; i += RS_NT) {
-      const int t = i / K, sl = c0 * K + i;
-      const int e = sidx[sl];
-      const uint32_t lo = msk[e][0], hi = msk[e][1];
-      const int r = t < 32 ? __popc(lo & ((1u << t) - 1u))
-                           : __popc(lo) + __popc(hi & ((1u << (t - 32)) - 1u));
-      const int pos = offs[e] + runc[e] + r;
-      a.perm[pos] = c0 + t;
-      a.slot_pos[sl] = pos;
-    }
-    if (c0 + 64 < N) {
-      __syncthreads();
-      for (int e = tid; e < E; e += RS_NT) runc[e] += __popc(msk[e][0]) + __popc(msk[e][1]);
-      __syncthreads();
-    }
-  }
+  route_dispatch_body<BF16, NJ>(a, reinterpret_cast<int*>(rs_dyn), rs_part, cnt, offs, runc, msk);
   if (tid == 0) __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -854,4 +871,46 @@ void mxm_launch_route_small(const RouteSmallArgs& a, bool bf16, hipStream_t s) {
     launch_route_small_dt<uint16_t, true>(a, s);
   else
     launch_route_small_dt<float, false>(a, s);
+}
+
+namespace {
+
+template <bool BF16, int NJ>
+__global__ __launch_bounds__(RS_NT, 1) void route_dispatch_kernel(RouteSmallArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float rd_dyn[];  // the slots
+  __shared__ float rs_part[RS_PART_FLOATS];
+  __shared__ int cnt[MXM_MAX_EXPERTS];
+  __shared__ int offs[MXM_MAX_EXPERTS];
+  __shared__ int runc[MXM_MAX_EXPERTS];
+  __shared__ uint32_t msk[MXM_MAX_EXPERTS][2];
+  for (int e = threadIdx.x; e < a.E; e += RS_NT) {
+    cnt[e] = 0;
+    runc[e] = 0;
+    msk[e][0] = 0u;
+    msk[e][1] = 0u;
+  }
+  __syncthreads();
+  route_dispatch_body<BF16, NJ>(a, reinterpret_cast<int*>(rd_dyn), rs_part, cnt, offs, runc, msk);
+}
+
+template <bool BF16>
+void launch_route_dispatch_b(const RouteSmallArgs& a, hipStream_t s) {
+  const size_t lds = ((size_t)a.N * a.K * 4 + 15) / 16 * 16;
+  if (a.E <= 64)
+    hipLaunchKernelGGL((route_dispatch_kernel<BF16, 1>), dim3(1), dim3(RS_NT), lds, s, a);
+  else if (a.E <= 128)
+    hipLaunchKernelGGL((route_dispatch_kernel<BF16, 2>), dim3(1), dim3(RS_NT), lds, s, a);
+  else if (a.E <= 192)
+    hipLaunchKernelGGL((route_dispatch_kernel<BF16, 3>), dim3(1), dim3(RS_NT), lds, s, a);
+  else
+    hipLaunchKernelGGL((route_dispatch_kernel<BF16, 4>), dim3(1), dim3(RS_NT), lds, s, a);
+}
+
+}  // namespace
+
+void mxm_launch_route_dispatch(const RouteSmallArgs& a, bool bf16, hipStream_t s) {
+  if (bf16)
+    launch_route_dispatch_b<true>(a, s);
+  else
+    launch_route_dispatch_b<false>(a, s);
 }
