@@ -265,8 +265,11 @@ int mxm_moe_stage_times(int64_t op, float* ms, int n);
  * the kernels run at (ffn, or ffn rounded up to the tiles: 128 for MFMA, 64
  * for int8, with zero weights in the padding), info[5] = the down
  * projection's output width (D, or D rounded up to 128 / 16), info[6] = the
- * up projection's reduction length (D, or D rounded up to 64).  Returns the
- * number of entries written (at most n, at most 7). */
+ * up projection's reduction length (D, or D rounded up to 64), info[7] = how
+ * the last forward ran its routing: 0 with the dispatch (counts, offsets,
+ * permutation), 1 the int8 decode flow (per-token results only; the expert
+ * kernels find their rows from the top-k picks), -1 no forward yet.  Returns
+ * the number of entries written (at most n, at most 8). */
 int mxm_moe_info(int64_t op, int64_t* info, int n);
 
 #ifdef __cplusplus

@@ -1965,12 +1965,13 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t vals[7] = {op->q8 ? 2 : op->mfma ? 1 : 0,
+  const int64_t flow = !op->have_last ? -1 : op->last_decode ? 1 : 0;
+  const int64_t vals[8] = {op->q8 ? 2 : op->mfma ? 1 : 0,
                            (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM),
-                           (int64_t)op->Fk, (int64_t)op->Dk, (int64_t)op->Kx};
+                           (int64_t)op->Fk, (int64_t)op->Dk, (int64_t)op->Kx, flow};
   int w = 0;
-  for (; w < n && w < 7; ++w) info[w] = vals[w];
+  for (; w < n && w < 8; ++w) info[w] = vals[w];
   return w;
 }
 

@@ -223,12 +223,14 @@ class MoEFeedForward:
         """mfma / int8: the expert kernel family; ffn_kernel, d_kernel and
         d_reduce: the expert width, the down projection's output width and
         the up projection's reduction length the kernels run at (the op's
-        ffn and D, or those rounded up to the tiles with zero weights)."""
-        arr = (ctypes.c_int64 * 7)()
-        self._lib.mxm_moe_info(self.handle, arr, 7)
+        ffn and D, or those rounded up to the tiles with zero weights);
+        route_flow: how the last forward routed (0 with the dispatch, 1 the
+        int8 decode flow, -1 before any forward)."""
+        arr = (ctypes.c_int64 * 8)()
+        self._lib.mxm_moe_info(self.handle, arr, 8)
         return dict(mfma=arr[0] == 1, int8=arr[0] == 2, workspace_bytes=int(arr[1]),
                     gemm_bm=int(arr[2]), router_tiles=int(arr[3]), ffn_kernel=int(arr[4]),
-                    d_kernel=int(arr[5]), d_reduce=int(arr[6]))
+                    d_kernel=int(arr[5]), d_reduce=int(arr[6]), route_flow=int(arr[7]))
 
     def close(self) -> None:
         if getattr(self, "handle", 0):

@@ -355,6 +355,69 @@ def test_int8_expert_types(gpu_lib, name, etype, act, slope):
     assert err_exact <= MFMA_TIGHT
 
 
+# (N, D, E, K, F, etype, act) of int8 decode batches
+FLOW_CASES = [
+    (64, 512, 16, 4, 320, 0, 0),     # C5-like: most experts have rows
+    (1, 256, 8, 2, 192, 0, 0),       # one token: weights requested after the scan
+    (200, 544, 64, 8, 448, 2, 1),    # padded x rows, 32 rows per pass
+    (96, 200, 12, 3, 128, 1, 1),     # K does not divide 64
+    (64, 256, 96, 4, 128, 0, 0),     # E > 64: two expert groups per token
+    (300, 256, 8, 2, 128, 0, 0),     # several row passes per expert
+    (48, 196, 8, 2, 128, 0, 0),      # D not a multiple of 8
+]
+
+
+@pytest.mark.parametrize("shape", FLOW_CASES, ids=[str(c) for c in FLOW_CASES])
+def test_int8_decode_flows_agree(gpu_lib, monkeypatch, shape):
+    """The int8 decode shapes' two routing flows (MXM_DECODE_FLOW: 0 the
+    one-launch router's dispatch, 1 the per-token results, the expert
+    kernels finding their rows from the picks and y stored token-major) give
+    the same routing, delta, aux and entropy bit for bit, on two calls in a
+    row with different x, and both match the restatement."""
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import quantize_int8
+
+    N, D, E, K, F, etype, act = shape
+    rng = np.random.default_rng(N * 7 + D + E)
+    wpe = 2 if etype == 2 else 3
+    xs = [round_bf16(rng.standard_normal((N, D), dtype=np.float32)) for _ in range(2)]
+    wr = round_bf16(rng.standard_normal((D, E), dtype=np.float32) * np.float32(0.08))
+    q8 = [[quantize_int8(rng.standard_normal(((F, D) if j == wpe - 1 else (D, F)),
+                                             dtype=np.float32) * np.float32(0.02))
+           for j in range(wpe)] for _ in range(E)]
+    results = {}
+    for flow in (0, 1):
+        monkeypatch.setenv("MXM_DECODE_FLOW", str(flow))
+        print(f"int8 flows N {N} D {D} E {E} K {K} F {F} kind {etype}/{act} flow {flow}", flush=True)
+        with MoEFeedForward([1, N, D, E, K, etype, F, act], [0.0], compute_dtype="bf16",
+                            flags=_lib.MXM_FLAG_INT8_WEIGHTS) as op:
+            op.set_input(1, bf16_bits(wr))
+            for e in range(E):
+                for j in range(wpe):
+                    op.set_input_q8(2 + e * wpe + j, *q8[e][j])
+            out = []
+            for x in xs:
+                delta, aux, ent = op.forward_host(bf16_bits(x))
+                info = op.info()
+                out.append((delta, aux, ent, op.routing()))
+            assert info["route_flow"] == flow, (flow, info)
+        results[flow] = out
+    exact = [[(q.astype(np.float32) * s[None, :]).astype(np.float32) for q, s in ws] for ws in q8]
+    for i, x in enumerate(xs):
+        d0, a0, e0, r0 = results[0][i]
+        want = oracle.moe_forward(x, wr, exact, top_k=K, expert_type=etype, activation=act,
+                                  bf16=True, prerounded=True)
+        assert_routing_equal(r0, want)
+        assert rel_l2(d0, want["delta"]) <= MFMA_TIGHT
+        d, a, en, r = results[1][i]
+        assert_routing_equal(r, want)
+        for key in ("top_idx", "gates", "counts", "offsets", "perm"):
+            assert same_bits(r[key], r0[key]), (i, key)
+        assert same_bits(d, d0), i
+        assert same_bits(np.float32(a), np.float32(a0)), (i, a, a0)
+        assert same_bits(np.float32(en), np.float32(e0)), (i, en, e0)
+
+
 def _block_case(seed, N, D, E, F, bf16, x_fp32_in_bf16_flow=False):
     rng = np.random.default_rng(seed)
     x, wr, experts = random_case(seed, N, D, E, F)
