@@ -439,15 +439,16 @@ def main() -> int:
             "ms_per_step": d["ms_per_step"],
             "routed_experts": wb["routed_experts"],
             "hbm_gbs_forward": layer_gbs,
-            "layer_roofline": {"bound": "hbm", "kernel": "whole decode forward (all launches)",
-                               "achieved": layer_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                               "frac": layer_gbs / PEAK_HBM_GBS,
-                               "traffic": layer_traffic("C5", ("route_small", "gemm_up",
-                                                               "gemm_down", "combine"), 0)},
-            "roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
-                         "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": up_gbs / PEAK_HBM_GBS,
-                         "traffic": measured_traffic("C5", "gemm_up", 0)},
+            # the decode layer as a whole: all launches of one forward
+            "roofline": {"bound": "hbm", "kernel": "whole decode forward (all launches)",
+                         "achieved": layer_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": layer_gbs / PEAK_HBM_GBS,
+                         "traffic": layer_traffic("C5", ("route_small", "gemm_up",
+                                                         "gemm_down", "combine"), 0)},
+            "up_roofline": {"bound": "hbm", "kernel": "gemm_up (int8 gate+up weight stream)",
+                            "achieved": up_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": up_gbs / PEAK_HBM_GBS,
+                            "traffic": measured_traffic("C5", "gemm_up", 0)},
             "gemm_down_gbs": (wb["gemm_down"]) / (ds["gemm_down"] * 1e-3) / 1e9,
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
         }
