@@ -388,6 +388,9 @@ def main() -> int:
                          "grouped GEMM's two launches (in a child process)")
     ap.add_argument("--vendor-gemm-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the int8 decode (C5) section")
+    ap.add_argument("--decode-steps", type=int, default=0, metavar="K",
+                    help="timed (and stage-timed) C5 forwards; default max(steps, 200) with "
+                         "max(warmup, 20) warm-up (counter collection runs want a few)")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward section")
     ap.add_argument("--backward-only", nargs="?", const="C2", default=None, metavar="CONFIG",
                     help="only time the bf16 backward at the shape of CONFIG (default C2; 10 "
@@ -427,7 +430,9 @@ def main() -> int:
     decode = None
     if not args.no_decode:
         c5 = CONFIGS["C5"]
-        _, d = run_config(c5, max(args.steps, 200), max(args.warmup, 20), stage_repeats=10)
+        dsteps, dwarm = ((args.decode_steps, min(args.warmup, args.decode_steps))
+                         if args.decode_steps else (max(args.steps, 200), max(args.warmup, 20)))
+        _, d = run_config(c5, dsteps, dwarm, stage_repeats=10)
         ds = d["stages"]
         wb = int8_weight_bytes(c5, d["counts"])
         xb = c5.N * c5.D * 2

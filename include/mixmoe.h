@@ -239,7 +239,10 @@ int mxm_moe_synchronize(int64_t op);
  * (argsort(-probs)[:, :K], gpu/ir.cpp:1108-1109), gates [rows, K] fp32
  * (top_norm, gpu/ir.cpp:1110-1111), counts [E], offsets [E+1] and perm
  * [rows*K] (expert-grouped token ids).  Any pointer may be NULL.  to_host
- * selects host (1) or device (0) destinations. */
+ * selects host (1) or device (0) destinations.  A forward of the int8
+ * decode flow (mxm_moe_info entry 7) computes only the per-token picks and
+ * gates; this call then computes counts, offsets and perm from them on the
+ * device first (the same tables, bit for bit). */
 int mxm_moe_routing(int64_t op, int32_t* top_idx, float* gates, int32_t* counts,
                     int32_t* offsets, int32_t* perm, int to_host);
 
