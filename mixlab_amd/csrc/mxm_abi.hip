@@ -215,9 +215,8 @@ struct MoeOp {
   // and of the forward's expert outputs, for the fp32 backward kernels
   bool bw_w32_ready = false;
   DevBuf bw_w1_32, bw_w1b_32, bw_w2_32, bw_wr32, bw_x32, bw_y32;
-  // bf16 ops of the MFMA family: bf16 intermediates of the MFMA backward, the
-  // weights re-laid for its products (W_down [F][D], W1 [D][NC]), a rocBLAS
-  // handle for the weight gradients
+  // bf16 ops of the MFMA family: bf16 intermediates of the MFMA backward and
+  // the weights re-laid for its products (W_down [F][D], W1 [D][NC])
   bool bw_wbf_ready = false;
   DevBuf bw_dhb, bw_gub, bw_dgub, bw_dxeb, bw_zero, bw_ms, bw_w2o, bw_w1u, bw_wscr,
       bw_ddb, bw_gp, bw_dgp, bw_dlb, bw_dwr2;

@@ -1143,8 +1143,9 @@ void mxm_launch_backward_router(const BackwardArgs& a, hipStream_t s) {
   (void)K;
 }
 
-// The fp32 experts' elementwise parts; their products are per-expert rocBLAS
-// GEMMs issued by the library's host code.
+// The fp32 backward's operand planes and elementwise parts; its products run
+// on the MFMA grouped GEMM and weight-gradient kernels over bf16 planes
+// (three plane pairs per fp32 product, fp32 accumulation).
 void mxm_launch_planes3(const float* src, int64_t rows, int cols, int lds, int ldq, bool hlh,
                         uint16_t* dst, hipStream_t s) {
   const int64_t n = rows * ldq;
