@@ -382,7 +382,7 @@ def main() -> int:
     ap.add_argument("--flags", type=int, default=0, help="mxm_moe_create flags (include/mixmoe.h)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
-    ap.add_argument("--no-configs", action="store_true", help="skip the C2 / C3 sections")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1, C2, C3 and C4F sections")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time hipBLASLt (torch.matmul) on the dense equivalents of the "
                          "grouped GEMM's two launches (in a child process)")
@@ -481,6 +481,15 @@ def main() -> int:
     # by the library; the figures count the op's own F)
     extra = {}
     if not args.no_configs:
+        # C1, the reference's CPU-runnable moe_tiny-scale case: fp32 on the
+        # exact-order SIMT kernels (no MFMA figure)
+        c1 = CONFIGS["C1"]
+        _, r1 = run_config(c1, max(args.steps, 100), max(args.warmup, 10))
+        extra["C1"] = {"tokens": c1.N, "d_model": c1.D, "experts": c1.E, "top_k": c1.K,
+                       "expert_hidden": c1.F, "dtype": c1.dtype,
+                       "tokens_per_s": r1["tokens_per_s"], "ms_per_step": r1["ms_per_step"],
+                       "stages_ms": {k: v for k, v in r1["stages"].items() if k != "forwards"},
+                       "executor": r1["info"]}
         for name in ("C2", "C3", "C4F"):
             if name == cfg.name:
                 continue

@@ -269,10 +269,12 @@ int mxm_moe_stage_times(int64_t op, float* ms, int n);
  * for int8, with zero weights in the padding), info[5] = the down
  * projection's output width (D, or D rounded up to 128 / 16), info[6] = the
  * up projection's reduction length (D, or D rounded up to 64), info[7] = how
- * the last forward ran its routing: 0 with the dispatch (counts, offsets,
- * permutation), 1 the int8 decode flow (per-token results only; the expert
- * kernels find their rows from the top-k picks), -1 no forward yet.  Returns
- * the number of entries written (at most n, at most 8). */
+ * the last forward routed: 0 the tiled router, scan and scatter (three
+ * launches), 1 the one-launch router (a workgroup per token, the dispatch in
+ * its last workgroup), 2 the int8 decode flow (the one-launch router's
+ * per-token results only; the expert kernels find their rows from the top-k
+ * picks), -1 no forward yet.  Returns the number of entries written (at most
+ * n, at most 8). */
 int mxm_moe_info(int64_t op, int64_t* info, int n);
 
 #ifdef __cplusplus

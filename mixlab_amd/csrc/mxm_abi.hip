@@ -277,6 +277,22 @@ int fenced(F&& f) {
     return MXM_ERR_OP;                                  \
   }
 
+// Whether a batch that the one-launch router can take is faster there than
+// on the tiled router + scan + scatter.  The one-launch router's time grows
+// with N (a workgroup per token, then one workgroup's dispatch of the N*K
+// slots); the three-launch path's hardly does at these sizes.  So the one
+// launch pays while each token brings enough logit work: measured on MI355X
+// at N = 512-1024 over D*E = 512 .. 131072 (bf16 and fp32), it is the faster
+// one for every N <= 512, up to N = 768 from D*E = 4096 on, and up to
+// N = 1024 from D*E = 16384 on (the crossover lies at N ~ 560-600 for D*E of
+// 512-2048, ~750 for 4096, ~800-900 for 8192; results are bit for bit the
+// same either way).  The int8 decode flow is built on the one-launch router
+// and keeps it wherever it fits.
+bool small_route_pays(int N, int D, int E) {
+  const int64_t de = (int64_t)D * E;
+  return N <= 512 || (N <= 768 && de >= 4096) || de >= 16384;
+}
+
 // Row-tile heights and tile counts of the forward's kernels; a function of
 // the op's parameters only.
 void set_schedule(MoeOp& o) {
@@ -999,7 +1015,10 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     const size_t F1 = (size_t)o->Kx * o->Fk, F2 = (size_t)o->Fk * o->Dk;  // padded matrices
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
-    o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K);
+    o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K) &&
+                     (o->q8 || small_route_pays(o->N, o->D, o->E));
+    if (const char* v = std::getenv("MXM_SMALL_ROUTE"))
+      o->small_route = std::atoi(v) != 0 && mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
     if (o->small_route) {
       o->ldw = (o->D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
@@ -1964,7 +1983,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
-  const int64_t flow = !op->have_last ? -1 : op->last_decode ? 1 : 0;
+  const int64_t flow = !op->have_last ? -1 : op->last_decode ? 2 : op->small_route ? 1 : 0;
   const int64_t vals[8] = {op->q8 ? 2 : op->mfma ? 1 : 0,
                            (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM),

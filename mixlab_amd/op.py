@@ -224,8 +224,9 @@ class MoEFeedForward:
         d_reduce: the expert width, the down projection's output width and
         the up projection's reduction length the kernels run at (the op's
         ffn and D, or those rounded up to the tiles with zero weights);
-        route_flow: how the last forward routed (0 with the dispatch, 1 the
-        int8 decode flow, -1 before any forward)."""
+        route_flow: how the last forward routed (0 tiled router + scan +
+        scatter, 1 the one-launch router, 2 the int8 decode flow, -1 before
+        any forward)."""
         arr = (ctypes.c_int64 * 8)()
         self._lib.mxm_moe_info(self.handle, arr, 8)
         return dict(mfma=arr[0] == 1, int8=arr[0] == 2, workspace_bytes=int(arr[1]),

@@ -400,7 +400,7 @@ def test_int8_decode_flows_agree(gpu_lib, monkeypatch, shape):
                 delta, aux, ent = op.forward_host(bf16_bits(x))
                 info = op.info()
                 out.append((delta, aux, ent, op.routing()))
-            assert info["route_flow"] == flow, (flow, info)
+            assert info["route_flow"] == (2 if flow else 1), (flow, info)
         results[flow] = out
     exact = [[(q.astype(np.float32) * s[None, :]).astype(np.float32) for q, s in ws] for ws in q8]
     for i, x in enumerate(xs):
@@ -596,10 +596,13 @@ def test_many_experts(gpu_lib, E, N, bf16):
     (8, 16384, 64, 4, True),     # D at the one-launch router's limit (64 KB x row in LDS)
     (8, 16388, 64, 4, False),    # D past it: the tiled router
 ])
-def test_decode_router_shapes(gpu_lib, N, D, E, K, bf16):
+def test_decode_router_shapes(gpu_lib, monkeypatch, N, D, E, K, bf16):
     """Decode-sized batches route in one launch (logits, softmax, top-k, then
     counts, offsets, permutation, aux and entropy in the last workgroup);
-    routing bit-exact at its edges and on the tiled router just past them."""
+    routing bit-exact at its edges and on the tiled router just past them.
+    MXM_SMALL_ROUTE=1 takes the one-launch router wherever it fits, also
+    where the library would choose the tiled one."""
+    monkeypatch.setenv("MXM_SMALL_ROUTE", "1")
     F = 32
     x, wr, experts = random_case(300 + N + D + E + K, N, D, E, F)
     if bf16:
@@ -613,6 +616,73 @@ def test_decode_router_shapes(gpu_lib, N, D, E, K, bf16):
     assert rel_l2(delta, want["delta"]) <= (BF16_TOL if bf16 else FP32_TOL)
     assert abs(aux - want["aux"]) <= (1e-2 if bf16 else 1e-5) * abs(want["aux"])
     assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"])
+
+
+# (N, D, E, K, dtype, int8, the router the library picks): 0 tiled router +
+# scan + scatter, 1 the one-launch router, 2 the int8 decode flow
+ROUTER_CHOICE = [
+    (1024, 128, 4, 2, "fp32", False, 0),    # C1, the reference's moe_tiny scale: D*E = 512
+    (512, 128, 4, 2, "fp32", False, 1),
+    (768, 512, 8, 2, "bf16", False, 1),     # D*E = 4096
+    (1024, 512, 8, 2, "bf16", False, 0),
+    (1024, 2048, 8, 2, "bf16", False, 1),   # D*E = 16384
+    (1024, 256, 8, 2, "bf16", True, 2),     # int8 keeps the decode flow
+    (1100, 2048, 64, 8, "bf16", False, 0),  # past the one-launch router's limit
+]
+
+
+@pytest.mark.parametrize("N,D,E,K,dtype,int8,want", ROUTER_CHOICE,
+                         ids=[f"{c[0]}-{c[1]}-{c[2]}-{c[4]}{'-int8' if c[5] else ''}"
+                              for c in ROUTER_CHOICE])
+def test_router_choice(gpu_lib, monkeypatch, N, D, E, K, dtype, int8, want):
+    """The router the library picks for a batch (the one-launch router while
+    its per-token workgroups pay for themselves, measured on MI355X), and
+    the other path forced through MXM_SMALL_ROUTE: the same routing and
+    delta bit for bit; aux and entropy within a few ulps (each path sums the
+    per-token terms over the batch in its own order: tiles, then tiles in
+    order, against token-strided partials and a butterfly)."""
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import quantize_int8
+
+    F = 128
+    bf16 = dtype == "bf16"
+    x, wr, experts = random_case(400 + N + D + E, N, D, E, F)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    up = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
+
+    def run(force):
+        if force is None:
+            monkeypatch.delenv("MXM_SMALL_ROUTE", raising=False)
+        else:
+            monkeypatch.setenv("MXM_SMALL_ROUTE", force)
+        flags = _lib.MXM_FLAG_INT8_WEIGHTS if int8 else 0
+        with MoEFeedForward([1, N, D, E, K, 0, F, 0], [0.0], compute_dtype=dtype,
+                            flags=flags) as op:
+            op.set_input(1, up(wr))
+            for e in range(E):
+                for j in range(3):
+                    if int8:
+                        op.set_input_q8(2 + 3 * e + j, *quantize_int8(experts[e][j]))
+                    else:
+                        op.set_input(2 + 3 * e + j, up(experts[e][j]))
+            delta, aux, ent = op.forward_host(up(x))
+            return delta, aux, ent, op.routing(), op.info()["route_flow"]
+
+    got = run(None)
+    assert got[4] == want
+    fits = N <= 1024 and N * K <= 16384  # the one-launch router's limits
+    other = run("0" if want else "1")
+    assert other[4] == (0 if want or not fits else 1)
+    for key in ("top_idx", "gates", "counts", "offsets", "perm"):
+        assert same_bits(got[3][key], other[3][key]), key
+    assert same_bits(got[0], other[0])
+    assert abs(got[1] - other[1]) <= 1e-6 * abs(got[1])
+    assert abs(got[2] - other[2]) <= 1e-6 * abs(got[2])
+    if not int8:
+        want_o = run_oracle(x, wr, experts, K=K, bf16=bf16)
+        assert_routing_equal(got[3], want_o)
 
 
 def test_decode_router_repeated_calls(gpu_lib):
