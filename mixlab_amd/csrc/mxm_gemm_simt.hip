@@ -78,14 +78,17 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[b][i][j] = 0.0f;
 
-  for (int k0 = 0; k0 < Kd; k0 += BK) {
-    __syncthreads();
+  // The k tile after the current one is loaded into registers while the
+  // current one is summed (its loads' latency is then hidden behind 16 k
+  // steps); only the time of the loads changes, not the order of the sums.
+  float pa[4], pb[NB][4];
+  auto fetch = [&](int k0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int idx = tid + NT * r;
       const int row = idx / BK, kk = idx % BK;
       const int k = k0 + kk;
-      As[kk][row] = (arow[r] != nullptr && k < Kd) ? lda_f32<TA>(arow[r] + k) : 0.0f;
+      pa[r] = (arow[r] != nullptr && k < Kd) ? lda_f32<TA>(arow[r] + k) : 0.0f;
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -95,10 +98,27 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
         const int idx = tid + NT * r;
         const int kk = idx / BN, col = idx % BN;
         const int k = k0 + kk, c = n0 + col;
-        Bs[b][kk][col] = (k < Kd && c < NC) ? Bm[(size_t)k * NC + c] : 0.0f;
+        pb[b][r] = (k < Kd && c < NC) ? Bm[(size_t)k * NC + c] : 0.0f;
       }
     }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < Kd; k0 += BK) {
+    __syncthreads();  // every thread has finished reading the previous tile
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int idx = tid + NT * r;
+      As[idx % BK][idx / BK] = pa[r];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = tid + NT * r;
+        Bs[b][idx / BN][idx % BN] = pb[b][r];
+      }
     __syncthreads();
+    if (k0 + BK < Kd) fetch(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; ++kk) {
       const float4 av = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
