@@ -174,6 +174,7 @@ struct MoeOp {
 
   // tile schedule of the forward (set at create from the op's parameters)
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
+  int simt_tile = 0;  // MXM_SIMT_TILE at creation: the SIMT family's tile (0 picks)
   // the op's own workspace, allocated at the first forward; `last` is the
   // workspace the latest forward used (the op's own, or the device scratch
   // of mxm_moe_forward_noalloc), which the routing queries read
@@ -319,7 +320,12 @@ void set_schedule(MoeOp& o) {
     o.bm1 = mxm_mfma_tile_rows(nc1, o.Kx, o.fam1);
     o.bm2 = mxm_mfma_tile_rows(o.Dk, o.hsplit ? 2 * o.Fk : o.Fk, o.fam2);
   } else {
-    o.bm1 = o.bm2 = mxm_simt_bm();
+    // 64 x 64 tiles where their grid covers every CU, else 32 x 32 (C1's
+    // down projection: 72 tiles of 64 x 64 for 256 CUs); MXM_SIMT_TILE (32
+    // or 64, read at creation) overrides
+    o.bm1 = mxm_simt_bm((int64_t)NK, o.E, o.F, o.n_cu);
+    o.bm2 = mxm_simt_bm((int64_t)NK, o.E, o.D, o.n_cu);
+    if (o.simt_tile == 32 || o.simt_tile == 64) o.bm1 = o.bm2 = o.simt_tile;
   }
   o.max_mtiles1 = (int)((NK + o.bm1 - 1) / o.bm1) + o.E;
   o.max_mtiles2 = (int)((NK + o.bm2 - 1) / o.bm2) + o.E;
@@ -566,6 +572,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.Kd = o.Kx;
   g1.Ncols = (o.mfma && glu) ? 2 * o.Fk : o.Fk;
   g1.max_mtiles = o.max_mtiles1;
+  g1.simt_bm = o.bm1;
   g1.family = o.fam1;
   g1.expert_type = o.etype;
   g1.activation = o.act;
@@ -626,6 +633,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.h_split = o.hsplit;
   g2.Ncols = o.Dk;
   g2.max_mtiles = o.max_mtiles2;
+  g2.simt_bm = o.bm2;
   g2.family = o.fam2;
   g2.expert_type = o.etype;
   g2.activation = o.act;
@@ -943,6 +951,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     if (const char* v = std::getenv("MXM_ROUTER_WGRAD_MFMA")) o->dwr_mode = std::atoi(v) != 0;
     if (const char* v = std::getenv("MXM_FORCE_64BIT_OFFSETS")) o->force64 = std::atoi(v) != 0;
     if (const char* v = std::getenv("MXM_DECODE_FLOW")) o->decode_flow = std::atoi(v) != 0;
+    if (const char* v = std::getenv("MXM_SIMT_TILE")) o->simt_tile = std::atoi(v);
     o->B = int_params[0];
     o->T = int_params[1];
     o->D = int_params[2];

@@ -10,12 +10,16 @@
 // Row tiles are ragged per expert: blockIdx.y indexes the concatenation of
 // every expert's ceil(count/BM) row tiles (prefix `mstart`), so no host sync
 // is needed between dispatch and the GEMM.
+//
+// Two tiles, 256 threads each: 64 x 64 outputs (4 x 4 per thread), and 32 x
+// 32 (2 x 2 per thread) for launches whose 64 x 64 grid would leave CUs
+// idle -- four times the workgroups, each thread's chain a quarter as long
+// (GemmArgs::simt_bm picks; the schedule's row tiles must match).
 #include "mxm_kernels.h"
 
 namespace {
 
-constexpr int BM = 64, BN = 64, BK = 16, NT = 256;
-constexpr int LDA = BM + 4, LDB = BN + 4;
+constexpr int BK = 16, NT = 256;
 
 __device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mtile) {
   int lo = 0, hi = E - 1;
@@ -36,9 +40,31 @@ __device__ __forceinline__ float lda_f32<float>(const float* p) { return *p; }
 template <>
 __device__ __forceinline__ float lda_f32<uint16_t>(const uint16_t* p) { return mxm_bf2f(*p); }
 
-template <typename TA, bool BF16, int MODE>
+// T consecutive floats of LDS (T * 4-byte aligned) as one vector read.
+template <int T>
+__device__ __forceinline__ void lds_vec(const float* p, float (&v)[T]) {
+  static_assert(T == 2 || T == 4, "float2 or float4");
+  if constexpr (T == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+    const float2 q = *reinterpret_cast<const float2*>(p);
+    v[0] = q.x;
+    v[1] = q.y;
+  }
+}
+
+// BM x BN tile, TM x TN outputs per thread (a 16 x 16 thread grid).
+template <typename TA, bool BF16, int MODE, int BM, int BN>
 __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   constexpr int NB = (MODE == MXM_GEMM_GLU) ? 2 : 1;
+  constexpr int TM = BM / 16, TN = BN / 16;
+  constexpr int LA = BM * BK / NT, LB = BK * BN / NT;  // loads per thread per k tile
+  constexpr int LDA = BM + 4, LDB = BN + 4;
+  static_assert(LA * NT == BM * BK && LB * NT == BK * BN, "whole loads per thread");
   __shared__ float As[BK][LDA];
   __shared__ float Bs[NB][BK][LDB];
 
@@ -57,9 +83,9 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   const float* B1 = (NB == 2) ? static_cast<const float*>(a.b1) + (size_t)e * Kd * NC : nullptr;
 
   // A-tile rows this thread loads: idx = tid + 256*r -> row idx/BK, k idx%BK
-  const TA* arow[4];
+  const TA* arow[LA];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < LA; ++r) {
     const int row = (tid + NT * r) / BK;
     if (row < rows) {
       const int p = row0 + row;
@@ -70,21 +96,21 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
     }
   }
 
-  float acc[NB][4][4];
+  float acc[NB][TM][TN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[b][i][j] = 0.0f;
+      for (int j = 0; j < TN; ++j) acc[b][i][j] = 0.0f;
 
   // The k tile after the current one is loaded into registers while the
   // current one is summed (its loads' latency is then hidden behind 16 k
   // steps); only the time of the loads changes, not the order of the sums.
-  float pa[4], pb[NB][4];
+  float pa[LA], pb[NB][LB];
   auto fetch = [&](int k0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < LA; ++r) {
       const int idx = tid + NT * r;
       const int row = idx / BK, kk = idx % BK;
       const int k = k0 + kk;
@@ -94,7 +120,7 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
     for (int b = 0; b < NB; ++b) {
       const float* Bm = (b == 0) ? B0 : B1;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < LB; ++r) {
         const int idx = tid + NT * r;
         const int kk = idx / BN, col = idx % BN;
         const int k = k0 + kk, c = n0 + col;
@@ -106,14 +132,14 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   for (int k0 = 0; k0 < Kd; k0 += BK) {
     __syncthreads();  // every thread has finished reading the previous tile
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < LA; ++r) {
       const int idx = tid + NT * r;
       As[idx % BK][idx / BK] = pa[r];
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < LB; ++r) {
         const int idx = tid + NT * r;
         Bs[b][idx / BN][idx % BN] = pb[b][r];
       }
@@ -121,29 +147,29 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
     if (k0 + BK < Kd) fetch(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; ++kk) {
-      const float4 av = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
-      const float ar[4] = {av.x, av.y, av.z, av.w};
+      float ar[TM];
+      lds_vec<TM>(&As[kk][ty * TM], ar);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const float4 bv = *reinterpret_cast<const float4*>(&Bs[b][kk][tx * 4]);
-        const float br[4] = {bv.x, bv.y, bv.z, bv.w};
+        float br[TN];
+        lds_vec<TN>(&Bs[b][kk][tx * TN], br);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[b][i][j] = __builtin_fmaf(ar[i], br[j], acc[b][i][j]);
+          for (int j = 0; j < TN; ++j) acc[b][i][j] = __builtin_fmaf(ar[i], br[j], acc[b][i][j]);
       }
     }
   }
 
   float* out = static_cast<float*>(a.out);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = ty * 4 + i;
+  for (int i = 0; i < TM; ++i) {
+    const int row = ty * TM + i;
     if (row >= rows) continue;
     const size_t orow = (size_t)(row0 + row) * NC;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = n0 + tx * 4 + j;
+    for (int j = 0; j < TN; ++j) {
+      const int c = n0 + tx * TN + j;
       if (c >= NC) continue;
       float v;
       if (MODE == MXM_GEMM_GLU) {
@@ -166,30 +192,46 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   }
 }
 
-template <typename TA, bool BF16>
+template <typename TA, bool BF16, int T>
 void launch_t(const GemmArgs& a, hipStream_t s) {
-  const dim3 grid((a.Ncols + BN - 1) / BN, a.max_mtiles);
+  const dim3 grid((a.Ncols + T - 1) / T, a.max_mtiles);
   switch (a.mode) {
     case MXM_GEMM_GLU:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU, T, T>), grid, dim3(NT), 0, s, a);
       break;
     case MXM_GEMM_MLP:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP, T, T>), grid, dim3(NT), 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN, T, T>), grid, dim3(NT), 0,
+                         s, a);
       break;
   }
 }
 
 }  // namespace
 
-int mxm_simt_bm() { return BM; }
+int mxm_simt_bm(int64_t rows, int E, int ncols, int n_cu) {
+  // the 64 x 64 tile where its grid gives every CU one, else 32 x 32
+  // (measured: C1's down projection, 72 tiles of 64 x 64, is faster on 32 x
+  // 32; a 2048-row fp32 down projection of 320 tiles, over k = 2048, is
+  // faster on 64 x 64, whose threads reuse each LDS read for 4 outputs)
+  const int64_t tiles = ((rows + 63) / 64 + E) * ((ncols + 63) / 64);
+  return tiles >= (int64_t)n_cu ? 64 : 32;
+}
 
 void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s) {
   if (a.max_mtiles <= 0) return;
-  if (bf16)
-    launch_t<uint16_t, true>(a, s);
-  else
-    launch_t<float, false>(a, s);
+  const bool small = a.simt_bm == 32;
+  if (bf16) {
+    if (small)
+      launch_t<uint16_t, true, 32>(a, s);
+    else
+      launch_t<uint16_t, true, 64>(a, s);
+  } else {
+    if (small)
+      launch_t<float, false, 32>(a, s);
+    else
+      launch_t<float, false, 64>(a, s);
+  }
 }

@@ -174,6 +174,7 @@ struct GemmArgs {
   float slope;
   bool y_bf16;            // SIMT down: round y to bf16
   int family;             // MFMA tile family (MXM_TILE_*), MXM_TILE_AUTO picks
+  int simt_bm;            // SIMT family: tile height and width, 64 (0 too) or 32
   int rows_total;         // N*K routed rows (int8 family: picks rows per pass)
   // Split hidden (MFMA and int8 families, kinds whose hidden is fp32 in the
   // bf16 flow, !mxm_hidden_is_bf16): the up GEMM stores each fp32 hidden
@@ -259,7 +260,10 @@ struct WgradArgs {
 bool mxm_wgrad_fits(int M, int C);
 size_t mxm_wgrad_scratch_bytes(int M, int C);
 void mxm_launch_wgrad(const WgradArgs& a, hipStream_t s);
-int mxm_simt_bm();
+// The SIMT family's row-tile height (and tile width) for a launch of `rows`
+// routed rows over E experts and ncols output columns: 64, or 32 when the
+// 64 x 64 grid would not give every CU a tile.
+int mxm_simt_bm(int64_t rows, int E, int ncols, int n_cu);
 
 // Epilogue kinds: the hidden activation (expert type x activation) of the up
 // projections, or the plain bf16 store of the down projection.

@@ -117,8 +117,10 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
     want = run_oracle(x, wr, experts, K=2, expert_type=etype, activation=act, slope=slope,
                       bf16=bf16)
     assert info["mfma"] == flow.startswith("bf16_mfma")
+    # (the SIMT flows: 32 x 32 tiles at this size, the 64 x 64 grid would
+    # leave some of the 256 CUs without a tile)
     assert info["gemm_bm"] == {"bf16_mfma": 256, "bf16_mfma128": 128,
-                               "bf16_mfma256x128": 256}.get(flow, 64)
+                               "bf16_mfma256x128": 256}.get(flow, 32)
     assert_routing_equal(routing, want)
     if flow.startswith("bf16_mfma"):
         err = rel_l2(delta, want["delta"])
@@ -126,6 +128,31 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
         assert err <= MFMA_TIGHT
     else:
         assert same_bits(delta, want["delta"])
+
+
+@pytest.mark.parametrize("shape,bf16", [((1024, 128, 4, 2, 512, 0), False),  # C1
+                                        ((700, 96, 6, 3, 200, 2), True),      # bf16 below the MFMA tiles
+                                        ((3000, 64, 8, 2, 96, 1), False)])    # ragged tails
+def test_simt_tiles_agree(gpu_lib, monkeypatch, shape, bf16):
+    """The SIMT family's two tiles (64 x 64, 4 x 4 outputs per thread; 32 x
+    32, 2 x 2) sum every output in the same ascending-k order: bit for bit
+    the same delta, and bit-exact against the restatement (fp32 and the
+    bf16 dtype flow)."""
+    N, D, E, K, F, etype = shape
+    x, wr, experts = random_case(500 + N + D, N, D, E, F, expert_type=etype)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(m) for m in ws] for ws in experts]
+    out = {}
+    for tile in (32, 64):
+        monkeypatch.setenv("MXM_SIMT_TILE", str(tile))
+        delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, expert_type=etype,
+                                                 bf16=bf16)
+        assert not info["mfma"] and info["gemm_bm"] == tile
+        out[tile] = delta
+    assert same_bits(out[32], out[64])
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, bf16=bf16)
+    assert same_bits(out[32], want["delta"])
 
 
 def test_ties_go_to_lower_expert(gpu_lib):
