@@ -1,0 +1,105 @@
+"""A seeded sweep of op shapes through every flow, against the restatement.
+
+The other GPU tests pin chosen edges (tile multiples, router limits, padded
+widths, decode sizes).  This sweep draws its shapes at random -- tokens,
+model and expert widths off every tile, expert counts and top-k, all six
+expert kinds, fp32 / bf16 / int8 weights -- so that the interactions of the
+executor's choices (MFMA or SIMT family and tile, padding, router path,
+decode flow) meet shapes nobody chose.  Bars, per flow:
+* routing (top-k indices, gates, counts, offsets, permutation) bit-exact;
+* fp32, and bf16 on the SIMT kernels: delta bit-exact (the exact-order
+  kernels follow the restatement's summation order);
+* bf16 on the MFMA kernels: delta within 1e-3 relative L2 (accumulation
+  order only);
+* int8: delta within 1e-3 of the restatement fed the exact products q * s;
+* aux and entropy within 1e-5 (fp32) or 1e-2 / 1e-4 (bf16 flows).
+The cases are fixed by the seed; each prints its shape before it runs.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from mixlab_amd import _lib
+from mixlab_amd.workloads import bf16_bits, quantize_int8, round_bf16
+from tests.moe_testutil import assert_routing_equal, random_case, rel_l2, run_gpu, run_oracle, same_bits
+
+pytestmark = pytest.mark.gpu
+
+KINDS = [(0, 0), (1, 1), (2, 0), (2, 1), (2, 2), (2, 3)]  # (expert type, activation)
+
+
+def _cases(n=36, seed=2026):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        flow = ("fp32", "bf16", "int8")[len(cases) % 3]
+        etype, act = KINDS[int(rng.integers(len(KINDS)))]
+        E = int(rng.integers(1, 81))
+        K = int(rng.integers(1, min(E, 8) + 1))
+        N = int(rng.integers(1, 4001))
+        D = int(rng.integers(16, 1100))
+        F = int(rng.integers(16, 1500))
+        wpe = 2 if etype == 2 else 3
+        if N * K * D * F * wpe > 4e9:  # keeps each restatement run to about a second
+            continue
+        slope = float(np.round(rng.uniform(0.1, 0.5), 3)) if act == 3 else 0.0
+        cases.append((flow, N, D, E, K, F, etype, act, slope, int(rng.integers(1 << 30))))
+    return cases
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-N{c[1]}-D{c[2]}-E{c[3]}-K{c[4]}-F{c[5]}-k{c[6]}{c[7]}"
+                                             for c in CASES])
+def test_random_shapes(gpu_lib, case):
+    from mixlab_amd.op import MoEFeedForward
+
+    flow, N, D, E, K, F, etype, act, slope, seed = case
+    print(f"case {case}", flush=True)
+    x, wr, experts = random_case(seed, N, D, E, F, expert_type=etype)
+    if flow == "fp32":
+        delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, expert_type=etype,
+                                                 activation=act, slope=slope)
+        want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope)
+        assert_routing_equal(routing, want)
+        assert same_bits(delta, want["delta"])
+        assert abs(aux - want["aux"]) <= 1e-5 * abs(want["aux"]) + 1e-7
+        assert abs(ent - want["entropy"]) <= 1e-5 * abs(want["entropy"]) + 1e-7
+        return
+    x, wr = round_bf16(x), round_bf16(wr)
+    if flow == "bf16":
+        experts = [[round_bf16(m) for m in ws] for ws in experts]
+        delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, expert_type=etype,
+                                                 activation=act, slope=slope, bf16=True)
+        want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
+                          bf16=True)
+        assert_routing_equal(routing, want)
+        if info["mfma"]:
+            err = rel_l2(delta, want["delta"])
+            print(f"  mfma (widths {info['ffn_kernel']} / {info['d_kernel']}): rel L2 {err:.2e}")
+            assert err <= 1e-3
+        else:
+            assert same_bits(delta, want["delta"])
+    else:
+        wpe = 2 if etype == 2 else 3
+        q8 = [[quantize_int8(m) for m in ws] for ws in experts]
+        with MoEFeedForward([1, N, D, E, K, etype, F, act], [slope], compute_dtype="bf16",
+                            flags=_lib.MXM_FLAG_INT8_WEIGHTS) as op:
+            op.set_input(1, bf16_bits(wr))
+            for e in range(E):
+                for j in range(wpe):
+                    op.set_input_q8(2 + e * wpe + j, *q8[e][j])
+            delta, aux, ent = op.forward_host(bf16_bits(x))
+            routing = op.routing()
+            info = op.info()
+        exact = [[(q.astype(np.float32) * s[None, :]).astype(np.float32) for q, s in ws]
+                 for ws in q8]
+        want = oracle.moe_forward(x, wr, exact, top_k=K, expert_type=etype, activation=act,
+                                  leaky_slope=slope, bf16=True, prerounded=True)
+        assert_routing_equal(routing, want)
+        err = rel_l2(delta, want["delta"])
+        print(f"  int8 (route flow {info['route_flow']}): rel L2 {err:.2e}")
+        assert err <= 1e-3
+    assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"]) + 1e-6
+    assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"]) + 1e-6
