@@ -1603,8 +1603,39 @@ void run_backward_x3(MoeOp& o, BackwardArgs& b, bool own_forward) {
   };
   // x's planes (one row per token; the products gather them through perm)
   mxm_launch_planes3(b.x, (int64_t)N, D, D, Dq, false, x3, st);
-  // G|U = Xp W1 (fp32, W1's interleaved column order), H's planes
-  product(0, x3, o.bx_w1p.as<uint16_t>(), gu, 3 * Dq, NCq, true);
+  // G|U = Xp W1 (fp32, W1's interleaved column order), H's planes.  An fp32
+  // ReLU expert takes U from the exact-order SIMT projection instead -- the
+  // forward's own fp32 sums: ReLU's derivative jumps at 0, and the plane
+  // products (about 2^-16 relative) would flip the mask of the units whose
+  // pre-activation lies that close to 0, so the backward would not be the
+  // gradient of the forward's function
+  if (!o.bf16 && o.etype == MXM_EXPERT_MLP && o.act == MXM_ACT_RELU) {
+    if (Fq != F) HIPCK(hipMemsetAsync(gu, 0, NK * Fq * 4, st));  // the padding columns
+    GemmArgs g{};
+    g.mode = MXM_GEMM_MLP;
+    g.a = b.x;
+    g.perm = b.perm;
+    g.b0 = o.w1.p;
+    g.out = nullptr;
+    g.out2 = gu;
+    g.ld2 = Fq;
+    g.offsets = b.offsets;
+    g.mstart = o.ws.mstart1;
+    g.E = E;
+    g.Kd = D;
+    g.Ncols = F;
+    g.max_mtiles = o.max_mtiles1;
+    g.simt_bm = o.bm1;
+    g.expert_type = o.etype;
+    g.activation = o.act;
+    g.slope = o.slope;
+    if (!g.a || !g.b0 || !g.offsets || !g.mstart || !g.perm)
+      fail_rt("OP_MOE_FEED_FORWARD backward: an operand of the exact up projection is missing");
+    mxm_launch_gemm_simt(g, false, st);
+    HIPCK(hipGetLastError());
+  } else {
+    product(0, x3, o.bx_w1p.as<uint16_t>(), gu, 3 * Dq, NCq, true);
+  }
   mxm_launch_hidden_planes3(gu, (int64_t)NK, Fq, o.etype, o.act, o.slope, h3, st);
   HIPCK(hipGetLastError());
   if (own_forward) {

@@ -182,12 +182,13 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
       } else if (MODE == MXM_GEMM_MLP) {
         float u = acc[0][i][j];
         if (BF16) u = mxm_rbf(u);
+        if (a.out2) static_cast<float*>(a.out2)[(size_t)(row0 + row) * a.ld2 + c] = u;
         v = mxm_hidden<BF16>(MXM_EXPERT_MLP, a.activation, a.slope, 0.0f, u);
       } else {
         v = acc[0][i][j];
         if (a.y_bf16) v = mxm_rbf(v);
       }
-      out[orow + c] = v;
+      if (out) out[orow + c] = v;
     }
   }
 }

@@ -165,7 +165,10 @@ struct GemmArgs {
   const float* scale1;
   void* out;              // mode 0/1: H [N*K, F]; mode 2: Y [N*K, D]
   void* out2;             // MFMA up projections: if set, the raw bf16 projections too,
-                          // [N*K, Ncols] in W1's column order (the backward's G|U)
+                          // [N*K, Ncols] in W1's column order (the backward's G|U);
+                          // SIMT MLP up projection: the raw fp32 projections, rows
+                          // ld2 apart (out may then be null: no hidden stored)
+  int ld2;
   const int32_t* offsets; // [E + 1]
   const int32_t* mstart;  // [E + 1]
   int E, Kd, Ncols;       // reduction length, output columns (per matrix)

@@ -103,3 +103,68 @@ def test_random_shapes(gpu_lib, case):
         assert err <= 1e-3
     assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"]) + 1e-6
     assert abs(ent - want["entropy"]) <= 1e-4 * abs(want["entropy"]) + 1e-6
+
+
+def _bw_cases(n=16, seed=2027):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        flow = ("fp32", "bf16")[len(cases) % 2]
+        etype, act = KINDS[int(rng.integers(len(KINDS)))]
+        E = int(rng.integers(1, 41))
+        K = int(rng.integers(1, min(E, 8) + 1))
+        N = int(rng.integers(1, 1500))
+        D = int(rng.integers(16, 700))
+        F = int(rng.integers(16, 900))
+        wpe = 2 if etype == 2 else 3
+        if N * K * D * F * wpe > 1.5e9:  # the float64 restatement's products stay small
+            continue
+        slope = float(np.round(rng.uniform(0.1, 0.5), 3)) if act == 3 else 0.0
+        cases.append((flow, N, D, E, K, F, etype, act, slope, int(rng.integers(1 << 30))))
+    return cases
+
+
+BW_CASES = _bw_cases()
+
+
+@pytest.mark.parametrize("case", BW_CASES,
+                         ids=[f"{c[0]}-N{c[1]}-D{c[2]}-E{c[3]}-K{c[4]}-F{c[5]}-k{c[6]}{c[7]}"
+                              for c in BW_CASES])
+def test_random_shapes_backward(gpu_lib, case):
+    """mxm_moe_backward at random shapes (fp32, and bf16 on whichever kernels
+    the executor picks) against the float64 restatement (oracle/backward.py,
+    pinned by finite differences), routing held at the forward's: dx, d
+    router_w and every expert matrix within 1e-4 relative L2 (fp32) or 2e-2
+    (the bf16 flow's roundings)."""
+    from mixlab_amd.op import MoEFeedForward
+    from oracle.backward import backward64
+
+    flow, N, D, E, K, F, etype, act, slope, seed = case
+    print(f"case {case}", flush=True)
+    bf16 = flow == "bf16"
+    x, wr, experts = random_case(seed, N, D, E, F, expert_type=etype, wscale=0.1)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(m) for m in ws] for ws in experts]
+    dD = np.random.default_rng(seed + 1).standard_normal((N, D), dtype=np.float32)
+    up = bf16_bits if bf16 else (lambda a: a)
+    with MoEFeedForward([1, N, D, E, K, etype, F, act], [slope],
+                        compute_dtype="bf16" if bf16 else "fp32") as op:
+        op.set_weights(up(wr), [[up(m) for m in ws] for ws in experts])
+        dx, dwr, dexp = op.backward_host(x, dD, d_aux=0.3, d_entropy=-0.2)
+        routing = op.routing()
+        info = op.info()
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
+                      bf16=bf16)
+    assert_routing_equal(routing, want)
+    rdx, rdwr, rdexp = backward64(x, wr, experts, want["top_idx"].astype(np.int64), dD, 0.3, -0.2,
+                                  etype, act, slope)
+    tol = 2e-2 if bf16 else 1e-4
+    errs = [rel_l2(dx, rdx), rel_l2(dwr, rdwr)]
+    for m in range(len(experts[0])):
+        got = np.concatenate([dexp[e][m].ravel() for e in range(E)])
+        ref = np.concatenate([np.asarray(rdexp[e][m], np.float64).ravel() for e in range(E)])
+        errs.append(rel_l2(got, ref) if np.any(ref) else float(np.any(got)))
+    print(f"  {'mfma' if info['mfma'] else 'simt'}: rel L2 dx {errs[0]:.2e} dwr {errs[1]:.2e} "
+          f"experts {max(errs[2:]):.2e}")
+    assert max(errs) <= tol, errs
