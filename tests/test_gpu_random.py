@@ -168,3 +168,84 @@ def test_random_shapes_backward(gpu_lib, case):
     print(f"  {'mfma' if info['mfma'] else 'simt'}: rel L2 dx {errs[0]:.2e} dwr {errs[1]:.2e} "
           f"experts {max(errs[2:]):.2e}")
     assert max(errs) <= tol, errs
+
+
+def _block_cases(n=12, seed=2028):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        flow = ("fp32", "bf16", "int8")[len(cases) % 3]
+        etype, act = KINDS[int(rng.integers(len(KINDS)))]
+        E = int(rng.integers(1, 65))
+        K = int(rng.integers(1, min(E, 8) + 1))
+        N = int(rng.integers(1, 3000))
+        D = int(rng.integers(16, 1100))
+        F = int(rng.integers(16, 1500))
+        wpe = 2 if etype == 2 else 3
+        if N * K * D * F * wpe > 4e9:
+            continue
+        slope = float(np.round(rng.uniform(0.1, 0.5), 3)) if act == 3 else 0.0
+        with_scale = bool(rng.integers(2))
+        cases.append((flow, N, D, E, K, F, etype, act, slope, with_scale, int(rng.integers(1 << 30))))
+    return cases
+
+
+BLOCK_CASES = _block_cases()
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES,
+                         ids=[f"{c[0]}-N{c[1]}-D{c[2]}-E{c[3]}-K{c[4]}-F{c[5]}-k{c[6]}{c[7]}"
+                              f"{'-scale' if c[9] else ''}" for c in BLOCK_CASES])
+def test_random_blocks(gpu_lib, case):
+    """The fused block (RMSNorm, op 74, moe_scale, residual, aux weight) at
+    random shapes against the restatement: routing bit-exact (so the norm is
+    too); x_out bit-exact in fp32 (SIMT experts), the block's delta within
+    2e-2 (bf16) or 1e-3 (int8, against the exact products q * s)."""
+    from mixlab_amd.op import MoEFeedForward
+
+    flow, N, D, E, K, F, etype, act, slope, with_scale, seed = case
+    print(f"case {case}", flush=True)
+    rng = np.random.default_rng(seed)
+    x, wr, experts = random_case(seed, N, D, E, F, expert_type=etype)
+    x = x * np.float32(2.5)
+    ns = np.float32(1.0) + rng.standard_normal(D, dtype=np.float32) * np.float32(0.2)
+    ms = rng.standard_normal(D, dtype=np.float32) if with_scale else None
+    wpe = 2 if etype == 2 else 3
+    bf16 = flow != "fp32"
+    if bf16:
+        x, wr, ns = round_bf16(x), round_bf16(wr), round_bf16(ns)
+        ms = None if ms is None else round_bf16(ms)
+    conv = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
+    flags = _lib.MXM_FLAG_INT8_WEIGHTS if flow == "int8" else 0
+    with MoEFeedForward([1, N, D, E, K, etype, F, act], [slope],
+                        compute_dtype="bf16" if bf16 else "fp32", flags=flags) as op:
+        op.set_input(1, conv(wr))
+        if flow == "int8":
+            q8 = [[quantize_int8(m) for m in ws] for ws in experts]
+            for e in range(E):
+                for j in range(wpe):
+                    op.set_input_q8(2 + e * wpe + j, *q8[e][j])
+            feed = [[(q.astype(np.float32) * s[None, :]).astype(np.float32) for q, s in ws]
+                    for ws in q8]
+        else:
+            if bf16:
+                experts = [[round_bf16(m) for m in ws] for ws in experts]
+            for e in range(E):
+                for j in range(wpe):
+                    op.set_input(2 + e * wpe + j, conv(experts[e][j]))
+            feed = experts
+        out, aux, ent = op.block_forward_host(conv(x), conv(ns), None if ms is None else conv(ms),
+                                              eps=1e-5, aux_weight=0.03)
+        routing = op.routing()
+    want = oracle.block_forward(x, ns, wr, feed, top_k=K, expert_type=etype, activation=act,
+                                leaky_slope=slope, moe_scale=ms, eps=1e-5, aux_weight=0.03,
+                                bf16=bf16, prerounded=flow == "int8")
+    assert_routing_equal(routing, want)
+    if flow == "fp32":
+        assert same_bits(out, want["x_out"])
+    else:
+        err = rel_l2(out - x, want["x_out"] - x)
+        print(f"  {flow}: block delta rel L2 {err:.2e}")
+        assert err <= (1e-3 if flow == "int8" else 2e-2)
+    assert abs(aux - want["aux"]) <= (1e-5 if flow == "fp32" else 1e-2) * abs(want["aux"]) + 1e-7
+    assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"]) + 1e-7
