@@ -28,14 +28,14 @@ pytestmark = pytest.mark.gpu
 KINDS = [(0, 0), (1, 1), (2, 0), (2, 1), (2, 2), (2, 3)]  # (expert type, activation)
 
 
-def _cases(n=36, seed=2026):
+def _cases(n=36, seed=2026, max_e=80, max_k=8):
     rng = np.random.default_rng(seed)
     cases = []
     while len(cases) < n:
         flow = ("fp32", "bf16", "int8")[len(cases) % 3]
         etype, act = KINDS[int(rng.integers(len(KINDS)))]
-        E = int(rng.integers(1, 81))
-        K = int(rng.integers(1, min(E, 8) + 1))
+        E = int(rng.integers(1, max_e + 1))
+        K = int(rng.integers(1, min(E, max_k) + 1))
         N = int(rng.integers(1, 4001))
         D = int(rng.integers(16, 1100))
         F = int(rng.integers(16, 1500))
@@ -47,7 +47,9 @@ def _cases(n=36, seed=2026):
     return cases
 
 
-CASES = _cases()
+# the common regime, then wide routers: up to 256 experts (several expert
+# groups per lane) and top-k past one combine chunk of 8 slots
+CASES = _cases() + _cases(n=12, seed=2029, max_e=256, max_k=24)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-N{c[1]}-D{c[2]}-E{c[3]}-K{c[4]}-F{c[5]}-k{c[6]}{c[7]}"
