@@ -192,6 +192,106 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
   return ent_local;
 }
 
+// route_token for E <= SEG < 64 with 64 / SEG tokens on one wave at once:
+// lane l works on token slot l / SEG, expert e = l % SEG (SEG a power of
+// two).  Per token these are route_token's operations in route_token's
+// order: its butterfly steps of xor distance >= SEG only combine a lane
+// with lanes past E, which hold -inf (the max) or +0 (the sums), so
+// leaving them out changes no result (up to the sign of an all-zero
+// entropy term), and the rank counts the same larger keys (lanes past E
+// carry key 0).  Returns the token's entropy term in every lane of its
+// segment; p is -1 past E; lane e < K of a segment holds pick e.
+template <bool BF16, int SEG>
+__device__ __forceinline__ float route_token_seg(float v, int lane, int E, int K, float& p,
+                                                 int& pick_e, float& pick_g, RankScratch* rsc) {
+  const int e = lane & (SEG - 1), base = lane - e;
+  float m = e < E ? v : -__builtin_inff();
+#pragma unroll
+  for (int s = SEG / 2; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
+  const float ex = e < E ? mxm_exp(v - m) : 0.0f;
+  float sum = ex;
+#pragma unroll
+  for (int s = SEG / 2; s >= 1; s >>= 1) sum = sum + shfl_xor_f(sum, s);
+  float q = mxm_ftz(ex / sum);
+  if (BF16) q = mxm_rbf(q);
+  p = e < E ? q : -1.0f;
+  float ent = e < E ? q * logf(fmaxf(q, 1e-12f)) : 0.0f;
+#pragma unroll
+  for (int s = SEG / 2; s >= 1; s >>= 1) ent = ent + shfl_xor_f(ent, s);
+  // rank under (p desc, e asc) among the segment's keys, as route_token
+  const uint64_t key =
+      p >= 0.0f ? ((uint64_t)__builtin_bit_cast(uint32_t, p) << 6) | (uint64_t)(63 - e) : 0ull;
+  rsc->key[lane] = key;
+  __builtin_amdgcn_wave_barrier();
+  int rank = 0;
+#pragma unroll
+  for (int j2 = 0; j2 < SEG / 2; ++j2) {
+    const ulonglong2 q2 = reinterpret_cast<const ulonglong2*>(rsc->key + base)[j2];
+    rank += (q2.x > key) ? 1 : 0;
+    rank += (q2.y > key) ? 1 : 0;
+  }
+  if (rank < K) {
+    rsc->pick_p[base + rank] = p;
+    rsc->pick_e[base + rank] = e;
+  }
+  __builtin_amdgcn_wave_barrier();
+  float s_top = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const float bp = rsc->pick_p[base + k];
+    s_top = (k == 0) ? bp : s_top + bp;
+  }
+  float my_p = 0.0f;
+  pick_e = 0;
+  if (e < K) {
+    my_p = rsc->pick_p[base + e];
+    pick_e = rsc->pick_e[base + e];
+  }
+  __builtin_amdgcn_wave_barrier();  // rsc is free for the wave's next tokens
+  if (BF16) s_top = mxm_rbf(s_top);
+  pick_g = my_p / fmaxf(s_top, 1e-12f);
+  return ent;
+}
+
+// Phase 2 of the tiled router for E <= SEG: the wave's TPW tokens, 64 / SEG at
+// a time.  The per-expert probability sums (lane e) and the entropy sum take
+// the tokens one by one in token order, as the one-token-per-pass loop does.
+template <bool BF16, int SEG, int TPW, int LGS, int EPP>
+__device__ __forceinline__ void route_tile_seg(const float* lg, int wave, int lane, int n0, int N,
+                                               int E, int K, float* probs_out, int32_t* top_idx,
+                                               float* gates, uint32_t (*mask)[2], RankScratch* rsc,
+                                               float& psum, float& ent_acc) {
+  constexpr int S = 64 / SEG;  // tokens per pass
+  static_assert(TPW % S == 0, "whole passes");
+  const int sl = lane / SEG, e = lane & (SEG - 1);
+  for (int tt0 = 0; tt0 < TPW; tt0 += S) {
+    const int t = wave * TPW + tt0 + sl;
+    const int n = n0 + t;
+    const bool valid = n < N;
+    const float v = (valid && e < E) ? lg[t * LGS + e] : -__builtin_inff();
+    float p, pick_g;
+    int pick_e;
+    const float ent = route_token_seg<BF16, SEG>(v, lane, E, K, p, pick_e, pick_g, rsc);
+    // the pass's tokens one by one: lane e (< E) adds token s's p of expert e
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (n0 + wave * TPW + tt0 + s >= N) break;  // (tokens past N end the wave's list)
+      const float ps = __shfl(p, s * SEG + (lane & (SEG - 1)), 64);
+      const float es = __shfl(ent, s * SEG, 64);
+      if (lane < E) psum = psum + ps;
+      ent_acc = ent_acc + es;
+    }
+    if (valid) {
+      if (e < E && probs_out) probs_out[(size_t)n * E + e] = p;
+      if (e < K) {
+        top_idx[(size_t)n * K + e] = pick_e;
+        gates[(size_t)n * K + e] = pick_g;
+        atomicOr(&mask[pick_e][t >> 5], 1u << (t & 31));
+      }
+    }
+  }
+  (void)EPP;
+}
+
 // EPT = experts per thread in phase 1 (E padded to 16*EPT).
 template <typename TX, bool BF16, int EPT, bool VEC>
 __global__ __launch_bounds__(NT) void router_kernel(
@@ -365,7 +465,32 @@ __global__ __launch_bounds__(NT) void router_kernel(
   for (int j = 0; j < NJ; ++j) psum[j] = 0.0f;
   float ent_acc = 0.0f;
 
-  for (int tt = 0; tt < TM / NWAVE; ++tt) {
+  // E <= 32 (the EPT 1 and 2 instantiations): several tokens on one wave at
+  // once, a lane segment each
+  bool seg_done = false;
+  if constexpr (EPT <= 2) {
+    if (E <= 32) {
+      float ps = 0.0f;
+      constexpr int TPW = TM / NWAVE;
+      if (E <= 4)
+        route_tile_seg<BF16, 4, TPW, LG_STRIDE, EP>(lg, wave, lane, n0, N, E, K, probs_out, top_idx,
+                                                    gates, mask, &rank_scr[wave], ps, ent_acc);
+      else if (E <= 8)
+        route_tile_seg<BF16, 8, TPW, LG_STRIDE, EP>(lg, wave, lane, n0, N, E, K, probs_out, top_idx,
+                                                    gates, mask, &rank_scr[wave], ps, ent_acc);
+      else if (E <= 16)
+        route_tile_seg<BF16, 16, TPW, LG_STRIDE, EP>(lg, wave, lane, n0, N, E, K, probs_out,
+                                                     top_idx, gates, mask, &rank_scr[wave], ps,
+                                                     ent_acc);
+      else
+        route_tile_seg<BF16, 32, TPW, LG_STRIDE, EP>(lg, wave, lane, n0, N, E, K, probs_out,
+                                                     top_idx, gates, mask, &rank_scr[wave], ps,
+                                                     ent_acc);
+      psum[0] = ps;
+      seg_done = true;
+    }
+  }
+  for (int tt = 0; tt < TM / NWAVE && !seg_done; ++tt) {
     const int t = wave * (TM / NWAVE) + tt;
     const int n = n0 + t;
     if (n >= N) break;
