@@ -282,16 +282,18 @@ int fenced(F&& f) {
 // on the tiled router + scan + scatter.  The one-launch router's time grows
 // with N (a workgroup per token, then one workgroup's dispatch of the N*K
 // slots); the three-launch path's hardly does at these sizes.  So the one
-// launch pays while each token brings enough logit work: measured on MI355X
-// at N = 512-1024 over D*E = 512 .. 131072 (bf16 and fp32), it is the faster
-// one for every N <= 512, up to N = 768 from D*E = 4096 on, and up to
-// N = 1024 from D*E = 16384 on (the crossover lies at N ~ 560-600 for D*E of
-// 512-2048, ~750 for 4096, ~800-900 for 8192; results are bit for bit the
-// same either way).  The int8 decode flow is built on the one-launch router
-// and keeps it wherever it fits.
+// launch pays while each token brings enough logit work.  Measured on MI355X
+// over N = 64-1024 and D*E = 512 .. 131072 (bf16 and fp32; results are bit
+// for bit the same either way): for E > 32 it is the faster one for every
+// N <= 512, up to N = 768 from D*E = 4096 on and up to N = 1024 from
+// D*E = 16384 on; for E <= 32, where the tiled router routes several tokens
+// per wave, the crossover lies near N = 200-300 for D*E = 512, ~400 for
+// 4096, ~550 for 8192 and ~700 for 16384.  The int8 decode flow is built on
+// the one-launch router and keeps it wherever it fits.
 bool small_route_pays(int N, int D, int E) {
   const int64_t de = (int64_t)D * E;
-  return N <= 512 || (N <= 768 && de >= 4096) || de >= 16384;
+  if (E > 32) return N <= 512 || (N <= 768 && de >= 4096) || de >= 16384;
+  return N <= 256 || (N <= 512 && de >= 8192) || (N <= 640 && de >= 16384) || de >= 65536;
 }
 
 // Row-tile heights and tile counts of the forward's kernels; a function of

@@ -648,11 +648,17 @@ def test_decode_router_shapes(gpu_lib, monkeypatch, N, D, E, K, bf16):
 # (N, D, E, K, dtype, int8, the router the library picks): 0 tiled router +
 # scan + scatter, 1 the one-launch router, 2 the int8 decode flow
 ROUTER_CHOICE = [
+    # E <= 32 (the tiled router takes several tokens per wave)
     (1024, 128, 4, 2, "fp32", False, 0),    # C1, the reference's moe_tiny scale: D*E = 512
-    (512, 128, 4, 2, "fp32", False, 1),
-    (768, 512, 8, 2, "bf16", False, 1),     # D*E = 4096
-    (1024, 512, 8, 2, "bf16", False, 0),
-    (1024, 2048, 8, 2, "bf16", False, 1),   # D*E = 16384
+    (256, 128, 4, 2, "fp32", False, 1),
+    (512, 128, 4, 2, "fp32", False, 0),
+    (512, 256, 32, 4, "bf16", False, 1),    # D*E = 8192
+    (640, 1024, 16, 2, "bf16", False, 1),   # D*E = 16384
+    (1024, 1024, 16, 2, "bf16", False, 0),
+    # E > 32
+    (768, 128, 64, 8, "bf16", False, 1),    # D*E = 8192
+    (1024, 128, 64, 8, "bf16", False, 0),
+    (1024, 512, 64, 8, "bf16", False, 1),   # D*E = 32768
     (1024, 256, 8, 2, "bf16", True, 2),     # int8 keeps the decode flow
     (1100, 2048, 64, 8, "bf16", False, 0),  # past the one-launch router's limit
 ]
