@@ -19,7 +19,7 @@
 
 namespace {
 
-constexpr int BK = 16, NT = 256;
+constexpr int NT = 256;
 
 __device__ __forceinline__ int find_expert(const int32_t* mstart, int E, int mtile) {
   int lo = 0, hi = E - 1;
@@ -57,8 +57,9 @@ __device__ __forceinline__ void lds_vec(const float* p, float (&v)[T]) {
   }
 }
 
-// BM x BN tile, TM x TN outputs per thread (a 16 x 16 thread grid).
-template <typename TA, bool BF16, int MODE, int BM, int BN>
+// BM x BN tile, TM x TN outputs per thread (a 16 x 16 thread grid), k tiles
+// of BK.
+template <typename TA, bool BF16, int MODE, int BM, int BN, int BK>
 __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   constexpr int NB = (MODE == MXM_GEMM_GLU) ? 2 : 1;
   constexpr int TM = BM / 16, TN = BN / 16;
@@ -193,19 +194,25 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
   }
 }
 
+// k tiles of 16 for the 64 x 64 tile (each thread's 16 outputs per k step
+// amortise the tile's barriers), 32 for the 32 x 32 tile (4 outputs per k
+// step: half as many barrier and LDS round trips per k)
 template <typename TA, bool BF16, int T>
 void launch_t(const GemmArgs& a, hipStream_t s) {
+  constexpr int BK = T == 64 ? 16 : 32;
   const dim3 grid((a.Ncols + T - 1) / T, a.max_mtiles);
   switch (a.mode) {
     case MXM_GEMM_GLU:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU, T, T>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU, T, T, BK>), grid, dim3(NT), 0,
+                         s, a);
       break;
     case MXM_GEMM_MLP:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP, T, T>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP, T, T, BK>), grid, dim3(NT), 0,
+                         s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN, T, T>), grid, dim3(NT), 0,
-                         s, a);
+      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN, T, T, BK>), grid, dim3(NT),
+                         0, s, a);
       break;
   }
 }
