@@ -157,6 +157,71 @@ def test_noalloc_matches_forward(gpu_lib, name, big, small):
             op.close()
 
 
+def _random_pairs(n=6, seed=2030):
+    """Seeded pairs of op shapes over every flow, each workspace within the
+    scratch array (the draw is repeated otherwise)."""
+    rng = np.random.default_rng(seed)
+    kinds = [(0, 0), (1, 1), (2, 0), (2, 1), (2, 2), (2, 3)]
+    flows = [dict(dtype="fp32"), dict(dtype="bf16"), dict(dtype="bf16", int8=True)]
+
+    def draw(flow):
+        etype, act = kinds[int(rng.integers(len(kinds)))]
+        E = int(rng.integers(1, 65))
+        return dict(B=1, T=int(rng.integers(1, 3000)), D=int(rng.integers(16, 900)), E=E,
+                    K=int(rng.integers(1, min(E, 8) + 1)), F=int(rng.integers(16, 1200)),
+                    etype=etype, act=act, **flow)
+
+    def fits(c):
+        NK = c["T"] * c["K"]
+        # a generous bound on the workspace (H and Y at 4 bytes per element
+        # in padded widths, plus the routing tables)
+        return NK * (2 * (c["F"] + 128) + (c["D"] + 128)) * 4 + (8 << 20) < (48 << 20)
+
+    pairs = []
+    while len(pairs) < n:
+        flow = flows[len(pairs) % 3]
+        first, second = draw(flow), draw(flow)
+        if fits(first) and fits(second):
+            pairs.append((first, second))
+    return pairs
+
+
+RANDOM_PAIRS = _random_pairs()
+
+
+@pytest.mark.parametrize("first,second", RANDOM_PAIRS,
+                         ids=[f"{b.get('dtype')}{'-int8' if b.get('int8') else ''}-T{b['T']}"
+                              f"-D{b['D']}-E{b['E']}" for b, _ in RANDOM_PAIRS])
+def test_noalloc_random_pairs(gpu_lib, first, second):
+    """Random op shapes through the no-allocation forward, two ops in a row
+    on the shared scratch: bit for bit the allocating forward's results."""
+    lib = _lib.init()
+    print(f"no-alloc random {first} then {second}", flush=True)
+    ops = [_make_op(3, **first), _make_op(4, **second)]
+    ios = [IO(lib, op, xh) for op, xh in ops]
+    try:
+        for op, _ in ops:
+            assert op.info()["workspace_bytes"] <= _lib.MXM_NOALLOC_MAX_BYTES
+        got = []
+        for io in ios:
+            io.forward(noalloc=True)
+            got.append(io.results())
+        want = []
+        for io in ios:
+            io.forward(noalloc=False)
+            want.append(io.results())
+        for (d, a, e, r), (wd, wa, we, wr) in zip(got, want):
+            assert np.array_equal(d.view(np.uint32), wd.view(np.uint32))
+            assert a == wa and e == we
+            for k in ("top_idx", "gates", "counts", "offsets", "perm"):
+                assert np.array_equal(r[k], wr[k]), k
+    finally:
+        for io in ios:
+            io.free()
+        for op, _ in ops:
+            op.close()
+
+
 def test_noalloc_refuses_oversized_workspace(gpu_lib):
     """2^17 tokens x top-2 x F 256 in bf16 needs 128 MiB for H alone."""
     from mixlab_amd.op import MoEFeedForward
