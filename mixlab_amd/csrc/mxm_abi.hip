@@ -160,8 +160,9 @@ struct MoeOp {
   // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
   // bf16 [E][2F or F][D] (GLU interleaved), w2 = bf16 [E][D][F].
   DevBuf router, w1, w1b, w2;
-  // decode-sized batches: router_w in fp32, lane-interleaved (RouteSmallArgs::wr_t)
-  bool small_route = false;
+  // decode-sized batches, and the tiled router's matrix-core logits (32 < E
+  // <= 64): router_w lane-interleaved (RouteSmallArgs::wr_t)
+  bool small_route = false, mf_router = false;
   int ldw = 0;
   DevBuf router_t;
   // int8 family: q1 = gate (GLU) or up (MLP), q1b = up (GLU), q2 = down, in
@@ -512,6 +513,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     ra.tile_psum = w.tile_psum;
     ra.tile_ent = w.tile_ent;
     ra.probs_out = probs_keep;
+    ra.wr_t = o.mf_router ? o.router_t.p : nullptr;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_router(ra, o.bf16, st);
     HIPCK(hipGetLastError());
 
@@ -732,7 +734,7 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
       mxm_launch_to_bf16(src, dtype, o.router.as<uint16_t>(), (int64_t)n, st);
     else
       mxm_launch_to_f32(src, dtype, o.router.as<float>(), (int64_t)n, st);
-    if (o.small_route)
+    if (o.small_route || o.mf_router)
       mxm_launch_router_t(o.router.p, o.bf16, o.D, o.E, o.ldw, o.router_t.p, st);
   } else if (o.mfma) {
     // rows of Fk (W_down [Dk][Fk]) and of Kx (W1 [NC][Kx]); the padding stays
@@ -1031,7 +1033,9 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     if (const char* v = std::getenv("MXM_SMALL_ROUTE"))
       o->small_route = std::atoi(v) != 0 && mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
-    if (o->small_route) {
+    o->mf_router = o->E > 32 && o->E <= 64;
+    if (const char* v = std::getenv("MXM_ROUTER_MFMA")) o->mf_router = o->mf_router && std::atoi(v) != 0;
+    if (o->small_route || o->mf_router) {
       o->ldw = (o->D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
       o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * (o->bf16 ? 2 : 4));
     }

@@ -121,15 +121,20 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
   }
   if constexpr (NJ == 1) {
     // E <= 64: each lane's rank under the same order, from the wave's 64
-    // keys in LDS (broadcast reads): key = (bits of p) << 6 | (63 - lane), an
-    // integer order equal to (p desc, e asc) on p >= 0; lanes past E (p = -1)
-    // take key 0 and rank after every expert.  The lane of rank k < K leaves
-    // its probability and expert in pick slot k; every lane then reads the K
+    // keys in LDS (broadcast reads): key = (bits of p + 2) << 6 | (63 - lane),
+    // an integer order equal to (p desc, e asc) on p >= 0.  A NaN p (every p
+    // of a token with a non-finite logit) takes 64 | (63 - lane) and a lane
+    // past E (p = -1) 63 - lane, below every p >= 0: the 64 keys are distinct,
+    // so the ranks are a permutation and the K <= E picks distinct experts
+    // below E, whatever the inputs.  The lane of rank k < K leaves its
+    // probability and expert in pick slot k; every lane then reads the K
     // picks in k order.  (One wave owns rsc; its LDS operations complete in
     // program order.)
     const float pl = p[0];
-    const uint64_t key =
-        pl >= 0.0f ? ((uint64_t)__builtin_bit_cast(uint32_t, pl) << 6) | (uint64_t)(63 - lane) : 0ull;
+    const uint64_t lo = (uint64_t)(63 - lane);
+    const uint64_t key = pl >= 0.0f ? (((uint64_t)__builtin_bit_cast(uint32_t, pl) + 2) << 6) | lo
+                         : lane < E ? (64ull | lo)
+                                    : lo;
     rsc->key[lane] = key;
     __builtin_amdgcn_wave_barrier();
     int rank = 0;
@@ -155,14 +160,17 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
     __builtin_amdgcn_wave_barrier();  // rsc is free for the wave's next token
     (void)taken;
   } else {
+    // a NaN p (every p of a token with a non-finite logit) competes as -1.5,
+    // below every p >= 0, so each round picks an untaken expert below E
     for (int k = 0; k < K; ++k) {
       float bp = -2.0f;
       int be = 0x7fffffff;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
-        if (e < E && !((taken >> j) & 1u) && p[j] > bp) {
-          bp = p[j];
+        const float c = p[j] >= 0.0f ? p[j] : -1.5f;
+        if (e < E && !((taken >> j) & 1u) && c > bp) {
+          bp = c;
           be = e;
         }
       }
@@ -176,6 +184,7 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
         }
       }
       if ((be & 63) == lane) taken |= 1u << (be >> 6);
+      if (bp < 0.0f) bp = __builtin_nanf("");  // the NaN it stood for
       s_top = (k == 0) ? bp : s_top + bp;
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
@@ -199,7 +208,7 @@ __device__ __forceinline__ float route_token(const float (&v)[NJ], int lane, int
 // with lanes past E, which hold -inf (the max) or +0 (the sums), so
 // leaving them out changes no result (up to the sign of an all-zero
 // entropy term), and the rank counts the same larger keys (lanes past E
-// carry key 0).  Returns the token's entropy term in every lane of its
+// carry the lowest keys).  Returns the token's entropy term in every lane of its
 // segment; p is -1 past E; lane e < K of a segment holds pick e.
 template <bool BF16, int SEG>
 __device__ __forceinline__ float route_token_seg(float v, int lane, int E, int K, float& p,
@@ -219,8 +228,11 @@ __device__ __forceinline__ float route_token_seg(float v, int lane, int E, int K
 #pragma unroll
   for (int s = SEG / 2; s >= 1; s >>= 1) ent = ent + shfl_xor_f(ent, s);
   // rank under (p desc, e asc) among the segment's keys, as route_token
-  const uint64_t key =
-      p >= 0.0f ? ((uint64_t)__builtin_bit_cast(uint32_t, p) << 6) | (uint64_t)(63 - e) : 0ull;
+  // (distinct keys: NaN p below every p >= 0, lanes past E lowest)
+  const uint64_t lo = (uint64_t)(63 - e);
+  const uint64_t key = p >= 0.0f ? (((uint64_t)__builtin_bit_cast(uint32_t, p) + 2) << 6) | lo
+                       : e < E ? (64ull | lo)
+                               : lo;
   rsc->key[lane] = key;
   __builtin_amdgcn_wave_barrier();
   int rank = 0;
@@ -292,19 +304,150 @@ __device__ __forceinline__ void route_tile_seg(const float* lg, int wave, int la
   (void)EPP;
 }
 
-// EPT = experts per thread in phase 1 (E padded to 16*EPT).
-template <typename TX, bool BF16, int EPT, bool VEC>
+// ---- logits on the fp32 matrix cores (E in 33..64) -------------------------
+// v_mfma_f32_16x16x1_4b_f32 is four 16 x 16 blocks of fused multiply-adds
+// with one product each: D = C + A B rounded once, to nearest even,
+// denormals kept -- the fmaf of the logits' summation order, bit for bit
+// (checked on the part against fmaf chains over bf16-valued, fp32, wide-
+// exponent, denormal, signed-zero and cancelling operands).  A chain of them
+// over a chunk's d from +0 is therefore the SIMT path's chunk partial, at
+// twice the rate of the non-packed fp32 FMA.
+//
+// A wave computes 16 tokens x 64 experts.  A = tokens, broadcast to the four
+// blocks from lane group k = lane / 16 (cbsz 2, abid k); B = experts, lane l
+// holding expert l (blocks b = experts 16 b .. 16 b + 15).  The output's
+// register 4 b + q in lane l is token (l / 16) * 4 + q, expert 16 b + l % 16.
+// A round is 32 d: lane group k loads its token's d0 + 8k .. d0 + 8k + 7
+// from x (one 16-byte piece in bf16, two in fp32), and every lane its
+// expert's 32 d from the lane-interleaved router copy (4 or 8 pieces).
+typedef float mxm_lg16 __attribute__((ext_vector_type(16)));
+
+template <typename TX>
+struct LgRound {
+  static constexpr int P = 16 / (int)sizeof(TX);  // values per 16-byte piece
+  uint4 xu[8 / P];
+  uint4 wu[32 / P];
+};
+
+// value j (< P) of a 16-byte piece
+template <typename TX>
+__device__ __forceinline__ float lg_val(const uint4& u, int j) {
+  const int wi = sizeof(TX) == 2 ? (j >> 1) : j;
+  const uint32_t w = wi == 0 ? u.x : wi == 1 ? u.y : wi == 2 ? u.z : u.w;
+  if constexpr (sizeof(TX) == 2) return mxm_u2f((j & 1) ? (w & 0xffff0000u) : (w << 16));
+  else return mxm_u2f(w);
+}
+
+// x through a buffer descriptor over the wave's 16 token rows: the loads
+// are unconditional (a range check in the load returns zeros), so every
+// path leaves the same loads in flight and the wait before a round counts
+// only the older round's.  Word 3 of a gfx9 raw buffer descriptor: 32-bit
+// data format, no swizzle.
+constexpr int LG_RSRC_W3 = 0x00020000;
+constexpr int LG_OUT_OF_RANGE = 0x7ffffff0;  // above any wave's record count
+typedef uint32_t lg_u4 __attribute__((ext_vector_type(4)));
+
+// Round r's pieces.  x pieces at or past D (D % P == 0, so a piece is wholly
+// in or out) take an offset past the records and tokens past N lie past
+// them, so both load as zeros; the router copy is zero past D up to its
+// ldw, a multiple of 64 >= 32 * rounds.
+template <typename TX>
+__device__ __forceinline__ void lg_load(LgRound<TX>& R, __amdgpu_buffer_rsrc_t xs, int xoff, int D,
+                                        const uint4* wt, int lane, int r) {
+  constexpr int P = LgRound<TX>::P;
+  const int d0 = 32 * r + 8 * (lane >> 4);
+#pragma unroll
+  for (int h = 0; h < 8 / P; ++h) {
+    const int d = d0 + P * h;
+    const int off = d < D ? xoff + d * (int)sizeof(TX) : LG_OUT_OF_RANGE;
+    const lg_u4 v = __builtin_amdgcn_raw_buffer_load_b128(xs, off, 0, 0);
+    R.xu[h] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+  const uint4* wp = wt + (size_t)(32 / P) * r * 64 + lane;
+#pragma unroll
+  for (int c = 0; c < 32 / P; ++c) R.wu[c] = wp[c * 64];
+}
+
+// the 8 d of lane group KK: d0 + 8 KK + t, t ascending
+template <typename TX, int KK, bool FIRST>
+__device__ __forceinline__ void lg_group(const LgRound<TX>& R, mxm_lg16& c) {
+  constexpr int P = LgRound<TX>::P;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float a = lg_val<TX>(R.xu[t / P], t % P);
+    const float b = lg_val<TX>(R.wu[(8 * KK + t) / P], (8 * KK + t) % P);
+    if (FIRST && t == 0)
+      c = __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, mxm_lg16{}, 2, KK, 0);
+    else
+      c = __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 2, KK, 0);
+  }
+}
+
+// a round's 32 d in ascending order; FIRST starts the chunk partial at +0
+template <typename TX, bool FIRST>
+__device__ __forceinline__ void lg_round(const LgRound<TX>& R, mxm_lg16& c) {
+  lg_group<TX, 0, FIRST>(R, c);
+  lg_group<TX, 1, false>(R, c);
+  lg_group<TX, 2, false>(R, c);
+  lg_group<TX, 3, false>(R, c);
+}
+
+// The logits of tokens n0w .. n0w + 15 against the 64 (padded) experts: per
+// 64-d chunk (two rounds) a partial from +0, added to the logit (from +0) in
+// chunk order.  Both rounds of the last chunk run: past D the x pieces and
+// the router copy (zero up to ldw) are zeros, and fma(0, 0, c) = c for every
+// c a chain from +0 can reach (it never reaches -0).  The next round's
+// pieces are loaded while a round computes (after the last chunk, its
+// second round again, unused).  Needs 16 D sizeof(TX) < 2^30 (the launcher
+// checks).
+template <typename TX>
+__device__ __forceinline__ mxm_lg16 logits_mfma(const TX* x, const TX* wr_t, int N, int D,
+                                                int n0w, int lane) {
+  // (readfirstlane: the clamp is computed on the vector unit, and a
+  // descriptor in vector registers would be taken apart lane by lane)
+  const int rows = __builtin_amdgcn_readfirstlane(N - n0w >= 16 ? 16 : N - n0w > 0 ? N - n0w : 0);
+  const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<TX*>(rows > 0 ? x + (size_t)n0w * D : x), (short)0, rows * D * (int)sizeof(TX),
+      LG_RSRC_W3);
+  const int xoff = (lane & 15) * D * (int)sizeof(TX);
+  const uint4* wt = reinterpret_cast<const uint4*>(wr_t);
+  const int nch = (D + 63) / 64;
+  mxm_lg16 lgt = {};
+  LgRound<TX> ra, rb;
+  // (the scheduling barriers keep each round's loads issued before the
+  // other round's products instead of next to their own uses)
+  lg_load<TX>(ra, xs, xoff, D, wt, lane, 0);
+  for (int ch = 0; ch < nch; ++ch) {
+    lg_load<TX>(rb, xs, xoff, D, wt, lane, 2 * ch + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mxm_lg16 part;
+    lg_round<TX, true>(ra, part);
+    __builtin_amdgcn_sched_barrier(0);
+    lg_load<TX>(ra, xs, xoff, D, wt, lane, min(2 * ch + 2, 2 * nch - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    lg_round<TX, false>(rb, part);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lgt[i] = lgt[i] + part[i];
+  }
+  return lgt;
+}
+
+// EPT = experts per thread in phase 1 (E padded to 16*EPT).  MF: phase 1 on
+// the fp32 matrix cores (EPT 4 only; wr_t is the lane-interleaved router copy
+// [ldw/P][64][P], x 16-byte aligned with D % P == 0).
+template <typename TX, bool BF16, int EPT, bool VEC, bool MF = false>
 __global__ __launch_bounds__(NT) void router_kernel(
     const TX* __restrict__ x, const TX* __restrict__ wr, int N, int D, int E, int K,
     int32_t* __restrict__ top_idx, float* __restrict__ gates, int32_t* __restrict__ slot_rank,
     int32_t* __restrict__ tile_counts, float* __restrict__ tile_psum, float* __restrict__ tile_ent,
-    float* __restrict__ probs_out, int ntiles) {
+    float* __restrict__ probs_out, int ntiles,
+    const TX* __restrict__ wr_t) {
   constexpr int EP = 16 * EPT;
   constexpr int NJ = (EP + 63) / 64;  // experts per lane in phase 2
   constexpr int LG_STRIDE = EP + 1;
   constexpr int STAGE_FLOATS = BK * TM + BK * EP;
   constexpr int LG_FLOATS = TM * LG_STRIDE;
-  constexpr int SMEM_FLOATS = STAGE_FLOATS > LG_FLOATS ? STAGE_FLOATS : LG_FLOATS;
+  constexpr int SMEM_FLOATS = MF ? LG_FLOATS : STAGE_FLOATS > LG_FLOATS ? STAGE_FLOATS : LG_FLOATS;
   __shared__ __attribute__((aligned(16))) float smem[SMEM_FLOATS];
   __shared__ uint32_t mask[EP][2];
   constexpr int THREADS = NT;
@@ -323,139 +466,153 @@ __global__ __launch_bounds__(NT) void router_kernel(
   for (int i = tid; i < EP * 2; i += THREADS) (&mask[0][0])[i] = 0u;
 
   // ---- phase 1: logits --------------------------------------------------
-  const int ty = tid >> 4;  // tokens ty*4 .. ty*4+3
-  const int tx = tid & 15;  // experts tx*EPT .. tx*EPT+EPT-1
-  float acc[4][EPT];
+  if constexpr (MF) {
+    static_assert(EPT == 4, "the matrix-core logits cover 64 experts");
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;  // wv: uniform
+    const mxm_lg16 v = logits_mfma<TX>(x, wr_t, N, D, n0 + 16 * wv, ln);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
-
-  // products of one BK chunk held in LDS (BK is the logits' 64-d summation
-  // chunk): a partial from +0, then added to the logit
-  static_assert(BK == MXM_LOGIT_CHUNK, "one LDS chunk per summation chunk");
-  auto compute = [&]() {
-    float part[4][EPT];
+      for (int q = 0; q < 4; ++q) {
+        const int t = 16 * wv + (ln >> 4) * 4 + q;
+        lg[t * LG_STRIDE + 16 * b + (ln & 15)] = BF16 ? mxm_rbf(v[4 * b + q]) : v[4 * b + q];
+      }
+    __syncthreads();
+  } else {
+    const int ty = tid >> 4;  // tokens ty*4 .. ty*4+3
+    const int tx = tid & 15;  // experts tx*EPT .. tx*EPT+EPT-1
+    float acc[4][EPT];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < EPT; ++j) part[i][j] = 0.0f;
-#pragma unroll 4
-    for (int dd = 0; dd < BK; ++dd) {
-      const float4 xv = *reinterpret_cast<const float4*>(&xs[dd * TM + ty * 4]);
-      float wv[EPT];
+      for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
+
+    // products of one BK chunk held in LDS (BK is the logits' 64-d summation
+    // chunk): a partial from +0, then added to the logit
+    static_assert(BK == MXM_LOGIT_CHUNK, "one LDS chunk per summation chunk");
+    auto compute = [&]() {
+      float part[4][EPT];
 #pragma unroll
-      for (int j = 0; j < EPT; ++j) wv[j] = ws[dd * EP + tx * EPT + j];
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) part[i][j] = 0.0f;
+#pragma unroll 4
+      for (int dd = 0; dd < BK; ++dd) {
+        const float4 xv = *reinterpret_cast<const float4*>(&xs[dd * TM + ty * 4]);
+        float wv[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) wv[j] = ws[dd * EP + tx * EPT + j];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          part[0][j] = __builtin_fmaf(xv.x, wv[j], part[0][j]);
+          part[1][j] = __builtin_fmaf(xv.y, wv[j], part[1][j]);
+          part[2][j] = __builtin_fmaf(xv.z, wv[j], part[2][j]);
+          part[3][j] = __builtin_fmaf(xv.w, wv[j], part[3][j]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) acc[i][j] = acc[i][j] + part[i][j];
+    };
+    if constexpr (VEC) {
+      // 16-byte pieces of x (token-fastest across lanes, so the transposed LDS
+      // store is conflict-free) and of router_w rows.  The next chunk's pieces
+      // are loaded into registers while the current chunk's products run;
+      // pieces outside [N, D] x [D, E] are loaded from a valid address and
+      // zeroed when stored.
+      constexpr int PER = 16 / (int)sizeof(TX);
+      constexpr int XPC = TM * BK / PER;  // x pieces per chunk
+      constexpr int WPC = BK * EP / PER;  // router_w pieces per chunk
+      constexpr int XP = (XPC + NT - 1) / NT, WP = (WPC + NT - 1) / NT;
+      static_assert(WP <= 32 && XP <= 32, "validity masks are 32 bits");
+      uint4 xr[XP], wrr[WP];
+      uint32_t xok = 0u, wok = 0u;
+      auto load = [&](int d0) {
+        xok = 0u;
+        wok = 0u;
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+          const int i = tid + p * NT;
+          const int t = i % TM, dc = i / TM;
+          const int n = n0 + t, d = d0 + dc * PER;
+          const bool ok = i < XPC && n < N && d < D;
+          xr[p] = *reinterpret_cast<const uint4*>(x + (ok ? (size_t)n * D + d : 0));
+          xok |= ok ? (1u << p) : 0u;
+        }
+#pragma unroll
+        for (int p = 0; p < WP; ++p) {
+          const int j = tid + p * NT;
+          const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
+          const int d = d0 + dd;
+          const bool ok = j < WPC && d < D && ec < E;
+          wrr[p] = *reinterpret_cast<const uint4*>(wr + (ok ? (size_t)d * E + ec : 0));
+          wok |= ok ? (1u << p) : 0u;
+        }
+      };
+      auto store = [&]() {
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+          const int i = tid + p * NT;
+          if (i < XPC) {
+            const int t = i % TM, dc = i / TM;
+            float f[PER];
+            unpack16<TX>(xr[p], f);
+            const bool ok = (xok >> p) & 1u;
+#pragma unroll
+            for (int q = 0; q < PER; ++q) xs[(dc * PER + q) * TM + t] = ok ? f[q] : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < WP; ++p) {
+          const int j = tid + p * NT;
+          if (j < WPC) {
+            const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
+            float f[PER];
+            unpack16<TX>(wrr[p], f);
+            const bool ok = (wok >> p) & 1u;
+#pragma unroll
+            for (int q = 0; q < PER; q += 4)
+              *reinterpret_cast<float4*>(&ws[dd * EP + ec + q]) =
+                  ok ? make_float4(f[q], f[q + 1], f[q + 2], f[q + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+      };
+      load(0);
+      for (int d0 = 0; d0 < D; d0 += BK) {
+        __syncthreads();  // the previous chunk's products are done with LDS
+        store();
+        __syncthreads();
+        if (d0 + BK < D) load(d0 + BK);
+        compute();
+      }
+    } else {
+      for (int d0 = 0; d0 < D; d0 += BK) {
+        __syncthreads();
+        for (int i = tid; i < TM * BK; i += NT) {
+          const int t = i % TM, dd = i / TM;
+          const int n = n0 + t, d = d0 + dd;
+          xs[dd * TM + t] = (n < N && d < D) ? ld_as_f32<TX>(x + (size_t)n * D + d) : 0.0f;
+        }
+        for (int i = tid; i < BK * EP; i += NT) {
+          const int dd = i / EP, e = i % EP;
+          const int d = d0 + dd;
+          ws[i] = (d < D && e < E) ? ld_as_f32<TX>(wr + (size_t)d * E + e) : 0.0f;
+        }
+        __syncthreads();
+        compute();
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
-        part[0][j] = __builtin_fmaf(xv.x, wv[j], part[0][j]);
-        part[1][j] = __builtin_fmaf(xv.y, wv[j], part[1][j]);
-        part[2][j] = __builtin_fmaf(xv.z, wv[j], part[2][j]);
-        part[3][j] = __builtin_fmaf(xv.w, wv[j], part[3][j]);
+        const float v = acc[i][j];
+        lg[(ty * 4 + i) * LG_STRIDE + tx * EPT + j] = BF16 ? mxm_rbf(v) : v;
       }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) acc[i][j] = acc[i][j] + part[i][j];
-  };
-  if constexpr (VEC) {
-    // 16-byte pieces of x (token-fastest across lanes, so the transposed LDS
-    // store is conflict-free) and of router_w rows.  The next chunk's pieces
-    // are loaded into registers while the current chunk's products run;
-    // pieces outside [N, D] x [D, E] are loaded from a valid address and
-    // zeroed when stored.
-    constexpr int PER = 16 / (int)sizeof(TX);
-    constexpr int XPC = TM * BK / PER;  // x pieces per chunk
-    constexpr int WPC = BK * EP / PER;  // router_w pieces per chunk
-    constexpr int XP = (XPC + NT - 1) / NT, WP = (WPC + NT - 1) / NT;
-    static_assert(WP <= 32 && XP <= 32, "validity masks are 32 bits");
-    uint4 xr[XP], wrr[WP];
-    uint32_t xok = 0u, wok = 0u;
-    auto load = [&](int d0) {
-      xok = 0u;
-      wok = 0u;
-#pragma unroll
-      for (int p = 0; p < XP; ++p) {
-        const int i = tid + p * NT;
-        const int t = i % TM, dc = i / TM;
-        const int n = n0 + t, d = d0 + dc * PER;
-        const bool ok = i < XPC && n < N && d < D;
-        xr[p] = *reinterpret_cast<const uint4*>(x + (ok ? (size_t)n * D + d : 0));
-        xok |= ok ? (1u << p) : 0u;
-      }
-#pragma unroll
-      for (int p = 0; p < WP; ++p) {
-        const int j = tid + p * NT;
-        const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
-        const int d = d0 + dd;
-        const bool ok = j < WPC && d < D && ec < E;
-        wrr[p] = *reinterpret_cast<const uint4*>(wr + (ok ? (size_t)d * E + ec : 0));
-        wok |= ok ? (1u << p) : 0u;
-      }
-    };
-    auto store = [&]() {
-#pragma unroll
-      for (int p = 0; p < XP; ++p) {
-        const int i = tid + p * NT;
-        if (i < XPC) {
-          const int t = i % TM, dc = i / TM;
-          float f[PER];
-          unpack16<TX>(xr[p], f);
-          const bool ok = (xok >> p) & 1u;
-#pragma unroll
-          for (int q = 0; q < PER; ++q) xs[(dc * PER + q) * TM + t] = ok ? f[q] : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int p = 0; p < WP; ++p) {
-        const int j = tid + p * NT;
-        if (j < WPC) {
-          const int dd = j / (EP / PER), ec = (j % (EP / PER)) * PER;
-          float f[PER];
-          unpack16<TX>(wrr[p], f);
-          const bool ok = (wok >> p) & 1u;
-#pragma unroll
-          for (int q = 0; q < PER; q += 4)
-            *reinterpret_cast<float4*>(&ws[dd * EP + ec + q]) =
-                ok ? make_float4(f[q], f[q + 1], f[q + 2], f[q + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-    };
-    load(0);
-    for (int d0 = 0; d0 < D; d0 += BK) {
-      __syncthreads();  // the previous chunk's products are done with LDS
-      store();
-      __syncthreads();
-      if (d0 + BK < D) load(d0 + BK);
-      compute();
-    }
-  } else {
-    for (int d0 = 0; d0 < D; d0 += BK) {
-      __syncthreads();
-      for (int i = tid; i < TM * BK; i += NT) {
-        const int t = i % TM, dd = i / TM;
-        const int n = n0 + t, d = d0 + dd;
-        xs[dd * TM + t] = (n < N && d < D) ? ld_as_f32<TX>(x + (size_t)n * D + d) : 0.0f;
-      }
-      for (int i = tid; i < BK * EP; i += NT) {
-        const int dd = i / EP, e = i % EP;
-        const int d = d0 + dd;
-        ws[i] = (d < D && e < E) ? ld_as_f32<TX>(wr + (size_t)d * E + e) : 0.0f;
-      }
-      __syncthreads();
-      compute();
-    }
+    __syncthreads();
   }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const float v = acc[i][j];
-      lg[(ty * 4 + i) * LG_STRIDE + tx * EPT + j] = BF16 ? mxm_rbf(v) : v;
-    }
-  __syncthreads();
 
   // ---- phase 2: softmax, top-k, gates -----------------------------------
   const int lane = tid & 63;
@@ -948,19 +1105,27 @@ template <typename TX, bool BF16, int EPT>
 void launch_router_t(const RouterArgs& a, hipStream_t s) {
   const int ntiles = (a.N + TM - 1) / TM;
   constexpr int PER = 16 / (int)sizeof(TX);
-  const bool vec = a.D % PER == 0 && a.E % PER == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.x) % 16) == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.wr) % 16) == 0;
+  const bool xvec = a.D % PER == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+  const bool vec = xvec && a.E % PER == 0 && (reinterpret_cast<uintptr_t>(a.wr) % 16) == 0;
+  const TX* x = static_cast<const TX*>(a.x);
+  const TX* wr = static_cast<const TX*>(a.wr);
+  const TX* wr_t = static_cast<const TX*>(a.wr_t);
+  if constexpr (EPT == 4) {
+    if (wr_t && xvec && a.E > 32 && a.D <= (1 << 24)) {
+      hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true, true>), dim3(ntiles), dim3(NT), 0, s,
+                         x, wr, a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank,
+                         a.tile_counts, a.tile_psum, a.tile_ent, a.probs_out, ntiles, wr_t);
+      return;
+    }
+  }
   if (vec)
-    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true>), dim3(ntiles), dim3(NT), 0, s,
-                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
-                       a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts, a.tile_psum,
-                       a.tile_ent, a.probs_out, ntiles);
+    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true>), dim3(ntiles), dim3(NT), 0, s, x, wr,
+                       a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts,
+                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr);
   else
-    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false>), dim3(ntiles), dim3(NT), 0, s,
-                       static_cast<const TX*>(a.x), static_cast<const TX*>(a.wr), a.N, a.D, a.E,
-                       a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts, a.tile_psum,
-                       a.tile_ent, a.probs_out, ntiles);
+    hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false>), dim3(ntiles), dim3(NT), 0, s, x, wr,
+                       a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts,
+                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr);
 }
 
 template <typename TX, bool BF16>

@@ -718,6 +718,125 @@ def test_router_choice(gpu_lib, monkeypatch, N, D, E, K, dtype, int8, want):
         assert_routing_equal(got[3], want_o)
 
 
+# (N, D, E, K, dtype): partial last tiles and waves, D past whole chunks and
+# rounds (D % 64 in {8, 32, 40}, one 8-wide piece), 33..64 experts
+ROUTER_MFMA = [
+    (1100, 2048, 64, 8, "bf16"),
+    (2000, 520, 48, 4, "bf16"),
+    (1500, 8, 33, 3, "bf16"),
+    (1030, 96, 64, 8, "fp32"),
+    (1029, 1000, 40, 2, "fp32"),
+    (3000, 256, 64, 6, "bf16"),
+]
+
+
+@pytest.mark.parametrize("N,D,E,K,dtype", ROUTER_MFMA,
+                         ids=[f"{c[0]}-{c[1]}-{c[2]}-{c[4]}" for c in ROUTER_MFMA])
+def test_router_mfma_agrees(gpu_lib, monkeypatch, N, D, E, K, dtype):
+    """The tiled router's logits on the fp32 matrix cores (32 < E <= 64) and
+    on the vector unit (MXM_ROUTER_MFMA=0): probabilities, routing, delta,
+    aux and entropy bit for bit, and the routing bit for bit against the
+    oracle.  Rows of +0, of -0, of values whose products are denormal and of
+    mixed signs and magnitudes exercise the fused multiply-add's rounding,
+    denormals and signed zeros."""
+    bf16 = dtype == "bf16"
+    x, wr, experts = random_case(900 + N + D + E, N, D, E, 128)
+    rng = np.random.default_rng(N + D)
+    x[0] = 0.0
+    x[1] = -0.0
+    x[2] = x[2] * np.float32(1e-36)
+    x[3] = x[3] * np.exp2(rng.integers(-60, 40, size=D)).astype(np.float32)
+    if bf16:
+        x, wr = round_bf16(x), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    monkeypatch.setenv("MXM_SMALL_ROUTE", "0")
+    runs = []
+    for mf in ("1", "0"):
+        monkeypatch.setenv("MXM_ROUTER_MFMA", mf)
+        print(f"router N={N} D={D} E={E} K={K} {dtype} mfma={mf}", flush=True)
+        runs.append(run_gpu(x, wr, experts, B=1, T=N, K=K, bf16=bf16, want_probs=True))
+    (d1, a1, e1, r1, _), (d0, a0, e0, r0, _) = runs
+    for key in ("probs", "top_idx", "gates", "counts", "offsets", "perm"):
+        assert same_bits(r1[key], r0[key]), key
+    assert same_bits(d1, d0)
+    assert same_bits(np.float32(a1), np.float32(a0)) and same_bits(np.float32(e1), np.float32(e0))
+    want = run_oracle(x, wr, experts, K=K, bf16=bf16)
+    assert same_bits(r1["probs"], want["probs"])
+    assert_routing_equal(r1, want)
+
+
+# (N, D, E, K, dtype, int8, MXM_SMALL_ROUTE): every top-k path -- the tiled
+# router on the matrix cores (E 33..64), by lane segments (E <= 32) and by
+# argmax rounds (E > 64), the one-launch router, the int8 decode flow
+NON_FINITE = [
+    (300, 256, 64, 8, "bf16", False, "0"),
+    (300, 256, 16, 4, "bf16", False, "0"),
+    (300, 256, 96, 6, "fp32", False, "0"),
+    (300, 256, 64, 8, "bf16", False, "1"),
+    (300, 256, 96, 6, "fp32", False, "1"),
+    (64, 256, 64, 8, "bf16", True, None),
+]
+
+
+@pytest.mark.parametrize("N,D,E,K,dtype,int8,small", NON_FINITE,
+                         ids=[f"{c[0]}-{c[2]}-{c[4]}{'-int8' if c[5] else ''}-s{c[6]}"
+                              for c in NON_FINITE])
+def test_non_finite_rows_route_in_range(gpu_lib, monkeypatch, N, D, E, K, dtype, int8, small):
+    """Tokens whose logits are not finite (a NaN or an infinity in x) still
+    pick K distinct experts below E, so the dispatch tables stay consistent
+    (each token K times in perm, counts summing to N K), and every finite
+    row's routing and delta are the bits of a run with those rows zeroed."""
+    from mixlab_amd.op import MoEFeedForward
+    from mixlab_amd.workloads import quantize_int8
+
+    bf16 = dtype == "bf16"
+    x, wr, experts = random_case(77 + N + E, N, D, E, 128)
+    bad = [3, 10, 11, 40, N - 1]
+    xb = x.copy()
+    xb[3, 7] = np.nan
+    xb[10, 0] = np.inf
+    xb[11, 100] = -np.inf
+    xb[40] = np.nan
+    xb[N - 1, D - 1] = np.nan
+    xz = x.copy()
+    xz[bad] = 0.0
+    if bf16:
+        xb, xz, wr = round_bf16(xb), round_bf16(xz), round_bf16(wr)
+        experts = [[round_bf16(w) for w in ws] for ws in experts]
+    up = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
+    if small is None:
+        monkeypatch.delenv("MXM_SMALL_ROUTE", raising=False)
+    else:
+        monkeypatch.setenv("MXM_SMALL_ROUTE", small)
+
+    def run(xin):
+        print(f"non-finite N={N} E={E} K={K} {dtype} int8={int8} small={small}", flush=True)
+        flags = _lib.MXM_FLAG_INT8_WEIGHTS if int8 else 0
+        with MoEFeedForward([1, N, D, E, K, 0, 128, 0], [0.0], compute_dtype=dtype,
+                            flags=flags) as op:
+            op.set_input(1, up(wr))
+            for e in range(E):
+                for j in range(3):
+                    if int8:
+                        op.set_input_q8(2 + 3 * e + j, *quantize_int8(experts[e][j]))
+                    else:
+                        op.set_input(2 + 3 * e + j, up(experts[e][j]))
+            delta, _, _ = op.forward_host(up(xin))
+            return delta.reshape(N, D), op.routing()
+
+    db, rb = run(xb)
+    dz, rz = run(xz)
+    top = rb["top_idx"].reshape(N, K)
+    assert top.min() >= 0 and top.max() < E
+    assert all(len(set(row)) == K for row in top.tolist())
+    assert int(rb["counts"].sum()) == N * K
+    assert np.array_equal(np.bincount(rb["perm"], minlength=N), np.full(N, K))
+    good = np.setdiff1d(np.arange(N), bad)
+    assert np.array_equal(top[good], rz["top_idx"].reshape(N, K)[good])
+    assert same_bits(rb["gates"].reshape(N, K)[good], rz["gates"].reshape(N, K)[good])
+    assert same_bits(db[good], dz[good])
+
+
 def test_decode_router_repeated_calls(gpu_lib):
     """The one-launch router elects its dispatch workgroup with a ticket that
     the elected workgroup resets: consecutive forwards on one executor each
