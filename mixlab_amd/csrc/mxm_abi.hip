@@ -285,14 +285,18 @@ int fenced(F&& f) {
 // slots); the three-launch path's hardly does at these sizes.  So the one
 // launch pays while each token brings enough logit work.  Measured on MI355X
 // over N = 64-1024 and D*E = 512 .. 131072 (bf16 and fp32; results are bit
-// for bit the same either way): for E > 32 it is the faster one for every
-// N <= 512, up to N = 768 from D*E = 4096 on and up to N = 1024 from
-// D*E = 16384 on; for E <= 32, where the tiled router routes several tokens
-// per wave, the crossover lies near N = 200-300 for D*E = 512, ~400 for
-// 4096, ~550 for 8192 and ~700 for 16384.  The int8 decode flow is built on
-// the one-launch router and keeps it wherever it fits.
-bool small_route_pays(int N, int D, int E) {
+// for bit the same either way): where the tiled router's logits run on the
+// matrix cores (mf: 32 < E <= 64) it is the faster one for every N <= 640,
+// up to N = 768 from D*E = 8192 on, up to N = 896 from D*E = 65536 on and
+// up to N = 1024 from D*E = 98304 on; for E > 64 for every N <= 512, up to
+// N = 768 from D*E = 4096 on and up to N = 1024 from D*E = 16384 on; for
+// E <= 32, where the tiled router routes several tokens per wave, the
+// crossover lies near N = 200-300 for D*E = 512, ~400 for 4096, ~550 for
+// 8192 and ~700 for 16384.  The int8 decode flow is built on the one-launch
+// router and keeps it wherever it fits.
+bool small_route_pays(int N, int D, int E, bool mf) {
   const int64_t de = (int64_t)D * E;
+  if (mf) return N <= 640 || (N <= 768 && de >= 8192) || (N <= 896 && de >= 65536) || de >= 98304;
   if (E > 32) return N <= 512 || (N <= 768 && de >= 4096) || de >= 16384;
   return N <= 256 || (N <= 512 && de >= 8192) || (N <= 640 && de >= 16384) || de >= 65536;
 }
@@ -1028,13 +1032,15 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     const size_t F1 = (size_t)o->Kx * o->Fk, F2 = (size_t)o->Fk * o->Dk;  // padded matrices
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
+    o->mf_router = o->E > 32 && o->E <= 64;
+    if (const char* v = std::getenv("MXM_ROUTER_MFMA")) o->mf_router = o->mf_router && std::atoi(v) != 0;
+    // (the launcher also wants x 16-byte aligned; D decides it for the choice)
+    const bool mf_logits = o->mf_router && o->D % (o->bf16 ? 8 : 4) == 0 && o->D <= (1 << 24);
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K) &&
-                     (o->q8 || small_route_pays(o->N, o->D, o->E));
+                     (o->q8 || small_route_pays(o->N, o->D, o->E, mf_logits));
     if (const char* v = std::getenv("MXM_SMALL_ROUTE"))
       o->small_route = std::atoi(v) != 0 && mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
-    o->mf_router = o->E > 32 && o->E <= 64;
-    if (const char* v = std::getenv("MXM_ROUTER_MFMA")) o->mf_router = o->mf_router && std::atoi(v) != 0;
     if (o->small_route || o->mf_router) {
       o->ldw = (o->D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
       o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * (o->bf16 ? 2 : 4));

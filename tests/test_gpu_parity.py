@@ -655,10 +655,17 @@ ROUTER_CHOICE = [
     (512, 256, 32, 4, "bf16", False, 1),    # D*E = 8192
     (640, 1024, 16, 2, "bf16", False, 1),   # D*E = 16384
     (1024, 1024, 16, 2, "bf16", False, 0),
-    # E > 32
+    # 32 < E <= 64 (the tiled router's logits on the matrix cores)
+    (640, 128, 40, 2, "bf16", False, 1),    # D*E = 5120
+    (768, 128, 40, 2, "bf16", False, 0),
     (768, 128, 64, 8, "bf16", False, 1),    # D*E = 8192
     (1024, 128, 64, 8, "bf16", False, 0),
-    (1024, 512, 64, 8, "bf16", False, 1),   # D*E = 32768
+    (896, 1024, 64, 8, "bf16", False, 1),   # D*E = 65536
+    (1024, 512, 64, 8, "bf16", False, 0),   # D*E = 32768
+    (1024, 2048, 64, 8, "bf16", False, 1),  # D*E = 131072
+    # E > 64
+    (1024, 128, 96, 4, "bf16", False, 0),   # D*E = 12288
+    (1024, 256, 96, 4, "bf16", False, 1),   # D*E = 24576
     (1024, 256, 8, 2, "bf16", True, 2),     # int8 keeps the decode flow
     (1100, 2048, 64, 8, "bf16", False, 0),  # past the one-launch router's limit
 ]
