@@ -176,6 +176,7 @@ struct MoeOp {
   // tile schedule of the forward (set at create from the op's parameters)
   int ntiles = 0, bm1 = 0, bm2 = 0, max_mtiles1 = 0, max_mtiles2 = 0;
   int simt_tile = 0;  // MXM_SIMT_TILE at creation: the SIMT family's tile (0 picks)
+  int simt_vec = 0;   // MXM_SIMT_MFMA=0 at creation: 64 x 64 SIMT tiles on the vector unit
   // the op's own workspace, allocated at the first forward; `last` is the
   // workspace the latest forward used (the op's own, or the device scratch
   // of mxm_moe_forward_noalloc), which the routing queries read
@@ -581,6 +582,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.Ncols = (o.mfma && glu) ? 2 * o.Fk : o.Fk;
   g1.max_mtiles = o.max_mtiles1;
   g1.simt_bm = o.bm1;
+  g1.simt_vec = o.simt_vec;
   g1.family = o.fam1;
   g1.expert_type = o.etype;
   g1.activation = o.act;
@@ -642,6 +644,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.Ncols = o.Dk;
   g2.max_mtiles = o.max_mtiles2;
   g2.simt_bm = o.bm2;
+  g2.simt_vec = o.simt_vec;
   g2.family = o.fam2;
   g2.expert_type = o.etype;
   g2.activation = o.act;
@@ -960,6 +963,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     if (const char* v = std::getenv("MXM_FORCE_64BIT_OFFSETS")) o->force64 = std::atoi(v) != 0;
     if (const char* v = std::getenv("MXM_DECODE_FLOW")) o->decode_flow = std::atoi(v) != 0;
     if (const char* v = std::getenv("MXM_SIMT_TILE")) o->simt_tile = std::atoi(v);
+    if (const char* v = std::getenv("MXM_SIMT_MFMA")) o->simt_vec = std::atoi(v) == 0;
     o->B = int_params[0];
     o->T = int_params[1];
     o->D = int_params[2];
@@ -1638,6 +1642,7 @@ void run_backward_x3(MoeOp& o, BackwardArgs& b, bool own_forward) {
     g.Ncols = F;
     g.max_mtiles = o.max_mtiles1;
     g.simt_bm = o.bm1;
+    g.simt_vec = o.simt_vec;
     g.expert_type = o.etype;
     g.activation = o.act;
     g.slope = o.slope;

@@ -15,6 +15,14 @@
 // 32 (2 x 2 per thread) for launches whose 64 x 64 grid would leave CUs
 // idle -- four times the workgroups, each thread's chain a quarter as long
 // (GemmArgs::simt_bm picks; the schedule's row tiles must match).
+//
+// The 64 x 64 tile's products run on the fp32 matrix cores (MF): each wave
+// owns a 32 x 32 quarter as 2 x 2 blocks of v_mfma_f32_16x16x1_4b_f32, one
+// instruction per k step and matrix.  That instruction adds one product per
+// output, rounded once like fmaf, denormals kept (checked on the part
+// against fmaf chains bit for bit), so each output is the same fmaf chain
+// over the same k steps, zero padding included, as on the vector unit, at
+// twice the non-packed fp32 rate.
 #include "mxm_kernels.h"
 
 namespace {
@@ -57,10 +65,17 @@ __device__ __forceinline__ void lds_vec(const float* p, float (&v)[T]) {
   }
 }
 
+typedef float mf_v16 __attribute__((ext_vector_type(16)));
+
 // BM x BN tile, TM x TN outputs per thread (a 16 x 16 thread grid), k tiles
-// of BK.
-template <typename TA, bool BF16, int MODE, int BM, int BN, int BK>
+// of BK.  MF (BM = BN = 64): wave w owns rows 32 (w >> 1) .. + 31 and columns
+// 32 (w & 1) .. + 31 of the tile; block b of its MFMA covers rows 16 (b >> 1)
+// .. and columns 16 (b & 1) .. of that quarter, A from lanes 16 b + i (row
+// i), B from lanes 16 b + j (column j); register 4 b + q of lane l holds row
+// (l >> 4) * 4 + q, column l & 15 of block b.
+template <typename TA, bool BF16, int MODE, int BM, int BN, int BK, bool MF = false>
 __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
+  static_assert(!MF || (BM == 64 && BN == 64), "the matrix-core tile is 64 x 64");
   constexpr int NB = (MODE == MXM_GEMM_GLU) ? 2 : 1;
   constexpr int TM = BM / 16, TN = BN / 16;
   constexpr int LA = BM * BK / NT, LB = BK * BN / NT;  // loads per thread per k tile
@@ -104,6 +119,14 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[b][i][j] = 0.0f;
+  // MF: the wave's quarter and this lane's A row / B column in it
+  mf_v16 accm[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) accm[b] = mf_v16{};
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wr0 = 32 * (wave >> 1), wc0 = 32 * (wave & 1);
+  const int arow_l = wr0 + 16 * ((lane >> 4) >> 1) + (lane & 15);
+  const int bcol_l = wc0 + 16 * ((lane >> 4) & 1) + (lane & 15);
 
   // The k tile after the current one is loaded into registers while the
   // current one is summed (its loads' latency is then hidden behind 16 k
@@ -146,47 +169,62 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
       }
     __syncthreads();
     if (k0 + BK < Kd) fetch(k0 + BK);
+    if constexpr (MF) {
 #pragma unroll
-    for (int kk = 0; kk < BK; ++kk) {
-      float ar[TM];
-      lds_vec<TM>(&As[kk][ty * TM], ar);
+      for (int kk = 0; kk < BK; ++kk) {
+        const float av = As[kk][arow_l];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        float br[TN];
-        lds_vec<TN>(&Bs[b][kk][tx * TN], br);
+        for (int b = 0; b < NB; ++b)
+          accm[b] = __builtin_amdgcn_mfma_f32_16x16x1f32(av, Bs[b][kk][bcol_l], accm[b], 0, 0, 0);
+      }
+    } else {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+      for (int kk = 0; kk < BK; ++kk) {
+        float ar[TM];
+        lds_vec<TM>(&As[kk][ty * TM], ar);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[b][i][j] = __builtin_fmaf(ar[i], br[j], acc[b][i][j]);
+        for (int b = 0; b < NB; ++b) {
+          float br[TN];
+          lds_vec<TN>(&Bs[b][kk][tx * TN], br);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[b][i][j] = __builtin_fmaf(ar[i], br[j], acc[b][i][j]);
+        }
       }
     }
   }
 
   float* out = static_cast<float*>(a.out);
+  // the outputs this thread holds: TM x TN of its 16 x 16 grid cell, or
+  // (MF) 16 registers of the wave's quarter
+  constexpr int OI = MF ? 16 : TM, OJ = MF ? 1 : TN;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int row = ty * TM + i;
+  for (int i = 0; i < OI; ++i) {
+    const int row = MF ? wr0 + 16 * ((i >> 2) >> 1) + (lane >> 4) * 4 + (i & 3) : ty * TM + i;
     if (row >= rows) continue;
     const size_t orow = (size_t)(row0 + row) * NC;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n0 + tx * TN + j;
+    for (int j = 0; j < OJ; ++j) {
+      const int c = MF ? n0 + wc0 + 16 * ((i >> 2) & 1) + (lane & 15) : n0 + tx * TN + j;
       if (c >= NC) continue;
+      auto A_ = [&](int b) { return MF ? accm[b][i] : acc[b][MF ? 0 : i][MF ? 0 : j]; };
       float v;
       if (MODE == MXM_GEMM_GLU) {
-        float g = acc[0][i][j], u = acc[NB - 1][i][j];
+        float g = A_(0), u = A_(NB - 1);
         if (BF16) {
           g = mxm_rbf(g);
           u = mxm_rbf(u);
         }
         v = mxm_hidden<BF16>(a.expert_type, a.activation, a.slope, g, u);
       } else if (MODE == MXM_GEMM_MLP) {
-        float u = acc[0][i][j];
+        float u = A_(0);
         if (BF16) u = mxm_rbf(u);
         if (a.out2) static_cast<float*>(a.out2)[(size_t)(row0 + row) * a.ld2 + c] = u;
         v = mxm_hidden<BF16>(MXM_EXPERT_MLP, a.activation, a.slope, 0.0f, u);
       } else {
-        v = acc[0][i][j];
+        v = A_(0);
         if (a.y_bf16) v = mxm_rbf(v);
       }
       if (out) out[orow + c] = v;
@@ -197,24 +235,34 @@ __global__ __launch_bounds__(NT) void gemm_simt_kernel(GemmArgs a) {
 // k tiles of 16 for the 64 x 64 tile (each thread's 16 outputs per k step
 // amortise the tile's barriers), 32 for the 32 x 32 tile (4 outputs per k
 // step: half as many barrier and LDS round trips per k)
-template <typename TA, bool BF16, int T>
+template <typename TA, bool BF16, int T, bool MF>
 void launch_t(const GemmArgs& a, hipStream_t s) {
   constexpr int BK = T == 64 ? 16 : 32;
   const dim3 grid((a.Ncols + T - 1) / T, a.max_mtiles);
   switch (a.mode) {
     case MXM_GEMM_GLU:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU, T, T, BK>), grid, dim3(NT), 0,
-                         s, a);
-      break;
-    case MXM_GEMM_MLP:
-      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP, T, T, BK>), grid, dim3(NT), 0,
-                         s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN, T, T, BK>), grid, dim3(NT),
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_GLU, T, T, BK, MF>), grid, dim3(NT),
                          0, s, a);
       break;
+    case MXM_GEMM_MLP:
+      hipLaunchKernelGGL((gemm_simt_kernel<TA, BF16, MXM_GEMM_MLP, T, T, BK, MF>), grid, dim3(NT),
+                         0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_simt_kernel<float, BF16, MXM_GEMM_DOWN, T, T, BK, MF>), grid,
+                         dim3(NT), 0, s, a);
+      break;
   }
+}
+
+template <typename TA, bool BF16>
+void launch_tile(const GemmArgs& a, hipStream_t s) {
+  if (a.simt_bm == 32)
+    launch_t<TA, BF16, 32, false>(a, s);
+  else if (a.simt_vec)
+    launch_t<TA, BF16, 64, false>(a, s);
+  else
+    launch_t<TA, BF16, 64, true>(a, s);
 }
 
 }  // namespace
@@ -230,16 +278,8 @@ int mxm_simt_bm(int64_t rows, int E, int ncols, int n_cu) {
 
 void mxm_launch_gemm_simt(const GemmArgs& a, bool bf16, hipStream_t s) {
   if (a.max_mtiles <= 0) return;
-  const bool small = a.simt_bm == 32;
-  if (bf16) {
-    if (small)
-      launch_t<uint16_t, true, 32>(a, s);
-    else
-      launch_t<uint16_t, true, 64>(a, s);
-  } else {
-    if (small)
-      launch_t<float, false, 32>(a, s);
-    else
-      launch_t<float, false, 64>(a, s);
-  }
+  if (bf16)
+    launch_tile<uint16_t, true>(a, s);
+  else
+    launch_tile<float, false>(a, s);
 }

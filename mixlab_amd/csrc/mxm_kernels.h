@@ -182,6 +182,8 @@ struct GemmArgs {
   bool y_bf16;            // SIMT down: round y to bf16
   int family;             // MFMA tile family (MXM_TILE_*), MXM_TILE_AUTO picks
   int simt_bm;            // SIMT family: tile height and width, 64 (0 too) or 32
+  int simt_vec;           // SIMT family: 1 keeps the 64 x 64 tile's products on the
+                          // vector unit (0: the fp32 matrix cores, same bits)
   int rows_total;         // N*K routed rows (int8 family: picks rows per pass)
   // Split hidden (MFMA and int8 families, kinds whose hidden is fp32 in the
   // bf16 flow, !mxm_hidden_is_bf16): the up GEMM stores each fp32 hidden

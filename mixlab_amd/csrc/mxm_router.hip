@@ -397,8 +397,10 @@ __device__ __forceinline__ void lg_round(const LgRound<TX>& R, mxm_lg16& c) {
 // The logits of tokens n0w .. n0w + 15 against the 64 (padded) experts: per
 // 64-d chunk (two rounds) a partial from +0, added to the logit (from +0) in
 // chunk order.  Both rounds of the last chunk run: past D the x pieces and
-// the router copy (zero up to ldw) are zeros, and fma(0, 0, c) = c for every
-// c a chain from +0 can reach (it never reaches -0).  The next round's
+// the router copy (zero up to ldw) are zeros, and fma(0, 0, c) = c except
+// that a -0 partial (a product that underflowed to -0) becomes +0, which
+// the logit's addition absorbs (the logit, a sum from +0, is never -0, and
+// adding either zero leaves it as it is).  The next round's
 // pieces are loaded while a round computes (after the last chunk, its
 // second round again, unused).  Needs 16 D sizeof(TX) < 2^30 (the launcher
 // checks).
