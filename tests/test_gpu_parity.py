@@ -132,27 +132,33 @@ def test_expert_types(gpu_lib, name, etype, act, slope, flow):
 
 @pytest.mark.parametrize("shape,bf16", [((1024, 128, 4, 2, 512, 0), False),  # C1
                                         ((700, 96, 6, 3, 200, 2), True),      # bf16 below the MFMA tiles
-                                        ((3000, 64, 8, 2, 96, 1), False)])    # ragged tails
+                                        ((3000, 64, 8, 2, 96, 1), False),     # ragged tails
+                                        ((1500, 100, 5, 2, 136, 0), False),   # k past whole tiles
+                                        ((2048, 256, 4, 2, 512, 2), False)])  # one matrix, 64 x 64
 def test_simt_tiles_agree(gpu_lib, monkeypatch, shape, bf16):
-    """The SIMT family's two tiles (64 x 64, 4 x 4 outputs per thread; 32 x
-    32, 2 x 2) sum every output in the same ascending-k order: bit for bit
-    the same delta, and bit-exact against the restatement (fp32 and the
-    bf16 dtype flow)."""
+    """The SIMT family's tiles -- 32 x 32 (2 x 2 outputs per thread), 64 x
+    64 on the vector unit (4 x 4 per thread, MXM_SIMT_MFMA=0) and 64 x 64 on
+    the fp32 matrix cores (k = 1 MFMA chains) -- sum every output in the
+    same ascending-k order: bit for bit the same delta, and bit-exact
+    against the restatement (fp32 and the bf16 dtype flow)."""
     N, D, E, K, F, etype = shape
     x, wr, experts = random_case(500 + N + D, N, D, E, F, expert_type=etype)
     if bf16:
         x, wr = round_bf16(x), round_bf16(wr)
         experts = [[round_bf16(m) for m in ws] for ws in experts]
     out = {}
-    for tile in (32, 64):
+    for tile, mf in ((32, "1"), (64, "0"), (64, "1")):
         monkeypatch.setenv("MXM_SIMT_TILE", str(tile))
+        monkeypatch.setenv("MXM_SIMT_MFMA", mf)
+        print(f"simt tile {tile} mfma {mf} shape {shape} bf16 {bf16}", flush=True)
         delta, aux, ent, routing, info = run_gpu(x, wr, experts, B=1, T=N, K=K, expert_type=etype,
                                                  bf16=bf16)
         assert not info["mfma"] and info["gemm_bm"] == tile
-        out[tile] = delta
-    assert same_bits(out[32], out[64])
+        out[(tile, mf)] = delta
+    assert same_bits(out[(32, "1")], out[(64, "0")])
+    assert same_bits(out[(32, "1")], out[(64, "1")])
     want = run_oracle(x, wr, experts, K=K, expert_type=etype, bf16=bf16)
-    assert same_bits(out[32], want["delta"])
+    assert same_bits(out[(32, "1")], want["delta"])
 
 
 def test_ties_go_to_lower_expert(gpu_lib):
