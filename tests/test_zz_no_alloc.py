@@ -113,6 +113,9 @@ FAMILIES = [
      dict(B=1, T=64, D=512, E=8, K=2, F=512, int8=True)),
     ("fp32_simt", dict(B=1, T=2400, D=128, E=4, K=2, F=256, dtype="fp32"),
      dict(B=1, T=33, D=128, E=4, K=2, F=128, dtype="fp32")),
+    # the tiled router's logits on the matrix cores (32 < E <= 64)
+    ("bf16_router64", dict(B=1, T=1100, D=256, E=64, K=8, F=256),
+     dict(B=1, T=1030, D=128, E=48, K=4, F=128)),
 ]
 
 
