@@ -382,7 +382,8 @@ def main() -> int:
     ap.add_argument("--flags", type=int, default=0, help="mxm_moe_create flags (include/mixmoe.h)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
-    ap.add_argument("--no-configs", action="store_true", help="skip the C1, C2, C3 and C4F sections")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the C1, C2fp32, C2, C3 and C4F sections")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time hipBLASLt (torch.matmul) on the dense equivalents of the "
                          "grouped GEMM's two launches (in a child process)")
@@ -490,6 +491,23 @@ def main() -> int:
                        "tokens_per_s": r1["tokens_per_s"], "ms_per_step": r1["ms_per_step"],
                        "stages_ms": {k: v for k, v in r1["stages"].items() if k != "forwards"},
                        "executor": r1["info"]}
+        # the fp32 flow at C2's size: the exact-order kernels (fmaf chains in
+        # ascending k, the 64 x 64 tile's on the fp32 matrix cores; bit-exact
+        # against the oracle), against the fp32 dense peak
+        import dataclasses
+        c2f = dataclasses.replace(CONFIGS["C2"], dtype="fp32", name="C2fp32")
+        _, rf = run_config(c2f, args.steps, args.warmup)
+        flf = c2f.flops()
+        gms = rf["stages"]["gemm_up"] + rf["stages"]["gemm_down"]
+        extra["C2fp32"] = {"tokens": c2f.N, "d_model": c2f.D, "experts": c2f.E,
+                           "top_k": c2f.K, "expert_hidden": c2f.F, "dtype": "fp32",
+                           "tokens_per_s": rf["tokens_per_s"], "ms_per_step": rf["ms_per_step"],
+                           "expert_gemm": {"ms": gms,
+                                           "tflops": flf["experts"] / (gms * 1e-3) / 1e12,
+                                           "frac_fp32_peak": flf["experts"] / (gms * 1e-3) / 1e12
+                                           / PEAK_FP32_TFLOPS},
+                           "stages_ms": {k: v for k, v in rf["stages"].items() if k != "forwards"},
+                           "executor": rf["info"]}
         for name in ("C2", "C3", "C4F"):
             if name == cfg.name:
                 continue
