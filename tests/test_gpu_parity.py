@@ -739,6 +739,7 @@ ROUTER_MFMA = [
     (1500, 8, 33, 3, "bf16"),
     (1030, 96, 64, 8, "fp32"),
     (1029, 1000, 40, 2, "fp32"),
+    (1031, 100, 36, 3, "fp32"),   # the last 8-d group half past D
     (3000, 256, 64, 6, "bf16"),
 ]
 
