@@ -160,8 +160,8 @@ struct MoeOp {
   // up (GLU) fp32 [E][D][F], w2 = down fp32 [E][F][D].  MFMA family: w1 =
   // bf16 [E][2F or F][D] (GLU interleaved), w2 = bf16 [E][D][F].
   DevBuf router, w1, w1b, w2;
-  // decode-sized batches, and the tiled router's matrix-core logits (32 < E
-  // <= 64): router_w lane-interleaved (RouteSmallArgs::wr_t)
+  // decode-sized batches, and the tiled router's matrix-core logits (E >
+  // 32): router_w lane-interleaved (RouteSmallArgs::wr_t)
   bool small_route = false, mf_router = false;
   int ldw = 0;
   DevBuf router_t;
@@ -297,7 +297,8 @@ int fenced(F&& f) {
 // router and keeps it wherever it fits.
 bool small_route_pays(int N, int D, int E, bool mf) {
   const int64_t de = (int64_t)D * E;
-  if (mf) return N <= 640 || (N <= 768 && de >= 8192) || (N <= 896 && de >= 65536) || de >= 98304;
+  if (mf && E <= 64)
+    return N <= 640 || (N <= 768 && de >= 8192) || (N <= 896 && de >= 65536) || de >= 98304;
   if (E > 32) return N <= 512 || (N <= 768 && de >= 4096) || de >= 16384;
   return N <= 256 || (N <= 512 && de >= 8192) || (N <= 640 && de >= 16384) || de >= 65536;
 }
@@ -519,6 +520,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     ra.tile_ent = w.tile_ent;
     ra.probs_out = probs_keep;
     ra.wr_t = o.mf_router ? o.router_t.p : nullptr;
+    ra.ldw = o.ldw;
     for (int rep = 0; rep < reps; ++rep) mxm_launch_router(ra, o.bf16, st);
     HIPCK(hipGetLastError());
 
@@ -1036,7 +1038,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     const size_t DE = (size_t)o->D * o->E, DF = (size_t)o->D * o->F, EE = (size_t)o->E;
     const size_t F1 = (size_t)o->Kx * o->Fk, F2 = (size_t)o->Fk * o->Dk;  // padded matrices
     o->router.alloc(DE * (o->bf16 ? 2 : 4));
-    o->mf_router = o->E > 32 && o->E <= 64;
+    o->mf_router = o->E > 32;
     if (const char* v = std::getenv("MXM_ROUTER_MFMA")) o->mf_router = o->mf_router && std::atoi(v) != 0;
     // (the launcher also wants x 16-byte aligned; D decides it for the choice)
     const bool mf_logits = o->mf_router && o->D % (o->bf16 ? 8 : 4) == 0 && o->D <= (1 << 24);

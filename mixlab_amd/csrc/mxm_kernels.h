@@ -60,9 +60,10 @@ struct RouterArgs {
   float* tile_ent;       // [ntiles] sum over the tile of sum_e p log max(p, 1e-12)
   float* probs_out;      // optional [N, E]
   // optional: router_w lane-interleaved as RouteSmallArgs::wr_t (ldw a
-  // multiple of 64 >= D); for 32 < E <= 64 the logits then run on the fp32
-  // matrix cores (same bits)
+  // multiple of 64 >= D); for E > 32 the logits then run on the fp32 matrix
+  // cores (same bits)
   const void* wr_t;
+  int ldw;
 };
 void mxm_launch_router(const RouterArgs& a, bool bf16, hipStream_t s);
 

@@ -437,15 +437,15 @@ __device__ __forceinline__ mxm_lg16 logits_mfma(const TX* x, const TX* wr_t, int
 }
 
 // EPT = experts per thread in phase 1 (E padded to 16*EPT).  MF: phase 1 on
-// the fp32 matrix cores (EPT 4 only; wr_t is the lane-interleaved router copy
-// [ldw/P][64][P], x 16-byte aligned with D % P == 0).
+// the fp32 matrix cores (EPT 4, 8 or 16; wr_t is the lane-interleaved router
+// copy [EPT/4][ldw/P][64][P], x 16-byte aligned with D % P == 0).
 template <typename TX, bool BF16, int EPT, bool VEC, bool MF = false>
 __global__ __launch_bounds__(NT) void router_kernel(
     const TX* __restrict__ x, const TX* __restrict__ wr, int N, int D, int E, int K,
     int32_t* __restrict__ top_idx, float* __restrict__ gates, int32_t* __restrict__ slot_rank,
     int32_t* __restrict__ tile_counts, float* __restrict__ tile_psum, float* __restrict__ tile_ent,
     float* __restrict__ probs_out, int ntiles,
-    const TX* __restrict__ wr_t) {
+    const TX* __restrict__ wr_t, int ldw) {
   constexpr int EP = 16 * EPT;
   constexpr int NJ = (EP + 63) / 64;  // experts per lane in phase 2
   constexpr int LG_STRIDE = EP + 1;
@@ -471,16 +471,22 @@ __global__ __launch_bounds__(NT) void router_kernel(
 
   // ---- phase 1: logits --------------------------------------------------
   if constexpr (MF) {
-    static_assert(EPT == 4, "the matrix-core logits cover 64 experts");
+    // one pass of 64 experts per group of the lane-interleaved copy (its
+    // groups lie ldw * 64 elements apart); each pass reads the wave's x rows
+    // again
+    static_assert(EP % 64 == 0, "the matrix-core logits cover groups of 64 experts");
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;  // wv: uniform
-    const mxm_lg16 v = logits_mfma<TX>(x, wr_t, N, D, n0 + 16 * wv, ln);
+    for (int g = 0; g < EP / 64; ++g) {
+      const mxm_lg16 v = logits_mfma<TX>(x, wr_t + (size_t)g * ldw * 64, N, D, n0 + 16 * wv, ln);
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = 16 * wv + (ln >> 4) * 4 + q;
-        lg[t * LG_STRIDE + 16 * b + (ln & 15)] = BF16 ? mxm_rbf(v[4 * b + q]) : v[4 * b + q];
-      }
+        for (int q = 0; q < 4; ++q) {
+          const int t = 16 * wv + (ln >> 4) * 4 + q;
+          lg[t * LG_STRIDE + 64 * g + 16 * b + (ln & 15)] =
+              BF16 ? mxm_rbf(v[4 * b + q]) : v[4 * b + q];
+        }
+    }
     __syncthreads();
   } else {
     const int ty = tid >> 4;  // tokens ty*4 .. ty*4+3
@@ -1114,22 +1120,22 @@ void launch_router_t(const RouterArgs& a, hipStream_t s) {
   const TX* x = static_cast<const TX*>(a.x);
   const TX* wr = static_cast<const TX*>(a.wr);
   const TX* wr_t = static_cast<const TX*>(a.wr_t);
-  if constexpr (EPT == 4) {
+  if constexpr (EPT >= 4) {
     if (wr_t && xvec && a.E > 32 && a.D <= (1 << 24)) {
       hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true, true>), dim3(ntiles), dim3(NT), 0, s,
                          x, wr, a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank,
-                         a.tile_counts, a.tile_psum, a.tile_ent, a.probs_out, ntiles, wr_t);
+                         a.tile_counts, a.tile_psum, a.tile_ent, a.probs_out, ntiles, wr_t, a.ldw);
       return;
     }
   }
   if (vec)
     hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, true>), dim3(ntiles), dim3(NT), 0, s, x, wr,
                        a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts,
-                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr);
+                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr, 0);
   else
     hipLaunchKernelGGL((router_kernel<TX, BF16, EPT, false>), dim3(ntiles), dim3(NT), 0, s, x, wr,
                        a.N, a.D, a.E, a.K, a.top_idx, a.gates, a.slot_rank, a.tile_counts,
-                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr);
+                       a.tile_psum, a.tile_ent, a.probs_out, ntiles, nullptr, 0);
 }
 
 template <typename TX, bool BF16>

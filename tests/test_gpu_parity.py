@@ -732,7 +732,7 @@ def test_router_choice(gpu_lib, monkeypatch, N, D, E, K, dtype, int8, want):
 
 
 # (N, D, E, K, dtype): partial last tiles and waves, D past whole chunks and
-# rounds (D % 64 in {8, 32, 40}, one 8-wide piece), 33..64 experts
+# rounds (D % 64 in {8, 32, 40}, one 8-wide piece), 33..256 experts
 ROUTER_MFMA = [
     (1100, 2048, 64, 8, "bf16"),
     (2000, 520, 48, 4, "bf16"),
@@ -741,14 +741,19 @@ ROUTER_MFMA = [
     (1029, 1000, 40, 2, "fp32"),
     (1031, 100, 36, 3, "fp32"),   # the last 8-d group half past D
     (3000, 256, 64, 6, "bf16"),
+    # several groups of 64 experts: one pass over x per group
+    (1100, 512, 96, 6, "bf16"),
+    (1300, 264, 128, 8, "bf16"),
+    (1029, 160, 200, 8, "fp32"),
+    (2000, 1024, 256, 8, "bf16"),
 ]
 
 
 @pytest.mark.parametrize("N,D,E,K,dtype", ROUTER_MFMA,
                          ids=[f"{c[0]}-{c[1]}-{c[2]}-{c[4]}" for c in ROUTER_MFMA])
 def test_router_mfma_agrees(gpu_lib, monkeypatch, N, D, E, K, dtype):
-    """The tiled router's logits on the fp32 matrix cores (32 < E <= 64) and
-    on the vector unit (MXM_ROUTER_MFMA=0): probabilities, routing, delta,
+    """The tiled router's logits on the fp32 matrix cores (E > 32) and on
+    the vector unit (MXM_ROUTER_MFMA=0): probabilities, routing, delta,
     aux and entropy bit for bit, and the routing bit for bit against the
     oracle.  Rows of +0, of -0, of values whose products are denormal and of
     mixed signs and magnitudes exercise the fused multiply-add's rounding,
