@@ -287,10 +287,12 @@ int fenced(F&& f) {
 // launch pays while each token brings enough logit work.  Measured on MI355X
 // over N = 64-1024 and D*E = 512 .. 131072 (bf16 and fp32; results are bit
 // for bit the same either way): where the tiled router's logits run on the
-// matrix cores (mf: 32 < E <= 64) it is the faster one for every N <= 640,
+// matrix cores (mf) and E <= 64 it is the faster one for every N <= 640,
 // up to N = 768 from D*E = 8192 on, up to N = 896 from D*E = 65536 on and
 // up to N = 1024 from D*E = 98304 on; for E > 64 for every N <= 512, up to
-// N = 768 from D*E = 4096 on and up to N = 1024 from D*E = 16384 on; for
+// N = 768 from D*E = 4096 on and up to N = 1024 from D*E = 16384 on (with
+// or without the matrix-core logits: the tiled router has only N / 64
+// workgroups at these sizes); for
 // E <= 32, where the tiled router routes several tokens per wave, the
 // crossover lies near N = 200-300 for D*E = 512, ~400 for 4096, ~550 for
 // 8192 and ~700 for 16384.  The int8 decode flow is built on the one-launch

@@ -6,9 +6,10 @@
 // experts.  Phase 1 computes the logits in their summation order
 // (mxm_numerics.h): per 64-d chunk of d, a partial by fmaf over the chunk's
 // d ascending from +0, added to the logit in chunk order -- the order the
-// CPU restatement uses, so logits are bit-identical.  For 32 < E <= 64 the
-// fmaf chains run on the fp32 matrix cores (logits_mfma), otherwise as a
-// register-tiled SIMT product on the vector unit.  Phase 2
+// CPU restatement uses, so logits are bit-identical.  For E > 32 the fmaf
+// chains run on the fp32 matrix cores (logits_mfma, a pass per group of 64
+// experts), otherwise as a register-tiled SIMT product on the vector unit.
+// Phase 2
 // gives each wavefront 16 tokens: one lane per expert (lane l holds experts
 // l, l+64, ...), softmax with a fixed xor-butterfly sum, top-k by K rounds of
 // a wave-wide argmax under the total order (p desc, expert asc), i.e. the
