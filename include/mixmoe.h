@@ -141,7 +141,10 @@ int mxm_moe_set_input_q8(int64_t op, int input_index, const int8_t* q, const flo
  * [rows, D] fp32, aux [1] fp32 and entropy [1] fp32.  All pointers are
  * device memory; the call is asynchronous on the op's stream.  aux and
  * entropy may be NULL.  Replaces the case OP_MOE_FEED_FORWARD dispatch
- * (gpu/ir.cpp:4816-4824) of moe_feed_forward (gpu/ir.cpp:1073-1164). */
+ * (gpu/ir.cpp:4816-4824) of moe_feed_forward (gpu/ir.cpp:1073-1164).
+ * A row whose logits are not finite (a NaN or infinity in x or router_w)
+ * gets NaN probabilities and gates and still picks K distinct experts
+ * (the lowest ids), so the dispatch of every other row is unaffected. */
 int mxm_moe_forward(int64_t op, const void* x, int x_dtype, int64_t rows, float* delta,
                     float* aux, float* entropy);
 
