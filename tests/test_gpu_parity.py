@@ -848,6 +848,8 @@ def test_non_finite_rows_route_in_range(gpu_lib, monkeypatch, N, D, E, K, dtype,
     top = rb["top_idx"].reshape(N, K)
     assert top.min() >= 0 and top.max() < E
     assert all(len(set(row)) == K for row in top.tolist())
+    # a row whose probabilities are NaN picks the K lowest experts in order
+    assert np.array_equal(top[bad], np.tile(np.arange(K, dtype=top.dtype), (len(bad), 1)))
     assert int(rb["counts"].sum()) == N * K
     assert np.array_equal(np.bincount(rb["perm"], minlength=N), np.full(N, K))
     good = np.setdiff1d(np.arange(N), bad)
