@@ -266,10 +266,13 @@ int mxm_moe_set_profiling(int64_t op, int enable);
 int mxm_moe_stage_times(int64_t op, float* ms, int n);
 
 /* Executor facts: info[0] = expert kernel family (0 SIMT, 1 bf16 MFMA, 2 int8
- * weights), info[1] = workspace bytes, info[2] = row-tile height of the
- * grouped GEMM, info[3] = number of router tiles, info[4] = the expert width
- * the kernels run at (ffn, or ffn rounded up to the tiles: 128 for MFMA, 64
- * for int8, with zero weights in the padding), info[5] = the down
+ * weights on the int8 kernels, 3 int8 weights on the bf16 MFMA tiles: the
+ * integers as bf16, the scales applied to the fp32 accumulators, for batches
+ * past the decode sizes), info[1] = workspace bytes, info[2] = row-tile
+ * height of the grouped GEMM, info[3] = number of router tiles, info[4] = the
+ * expert width the kernels run at (ffn, or ffn rounded up to the tiles: 128
+ * for MFMA, 64 for the int8 kernels, with zero weights in the padding),
+ * info[5] = the down
  * projection's output width (D, or D rounded up to 128 / 16), info[6] = the
  * up projection's reduction length (D, or D rounded up to 64), info[7] = how
  * the last forward routed: 0 the tiled router, scan and scatter (three

@@ -168,6 +168,13 @@ struct MoeOp {
   // int8 family: q1 = gate (GLU) or up (MLP), q1b = up (GLU), q2 = down, in
   // the 1 KB block layout; s1, s1b, s2 = fp32 per-output-channel scales.
   DevBuf q1, q1b, q2, s1, s1b, s2;
+  // int8 weights on the MFMA kernels (batches of 80 or more routed rows per
+  // expert, which are compute-bound): w1 / w2 hold the
+  // integers q as bf16 (exact) in the MFMA layout and s1 / s1b / s2 the
+  // scales [E][Fk] / [E][Dk], which the epilogue applies to the fp32
+  // accumulators; q1, q1b and q2 are not allocated
+  bool q8_mfma = false;
+  bool int8_kernels() const { return q8 && !q8_mfma; }
   int n_cu = 256;        // CUs of the op's device
   int fam1 = 0, fam2 = 0;  // MFMA tile families of the up and down GEMMs
   int fam_dh = 0;           // ... of the backward's dH = dY W_down^T (dX uses fam2)
@@ -305,13 +312,26 @@ bool small_route_pays(int N, int D, int E, bool mf) {
   return N <= 256 || (N <= 512 && de >= 8192) || (N <= 640 && de >= 16384) || de >= 65536;
 }
 
+// Whether an int8 op runs its expert GEMMs on the MFMA kernels (bf16 copies
+// of the integers q, scales in the epilogue) rather than on the int8
+// kernels.  The int8 kernels stream half the weight bytes and win while the
+// weights are the traffic; with more routed rows per expert (N*K/E) the
+// products turn compute-bound, where the int8 kernels reach 60-250 TFLOP/s
+// and the MFMA tiles 0.8-1.1 PFLOP/s.  To first order the weight bytes
+// cancel out of the comparison and the crossover is a number of rows per
+// expert: measured on MI355X (whole forwards) near 60 for D 2048 / E 64 /
+// K 8 / ffn 1408, 64 for D 1024 / E 32 / K 4 / ffn 1024, 80-90 for D 512 /
+// E 8 / K 2 / ffn 2048 and D 1024 / E 16 / K 2 / ffn 4096, and 75-150 for D
+// 256 with ffn 128-192, whose forwards are launch-bound either way.
+bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 80 * (int64_t)E; }
+
 // Row-tile heights and tile counts of the forward's kernels; a function of
 // the op's parameters only.
 void set_schedule(MoeOp& o) {
   const size_t NK = (size_t)o.N * o.K;
   o.ntiles = (int)(((size_t)o.N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM);
   const bool glu = o.etype != MXM_EXPERT_MLP;
-  if (o.q8) {
+  if (o.int8_kernels()) {
     o.bm1 = o.bm2 = 256;  // tile schedules are not used by the int8 kernels
   } else if (o.mfma) {
     // Unless a family was requested: 256 x 256 tiles where the columns allow
@@ -399,7 +419,7 @@ void alloc_workspace(MoeOp& o) {
 // would otherwise read through a null pointer).
 void require_operands(const GemmArgs& g, bool second_matrix, bool scaled) {
   if (!g.a || !g.b0 || !g.out || !g.offsets || !g.mstart || (second_matrix && !g.b1) ||
-      (scaled && (!g.scale0 || (second_matrix && !g.scale1))) ||
+      (scaled && (!g.scale0 || (g.mode == MXM_GEMM_GLU && !g.scale1))) ||
       (g.mode != MXM_GEMM_DOWN && !g.perm))
     fail_rt("OP_MOE_FEED_FORWARD internal error: expert GEMM operand not allocated (mode %d)", g.mode);
 }
@@ -435,7 +455,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   // down projection stores y token-major and the combine computes aux and
   // entropy, so no launch waits for a dispatch (mxm_moe_routing computes it
   // on demand)
-  const bool decode_flow = o.q8 && o.small_route && o.decode_flow;
+  const bool decode_flow = o.int8_kernels() && o.small_route && o.decode_flow;
   o.last_decode = decode_flow;
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
@@ -592,7 +612,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.activation = o.act;
   g1.slope = o.slope;
   g1.rows_total = o.N * o.K;
-  if (o.q8) {
+  if (o.int8_kernels()) {
     g1.b0 = o.q1.p;
     g1.b1 = o.q1b.p;
     g1.scale0 = o.s1.as<float>();
@@ -620,7 +640,11 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
   } else if (o.mfma) {
     g1.out2 = pre_out;  // the backward keeps the raw projections (and no hidden)
-    require_operands(g1, false, false);
+    if (o.q8_mfma) {
+      g1.scale0 = o.s1.as<float>();
+      g1.scale1 = glu ? o.s1b.as<float>() : nullptr;
+    }
+    require_operands(g1, false, o.q8_mfma);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g1, st);
     if (pre_out && !o.up_only)  // a kept forward: the hidden from them, as the epilogue would
       mxm_launch_hidden_from_raw_bf16(pre_out, o.N * o.K, o.Fk, o.etype, o.act, o.slope, o.hsplit,
@@ -655,7 +679,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.slope = o.slope;
   g2.y_bf16 = o.bf16 && mxm_hidden_is_bf16(o.etype, o.act);
   g2.rows_total = o.N * o.K;
-  if (o.q8) {
+  if (o.int8_kernels()) {
     g2.b0 = o.q2.p;
     g2.scale0 = o.s2.as<float>();
     if (decode_flow) {
@@ -668,7 +692,8 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
     require_operands(g2, false, true);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g2, st);
   } else if (o.mfma) {
-    require_operands(g2, false, false);
+    if (o.q8_mfma) g2.scale0 = o.s2.as<float>();
+    require_operands(g2, false, o.q8_mfma);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_mfma(g2, st);
   } else {
     require_operands(g2, false, false);
@@ -810,13 +835,28 @@ void set_weight_q8(MoeOp& o, int idx, const int8_t* q, const float* scales, cons
     HIPCK(hipMemcpyAsync(sq.p, q, n, hipMemcpyHostToDevice, st));
     src = sq.as<int8_t>();
   }
-  DevBuf* qdst = down ? &o.q2 : (o.wpe == 3 && j == 1) ? &o.q1b : &o.q1;
   DevBuf* sdst = down ? &o.s2 : (o.wpe == 3 && j == 1) ? &o.s1b : &o.s1;
-  // padded to [Kx][Fk] (up) or [Fk][Dk] (down) with zero weights; the
-  // padded columns' scales stay zero from the allocation
-  const int rows_k = down ? o.Fk : o.Kx, cols_k = down ? o.Dk : o.Fk;
-  mxm_launch_shuffle_q8(src, rows, cols, rows_k, cols_k,
-                        qdst->as<uint8_t>() + (size_t)e * rows_k * cols_k, st);
+  const int cols_k = down ? o.Dk : o.Fk;
+  if (o.q8_mfma) {
+    // the integers as bf16 in the MFMA layout (as mxm_moe_set_input's), the
+    // padding zero from the allocation
+    const bool glu = o.wpe == 3;
+    if (down) {
+      uint16_t* dst = o.w2.as<uint16_t>() + (size_t)e * o.Dk * o.Fk;
+      mxm_launch_transpose_bf16(src, MXM_DTYPE_I8, o.F, o.D, -1, dst, st, o.Fk);
+    } else {
+      const size_t ncols1 = glu ? 2 * (size_t)o.Fk : (size_t)o.Fk;
+      uint16_t* dst = o.w1.as<uint16_t>() + (size_t)e * ncols1 * o.Kx;
+      mxm_launch_transpose_bf16(src, MXM_DTYPE_I8, o.D, o.F, glu ? j : -1, dst, st, o.Kx);
+    }
+  } else {
+    DevBuf* qdst = down ? &o.q2 : (o.wpe == 3 && j == 1) ? &o.q1b : &o.q1;
+    // padded to [Kx][Fk] (up) or [Fk][Dk] (down) with zero weights; the
+    // padded columns' scales stay zero from the allocation
+    const int rows_k = down ? o.Fk : o.Kx;
+    mxm_launch_shuffle_q8(src, rows, cols, rows_k, cols_k,
+                          qdst->as<uint8_t>() + (size_t)e * rows_k * cols_k, st);
+  }
   HIPCK(hipMemcpyAsync(sdst->as<float>() + (size_t)e * cols_k, scales, (size_t)cols * 4,
                        on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
   HIPCK(hipGetLastError());
@@ -1021,6 +1061,13 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->q8 = (flags & MXM_FLAG_INT8_WEIGHTS) != 0;
     if (o->q8) {
       if (!o->bf16) fail("OP_MOE_FEED_FORWARD int8 weights need bf16 compute");
+      // from 80 routed rows per expert on the MFMA kernels on the integers q,
+      // where their tiles fit the padded widths (MXM_Q8_MFMA: 0 never, 1
+      // whenever they fit)
+      o->q8_mfma = o->mfma && q8_mfma_pays(o->N, o->E, o->K);
+      if (const char* v = std::getenv("MXM_Q8_MFMA")) o->q8_mfma = o->mfma && std::atoi(v) != 0;
+    }
+    if (o->int8_kernels()) {
       // the int8 kernels: reduction lengths multiples of 64, output columns
       // multiples of 16; one expert's matrix addressed with 32-bit offsets
       o->mfma = false;
@@ -1045,7 +1092,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     // (the launcher also wants x 16-byte aligned; D decides it for the choice)
     const bool mf_logits = o->mf_router && o->D % (o->bf16 ? 8 : 4) == 0 && o->D <= (1 << 24);
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K) &&
-                     (o->q8 || small_route_pays(o->N, o->D, o->E, mf_logits));
+                     (o->int8_kernels() || small_route_pays(o->N, o->D, o->E, mf_logits));
     if (const char* v = std::getenv("MXM_SMALL_ROUTE"))
       o->small_route = std::atoi(v) != 0 && mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
@@ -1053,7 +1100,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
       o->ldw = (o->D + MXM_LOGIT_CHUNK - 1) / MXM_LOGIT_CHUNK * MXM_LOGIT_CHUNK;
       o->router_t.alloc((size_t)((o->E + 63) / 64) * o->ldw * 64 * (o->bf16 ? 2 : 4));
     }
-    if (o->q8) {
+    if (o->int8_kernels()) {
       o->q1.alloc(EE * F1);
       if (o->wpe == 3) o->q1b.alloc(EE * F1);
       o->q2.alloc(EE * F2);
@@ -1074,6 +1121,18 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
       if (F1 != DF || F2 != DF) {
         HIPCK(hipMemsetAsync(o->w1.p, 0, o->w1.bytes, o->stream));
         HIPCK(hipMemsetAsync(o->w2.p, 0, o->w2.bytes, o->stream));
+        HIPCK(hipStreamSynchronize(o->stream));
+      }
+      if (o->q8_mfma) {
+        // padded output channels keep a zero scale (their weights are zero)
+        o->s1.alloc(EE * o->Fk * 4);
+        HIPCK(hipMemsetAsync(o->s1.p, 0, o->s1.bytes, o->stream));
+        if (o->wpe == 3) {
+          o->s1b.alloc(EE * o->Fk * 4);
+          HIPCK(hipMemsetAsync(o->s1b.p, 0, o->s1b.bytes, o->stream));
+        }
+        o->s2.alloc(EE * o->Dk * 4);
+        HIPCK(hipMemsetAsync(o->s2.p, 0, o->s2.bytes, o->stream));
         HIPCK(hipStreamSynchronize(o->stream));
       }
     } else {
@@ -1317,7 +1376,7 @@ int mxm_moe_block_forward_host(int64_t h, const void* x, int x_dtype, int64_t ro
 // caller's rows as they are).
 bool mfma_backward_fits(const MoeOp& o) {
   const int NC = o.wpe == 3 ? 2 * o.Fk : o.Fk;
-  return o.mfma && o.Dk == o.D && o.Kx == o.D && o.Fk % 32 == 0 &&
+  return o.mfma && !o.q8 && o.Dk == o.D && o.Kx == o.D && o.Fk % 32 == 0 &&
          mxm_mfma_tile_rows(o.Fk, o.D, o.family) > 0 &&
          mxm_mfma_tile_rows(NC, o.D, o.family) > 0 && mxm_mfma_tile_rows(o.D, NC, o.family) > 0;
 }
@@ -2045,7 +2104,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
   const int64_t flow = !op->have_last ? -1 : op->last_decode ? 2 : op->small_route ? 1 : 0;
-  const int64_t vals[8] = {op->q8 ? 2 : op->mfma ? 1 : 0,
+  const int64_t vals[8] = {op->q8_mfma ? 3 : op->q8 ? 2 : op->mfma ? 1 : 0,
                            (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM),
                            (int64_t)op->Fk, (int64_t)op->Dk, (int64_t)op->Kx, flow};

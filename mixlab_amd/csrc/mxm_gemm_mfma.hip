@@ -213,6 +213,25 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  // int8 weights (the bf16 B holds the integers q): this lane's output
+  // columns' scales, read before the k loop so their latency is hidden.
+  // Lane l's accumulators of column tile j are column j*32 + l%32 of the
+  // wave's; GLU tiles alternate gate (scale0) and up (scale1) over the same
+  // 32 hidden units.
+  float scv[TN];
+  if constexpr (Epi<EPI>::SCALED) {
+    const int wc0 = n0 + wn * TN * 32;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (MODE == MXM_GEMM_GLU) {
+        const int hc = a.Ncols / 2;
+        const float* sp = (j & 1) ? a.scale1 : a.scale0;
+        scv[j] = sp[(size_t)e * hc + wc0 / 2 + (j >> 1) * 32 + (lane & 31)];
+      } else {
+        scv[j] = a.scale0[(size_t)e * a.Ncols + wc0 + j * 32 + (lane & 31)];
+      }
+    }
+  }
 
   const uint16_t* __restrict__ A = static_cast<const uint16_t*>(a.a);
   // B rows hold Kb k values; the split down projection reads W_down [D][F]
@@ -420,6 +439,14 @@ __global__ __launch_bounds__(TL::NT, TL::WPS * 256 / TL::NT) void gemm_kernel(Ge
 #undef MXM_COMPUTE
 #undef MXM_KSTEP
 
+  if constexpr (Epi<EPI>::SCALED) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] *= scv[j];
+  }
   if constexpr (Epi<EPI>::Y_F32) {
     // y in fp32, straight from the accumulators: register r of lane l holds
     // C[(r/4)*8 + (l/32)*4 + r%4][l%32], so each store instruction writes
@@ -664,11 +691,14 @@ void launch_epi(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
 template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK>
 void launch_family(const GemmArgs& a, hipStream_t s);
 
-// An up projection that also keeps its raw projections (GemmArgs::out2).
+// An up projection that also keeps its raw projections (GemmArgs::out2),
+// or whose weights are int8 integers with per-column scales (scale0).
 template <int BM, int BN, int WM, int WN, int WPS, int NSTG, int BKK, int EPI>
 void launch_up(const GemmArgs& a, hipStream_t s, int blocks, int ngroups) {
   if (a.out2)
     launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_KEEP + EPI>(a, s, blocks, ngroups);
+  else if (a.scale0)
+    launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SCALE + EPI>(a, s, blocks, ngroups);
   else
     launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI>(a, s, blocks, ngroups);
 }
@@ -679,7 +709,11 @@ void launch_family(const GemmArgs& a, hipStream_t s) {
   const int per_group = GM * (a.Ncols / BN);
   const int blocks = ((ngroups + 7) / 8) * 8 * per_group;
   if (a.mode == MXM_GEMM_DOWN) {
-    if (a.h_split)
+    if (a.scale0 && a.h_split)
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SCALE + EPI_DOWN_F32>(a, s, blocks, ngroups);
+    else if (a.scale0)
+      launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_SCALE + EPI_DOWN>(a, s, blocks, ngroups);
+    else if (a.h_split)
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_DOWN_F32>(a, s, blocks, ngroups);
     else if (a.f32_out)
       launch_epi<BM, BN, WM, WN, WPS, NSTG, BKK, EPI_F32>(a, s, blocks, ngroups);

@@ -284,11 +284,17 @@ enum { EPI_SWIGLU, EPI_GEGLU, EPI_MLP_SILU, EPI_MLP_GELU, EPI_MLP_RELU, EPI_MLP_
 // GemmArgs::out2 instead of the hidden (the MFMA backward derives H from
 // them in its activation pass).
 constexpr int EPI_KEEP = 16;
+// EPI_SCALE + a kind: the accumulators are multiplied by a per-output-column
+// fp32 scale (GemmArgs::scale0, and scale1 for the up matrix of a GLU pair,
+// each [E][output columns]) before anything else; the int8 weights' flow on
+// the MFMA kernels, whose bf16 weights hold the integers q.
+constexpr int EPI_SCALE = 32;
 
 template <int EPI_>
 struct Epi {
-  static constexpr int EPI = EPI_ % EPI_KEEP;
-  static constexpr bool KEEP_RAW = EPI_ >= EPI_KEEP;
+  static constexpr int EPI = EPI_ & (EPI_KEEP - 1);
+  static constexpr bool KEEP_RAW = (EPI_ & EPI_KEEP) != 0;
+  static constexpr bool SCALED = (EPI_ & EPI_SCALE) != 0;
   static constexpr int MODE = EPI <= EPI_GEGLU ? MXM_GEMM_GLU
                               : (EPI == EPI_DOWN || EPI == EPI_DOWN_F32 || EPI == EPI_F32)
                                   ? MXM_GEMM_DOWN
@@ -375,7 +381,8 @@ void mxm_launch_rows_to_f32(const void* src, int src_dtype, int64_t rows, int co
 void mxm_launch_pad_rows_bf16(const uint16_t* src, int64_t rows, int cols, int ldd, uint16_t* dst,
                               hipStream_t s);
 void mxm_launch_to_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n, hipStream_t s);
-// Transposed bf16 copy of one weight matrix src [Kd, C] (x.W layout):
+// Transposed bf16 copy of one weight matrix src [Kd, C] (x.W layout; fp32,
+// bf16 or int8 by src_dtype, an MXM_DTYPE_* value):
 // dst[q * ldd + k] = bf16(src[k, c]) with q = c (slot < 0), or, for the GLU
 // interleave, q = (c/32)*64 + slot*32 + c%32 with slot 0 = gate, 1 = up;
 // ldd = Kd by default (a larger ldd leaves each row's padded tail as it is).

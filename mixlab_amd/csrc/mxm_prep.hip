@@ -1,11 +1,13 @@
 // Weight preparation, run once when weights are uploaded: dtype conversion
 // to the flow's storage type and the transposed / GLU-interleaved layout of
-// the MFMA family.  Source dtypes: 1 = fp32, 2 = bf16 bits.
+// the MFMA family.  Source dtypes: 1 = fp32, 2 = bf16 bits, 3 = int8 (the
+// integers of int8 weights, exact in bf16: |q| <= 128 needs 8 bits).
 #include "mxm_kernels.h"
 
 namespace {
 
 __device__ __forceinline__ float src_at(const void* p, int dtype, size_t i) {
+  if (dtype == 3) return (float)static_cast<const int8_t*>(p)[i];
   return dtype == 2 ? mxm_bf2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 

@@ -345,11 +345,14 @@ def test_c5_int8_decode(gpu_lib):
 
 
 @pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
-def test_int8_expert_types(gpu_lib, name, etype, act, slope):
+def test_int8_expert_types(gpu_lib, monkeypatch, name, etype, act, slope):
     """All expert kinds through the int8 kernels, with experts far above 16
-    rows (several row passes) and some with none."""
+    rows (several row passes) and some with none (MXM_Q8_MFMA=0: at 100
+    rows per expert the op would otherwise run on the MFMA tiles)."""
     from mixlab_amd.op import MoEFeedForward
     from mixlab_amd.workloads import bf16_bits, quantize_int8
+
+    monkeypatch.setenv("MXM_Q8_MFMA", "0")
 
     rng = np.random.default_rng(100 + etype * 4 + act)
     N, D, E, K, F = 300, 256, 6, 2, 192
@@ -372,6 +375,7 @@ def test_int8_expert_types(gpu_lib, name, etype, act, slope):
                 op.set_input_q8(2 + e * wpe + j, *q8[e][j])
         delta, aux, ent = op.forward_host(bf16_bits(x))
         routing = op.routing()
+        assert op.info()["int8_kernels"]
     want = run_oracle(x, wr, deq, K=K, expert_type=etype, activation=act, slope=slope, bf16=True)
     assert_routing_equal(routing, want)
     assert routing["counts"][5] == 0 and routing["counts"].max() > 48
@@ -411,6 +415,7 @@ def test_int8_decode_flows_agree(gpu_lib, monkeypatch, shape):
     from mixlab_amd.workloads import quantize_int8
 
     N, D, E, K, F, etype, act = shape
+    monkeypatch.setenv("MXM_Q8_MFMA", "0")  # the int8 kernels' flows at every shape here
     rng = np.random.default_rng(N * 7 + D + E)
     wpe = 2 if etype == 2 else 3
     xs = [round_bf16(rng.standard_normal((N, D), dtype=np.float32)) for _ in range(2)]
@@ -449,6 +454,125 @@ def test_int8_decode_flows_agree(gpu_lib, monkeypatch, shape):
         assert same_bits(d, d0), i
         assert same_bits(np.float32(a), np.float32(a0)), (i, a, a0)
         assert same_bits(np.float32(en), np.float32(e0)), (i, en, e0)
+
+
+# (N, D, E, K, F, MXM_FLAG_MFMA_TILE_*) of int8 ops past the decode sizes,
+# which run on the MFMA tiles with the integers q as bf16: D and F on the
+# tiles; D and F off them (x padded to 256, F run at 256 with zero weights and
+# zero scales); the two other tile families
+Q8_MFMA_SHAPES = [(1100, 256, 6, 2, 192, 0), (1300, 200, 5, 2, 150, 0),
+                  (1100, 256, 6, 2, 256, 4), (1100, 256, 6, 2, 256, 8)]
+
+
+def _int8_case(rng, N, D, E, F, etype):
+    wpe = 2 if etype == 2 else 3
+    from mixlab_amd.workloads import quantize_int8
+    x = round_bf16(rng.standard_normal((N, D), dtype=np.float32))
+    wr = round_bf16(rng.standard_normal((D, E), dtype=np.float32) * np.float32(0.08))
+    q8 = [[quantize_int8(rng.standard_normal(((F, D) if j == wpe - 1 else (D, F)),
+                                             dtype=np.float32) * np.float32(0.02))
+           for j in range(wpe)] for _ in range(E)]
+    return x, wr, q8
+
+
+def _run_int8(x, wr, q8, K, etype, act, slope, flags=0):
+    from mixlab_amd.op import MoEFeedForward
+
+    N, D = x.shape
+    E, wpe = len(q8), len(q8[0])
+    F = q8[0][0][0].shape[1]
+    with MoEFeedForward([1, N, D, E, K, etype, F, act], [slope], compute_dtype="bf16",
+                        flags=_lib.MXM_FLAG_INT8_WEIGHTS | flags) as op:
+        op.set_input(1, bf16_bits(wr))
+        for e in range(E):
+            for j in range(wpe):
+                op.set_input_q8(2 + e * wpe + j, *q8[e][j])
+        delta, aux, ent = op.forward_host(bf16_bits(x))
+        return delta, aux, ent, op.routing(), op.info()
+
+
+@pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
+@pytest.mark.parametrize("shape", Q8_MFMA_SHAPES, ids=[f"{s[0]}x{s[1]}f{s[4]}t{s[5]}"
+                                                       for s in Q8_MFMA_SHAPES])
+def test_int8_mfma_expert_types(gpu_lib, monkeypatch, shape, name, etype, act, slope):
+    """int8 weights past the decode sizes: the MFMA tiles multiply by the
+    integers q held as bf16 and scale the fp32 accumulators per output
+    column before the activation -- the int8 kernels' arithmetic in another
+    order.  The MFMA flow (the default at these sizes) and the int8 kernels
+    on the same op (MXM_Q8_MFMA=0) are each checked against the restatement
+    fed the exact q * s (only the accumulation order differs) and fed
+    bf16(q * s), with the same routing, aux and entropy bit for bit."""
+    N, D, E, K, F, fam = shape
+    if fam and etype != 0:
+        pytest.skip("tile families are covered on one expert kind")
+    x, wr, q8 = _int8_case(np.random.default_rng(500 + N + D + etype * 4 + act), N, D, E, F,
+                           etype)
+    out = {}
+    for mf in (None, "0"):
+        if mf is None:
+            monkeypatch.delenv("MXM_Q8_MFMA", raising=False)
+        else:
+            monkeypatch.setenv("MXM_Q8_MFMA", mf)
+        print(f"int8 Q8_MFMA={mf} {name} N {N} D {D} E {E} F {F} family flag {fam}", flush=True)
+        out[mf] = _run_int8(x, wr, q8, K, etype, act, slope, flags=fam)
+    info = out[None][4]
+    assert info["int8"] and info["mfma"] and not info["int8_kernels"], info
+    assert info["ffn_kernel"] == (F + 127) // 128 * 128 and info["d_reduce"] == (D + 63) // 64 * 64
+    assert out["0"][4]["int8_kernels"] and not out["0"][4]["mfma"]
+    exact = [[q.astype(np.float32) * s[None, :] for q, s in ws] for ws in q8]
+    deq = [[round_bf16(m) for m in ws] for ws in exact]
+    want_exact = oracle.moe_forward(x, wr, exact, top_k=K, expert_type=etype, activation=act,
+                                    leaky_slope=slope, bf16=True, prerounded=True)
+    want = run_oracle(x, wr, deq, K=K, expert_type=etype, activation=act, slope=slope, bf16=True)
+    for mf, (delta, aux, ent, routing, _) in out.items():
+        assert_routing_equal(routing, want_exact)
+        err_exact = rel_l2(delta, want_exact["delta"])
+        err = rel_l2(delta, want["delta"])
+        print(f"  Q8_MFMA={mf}: rel L2 {err_exact:.3e} (exact q*s), {err:.3e} (bf16(q*s))")
+        assert err_exact <= MFMA_TIGHT
+        assert err <= BF16_TOL
+    assert same_bits(np.float32(out[None][1]), np.float32(out["0"][1]))
+    assert same_bits(np.float32(out[None][2]), np.float32(out["0"][2]))
+    assert abs(out[None][1] - want_exact["aux"]) <= 1e-2 * abs(want_exact["aux"])
+    assert abs(out[None][2] - want_exact["entropy"]) <= 1e-3 * abs(want_exact["entropy"])
+
+
+def test_c2_int8_mfma_full(gpu_lib, monkeypatch):
+    """C2's shape with int8 weights (16,384 tokens, past the decode sizes):
+    the MFMA flow against the restatement on sampled rows (exact q * s and
+    bf16(q * s)), and on every row against the int8 kernels, an independent
+    implementation of the same arithmetic (MXM_Q8_MFMA=0)."""
+    import dataclasses
+
+    cfg = dataclasses.replace(CONFIGS["C2"], int8_weights=True, name="C2int8")
+    w = make_workload(cfg)
+    monkeypatch.delenv("MXM_Q8_MFMA", raising=False)
+    print("C2 int8 on the MFMA tiles", flush=True)
+    delta, aux, ent, routing, info = run_gpu_workload(w)
+    assert info["int8"] and info["mfma"] and not info["int8_kernels"], info
+    rows = np.sort(np.random.default_rng(2).choice(cfg.N, size=256, replace=False)).astype(np.int32)
+    exact = [[q.astype(np.float32) * s[None, :] for q, s in ws] for ws in w.q8]
+    want_exact = oracle.moe_forward(w.x, w.router_w, exact, top_k=cfg.K, bf16=True, rows=rows,
+                                    prerounded=True)
+    want = run_oracle_workload(w, rows=rows)
+    assert_routing_equal(routing, want_exact)
+    err_exact = rel_l2(delta[rows], want_exact["delta"][rows])
+    err = rel_l2(delta[rows], want["delta"][rows])
+    monkeypatch.setenv("MXM_Q8_MFMA", "0")
+    print("C2 int8 on the int8 kernels", flush=True)
+    kdelta, kaux, kent, krouting, kinfo = run_gpu_workload(w)
+    assert kinfo["int8_kernels"]
+    assert_routing_equal(krouting, want_exact)
+    err_all = rel_l2(delta, kdelta)
+    num = np.linalg.norm((delta - kdelta).astype(np.float64), axis=1)
+    den = np.linalg.norm(kdelta.astype(np.float64), axis=1)
+    worst = float(np.max(num / np.maximum(den, 1e-30)))
+    print(f"C2 int8 MFMA: sampled rel L2 {err_exact:.3e} (exact q*s), {err:.3e} (bf16(q*s)); "
+          f"all rows against the int8 kernels {err_all:.3e}, worst row {worst:.3e}")
+    assert err_exact <= MFMA_TIGHT and err <= BF16_TOL
+    assert err_all <= MFMA_TIGHT and worst <= BF16_TOL
+    assert same_bits(np.float32(aux), np.float32(kaux))
+    assert same_bits(np.float32(ent), np.float32(kent))
 
 
 def _block_case(seed, N, D, E, F, bf16, x_fp32_in_bf16_flow=False):
@@ -672,7 +796,8 @@ ROUTER_CHOICE = [
     # E > 64
     (1024, 128, 96, 4, "bf16", False, 0),   # D*E = 12288
     (1024, 256, 96, 4, "bf16", False, 1),   # D*E = 24576
-    (1024, 256, 8, 2, "bf16", True, 2),     # int8 keeps the decode flow
+    (256, 256, 8, 2, "bf16", True, 2),      # int8 below 80 rows per expert: the decode flow
+    (1024, 256, 8, 2, "bf16", True, 0),     # int8 from 80 on: MFMA tiles, bf16's router choice
     (1100, 2048, 64, 8, "bf16", False, 0),  # past the one-launch router's limit
 ]
 

@@ -109,8 +109,11 @@ FAMILIES = [
      dict(B=1, T=64, D=256, E=8, K=2, F=256)),
     ("geglu_split", dict(B=1, T=1500, D=256, E=6, K=2, F=512, etype=1, act=1),
      dict(B=1, T=100, D=256, E=6, K=2, F=256, etype=1, act=1)),
-    ("int8_decode", dict(B=1, T=512, D=1024, E=16, K=4, F=768, int8=True),
+    ("int8_decode", dict(B=1, T=512, D=1024, E=32, K=4, F=1024, int8=True),
      dict(B=1, T=64, D=512, E=8, K=2, F=512, int8=True)),
+    # int8 weights at 80 or more rows per expert: the MFMA tiles, scaled
+    ("int8_mfma", dict(B=1, T=1100, D=512, E=8, K=2, F=1024, int8=True),
+     dict(B=1, T=700, D=256, E=4, K=2, F=512, int8=True)),
     ("fp32_simt", dict(B=1, T=2400, D=128, E=4, K=2, F=256, dtype="fp32"),
      dict(B=1, T=33, D=128, E=4, K=2, F=128, dtype="fp32")),
     # the tiled router's logits on the matrix cores (32 < E <= 64)
@@ -130,6 +133,9 @@ def test_noalloc_matches_forward(gpu_lib, name, big, small):
             assert op.info()["workspace_bytes"] <= _lib.MXM_NOALLOC_MAX_BYTES
         # the first op's workspace is well above the memory check's slack
         assert ops[0][0].info()["workspace_bytes"] > 6 << 20
+        if big.get("int8"):  # the int8 kernels, or the MFMA tiles scaled
+            for op, _ in ops:
+                assert op.info()["int8_kernels"] == (name == "int8_decode")
         for io in ios:  # first launches: the runtime's own lazy setup
             io.forward(noalloc=True)
             io.results()
