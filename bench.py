@@ -7,7 +7,8 @@ in HBM.  The headline workload is C4: d_model 2048, 64 experts, top-8, gated
 expert hidden 1024, 65,536 tokens, bf16; `roofline` is its grouped GEMM
 (both launches) against the bf16 MFMA peak.  The same run also measures C2
 and C3 (the near-uniform and the Zipf-ragged MFMA-bound configurations,
-under "configs"), C5, the decode shape with int8 expert weights (64 tokens;
+under "configs", with C2 also with int8 expert weights), C5, the decode
+shape with int8 expert weights (64 tokens;
 HBM-bound, under "decode_int8"), the backward on the C2 shape (fp32 and
 bf16), on the Zipf-ragged C3 shape and on the headline shape (bf16), and the
 CPU baseline.  Prints one JSON line.
@@ -383,7 +384,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="target seconds per timed run of the CPU baseline (0 disables it)")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the C1, C2fp32, C2, C3 and C4F sections")
+                    help="skip the C1, C2fp32, C2, C2int8, C3 and C4F sections")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time hipBLASLt (torch.matmul) on the dense equivalents of the "
                          "grouped GEMM's two launches (in a child process)")
@@ -508,14 +509,21 @@ def main() -> int:
                                            / PEAK_FP32_TFLOPS},
                            "stages_ms": {k: v for k, v in rf["stages"].items() if k != "forwards"},
                            "executor": rf["info"]}
-        for name in ("C2", "C3", "C4F"):
+        # C2int8: C2 with int8 expert weights, a prefill-sized int8 batch (256
+        # routed rows per expert), which runs on the MFMA tiles with the
+        # integers as bf16 and the scales in the epilogue
+        c2q = dataclasses.replace(CONFIGS["C2"], int8_weights=True, name="C2int8")
+        for name in ("C2", "C2int8", "C3", "C4F"):
             if name == cfg.name:
                 continue
-            c = CONFIGS[name]
+            c = c2q if name == "C2int8" else CONFIGS[name]
             _, rc = run_config(c, args.steps, args.warmup)
             counts = np.asarray(rc["counts"])
             extra[name] = {"tokens": c.N, "d_model": c.D, "experts": c.E, "top_k": c.K,
-                           "expert_hidden": c.F, "tokens_per_s": rc["tokens_per_s"],
+                           "expert_hidden": c.F,
+                           "weights": "int8, fp32 per-output-channel scales"
+                                      if c.int8_weights else c.dtype,
+                           "tokens_per_s": rc["tokens_per_s"],
                            "ms_per_step": rc["ms_per_step"],
                            "grouped_gemm": grouped_gemm_summary(c, rc["stages"]),
                            "stages_ms": {k: v for k, v in rc["stages"].items() if k != "forwards"},
