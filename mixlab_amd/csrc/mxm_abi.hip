@@ -175,6 +175,13 @@ struct MoeOp {
   // accumulators; q1, q1b and q2 are not allocated
   bool q8_mfma = false;
   bool int8_kernels() const { return q8 && !q8_mfma; }
+  // bf16 ops at decode sizes (few routed rows per expert): the expert
+  // weights also in the decode kernels' block layout at 2 bytes per weight
+  // (d1 = gate or up, d1b = up, d2 = down), which the forward streams
+  // instead of running the MFMA tiles; the MFMA layout (w1, w2) stays for
+  // the backward, whose own forwards keep the tiles
+  bool dec16 = false;
+  DevBuf d1, d1b, d2;
   int n_cu = 256;        // CUs of the op's device
   int fam1 = 0, fam2 = 0;  // MFMA tile families of the up and down GEMMs
   int fam_dh = 0;           // ... of the backward's dH = dY W_down^T (dX uses fam2)
@@ -194,6 +201,7 @@ struct MoeOp {
   // offsets, perm, slot_pos) is computed when the routing is queried, from
   // its per-token results and the probabilities at last_probs
   bool last_decode = false;
+  bool last_stream = false;  // ... and ran on the decode kernels
   float* last_probs = nullptr;
   // the int8 decode flow (1, default) or the dispatch of the one-launch
   // router (0): MXM_DECODE_FLOW at creation, for measurements of the two
@@ -325,6 +333,21 @@ bool small_route_pays(int N, int D, int E, bool mf) {
 // 256 with ffn 128-192, whose forwards are launch-bound either way.
 bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 80 * (int64_t)E; }
 
+// Whether a bf16 op at decode sizes streams its weights through the decode
+// kernels rather than running the MFMA tiles.  Both read the same bf16
+// bytes, but the tiles, built for compute-bound products, stream weights at
+// about 3.4 TB/s, the decode kernels at 5-5.5.  The decode kernels take 16
+// rows per pass, 32 once an expert averages more than 12, and stream an
+// expert's weights once per pass, so past about 24 routed rows per expert
+// (N*K/E) the second passes make them the slower.  Measured on MI355X
+// (whole forwards, tiles against stream): D 2048 / E 64 / K 8 / ffn 1408 at
+// N 64 0.355 against 0.224 ms, N 128 0.351 / 0.260, N 256 0.364 / 0.459;
+// ffn 1024 at N 64 0.260 / 0.166, N 256 0.274 / 0.331; D 512 / E 8 / K 2 /
+// ffn 2048 at N 32 0.071 / 0.044, N 64 0.072 / 0.048, N 128 0.074 / 0.079;
+// D 1024 / E 32 / K 4 / ffn 1024 at N 128 0.073 / 0.061, N 256 0.080 / 0.095.
+constexpr int DEC16_MAX_RPE = 24;
+bool dec16_pays(int N, int E, int K) { return (int64_t)N * K < DEC16_MAX_RPE * (int64_t)E; }
+
 // Row-tile heights and tile counts of the forward's kernels; a function of
 // the op's parameters only.
 void set_schedule(MoeOp& o) {
@@ -455,8 +478,13 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   // down projection stores y token-major and the combine computes aux and
   // entropy, so no launch waits for a dispatch (mxm_moe_routing computes it
   // on demand)
-  const bool decode_flow = o.int8_kernels() && o.small_route && o.decode_flow;
+  // bf16 weights at decode sizes stream through the same kernels, except in
+  // the backward's own forwards (which keep the tiles' raw projections)
+  const bool dec16 = o.dec16 && !pre_out && !o.up_only && !o.route_only && !o.keep_probs;
+  const bool stream = o.int8_kernels() || dec16;  // the decode kernels
+  const bool decode_flow = stream && o.small_route && o.decode_flow;
   o.last_decode = decode_flow;
+  o.last_stream = stream;
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
     mxm_launch_to_bf16(x, MXM_DTYPE_F32, static_cast<uint16_t*>(w.xcast), (int64_t)o.N * o.D, st);
@@ -603,7 +631,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.mstart = sa.mstart1;
   g1.E = o.E;
   g1.Kd = o.Kx;
-  g1.Ncols = (o.mfma && glu) ? 2 * o.Fk : o.Fk;
+  g1.Ncols = (o.mfma && glu && !stream) ? 2 * o.Fk : o.Fk;
   g1.max_mtiles = o.max_mtiles1;
   g1.simt_bm = o.bm1;
   g1.simt_vec = o.simt_vec;
@@ -612,11 +640,17 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g1.activation = o.act;
   g1.slope = o.slope;
   g1.rows_total = o.N * o.K;
-  if (o.int8_kernels()) {
-    g1.b0 = o.q1.p;
-    g1.b1 = o.q1b.p;
-    g1.scale0 = o.s1.as<float>();
-    g1.scale1 = o.s1b.as<float>();
+  if (stream) {
+    if (o.q8) {
+      g1.b0 = o.q1.p;
+      g1.b1 = o.q1b.p;
+      g1.scale0 = o.s1.as<float>();
+      g1.scale1 = o.s1b.as<float>();
+    } else {
+      g1.b0 = o.d1.p;
+      g1.b1 = o.d1b.p;
+      g1.w_bf16 = true;
+    }
     if (decode_flow) {
       g1.top_idx = w.top_idx;
       g1.topk = o.K;
@@ -636,7 +670,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
       g1.daux.aux_weight = blk ? blk->aux_weight : 1.0f;
       g1.daux.aux_scaled = blk ? blk->aux_scaled : nullptr;
     }
-    require_operands(g1, glu, true);
+    require_operands(g1, glu, o.q8);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g1, st);
   } else if (o.mfma) {
     g1.out2 = pre_out;  // the backward keeps the raw projections (and no hidden)
@@ -667,7 +701,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.mstart = sa.mstart2;
   g2.E = o.E;
   // the split MFMA down projection reduces over both planes of H
-  g2.Kd = (o.hsplit && o.mfma) ? 2 * o.Fk : o.Fk;
+  g2.Kd = (o.hsplit && o.mfma && !stream) ? 2 * o.Fk : o.Fk;
   g2.h_split = o.hsplit;
   g2.Ncols = o.Dk;
   g2.max_mtiles = o.max_mtiles2;
@@ -679,9 +713,14 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   g2.slope = o.slope;
   g2.y_bf16 = o.bf16 && mxm_hidden_is_bf16(o.etype, o.act);
   g2.rows_total = o.N * o.K;
-  if (o.int8_kernels()) {
-    g2.b0 = o.q2.p;
-    g2.scale0 = o.s2.as<float>();
+  if (stream) {
+    if (o.q8) {
+      g2.b0 = o.q2.p;
+      g2.scale0 = o.s2.as<float>();
+    } else {
+      g2.b0 = o.d2.p;
+      g2.w_bf16 = true;
+    }
     if (decode_flow) {
       // the rows the up projection handed on (offsets, counts, y rows)
       g2.top_idx = w.top_idx;
@@ -689,7 +728,7 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
       g2.tk_counts = w.counts;
       g2.tk_ypos = w.slot_rank;
     }
-    require_operands(g2, false, true);
+    require_operands(g2, false, o.q8);
     for (int rep = 0; rep < reps; ++rep) mxm_launch_gemm_q8(g2, st);
   } else if (o.mfma) {
     if (o.q8_mfma) g2.scale0 = o.s2.as<float>();
@@ -779,10 +818,17 @@ void set_weight(MoeOp& o, int idx, int dtype, const int64_t* shape, int ndim, co
     if (j == o.wpe - 1) {
       uint16_t* dst = o.w2.as<uint16_t>() + (size_t)e * o.Dk * o.Fk;
       mxm_launch_transpose_bf16(src, dtype, o.F, o.D, -1, dst, st, o.Fk);
+      if (o.dec16)
+        mxm_launch_shuffle_bf16(src, dtype, o.F, o.D, o.Fk, o.Dk,
+                                o.d2.as<uint16_t>() + (size_t)e * o.Fk * o.Dk, st);
     } else {
       const size_t ncols1 = glu ? 2 * (size_t)o.Fk : (size_t)o.Fk;
       uint16_t* dst = o.w1.as<uint16_t>() + (size_t)e * ncols1 * o.Kx;
       mxm_launch_transpose_bf16(src, dtype, o.D, o.F, glu ? j : -1, dst, st, o.Kx);
+      if (o.dec16)
+        mxm_launch_shuffle_bf16(src, dtype, o.D, o.F, o.Kx, o.Fk,
+                                (j == 1 ? o.d1b : o.d1).as<uint16_t>() + (size_t)e * o.Kx * o.Fk,
+                                st);
     }
   } else {
     // SIMT family keeps the reference layout in fp32 storage, values rounded
@@ -1080,6 +1126,14 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     }
     o->family = (flags & MXM_FLAG_MFMA_TILE_MASK) >> 2;
     o->hsplit = (o->mfma || o->q8) && !mxm_hidden_is_bf16(o->etype, o->act);
+    // bf16 weights at decode sizes: the decode kernels' weight stream
+    // (MXM_BF16_DECODE: 0 never, 1 at every decode size); not for ops kept
+    // for the backward, whose forward keeps the tiles' raw projections
+    {
+      const bool can = o->mfma && !o->q8 && !o->train && mxm_route_small_fits(o->N, o->D, o->E, o->K);
+      o->dec16 = can && dec16_pays(o->N, o->E, o->K);
+      if (const char* v = std::getenv("MXM_BF16_DECODE")) o->dec16 = can && std::atoi(v) != 0;
+    }
     o->have.assign((size_t)n_inputs, 0);
     HIPCK(hipGetDevice(&o->device));
     HIPCK(hipDeviceGetAttribute(&o->n_cu, hipDeviceAttributeMultiprocessorCount, o->device));
@@ -1092,7 +1146,8 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     // (the launcher also wants x 16-byte aligned; D decides it for the choice)
     const bool mf_logits = o->mf_router && o->D % (o->bf16 ? 8 : 4) == 0 && o->D <= (1 << 24);
     o->small_route = mxm_route_small_fits(o->N, o->D, o->E, o->K) &&
-                     (o->int8_kernels() || small_route_pays(o->N, o->D, o->E, mf_logits));
+                     (o->int8_kernels() || o->dec16 ||
+                      small_route_pays(o->N, o->D, o->E, mf_logits));
     if (const char* v = std::getenv("MXM_SMALL_ROUTE"))
       o->small_route = std::atoi(v) != 0 && mxm_route_small_fits(o->N, o->D, o->E, o->K);
     set_schedule(*o);
@@ -1122,6 +1177,12 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
         HIPCK(hipMemsetAsync(o->w1.p, 0, o->w1.bytes, o->stream));
         HIPCK(hipMemsetAsync(o->w2.p, 0, o->w2.bytes, o->stream));
         HIPCK(hipStreamSynchronize(o->stream));
+      }
+      if (o->dec16) {
+        // (every element, padding included, is written at binding)
+        o->d1.alloc(EE * F1 * 2);
+        if (o->wpe == 3) o->d1b.alloc(EE * F1 * 2);
+        o->d2.alloc(EE * F2 * 2);
       }
       if (o->q8_mfma) {
         // padded output channels keep a zero scale (their weights are zero)
@@ -2104,7 +2165,7 @@ int mxm_moe_stage_times(int64_t h, float* ms, int n) {
 int mxm_moe_info(int64_t h, int64_t* info, int n) {
   OP_OR_RETURN(h);
   const int64_t flow = !op->have_last ? -1 : op->last_decode ? 2 : op->small_route ? 1 : 0;
-  const int64_t vals[8] = {op->q8_mfma ? 3 : op->q8 ? 2 : op->mfma ? 1 : 0,
+  const int64_t vals[8] = {op->q8_mfma ? 3 : op->q8 ? 2 : op->dec16 ? 4 : op->mfma ? 1 : 0,
                            (int64_t)layout_workspace(*op, nullptr).bytes, (int64_t)op->bm1,
                            (int64_t)((op->N + MXM_ROUTER_TM - 1) / MXM_ROUTER_TM),
                            (int64_t)op->Fk, (int64_t)op->Dk, (int64_t)op->Kx, flow};

@@ -19,6 +19,13 @@
 // an integer in [0, 255], which bf16 holds exactly; the +128 offset is
 // removed after the loop with the rows' sums (an MFMA against ones).
 //
+// bf16 weights (GemmArgs::w_bf16, bf16 ops at decode sizes): the same
+// blocks at 2 bytes per weight (mxm_launch_shuffle_bf16), 2 KB each, lane l
+// holding its 16 values at bytes 32*l .. 32*l+31 as two 16-byte pieces; no
+// conversion, no offset and no scale -- the accumulators are the bf16 flow's
+// fp32 products.  The ring holds half as many blocks, so the bytes in
+// flight and the registers stay those of the int8 stream.
+//
 // Split hidden (kinds whose hidden is fp32 in the bf16 flow, GemmArgs::
 // h_split): the up projection stores H as the planes hi | lo, and the down
 // projection stages a pass's 16 rows twice -- row group 0 from the hi
@@ -40,6 +47,15 @@
 #endif
 #ifndef MXM_Q8_DEPTH_ONE
 #define MXM_Q8_DEPTH_ONE 8
+#endif
+// bf16 weights: 2 KB blocks.  Measured (64 tokens, D 2048, E 64, top-8):
+// gate+up 143.3 us at a ring of 3, 140.1 at 4, 154.8 at 5; down 74.3 us at
+// 4, 72.6 at 6, 72.6 at 8, but at ffn 1024 57.6 / 61.4 / 60.1
+#ifndef MXM_D16_DEPTH_GLU
+#define MXM_D16_DEPTH_GLU 4
+#endif
+#ifndef MXM_D16_DEPTH_ONE
+#define MXM_D16_DEPTH_ONE 4
 #endif
 
 // Weight blocks are read once per forward, so they are loaded nontemporal
@@ -128,9 +144,12 @@ __device__ void decode_aux(const DecodeAux& a, void* scratch) {
 // each row's token-major y row (n * K + j, j the expert's place among the
 // token's experts in ascending order) to the down projection, which reads
 // them as the dispatch's offsets would be read and stores y token-major.
-template <int EPI, int P, int RG, bool TOPK>
+// W16: bf16 weights (2 KB blocks, two 16-byte pieces per lane).
+template <int EPI, int P, int RG, bool TOPK, bool W16>
 __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
   constexpr int MODE = Epi<EPI>::MODE;
+  constexpr int BW = W16 ? 2 : 1;    // bytes per weight
+  constexpr int NPC = W16 ? 2 : 1;   // 16-byte pieces per lane per block
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // up: store H as hi | lo planes
   constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // down: row group = plane, y fp32
   static_assert(!DOWN_SPLIT || RG == 2, "the split down projection stages both planes");
@@ -172,7 +191,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   }
   const int Kd = a.Kd, NC = a.Ncols;  // NC: output columns per matrix
   const int kblocks = Kd / 64;
-  const size_t kstride = (size_t)NC * 64;  // bytes between k blocks of one column block
+  const size_t kstride = (size_t)NC * 64 * BW;  // bytes between k blocks of one column block
   // rows are staged in chunks: all of Kd when it fits the LDS, else chunks of
   // CH k blocks (a multiple of the ring depth, so every chunk starts on ring
   // slot 0); the weight ring runs on across chunk boundaries
@@ -187,9 +206,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt) {
     const void* base = (mt == 0) ? a.b0 : a.b1;
-    W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd +
-            (size_t)(active ? cb : 0) * 1024 + 16 * lane;
-    sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
+    W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd * BW +
+            (size_t)(active ? cb : 0) * 1024 * BW + 16 * BW * lane;
+    if constexpr (W16)
+      sc[mt] = 1.0f;
+    else
+      sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
   }
   const uint16_t* X = static_cast<const uint16_t*>(a.a);
   const size_t ldx = DOWN_SPLIT ? 2 * (size_t)Kd : (size_t)Kd;  // A row stride
@@ -197,13 +219,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
 
-  u32x4_t wb[P][NMAT];
+  u32x4_t wb[P][NMAT][NPC];
+  auto wload = [&](int s, int kbl) {
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int h = 0; h < NPC; ++h)
+        wb[s][mt][h] = MXM_WLD(W[mt] + (size_t)kbl * kstride + 16 * h);
+  };
   auto prologue = [&]() {
 #pragma unroll
-    for (int s = 0; s < P; ++s)
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt)
-        wb[s][mt] = MXM_WLD(W[mt] + (size_t)clamp_kb(s, kblocks) * kstride);
+    for (int s = 0; s < P; ++s) wload(s, clamp_kb(s, kblocks));
   };
   // the first blocks of the weight stream are requested before the rows are
   // staged, so HBM is busy from the workgroup's start (TOPK: when most experts
@@ -316,12 +342,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
       a0[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);    \
       a1[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);    \
-      rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], ones, rs[rg], 0, 0, 0);       \
-      rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], ones, rs[rg], 0, 0, 0);       \
+      if constexpr (!W16) {                                                                  \
+        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], ones, rs[rg], 0, 0, 0);     \
+        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], ones, rs[rg], 0, 0, 0);     \
+      }                                                                                      \
     }                                                                                        \
     _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
-      const bf16x8_t b0 = u8x8_to_bf16(wb[s][mt].x, wb[s][mt].y);                            \
-      const bf16x8_t b1 = u8x8_to_bf16(wb[s][mt].z, wb[s][mt].w);                            \
+      const bf16x8_t b0 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                   \
+                              : u8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                \
+      const bf16x8_t b1 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])             \
+                              : u8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                \
       _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                    \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt], 0, 0, 0); \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt], 0, 0, 0); \
@@ -334,10 +364,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 #pragma unroll
       for (int s = 0; s < P; ++s) {
         MXM_Q8_STEP(s, kb + s - k0);
-        const int nk = clamp_kb(kb + P + s, kblocks);
-#pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt)
-          wb[s][mt] = MXM_WLD(W[mt] + (size_t)nk * kstride);
+        wload(s, clamp_kb(kb + P + s, kblocks));
       }
     }
     // the chunk's last group; its slots take the next chunk's first blocks
@@ -345,12 +372,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     for (int s = 0; s < P; ++s)
       if (kb + s < k1) {
         MXM_Q8_STEP(s, kb + s - k0);
-        if (k1 < kblocks) {
-          const int nk = clamp_kb(kb + P + s, kblocks);
-#pragma unroll
-          for (int mt = 0; mt < NMAT; ++mt)
-            wb[s][mt] = MXM_WLD(W[mt] + (size_t)nk * kstride);
-        }
+        if (k1 < kblocks) wload(s, clamp_kb(kb + P + s, kblocks));
       }
     }  // k chunks
     if (!active) continue;
@@ -362,8 +384,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       for (int i = 0; i < 4; ++i) {
         const int r = rc + 4 * g + i;
         if (r >= count) continue;
-        const float hi = acc[0][0][i] - 128.0f * rs[0][i];
-        const float lo = acc[1][0][i] - 128.0f * rs[1][i];
+        const float hi = W16 ? acc[0][0][i] : acc[0][0][i] - 128.0f * rs[0][i];
+        const float lo = W16 ? acc[1][0][i] : acc[1][0][i] - 128.0f * rs[1][i];
         const int yr = TOPK ? s_ypos[r] : row_begin + r;
         static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0];
       }
@@ -377,7 +399,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       if (r >= count) continue;
       float v[NMAT];
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) v[mt] = (acc[rg][mt][i] - 128.0f * rs[rg][i]) * sc[mt];
+      for (int mt = 0; mt < NMAT; ++mt)
+        v[mt] = W16 ? acc[rg][mt][i] : (acc[rg][mt][i] - 128.0f * rs[rg][i]) * sc[mt];
       float out;
       if (MODE == MXM_GEMM_GLU) {
         out = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(v[0]),
@@ -402,28 +425,37 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   }
 }
 
-template <int EPI, int P, int RG>
-void launch_q8(const GemmArgs& a, hipStream_t s) {
+template <int EPI, int P, int RG, bool W16>
+void launch_q8w(const GemmArgs& a, hipStream_t s) {
   const int ncb = a.Ncols / 16;
   const int gpe = (ncb + NW - 1) / NW;
   if (a.top_idx)
-    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, true>), dim3(a.E * gpe + (a.daux.aux ? 1 : 0)),
-                       dim3(NW * 64), 0, s, a, gpe);
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, true, W16>),
+                       dim3(a.E * gpe + (a.daux.aux ? 1 : 0)), dim3(NW * 64), 0, s, a, gpe);
   else
-    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, false>), dim3(a.E * gpe), dim3(NW * 64), 0, s,
-                       a, gpe);
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, false, W16>), dim3(a.E * gpe), dim3(NW * 64),
+                       0, s, a, gpe);
+}
+// P int8 blocks in flight per matrix, or P16 bf16 blocks
+template <int EPI, int P, int P16, int RG>
+void launch_q8(const GemmArgs& a, hipStream_t s) {
+  if (a.w_bf16)
+    launch_q8w<EPI, P16, RG, true>(a, s);
+  else
+    launch_q8w<EPI, P, RG, false>(a, s);
 }
 template <int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s) {
   constexpr bool two = Epi<EPI>::MODE == MXM_GEMM_GLU;
   constexpr int P = two ? MXM_Q8_DEPTH_GLU : MXM_Q8_DEPTH_ONE;
+  constexpr int P16 = two ? MXM_D16_DEPTH_GLU : MXM_D16_DEPTH_ONE;
   // 32 rows per pass once an expert averages more than 12 rows (the weights
   // of an expert with r rows are streamed ceil(r / rows per pass) times; one
   // row group keeps the LDS at 64 KB, two workgroups per CU)
   if (a.rows_total > 12 * a.E)
-    launch_q8<EPI, P, 2>(a, s);
+    launch_q8<EPI, P, P16, 2>(a, s);
   else
-    launch_q8<EPI, P, 1>(a, s);
+    launch_q8<EPI, P, P16, 1>(a, s);
 }
 
 // Reorder one int8 matrix src [Kd][C] into the 1 KB block layout of a
@@ -452,7 +484,7 @@ __global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
   if (a.mode == MXM_GEMM_DOWN) {
     if (a.h_split)
-      launch_q8<EPI_DOWN_F32, MXM_Q8_DEPTH_ONE, 2>(a, s);
+      launch_q8<EPI_DOWN_F32, MXM_Q8_DEPTH_ONE, MXM_D16_DEPTH_ONE, 2>(a, s);
     else
       launch_epi<EPI_DOWN>(a, s);
     return;

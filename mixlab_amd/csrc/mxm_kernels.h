@@ -206,6 +206,10 @@ struct GemmArgs {
   // out [rows][Ncols] fp32 (the products of the fp32 backward, each an
   // A . B^T over bf16 planes concatenated along k)
   bool f32_out;
+  // decode kernels (mxm_launch_gemm_q8): the weights are bf16 in the 2 KB
+  // block layout of mxm_launch_shuffle_bf16, without scales (bf16 ops at
+  // decode sizes), instead of int8 with scale0 / scale1
+  bool w_bf16;
   // int8 family, decode batches (N <= MXM_SMALL_BATCH): if set, the kernels
   // take each expert's rows from the top-k picks [rows_total = N * topk]
   // instead of offsets / perm (H at the same offsets as the dispatch's), and
@@ -409,6 +413,13 @@ void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s);
 // past the source's rows or columns are 0.
 void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, int Kdp, int Cp, uint8_t* dst,
                            hipStream_t s);
+// src [Kd][C] (fp32 or bf16 by src_dtype, x.W layout) -> bf16 in the decode
+// kernels' block layout of a [Kdp][Cp] matrix at 2 bytes per weight: block
+// (cb, kb) of 64 k x 16 columns at element ((kb * Cp/16) + cb) * 1024, lane
+// l's 16 values W[64kb + 16*(l/16) + i][16cb + l%16], i = 0..15, at
+// elements 16*l .. 16*l+15; entries past the source's rows or columns are 0.
+void mxm_launch_shuffle_bf16(const void* src, int src_dtype, int Kd, int C, int Kdp, int Cp,
+                             uint16_t* dst, hipStream_t s);
 
 // Backward of op 74 (fp32 flow).  Uses the routing and probabilities of a
 // forward on the same x and the expert outputs Y (the forward's, or under

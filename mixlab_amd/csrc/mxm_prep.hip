@@ -103,6 +103,36 @@ void mxm_launch_pad_rows_bf16(const uint16_t* src, int64_t rows, int cols, int l
                        ldd, dst);
 }
 
+namespace {
+
+__global__ void shuffle_bf16_kernel(const void* src, int dtype, int Kd, int C, int Kdp, int Cp,
+                                    uint16_t* __restrict__ dst) {
+  const size_t total = (size_t)Kdp * Cp;
+  const int ncb = Cp / 16;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+       o += (size_t)gridDim.x * blockDim.x) {
+    const size_t blk = o >> 10;
+    const int within = (int)(o & 1023);
+    const int l = within >> 4, i = within & 15;
+    const int kb = (int)(blk / ncb), cb = (int)(blk % ncb);
+    const int k = 64 * kb + 16 * (l >> 4) + i;
+    const int c = 16 * cb + (l & 15);
+    dst[o] = (k < Kd && c < C) ? mxm_f2bf(src_at(src, dtype, (size_t)k * C + c)) : (uint16_t)0;
+  }
+}
+
+}  // namespace
+
+void mxm_launch_shuffle_bf16(const void* src, int src_dtype, int Kd, int C, int Kdp, int Cp,
+                             uint16_t* dst, hipStream_t s) {
+  const size_t total = (size_t)Kdp * Cp;
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 65536) blocks = 65536;
+  if (blocks > 0)
+    hipLaunchKernelGGL(shuffle_bf16_kernel, dim3(blocks), dim3(256), 0, s, src, src_dtype, Kd, C,
+                       Kdp, Cp, dst);
+}
+
 void mxm_launch_transpose_bf16(const void* src, int src_dtype, int Kd, int C, int slot,
                                uint16_t* dst, hipStream_t s, int ldd) {
   const dim3 grid((C + 31) / 32, (Kd + 31) / 32);

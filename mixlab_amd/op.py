@@ -220,9 +220,11 @@ class MoEFeedForward:
         return out
 
     def info(self) -> dict:
-        """mfma: the expert GEMMs run on the MFMA tiles; int8: the op's expert
-        weights are int8 (int8_kernels: on the int8 kernels, else on the
-        MFMA tiles with the integers as bf16); ffn_kernel, d_kernel and
+        """mfma: the op's bf16 expert weights are on the MFMA family (bf16_stream:
+        at these decode sizes the forward streams them through the decode
+        kernels instead of the tiles); int8: the op's expert weights are int8
+        (int8_kernels: on the int8 kernels, else on the MFMA tiles with the
+        integers as bf16); ffn_kernel, d_kernel and
         d_reduce: the expert width, the down projection's output width and
         the up projection's reduction length the kernels run at (the op's
         ffn and D, or those rounded up to the tiles with zero weights);
@@ -232,7 +234,8 @@ class MoEFeedForward:
         arr = (ctypes.c_int64 * 8)()
         self._lib.mxm_moe_info(self.handle, arr, 8)
         kind = int(arr[0])
-        return dict(mfma=kind in (1, 3), int8=kind in (2, 3), int8_kernels=kind == 2,
+        return dict(mfma=kind in (1, 3, 4), int8=kind in (2, 3), int8_kernels=kind == 2,
+                    bf16_stream=kind == 4,
                     workspace_bytes=int(arr[1]),
                     gemm_bm=int(arr[2]), router_tiles=int(arr[3]), ffn_kernel=int(arr[4]),
                     d_kernel=int(arr[5]), d_reduce=int(arr[6]), route_flow=int(arr[7]))

@@ -575,6 +575,86 @@ def test_c2_int8_mfma_full(gpu_lib, monkeypatch):
     assert same_bits(np.float32(ent), np.float32(kent))
 
 
+# (N, D, E, K, F) of bf16 ops at decode sizes (fewer than 24 routed rows per
+# expert), whose forwards stream the weights through the decode kernels: D
+# and F on the tiles, D and F off them, one token, more rows than one pass
+BF16_STREAM_SHAPES = [(64, 256, 16, 2, 192), (48, 200, 8, 3, 150), (1, 256, 8, 2, 256),
+                      (90, 256, 8, 2, 128)]
+
+
+@pytest.mark.parametrize("name,etype,act,slope", EXPERTS, ids=[e[0] for e in EXPERTS])
+@pytest.mark.parametrize("shape", BF16_STREAM_SHAPES, ids=[f"{s[0]}x{s[1]}f{s[4]}"
+                                                           for s in BF16_STREAM_SHAPES])
+def test_bf16_stream_expert_types(gpu_lib, monkeypatch, shape, name, etype, act, slope):
+    """bf16 weights at decode sizes: the forward streams them through the
+    decode kernels (2 KB blocks of the bf16 weights, no conversion).  Its
+    two routing flows (MXM_DECODE_FLOW: the per-token decode flow and the
+    one-launch router's dispatch) agree bit for bit in routing, delta, aux
+    and entropy; the delta is within the tight bar of the restatement, as
+    is the MFMA tiles' on the same op (MXM_BF16_DECODE=0)."""
+    if shape[0] == 1 and etype != 0:
+        pytest.skip("the one-token case is covered on one expert kind")
+    N, D, E, K, F = shape
+    x, wr, experts = random_case(700 + N + D + etype * 4 + act, N, D, E, F, expert_type=etype)
+    x, wr = round_bf16(x), round_bf16(wr)
+    experts = [[round_bf16(m) for m in ws] for ws in experts]
+    out = {}
+    for key, env in (("stream", {}), ("dispatch", {"MXM_DECODE_FLOW": "0"}),
+                     ("tiles", {"MXM_BF16_DECODE": "0"})):
+        for v in ("MXM_DECODE_FLOW", "MXM_BF16_DECODE"):
+            monkeypatch.delenv(v, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        print(f"bf16 {key} {name} N {N} D {D} E {E} K {K} F {F}", flush=True)
+        out[key] = run_gpu(x, wr, experts, B=1, T=N, K=K, expert_type=etype, activation=act,
+                           slope=slope, bf16=True)
+    assert out["stream"][4]["bf16_stream"] and out["stream"][4]["mfma"], out["stream"][4]
+    assert out["stream"][4]["route_flow"] == 2 and out["dispatch"][4]["route_flow"] == 1
+    assert not out["tiles"][4]["bf16_stream"] and out["tiles"][4]["mfma"]
+    want = run_oracle(x, wr, experts, K=K, expert_type=etype, activation=act, slope=slope,
+                      bf16=True)
+    d0, a0, e0, r0, _ = out["stream"]
+    d1, a1, e1, r1, _ = out["dispatch"]
+    for key in ("top_idx", "gates", "counts", "offsets", "perm"):
+        assert same_bits(r0[key], r1[key]), key
+    assert same_bits(d0, d1)
+    assert same_bits(np.float32(a0), np.float32(a1)) and same_bits(np.float32(e0), np.float32(e1))
+    for key in ("stream", "tiles"):
+        delta, aux, ent, routing, _ = out[key]
+        assert_routing_equal(routing, want)
+        err = rel_l2(delta, want["delta"])
+        print(f"  {key}: rel L2 {err:.3e}")
+        assert err <= MFMA_TIGHT
+        assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+        assert abs(ent - want["entropy"]) <= 1e-3 * abs(want["entropy"])
+
+
+def test_c5_shape_bf16_stream(gpu_lib, monkeypatch):
+    """C5's decode shape with bf16 expert weights (64 tokens, D 2048, 64
+    experts top-8, ffn 1408): the weight stream against the restatement on
+    sampled rows, and on every row against the MFMA tiles."""
+    import dataclasses
+
+    cfg = dataclasses.replace(CONFIGS["C5"], int8_weights=False, name="C5bf16")
+    w = make_workload(cfg)
+    print("C5 shape, bf16 weights: the stream", flush=True)
+    delta, aux, ent, routing, info = run_gpu_workload(w)
+    assert info["bf16_stream"] and info["route_flow"] == 2, info
+    rows = np.arange(0, cfg.N, 4, dtype=np.int32)
+    want = run_oracle_workload(w, rows=rows)
+    assert_routing_equal(routing, want)
+    err = rel_l2(delta[rows], want["delta"][rows])
+    monkeypatch.setenv("MXM_BF16_DECODE", "0")
+    print("C5 shape, bf16 weights: the tiles", flush=True)
+    tdelta, taux, tent, trouting, tinfo = run_gpu_workload(w)
+    assert not tinfo["bf16_stream"]
+    assert_routing_equal(trouting, want)
+    err_all = rel_l2(delta, tdelta)
+    print(f"C5 bf16 stream: sampled rel L2 {err:.3e}; all rows against the tiles {err_all:.3e}")
+    assert err <= MFMA_TIGHT and err_all <= MFMA_TIGHT
+    assert abs(aux - want["aux"]) <= 1e-2 * abs(want["aux"])
+
+
 def _block_case(seed, N, D, E, F, bf16, x_fp32_in_bf16_flow=False):
     rng = np.random.default_rng(seed)
     x, wr, experts = random_case(seed, N, D, E, F)

@@ -106,7 +106,7 @@ FAMILIES = [
     ("bf16_mfma_tiled", dict(B=2, T=1100, D=512, E=8, K=2, F=1024),
      dict(B=1, T=1030, D=256, E=8, K=2, F=512)),
     ("bf16_mfma_decode", dict(B=1, T=700, D=512, E=16, K=4, F=512),
-     dict(B=1, T=64, D=256, E=8, K=2, F=256)),
+     dict(B=1, T=256, D=256, E=8, K=2, F=256)),
     ("geglu_split", dict(B=1, T=1500, D=256, E=6, K=2, F=512, etype=1, act=1),
      dict(B=1, T=100, D=256, E=6, K=2, F=256, etype=1, act=1)),
     ("int8_decode", dict(B=1, T=512, D=1024, E=32, K=4, F=1024, int8=True),
@@ -116,6 +116,10 @@ FAMILIES = [
      dict(B=1, T=700, D=256, E=4, K=2, F=512, int8=True)),
     ("fp32_simt", dict(B=1, T=2400, D=128, E=4, K=2, F=256, dtype="fp32"),
      dict(B=1, T=33, D=128, E=4, K=2, F=128, dtype="fp32")),
+    # bf16 weights at decode sizes, streamed by the decode kernels (split
+    # hidden: H in two planes, y fp32)
+    ("bf16_stream", dict(B=1, T=600, D=512, E=64, K=2, F=1024, etype=1, act=1),
+     dict(B=1, T=64, D=256, E=8, K=2, F=256)),
     # the tiled router's logits on the matrix cores (32 < E <= 64)
     ("bf16_router64", dict(B=1, T=1100, D=256, E=64, K=8, F=256),
      dict(B=1, T=1030, D=128, E=48, K=4, F=128)),
@@ -136,6 +140,8 @@ def test_noalloc_matches_forward(gpu_lib, name, big, small):
         if big.get("int8"):  # the int8 kernels, or the MFMA tiles scaled
             for op, _ in ops:
                 assert op.info()["int8_kernels"] == (name == "int8_decode")
+        for op, _ in ops:
+            assert op.info()["bf16_stream"] == (name == "bf16_stream")
         for io in ios:  # first launches: the runtime's own lazy setup
             io.forward(noalloc=True)
             io.results()
