@@ -246,8 +246,8 @@ int mxm_moe_synchronize(int64_t op);
  * (argsort(-probs)[:, :K], gpu/ir.cpp:1108-1109), gates [rows, K] fp32
  * (top_norm, gpu/ir.cpp:1110-1111), counts [E], offsets [E+1] and perm
  * [rows*K] (expert-grouped token ids).  Any pointer may be NULL.  to_host
- * selects host (1) or device (0) destinations.  A forward of the int8
- * decode flow (mxm_moe_info entry 7) computes only the per-token picks and
+ * selects host (1) or device (0) destinations.  A forward of the decode
+ * flow (mxm_moe_info entry 7) computes only the per-token picks and
  * gates; this call then computes counts, offsets and perm from them on the
  * device first (the same tables, bit for bit). */
 int mxm_moe_routing(int64_t op, int32_t* top_idx, float* gates, int32_t* counts,
@@ -272,7 +272,11 @@ int mxm_moe_stage_times(int64_t op, float* ms, int n);
 /* Executor facts: info[0] = expert kernel family (0 SIMT, 1 bf16 MFMA, 2 int8
  * weights on the int8 kernels, 3 int8 weights on the bf16 MFMA tiles: the
  * integers as bf16, the scales applied to the fp32 accumulators, for batches
- * past the decode sizes), info[1] = workspace bytes, info[2] = row-tile
+ * past the decode sizes, 4 bf16 MFMA family whose forwards stream the
+ * weights through the decode kernels: bf16 ops at decode sizes with fewer
+ * than 24 routed rows per expert, not created with
+ * MXM_FLAG_KEEP_FOR_BACKWARD; they hold the weights in both layouts, and
+ * their backward runs on the tiles), info[1] = workspace bytes, info[2] = row-tile
  * height of the grouped GEMM, info[3] = number of router tiles, info[4] = the
  * expert width the kernels run at (ffn, or ffn rounded up to the tiles: 128
  * for MFMA, 64 for the int8 kernels, with zero weights in the padding),
@@ -281,9 +285,9 @@ int mxm_moe_stage_times(int64_t op, float* ms, int n);
  * up projection's reduction length (D, or D rounded up to 64), info[7] = how
  * the last forward routed: 0 the tiled router, scan and scatter (three
  * launches), 1 the one-launch router (a workgroup per token, the dispatch in
- * its last workgroup), 2 the int8 decode flow (the one-launch router's
- * per-token results only; the expert kernels find their rows from the top-k
- * picks), -1 no forward yet.  Returns the number of entries written (at most
+ * its last workgroup), 2 the decode flow of the decode kernels (int8, or
+ * bf16 streamed: the one-launch router's per-token results only; the expert
+ * kernels find their rows from the top-k picks), -1 no forward yet.  Returns the number of entries written (at most
  * n, at most 8). */
 int mxm_moe_info(int64_t op, int64_t* info, int n);
 
