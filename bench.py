@@ -9,7 +9,8 @@ expert hidden 1024, 65,536 tokens, bf16; `roofline` is its grouped GEMM
 and C3 (the near-uniform and the Zipf-ragged MFMA-bound configurations,
 under "configs", with C2 also with int8 expert weights), C5, the decode
 shape with int8 expert weights (64 tokens;
-HBM-bound, under "decode_int8"), the backward on the C2 shape (fp32 and
+HBM-bound, under "decode_int8", with the same shape in bf16 under its
+"bf16_weights"), the backward on the C2 shape (fp32 and
 bf16), on the Zipf-ragged C3 shape and on the headline shape (bf16), and the
 CPU baseline.  Prints one JSON line.
 
@@ -58,6 +59,14 @@ def int8_weight_bytes(cfg, counts) -> dict:
     up = routed * ((2 if cfg.wpe == 3 else 1) * D * F + (2 if cfg.wpe == 3 else 1) * F * 4)
     down = routed * (F * D + D * 4)
     return {"routed_experts": routed, "gemm_up": up, "gemm_down": down}
+
+
+def bf16_weight_bytes(cfg, counts) -> dict:
+    """Expert weight bytes a bf16 decode forward streams: experts with rows."""
+    routed = int(np.count_nonzero(counts))
+    D, F = cfg.D, cfg.F
+    up = routed * (2 if cfg.wpe == 3 else 1) * D * F * 2
+    return {"routed_experts": routed, "gemm_up": up, "gemm_down": routed * F * D * 2}
 
 
 def measured_traffic(workload: str, stage: str, flags: int):
@@ -458,6 +467,23 @@ def main() -> int:
                             "traffic": measured_traffic("C5", "gemm_up", 0)},
             "gemm_down_gbs": (wb["gemm_down"]) / (ds["gemm_down"] * 1e-3) / 1e9,
             "stages_ms": {k: v for k, v in ds.items() if k != "forwards"},
+        }
+        # the same decode shape with bf16 expert weights (the reference's own
+        # precision): the weights streamed through the decode kernels
+        import dataclasses
+        c5b = dataclasses.replace(c5, int8_weights=False, name="C5bf16")
+        _, db = run_config(c5b, dsteps, dwarm, stage_repeats=10)
+        dbs = db["stages"]
+        wbb = bf16_weight_bytes(c5b, db["counts"])
+        totb = wbb["gemm_up"] + wbb["gemm_down"] + sum(stage_bytes(c5b).values()) + xb
+        decode["bf16_weights"] = {
+            "tokens_per_s": db["tokens_per_s"], "ms_per_step": db["ms_per_step"],
+            "hbm_gbs_forward": totb / (db["ms_per_step"] * 1e-3) / 1e9,
+            "frac_hbm_forward": totb / (db["ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "gemm_up_gbs": wbb["gemm_up"] / (dbs["gemm_up"] * 1e-3) / 1e9,
+            "gemm_down_gbs": wbb["gemm_down"] / (dbs["gemm_down"] * 1e-3) / 1e9,
+            "stages_ms": {k: v for k, v in dbs.items() if k != "forwards"},
+            "executor": db["info"],
         }
 
     w, r = run_config(cfg, args.steps, args.warmup, args.flags)
