@@ -336,16 +336,16 @@ bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 80 * (int64_t)
 // Whether a bf16 op at decode sizes streams its weights through the decode
 // kernels rather than running the MFMA tiles.  Both read the same bf16
 // bytes, but the tiles, built for compute-bound products, stream weights at
-// about 3.4 TB/s, the decode kernels at 5-5.5.  The decode kernels take 16
-// rows per pass, 32 once an expert averages more than 12, and stream an
-// expert's weights once per pass, so past about 24 routed rows per expert
-// (N*K/E) the second passes make them the slower.  Measured on MI355X
-// (whole forwards, tiles against stream): D 2048 / E 64 / K 8 / ffn 1408 at
-// N 64 0.355 against 0.224 ms, N 128 0.351 / 0.260, N 256 0.364 / 0.459;
-// ffn 1024 at N 64 0.260 / 0.166, N 256 0.274 / 0.331; D 512 / E 8 / K 2 /
-// ffn 2048 at N 32 0.071 / 0.044, N 64 0.072 / 0.048, N 128 0.074 / 0.079;
-// D 1024 / E 32 / K 4 / ffn 1024 at N 128 0.073 / 0.061, N 256 0.080 / 0.095.
-constexpr int DEC16_MAX_RPE = 24;
+// about 3.4 TB/s, the decode kernels at 5-5.5.  The decode kernels take up
+// to 64 rows per pass and stream an expert's weights once per pass, so with
+// more routed rows per expert (N*K/E) the second passes make them the
+// slower.  Measured on MI355X (whole forwards, tiles against stream): D 2048
+// / E 64 / K 8 / ffn 1408 at N 64 0.355 against 0.224 ms, N 128 0.351 /
+// 0.256, N 256 0.363 / 0.307, N 384 0.372 / 0.339, N 512 0.386 / 0.489; D
+// 512 / E 8 / K 2 / ffn 2048 at N 32 0.071 / 0.044, N 128 0.075 / 0.055, N
+// 192 0.078 / 0.057, N 256 0.081 / 0.092; D 1024 / E 32 / K 4 / ffn 1024 at
+// N 256 0.079 / 0.073, N 384 0.091 / 0.085, N 512 0.099 / 0.115.
+constexpr int DEC16_MAX_RPE = 56;
 bool dec16_pays(int N, int E, int K) { return (int64_t)N * K < DEC16_MAX_RPE * (int64_t)E; }
 
 // Row-tile heights and tile counts of the forward's kernels; a function of

@@ -57,6 +57,14 @@
 #ifndef MXM_D16_DEPTH_ONE
 #define MXM_D16_DEPTH_ONE 4
 #endif
+// 64 rows per pass once an expert averages more than this many rows (int8;
+// bf16 weights: MXM_D16_RG4_MIN)
+#ifndef MXM_Q8_RG4_MIN
+#define MXM_Q8_RG4_MIN 24
+#endif
+#ifndef MXM_D16_RG4_MIN
+#define MXM_D16_RG4_MIN 16
+#endif
 
 // Weight blocks are read once per forward, so they are loaded nontemporal
 // (the load's nt bit): the stream then does not displace the router's and
@@ -71,7 +79,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int NW = 8;          // waves (column blocks) per workgroup
-constexpr int MAX_KD = 2048;   // A staging: 16 rows x up to 2048 k bf16 per chunk in LDS (64 KB)
+// A staging: each row group's 16 rows x up to MAX_KD k bf16 per chunk in LDS
+// (64 KB), half that k at four row groups (64 rows per pass, 128 KB)
+constexpr int MAX_KD = 2048;
 
 // Eight offset-binary bytes (two dwords) -> eight bf16 of their value, exact.
 __device__ __forceinline__ bf16x8_t u8x8_to_bf16(unsigned lo, unsigned hi) {
@@ -155,8 +165,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   static_assert(!DOWN_SPLIT || RG == 2, "the split down projection stages both planes");
   constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 16 : 16 * RG;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
-  constexpr int ASZ = MAX_KD / 64 * 2 * 64;  // pieces of one row group
-  constexpr int CH = MAX_KD / 64 / P * P;    // k blocks per staged chunk
+  constexpr int MAXK = RG >= 4 ? MAX_KD / 2 : MAX_KD;
+  constexpr int ASZ = MAXK / 64 * 2 * 64;  // pieces of one row group
+  constexpr int CH = MAXK / 64 / P * P;    // k blocks per staged chunk
   // A rows of the current pass, per row group: [kb][half][lane] 16-byte
   // pieces; lane 16g + m holds row m, k = 64kb + 16g + 8*half .. +7.
   __shared__ u32x4_t ash[RG * ASZ];
@@ -195,7 +206,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   // rows are staged in chunks: all of Kd when it fits the LDS, else chunks of
   // CH k blocks (a multiple of the ring depth, so every chunk starts on ring
   // slot 0); the weight ring runs on across chunk boundaries
-  const int chunk = kblocks <= MAX_KD / 64 ? kblocks : CH;
+  const int chunk = kblocks <= MAXK / 64 ? kblocks : CH;
   const int cb = grp * NW + wave;
   const bool active = cb < NC / 16;   // wave-uniform
   const int g = lane >> 4, m = lane & 15;
@@ -449,10 +460,20 @@ void launch_epi(const GemmArgs& a, hipStream_t s) {
   constexpr bool two = Epi<EPI>::MODE == MXM_GEMM_GLU;
   constexpr int P = two ? MXM_Q8_DEPTH_GLU : MXM_Q8_DEPTH_ONE;
   constexpr int P16 = two ? MXM_D16_DEPTH_GLU : MXM_D16_DEPTH_ONE;
-  // 32 rows per pass once an expert averages more than 12 rows (the weights
-  // of an expert with r rows are streamed ceil(r / rows per pass) times; one
-  // row group keeps the LDS at 64 KB, two workgroups per CU)
-  if (a.rows_total > 12 * a.E)
+  // 32 rows per pass once an expert averages more than 12 rows, 64 once it
+  // averages more than 24 (int8) or 16 (bf16): the weights of an expert with
+  // r rows are streamed ceil(r / rows per pass) times; one row group keeps
+  // the LDS at 64 KB, two workgroups per CU, and four stage half of the
+  // reduction at a time.  The row group a row lands in does not change its
+  // arithmetic: results are the same bits at every pass height.  Measured
+  // (forwards, 32 against 64 rows per pass): D 2048 / E 64 / K 8 / ffn 1408
+  // int8 at N 256 0.271 / 0.238 ms, N 384 0.330 / 0.276, bf16 at N 256 0.449
+  // / 0.307, N 384 0.525 / 0.339; the switch at 16 rows measured better for
+  // bf16 (N 192: 0.317 against 0.294 ms) and worse for int8 (0.191 against
+  // 0.229)
+  if (a.rows_total > (a.w_bf16 ? MXM_D16_RG4_MIN : MXM_Q8_RG4_MIN) * a.E)
+    launch_q8<EPI, P, P16, 4>(a, s);
+  else if (a.rows_total > 12 * a.E)
     launch_q8<EPI, P, P16, 2>(a, s);
   else
     launch_q8<EPI, P, P16, 1>(a, s);
