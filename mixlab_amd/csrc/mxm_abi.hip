@@ -201,7 +201,6 @@ struct MoeOp {
   // offsets, perm, slot_pos) is computed when the routing is queried, from
   // its per-token results and the probabilities at last_probs
   bool last_decode = false;
-  bool last_stream = false;  // ... and ran on the decode kernels
   float* last_probs = nullptr;
   // the int8 decode flow (1, default) or the dispatch of the one-launch
   // router (0): MXM_DECODE_FLOW at creation, for measurements of the two
@@ -327,10 +326,12 @@ bool small_route_pays(int N, int D, int E, bool mf) {
 // products turn compute-bound, where the int8 kernels reach 60-250 TFLOP/s
 // and the MFMA tiles 0.8-1.1 PFLOP/s.  To first order the weight bytes
 // cancel out of the comparison and the crossover is a number of rows per
-// expert: measured on MI355X (whole forwards) near 60 for D 2048 / E 64 /
-// K 8 / ffn 1408, 64 for D 1024 / E 32 / K 4 / ffn 1024, 80-90 for D 512 /
-// E 8 / K 2 / ffn 2048 and D 1024 / E 16 / K 2 / ffn 4096, and 75-150 for D
-// 256 with ffn 128-192, whose forwards are launch-bound either way.
+// expert: measured on MI355X (whole forwards, with the int8 kernels' 64-row
+// passes) between 64 and 96 for D 2048 / E 64 / K 8 / ffn 1408 (N 512:
+// 0.388 against 0.394 ms, N 768: 0.492 against 0.423), near 96 for D 1024 /
+// E 32 / K 4 / ffn 1024, 80-96 for D 512 / E 8 / K 2 / ffn 2048 and D 1024 /
+// E 16 / K 2 / ffn 4096, and 75-150 for D 256 with ffn 128-192, whose
+// forwards are launch-bound either way.
 bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 80 * (int64_t)E; }
 
 // Whether a bf16 op at decode sizes streams its weights through the decode
@@ -484,7 +485,6 @@ void run_forward(MoeOp& o, const Workspace& w, const void* x, int x_dtype, float
   const bool stream = o.int8_kernels() || dec16;  // the decode kernels
   const bool decode_flow = stream && o.small_route && o.decode_flow;
   o.last_decode = decode_flow;
-  o.last_stream = stream;
   const void* xin = x;
   if (o.bf16 && x_dtype == MXM_DTYPE_F32) {
     mxm_launch_to_bf16(x, MXM_DTYPE_F32, static_cast<uint16_t*>(w.xcast), (int64_t)o.N * o.D, st);
