@@ -23,8 +23,9 @@
 // blocks at 2 bytes per weight (mxm_launch_shuffle_bf16), 2 KB each, lane l
 // holding its 16 values at bytes 32*l .. 32*l+31 as two 16-byte pieces; no
 // conversion, no offset and no scale -- the accumulators are the bf16 flow's
-// fp32 products.  The ring holds half as many blocks, so the bytes in
-// flight and the registers stay those of the int8 stream.
+// fp32 products.  The ring holds 4 blocks per matrix (against the int8
+// stream's 6 and 8), so the bytes in flight and the registers stay close to
+// the int8 stream's.
 //
 // Split hidden (kinds whose hidden is fp32 in the bf16 flow, GemmArgs::
 // h_split): the up projection stores H as the planes hi | lo, and the down
