@@ -66,6 +66,15 @@
 #ifndef MXM_D16_RG4_MIN
 #define MXM_D16_RG4_MIN 16
 #endif
+// the split down projection: 32 rows per pass (four row groups) once an
+// expert averages more than this many rows (bf16 weights; int8:
+// MXM_SPLIT_Q8_RG4_MIN)
+#ifndef MXM_SPLIT_RG4_MIN
+#define MXM_SPLIT_RG4_MIN 12
+#endif
+#ifndef MXM_SPLIT_Q8_RG4_MIN
+#define MXM_SPLIT_Q8_RG4_MIN 40
+#endif
 
 // Weight blocks are read once per forward, so they are loaded nontemporal
 // (the load's nt bit): the stream then does not displace the router's and
@@ -162,9 +171,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   constexpr int BW = W16 ? 2 : 1;    // bytes per weight
   constexpr int NPC = W16 ? 2 : 1;   // 16-byte pieces per lane per block
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // up: store H as hi | lo planes
-  constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;  // down: row group = plane, y fp32
-  static_assert(!DOWN_SPLIT || RG == 2, "the split down projection stages both planes");
-  constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 16 : 16 * RG;
+  // down over both planes of a split H: row group 2p + plane holds rows
+  // 16p .. 16p+15 of the pass from that plane; y fp32
+  constexpr bool DOWN_SPLIT = Epi<EPI>::DOWN_SPLIT;
+  static_assert(!DOWN_SPLIT || RG == 2 || RG == 4, "the split down projection stages both planes");
+  constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 8 * RG : 16 * RG;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
   constexpr int MAXK = RG >= 4 ? MAX_KD / 2 : MAX_KD;
   constexpr int ASZ = MAXK / 64 * 2 * 64;  // pieces of one row group
@@ -334,9 +345,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     __syncthreads();  // every wave has finished reading ash
     for (int i = tid; i < 16 * RG * pieces; i += NW * 64) {
       const int r = i / pieces, c8 = i - r * pieces;
-      // staged row r: row group r / 16 (the plane, when split), row r % 16
-      const int rr = DOWN_SPLIT ? (r & 15) : r;
-      const int col0 = (DOWN_SPLIT ? (r >> 4) * Kd : 0) + 64 * k0;
+      // staged row r: row group r / 16 (when split: rows 16 (r / 32) .. +15
+      // of the pass from plane (r / 16) % 2), row r % 16
+      const int rr = DOWN_SPLIT ? ((r >> 5) << 4) | (r & 15) : r;
+      const int col0 = (DOWN_SPLIT ? ((r >> 4) & 1) * Kd : 0) + 64 * k0;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
       if (rc + rr < count) {
         const int p = row_begin + rc + rr;
@@ -393,11 +405,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
     if constexpr (DOWN_SPLIT) {
 #pragma unroll
+      for (int pg = 0; pg < RG / 2; ++pg)
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = rc + 4 * g + i;
+        const int r = rc + 16 * pg + 4 * g + i;
         if (r >= count) continue;
-        const float hi = W16 ? acc[0][0][i] : acc[0][0][i] - 128.0f * rs[0][i];
-        const float lo = W16 ? acc[1][0][i] : acc[1][0][i] - 128.0f * rs[1][i];
+        const int h0 = 2 * pg, l0 = 2 * pg + 1;  // the hi and lo planes' row groups
+        const float hi = W16 ? acc[h0][0][i] : acc[h0][0][i] - 128.0f * rs[h0][i];
+        const float lo = W16 ? acc[l0][0][i] : acc[l0][0][i] - 128.0f * rs[l0][i];
         const int yr = TOPK ? s_ypos[r] : row_begin + r;
         static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0];
       }
@@ -505,7 +520,16 @@ __global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
 
 void mxm_launch_gemm_q8(const GemmArgs& a, hipStream_t s) {
   if (a.mode == MXM_GEMM_DOWN) {
-    if (a.h_split)
+    // split: 16 rows per pass from both planes, 32 once an expert averages
+    // more than 12 rows (bf16) or 40 (int8), bit-identical.  Measured
+    // (geglu, forwards, 16 against 32 rows per pass): D 2048 / E 64 / K 8 /
+    // ffn 1408 bf16 at N 128 0.318 / 0.284 ms, N 384 0.542 / 0.444; int8 at
+    // N 256 0.306 / 0.312, N 384 0.377 / 0.364; D 512 / E 8 / K 2 / ffn 2048
+    // int8 at N 128 0.068 / 0.076, N 192 0.084 / 0.080
+    if (a.h_split &&
+        a.rows_total > (a.w_bf16 ? MXM_SPLIT_RG4_MIN : MXM_SPLIT_Q8_RG4_MIN) * a.E)
+      launch_q8<EPI_DOWN_F32, MXM_Q8_DEPTH_ONE, MXM_D16_DEPTH_ONE, 4>(a, s);
+    else if (a.h_split)
       launch_q8<EPI_DOWN_F32, MXM_Q8_DEPTH_ONE, MXM_D16_DEPTH_ONE, 2>(a, s);
     else
       launch_epi<EPI_DOWN>(a, s);

@@ -400,6 +400,7 @@ FLOW_CASES = [
     (96, 200, 12, 3, 128, 1, 1),     # K does not divide 64
     (64, 256, 96, 4, 128, 0, 0),     # E > 64: two expert groups per token
     (300, 256, 8, 2, 128, 0, 0),     # several row passes per expert
+    (300, 256, 8, 2, 128, 1, 1),     # split hidden, 32-row passes of the down projection
     (48, 196, 8, 2, 128, 0, 0),      # D not a multiple of 8
 ]
 
