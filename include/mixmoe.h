@@ -133,7 +133,7 @@ int mxm_moe_set_input(int64_t op, int input_index, int dtype, const int64_t* sha
  * it serves decode-shaped serving, where the expert weights are the traffic.
  * Any D and ffn (widths that are not multiples of 64 are padded with zero
  * weights inside the library; one expert's matrix below 2^31 entries).  An
- * op whose batch routes 80 or more rows per expert (B*T*topK >= 80*E), which
+ * op whose batch routes 96 or more rows per expert (B*T*topK >= 96*E), which
  * is compute-bound, keeps the integers as bf16 (exact; twice the int8
  * bytes) for the bf16 MFMA tiles, which apply the scales to the fp32
  * accumulators: the same products and activation as the int8 kernels. */

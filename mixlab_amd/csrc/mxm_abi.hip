@@ -168,7 +168,7 @@ struct MoeOp {
   // int8 family: q1 = gate (GLU) or up (MLP), q1b = up (GLU), q2 = down, in
   // the 1 KB block layout; s1, s1b, s2 = fp32 per-output-channel scales.
   DevBuf q1, q1b, q2, s1, s1b, s2;
-  // int8 weights on the MFMA kernels (batches of 80 or more routed rows per
+  // int8 weights on the MFMA kernels (batches of 96 or more routed rows per
   // expert, which are compute-bound): w1 / w2 hold the
   // integers q as bf16 (exact) in the MFMA layout and s1 / s1b / s2 the
   // scales [E][Fk] / [E][Dk], which the epilogue applies to the fp32
@@ -326,13 +326,14 @@ bool small_route_pays(int N, int D, int E, bool mf) {
 // products turn compute-bound, where the int8 kernels reach 60-250 TFLOP/s
 // and the MFMA tiles 0.8-1.1 PFLOP/s.  To first order the weight bytes
 // cancel out of the comparison and the crossover is a number of rows per
-// expert: measured on MI355X (whole forwards, with the int8 kernels' 64-row
-// passes) between 64 and 96 for D 2048 / E 64 / K 8 / ffn 1408 (N 512:
-// 0.388 against 0.394 ms, N 768: 0.492 against 0.423), near 96 for D 1024 /
-// E 32 / K 4 / ffn 1024, 80-96 for D 512 / E 8 / K 2 / ffn 2048 and D 1024 /
-// E 16 / K 2 / ffn 4096, and 75-150 for D 256 with ffn 128-192, whose
-// forwards are launch-bound either way.
-bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 80 * (int64_t)E; }
+// expert: measured on MI355X (whole forwards, with the int8 kernels' 128-row
+// passes) near 96 for D 2048 / E 64 / K 8 / ffn 1408 (N 640: 0.399 against
+// 0.409 ms, N 768: 0.422 / 0.422, N 1024: 0.677 / 0.437), D 512 / E 8 / K 2
+// / ffn 2048 (N 384: 0.090 / 0.094, N 512: 0.149 / 0.094) and D 1024 / E 32
+// / K 4 / ffn 1024 (N 768: 0.126 / 0.129, N 1024: 0.167 / 0.147), and
+// 75-150 for D 256 with ffn 128-192, whose forwards are launch-bound either
+// way.
+bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 96 * (int64_t)E; }
 
 // Whether a bf16 op at decode sizes streams its weights through the decode
 // kernels rather than running the MFMA tiles.  Both read the same bf16
@@ -1107,7 +1108,7 @@ int64_t mxm_moe_create(const float* float_params, int n_float_params, const int3
     o->q8 = (flags & MXM_FLAG_INT8_WEIGHTS) != 0;
     if (o->q8) {
       if (!o->bf16) fail("OP_MOE_FEED_FORWARD int8 weights need bf16 compute");
-      // from 80 routed rows per expert on the MFMA kernels on the integers q,
+      // from 96 routed rows per expert on the MFMA kernels on the integers q,
       // where their tiles fit the padded widths (MXM_Q8_MFMA: 0 never, 1
       // whenever they fit)
       o->q8_mfma = o->mfma && q8_mfma_pays(o->N, o->E, o->K);

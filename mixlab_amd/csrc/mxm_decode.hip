@@ -66,6 +66,18 @@
 #ifndef MXM_D16_RG4_MIN
 #define MXM_D16_RG4_MIN 16
 #endif
+// 128 rows per pass (eight row groups) once an expert averages more than
+// this many rows.  Measured (forwards, 64 against 128 rows per pass, D 2048
+// / E 64 / K 8 / ffn 1408): int8 at N 640 0.481 / 0.399 ms, N 768 0.500 /
+// 0.422, bf16 at N 512 0.488 / 0.402, N 768 0.623 / 0.439; at 64 rows per
+// expert int8 measured mixed (D 1024 / E 32 / K 4 / ffn 1024, N 512: 0.095
+// / 0.106 ms), at 128 slower on every shape (two passes either way)
+#ifndef MXM_Q8_RG8_MIN
+#define MXM_Q8_RG8_MIN 64
+#endif
+#ifndef MXM_D16_RG8_MIN
+#define MXM_D16_RG8_MIN 48
+#endif
 // the split down projection: 32 rows per pass (four row groups) once an
 // expert averages more than this many rows (bf16 weights; int8:
 // MXM_SPLIT_Q8_RG4_MIN)
@@ -90,7 +102,8 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int NW = 8;          // waves (column blocks) per workgroup
 // A staging: each row group's 16 rows x up to MAX_KD k bf16 per chunk in LDS
-// (64 KB), half that k at four row groups (64 rows per pass, 128 KB)
+// (64 KB), half that k at four row groups (64 rows per pass, 128 KB) and a
+// quarter at eight (128 rows per pass, 128 KB)
 constexpr int MAX_KD = 2048;
 
 // Eight offset-binary bytes (two dwords) -> eight bf16 of their value, exact.
@@ -177,7 +190,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   static_assert(!DOWN_SPLIT || RG == 2 || RG == 4, "the split down projection stages both planes");
   constexpr int ROWS_PER_PASS = DOWN_SPLIT ? 8 * RG : 16 * RG;
   constexpr int NMAT = (MODE == MXM_GEMM_GLU) ? 2 : 1;
-  constexpr int MAXK = RG >= 4 ? MAX_KD / 2 : MAX_KD;
+  constexpr int MAXK = RG >= 8 ? MAX_KD / 4 : RG >= 4 ? MAX_KD / 2 : MAX_KD;
   constexpr int ASZ = MAXK / 64 * 2 * 64;  // pieces of one row group
   constexpr int CH = MAXK / 64 / P * P;    // k blocks per staged chunk
   // A rows of the current pass, per row group: [kb][half][lane] 16-byte
@@ -360,8 +373,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     __syncthreads();
     if (!active) continue;
 
+// (up to four row groups: every row group's A fragments first, then each
+// matrix's converted block against all of them; eight: one row group's
+// fragments at a time against both matrices' blocks, which keeps a quarter
+// of the A registers live.  Each accumulator sees the same MFMAs in the same
+// order either way.)
 #define MXM_Q8_STEP(s, kbi)                                                                  \
-  {                                                                                          \
+  if constexpr (RG <= 4) {                                                                   \
     bf16x8_t a0[RG], a1[RG];                                                                 \
     _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
       a0[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);    \
@@ -379,6 +397,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                    \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt], 0, 0, 0); \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt], 0, 0, 0); \
+      }                                                                                      \
+    }                                                                                        \
+  } else {                                                                                   \
+    bf16x8_t b0[NMAT], b1[NMAT];                                                             \
+    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
+      b0[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                              \
+                   : u8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                           \
+      b1[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])                        \
+                   : u8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                           \
+    }                                                                                        \
+    _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
+      const bf16x8_t a0 =                                                                    \
+          __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);         \
+      const bf16x8_t a1 =                                                                    \
+          __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);         \
+      if constexpr (!W16) {                                                                  \
+        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, rs[rg], 0, 0, 0);         \
+        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, rs[rg], 0, 0, 0);         \
+      }                                                                                      \
+      _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                  \
+        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[mt], acc[rg][mt], 0, 0, 0); \
+        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[mt], acc[rg][mt], 0, 0, 0); \
       }                                                                                      \
     }                                                                                        \
   }
@@ -487,7 +527,9 @@ void launch_epi(const GemmArgs& a, hipStream_t s) {
   // / 0.307, N 384 0.525 / 0.339; the switch at 16 rows measured better for
   // bf16 (N 192: 0.317 against 0.294 ms) and worse for int8 (0.191 against
   // 0.229)
-  if (a.rows_total > (a.w_bf16 ? MXM_D16_RG4_MIN : MXM_Q8_RG4_MIN) * a.E)
+  if (a.rows_total > (a.w_bf16 ? MXM_D16_RG8_MIN : MXM_Q8_RG8_MIN) * a.E)
+    launch_q8<EPI, P, P16, 8>(a, s);
+  else if (a.rows_total > (a.w_bf16 ? MXM_D16_RG4_MIN : MXM_Q8_RG4_MIN) * a.E)
     launch_q8<EPI, P, P16, 4>(a, s);
   else if (a.rows_total > 12 * a.E)
     launch_q8<EPI, P, P16, 2>(a, s);

@@ -878,8 +878,8 @@ ROUTER_CHOICE = [
     # E > 64
     (1024, 128, 96, 4, "bf16", False, 0),   # D*E = 12288
     (1024, 256, 96, 4, "bf16", False, 1),   # D*E = 24576
-    (256, 256, 8, 2, "bf16", True, 2),      # int8 below 80 rows per expert: the decode flow
-    (1024, 256, 8, 2, "bf16", True, 0),     # int8 from 80 on: MFMA tiles, bf16's router choice
+    (256, 256, 8, 2, "bf16", True, 2),      # int8 below 96 rows per expert: the decode flow
+    (1024, 256, 8, 2, "bf16", True, 0),     # int8 from 96 on: MFMA tiles, bf16's router choice
     (1100, 2048, 64, 8, "bf16", False, 0),  # past the one-launch router's limit
 ]
 

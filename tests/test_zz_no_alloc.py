@@ -111,7 +111,7 @@ FAMILIES = [
      dict(B=1, T=200, D=256, E=6, K=2, F=256, etype=1, act=1)),
     ("int8_decode", dict(B=1, T=512, D=1024, E=32, K=4, F=1024, int8=True),
      dict(B=1, T=64, D=512, E=8, K=2, F=512, int8=True)),
-    # int8 weights at 80 or more rows per expert: the MFMA tiles, scaled
+    # int8 weights at 96 or more rows per expert: the MFMA tiles, scaled
     ("int8_mfma", dict(B=1, T=1100, D=512, E=8, K=2, F=1024, int8=True),
      dict(B=1, T=700, D=256, E=4, K=2, F=512, int8=True)),
     ("fp32_simt", dict(B=1, T=2400, D=128, E=4, K=2, F=256, dtype="fp32"),
