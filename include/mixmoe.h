@@ -274,7 +274,7 @@ int mxm_moe_stage_times(int64_t op, float* ms, int n);
  * integers as bf16, the scales applied to the fp32 accumulators, for batches
  * past the decode sizes, 4 bf16 MFMA family whose forwards stream the
  * weights through the decode kernels: bf16 ops at decode sizes with fewer
- * than 56 routed rows per expert, not created with
+ * than 96 routed rows per expert, not created with
  * MXM_FLAG_KEEP_FOR_BACKWARD; they hold the weights in both layouts, and
  * their backward runs on the tiles), info[1] = workspace bytes, info[2] = row-tile
  * height of the grouped GEMM, info[3] = number of router tiles, info[4] = the

@@ -338,16 +338,16 @@ bool q8_mfma_pays(int N, int E, int K) { return (int64_t)N * K >= 96 * (int64_t)
 // Whether a bf16 op at decode sizes streams its weights through the decode
 // kernels rather than running the MFMA tiles.  Both read the same bf16
 // bytes, but the tiles, built for compute-bound products, stream weights at
-// about 3.4 TB/s, the decode kernels at 5-5.5.  The decode kernels take up
-// to 64 rows per pass and stream an expert's weights once per pass, so with
+// about 3.4 TB/s, the decode kernels at 5.5-6.  The decode kernels take up
+// to 128 rows per pass and stream an expert's weights once per pass, so with
 // more routed rows per expert (N*K/E) the second passes make them the
 // slower.  Measured on MI355X (whole forwards, tiles against stream): D 2048
-// / E 64 / K 8 / ffn 1408 at N 64 0.355 against 0.224 ms, N 128 0.351 /
-// 0.256, N 256 0.363 / 0.307, N 384 0.372 / 0.339, N 512 0.386 / 0.489; D
-// 512 / E 8 / K 2 / ffn 2048 at N 32 0.071 / 0.044, N 128 0.075 / 0.055, N
-// 192 0.078 / 0.057, N 256 0.081 / 0.092; D 1024 / E 32 / K 4 / ffn 1024 at
-// N 256 0.079 / 0.073, N 384 0.091 / 0.085, N 512 0.099 / 0.115.
-constexpr int DEC16_MAX_RPE = 56;
+// / E 64 / K 8 / ffn 1408 at N 64 0.347 against 0.186 ms, N 256 0.366 /
+// 0.275, N 512 0.387 / 0.376, N 768 0.423 / 0.408; D 512 / E 8 / K 2 / ffn
+// 2048 at N 64 0.071 / 0.038, N 256 0.081 / 0.071, N 384 0.093 / 0.081; D
+// 1024 / E 32 / K 4 / ffn 1024 at N 64 0.069 / 0.049, N 512 0.099 / 0.103,
+// N 768 0.129 / 0.121.
+constexpr int DEC16_MAX_RPE = 96;
 bool dec16_pays(int N, int E, int K) { return (int64_t)N * K < DEC16_MAX_RPE * (int64_t)E; }
 
 // Row-tile heights and tile counts of the forward's kernels; a function of

@@ -20,8 +20,9 @@
 // removed after the loop with the rows' sums (an MFMA against ones).
 //
 // bf16 weights (GemmArgs::w_bf16, bf16 ops at decode sizes): the same
-// blocks at 2 bytes per weight (mxm_launch_shuffle_bf16), 2 KB each, lane l
-// holding its 16 values at bytes 32*l .. 32*l+31 as two 16-byte pieces; no
+// blocks at 2 bytes per weight (mxm_launch_shuffle_bf16), 2 KB each as two
+// 1 KB halves, lane l's first 8 values at bytes 16*l of the first half and
+// its last 8 at 16*l of the second (each wave-load one coalesced 1 KB); no
 // conversion, no offset and no scale -- the accumulators are the bf16 flow's
 // fp32 products.  The ring holds 4 blocks per matrix (against the int8
 // stream's 6 and 8), so the bytes in flight and the registers stay close to
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   for (int mt = 0; mt < NMAT; ++mt) {
     const void* base = (mt == 0) ? a.b0 : a.b1;
     W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd * BW +
-            (size_t)(active ? cb : 0) * 1024 * BW + 16 * BW * lane;
+            (size_t)(active ? cb : 0) * 1024 * BW + 16 * lane;
     if constexpr (W16)
       sc[mt] = 1.0f;
     else
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
       for (int h = 0; h < NPC; ++h)
-        wb[s][mt][h] = MXM_WLD(W[mt] + (size_t)kbl * kstride + 16 * h);
+        wb[s][mt][h] = MXM_WLD(W[mt] + (size_t)kbl * kstride + 1024 * h);
   };
   auto prologue = [&]() {
 #pragma unroll

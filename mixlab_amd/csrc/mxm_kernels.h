@@ -416,8 +416,9 @@ void mxm_launch_shuffle_q8(const int8_t* src, int Kd, int C, int Kdp, int Cp, ui
 // src [Kd][C] (fp32 or bf16 by src_dtype, x.W layout) -> bf16 in the decode
 // kernels' block layout of a [Kdp][Cp] matrix at 2 bytes per weight: block
 // (cb, kb) of 64 k x 16 columns at element ((kb * Cp/16) + cb) * 1024, lane
-// l's 16 values W[64kb + 16*(l/16) + i][16cb + l%16], i = 0..15, at
-// elements 16*l .. 16*l+15; entries past the source's rows or columns are 0.
+// l's 16 values W[64kb + 16*(l/16) + i][16cb + l%16], i = 0..15, at elements
+// 512*(i/8) + 8*l + i%8 (two halves, each lane's 8 values contiguous in
+// each); entries past the source's rows or columns are 0.
 void mxm_launch_shuffle_bf16(const void* src, int src_dtype, int Kd, int C, int Kdp, int Cp,
                              uint16_t* dst, hipStream_t s);
 

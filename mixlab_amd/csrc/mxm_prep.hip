@@ -113,7 +113,8 @@ __global__ void shuffle_bf16_kernel(const void* src, int dtype, int Kd, int C, i
        o += (size_t)gridDim.x * blockDim.x) {
     const size_t blk = o >> 10;
     const int within = (int)(o & 1023);
-    const int l = within >> 4, i = within & 15;
+    // half h of the block holds value 8h + i' of every lane, lane l at 8 l
+    const int h = within >> 9, l = (within >> 3) & 63, i = 8 * h + (within & 7);
     const int kb = (int)(blk / ncb), cb = (int)(blk % ncb);
     const int k = 64 * kb + 16 * (l >> 4) + i;
     const int c = 16 * cb + (l & 15);

@@ -576,7 +576,7 @@ def test_c2_int8_mfma_full(gpu_lib, monkeypatch):
     assert same_bits(np.float32(ent), np.float32(kent))
 
 
-# (N, D, E, K, F) of bf16 ops at decode sizes (fewer than 56 routed rows per
+# (N, D, E, K, F) of bf16 ops at decode sizes (fewer than 96 routed rows per
 # expert), whose forwards stream the weights through the decode kernels: D
 # and F on the tiles (16 rows per pass), D and F off them (64 rows per pass),
 # one token, 128-row passes with experts of more than one pass, E > 64 (two
@@ -906,7 +906,7 @@ def test_router_choice(gpu_lib, monkeypatch, N, D, E, K, dtype, int8, want):
         experts = [[round_bf16(w) for w in ws] for ws in experts]
     up = bf16_bits if bf16 else (lambda a: np.ascontiguousarray(a, np.float32))
 
-    # (the routers of the tiles' flows: bf16 ops below 56 rows per expert
+    # (the routers of the tiles' flows: bf16 ops below 96 rows per expert
     # would otherwise stream their weights, which takes the decode flow)
     monkeypatch.setenv("MXM_BF16_DECODE", "0")
 

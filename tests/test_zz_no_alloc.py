@@ -106,9 +106,9 @@ FAMILIES = [
     ("bf16_mfma_tiled", dict(B=2, T=1100, D=512, E=8, K=2, F=1024),
      dict(B=1, T=1030, D=256, E=8, K=2, F=512)),
     ("bf16_mfma_decode", dict(B=1, T=700, D=512, E=16, K=4, F=512),
-     dict(B=1, T=256, D=256, E=8, K=2, F=256)),
+     dict(B=1, T=400, D=1024, E=8, K=2, F=256)),
     ("geglu_split", dict(B=1, T=1500, D=256, E=6, K=2, F=512, etype=1, act=1),
-     dict(B=1, T=200, D=256, E=6, K=2, F=256, etype=1, act=1)),
+     dict(B=1, T=300, D=256, E=6, K=2, F=256, etype=1, act=1)),
     ("int8_decode", dict(B=1, T=512, D=1024, E=32, K=4, F=1024, int8=True),
      dict(B=1, T=64, D=512, E=8, K=2, F=512, int8=True)),
     # int8 weights at 96 or more rows per expert: the MFMA tiles, scaled
