@@ -5,8 +5,8 @@
 // Weight layout (written at upload by mxm_launch_shuffle_q8): a matrix
 // W[Kd][C] (x.W layout) is cut into blocks of 64 k x 16 output columns; block
 // (cb, kb) occupies 1 KB at ((kb * C/16) + cb) * 1024 and holds, at bytes
-// 16*l .. 16*l+15, the 16 values W[64kb + 16*(l/16) + i][16cb + l%16] + 128
-// (offset binary, i.e. the int8 byte with its top bit flipped), i = 0..15.
+// 16*l .. 16*l+15, the 16 signed bytes W[64kb + 16*(l/16) + i][16cb + l%16],
+// i = 0..15.
 // Lane l of a wave therefore reads one contiguous 16-byte piece, a wave-load
 // is one coalesced 1 KB read, and the waves of a workgroup, which walk k in
 // step, read adjacent 1 KB blocks (a k block of all columns is C/16 KB
@@ -15,9 +15,11 @@
 // MFMA: v_mfma_f32_16x16x32_bf16.  Within a 64-k block, lane group g = l/16
 // owns k = 16g .. 16g+15; the first 8 feed one MFMA, the last 8 a second.
 // The A operand (16 of the expert's rows, bf16) uses the same k assignment,
-// so the sum over k is the plain dot product.  The offset-binary byte u is
-// an integer in [0, 255], which bf16 holds exactly; the +128 offset is
-// removed after the loop with the rows' sums (an MFMA against ones).
+// so the sum over k is the plain dot product.  A signed byte converts to
+// bf16 exactly (one sign-extending byte-select conversion to fp32 per byte,
+// then a pair pack), so the accumulators are sums of x * q.  (Stored offset
+// binary, q + 128, the stream needed two more MFMAs per block for the rows'
+// sums that remove the offset, at the same conversion count.)
 //
 // bf16 weights (GemmArgs::w_bf16, bf16 ops at decode sizes): the same
 // blocks at 2 bytes per weight (mxm_launch_shuffle_bf16), 2 KB each as two
@@ -107,13 +109,13 @@ constexpr int NW = 8;          // waves (column blocks) per workgroup
 // quarter at eight (128 rows per pass, 128 KB)
 constexpr int MAX_KD = 2048;
 
-// Eight offset-binary bytes (two dwords) -> eight bf16 of their value, exact.
-__device__ __forceinline__ bf16x8_t u8x8_to_bf16(unsigned lo, unsigned hi) {
+// Eight signed bytes (two dwords) -> eight bf16 of their value, exact.
+__device__ __forceinline__ bf16x8_t s8x8_to_bf16(unsigned lo, unsigned hi) {
   bf16x8_t r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    r[i] = (__bf16)(float)((lo >> (8 * i)) & 0xffu);
-    r[4 + i] = (__bf16)(float)((hi >> (8 * i)) & 0xffu);
+    r[i] = (__bf16)(float)(signed char)((lo >> (8 * i)) & 0xffu);
+    r[4 + i] = (__bf16)(float)(signed char)((hi >> (8 * i)) & 0xffu);
   }
   return r;
 }
@@ -252,9 +254,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   }
   const uint16_t* X = static_cast<const uint16_t*>(a.a);
   const size_t ldx = DOWN_SPLIT ? 2 * (size_t)Kd : (size_t)Kd;  // A row stride
-  bf16x8_t ones;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
 
   u32x4_t wb[P][NMAT][NPC];
   auto wload = [&](int s, int kbl) {
@@ -345,10 +344,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   for (int rc = 0; rc < count; rc += ROWS_PER_PASS) {
     if (active && rc > 0) prologue();
 
-    f32x4_t acc[RG][NMAT], rs[RG];
+    f32x4_t acc[RG][NMAT];
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
-      rs[rg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) acc[rg][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
@@ -385,16 +383,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
       a0[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);    \
       a1[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);    \
-      if constexpr (!W16) {                                                                  \
-        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], ones, rs[rg], 0, 0, 0);     \
-        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], ones, rs[rg], 0, 0, 0);     \
-      }                                                                                      \
     }                                                                                        \
     _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
       const bf16x8_t b0 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                   \
-                              : u8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                \
+                              : s8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                \
       const bf16x8_t b1 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])             \
-                              : u8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                \
+                              : s8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                \
       _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                    \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt], 0, 0, 0); \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt], 0, 0, 0); \
@@ -404,19 +398,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
     bf16x8_t b0[NMAT], b1[NMAT];                                                             \
     _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
       b0[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                              \
-                   : u8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                           \
+                   : s8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                           \
       b1[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])                        \
-                   : u8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                           \
+                   : s8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                           \
     }                                                                                        \
     _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
       const bf16x8_t a0 =                                                                    \
           __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);         \
       const bf16x8_t a1 =                                                                    \
           __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);         \
-      if constexpr (!W16) {                                                                  \
-        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, rs[rg], 0, 0, 0);         \
-        rs[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, rs[rg], 0, 0, 0);         \
-      }                                                                                      \
       _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                  \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[mt], acc[rg][mt], 0, 0, 0); \
         acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[mt], acc[rg][mt], 0, 0, 0); \
@@ -452,8 +442,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         const int r = rc + 16 * pg + 4 * g + i;
         if (r >= count) continue;
         const int h0 = 2 * pg, l0 = 2 * pg + 1;  // the hi and lo planes' row groups
-        const float hi = W16 ? acc[h0][0][i] : acc[h0][0][i] - 128.0f * rs[h0][i];
-        const float lo = W16 ? acc[l0][0][i] : acc[l0][0][i] - 128.0f * rs[l0][i];
+        const float hi = acc[h0][0][i];
+        const float lo = acc[l0][0][i];
         const int yr = TOPK ? s_ypos[r] : row_begin + r;
         static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0];
       }
@@ -468,7 +458,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       float v[NMAT];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        v[mt] = W16 ? acc[rg][mt][i] : (acc[rg][mt][i] - 128.0f * rs[rg][i]) * sc[mt];
+        v[mt] = W16 ? acc[rg][mt][i] : acc[rg][mt][i] * sc[mt];
       float out;
       if (MODE == MXM_GEMM_GLU) {
         out = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(v[0]),
@@ -539,8 +529,7 @@ void launch_epi(const GemmArgs& a, hipStream_t s) {
 }
 
 // Reorder one int8 matrix src [Kd][C] into the 1 KB block layout of a
-// [Kdp][Cp] matrix; entries past the source's rows or columns are 0 (byte
-// 0x80 in offset binary).
+// [Kdp][Cp] matrix; entries past the source's rows or columns are 0.
 __global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C, int Kdp, int Cp,
                                   uint8_t* __restrict__ dst) {
   const size_t total = (size_t)Kdp * Cp;
@@ -554,7 +543,7 @@ __global__ void shuffle_q8_kernel(const int8_t* __restrict__ src, int Kd, int C,
     const int k = 64 * kb + 16 * (l >> 4) + i;
     const int c = 16 * cb + (l & 15);
     const int8_t q = (k < Kd && c < C) ? src[(size_t)k * C + c] : (int8_t)0;
-    dst[o] = (uint8_t)((uint8_t)q ^ 0x80u);
+    dst[o] = (uint8_t)q;
   }
 }
 
