@@ -63,6 +63,19 @@
 #endif
 // 64 rows per pass once an expert averages more than this many rows (int8;
 // bf16 weights: MXM_D16_RG4_MIN)
+// int8 down projection at 16 rows per pass: two 16-column blocks per wave,
+// with the ring depth divided by MXM_Q8_CPW_PDIV (the same bytes in
+// flight).  Measured on the 64-token decode layer (D 2048, E 64, top-8, ffn
+// 1408): down 39-40 -> 37-37.5 us, its 1,024 workgroups halved to one round
+// on the 512 slots; for the gate+up projection it measured slower (67-69 ->
+// 75-77 us at half the ring depth, 72-73 at a third: the two-block kernel
+// needs more than the 128 registers of two workgroups per CU)
+#ifndef MXM_Q8_CPW
+#define MXM_Q8_CPW 2
+#endif
+#ifndef MXM_Q8_CPW_PDIV
+#define MXM_Q8_CPW_PDIV 2
+#endif
 #ifndef MXM_Q8_RG4_MIN
 #define MXM_Q8_RG4_MIN 24
 #endif
@@ -180,12 +193,19 @@ __device__ void decode_aux(const DecodeAux& a, void* scratch) {
 // each row's token-major y row (n * K + j, j the expert's place among the
 // token's experts in ascending order) to the down projection, which reads
 // them as the dispatch's offsets would be read and stores y token-major.
-// W16: bf16 weights (2 KB blocks, two 16-byte pieces per lane).
-template <int EPI, int P, int RG, bool TOPK, bool W16>
-__global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups_per_expert) {
+// W16: bf16 weights (2 KB blocks, two 16-byte pieces per lane).  CPW: 16-column
+// blocks per wave (int8: two adjacent blocks share each A fragment and halve
+// the workgroups, whose fixed costs -- start, row scan, staging, ring fill --
+// then weigh half as much; the arithmetic of every column is unchanged).
+// (one row group with two column blocks: four waves per SIMD, i.e. two
+// workgroups per CU, as the one-block kernel reaches by itself)
+template <int EPI, int P, int RG, bool TOPK, bool W16, int CPW>
+__global__ __launch_bounds__(NW * 64, (CPW == 2 && RG == 1) ? 4 : 1) void gemm_q8_kernel(
+    GemmArgs a, int groups_per_expert) {
   constexpr int MODE = Epi<EPI>::MODE;
   constexpr int BW = W16 ? 2 : 1;    // bytes per weight
   constexpr int NPC = W16 ? 2 : 1;   // 16-byte pieces per lane per block
+  static_assert(CPW == 1 || CPW == 2, "one or two column blocks per wave");
   constexpr bool H_SPLIT = Epi<EPI>::H_SPLIT;        // up: store H as hi | lo planes
   // down over both planes of a split H: row group 2p + plane holds rows
   // 16p .. 16p+15 of the pass from that plane; y fp32
@@ -235,33 +255,42 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   // CH k blocks (a multiple of the ring depth, so every chunk starts on ring
   // slot 0); the weight ring runs on across chunk boundaries
   const int chunk = kblocks <= MAXK / 64 ? kblocks : CH;
-  const int cb = grp * NW + wave;
-  const bool active = cb < NC / 16;   // wave-uniform
+  const int ncb = NC / 16;
+  const int cb0 = (grp * NW + wave) * CPW;  // this wave's first column block
+  const bool active = cb0 < ncb;             // wave-uniform
   const int g = lane >> 4, m = lane & 15;
-  const int c = cb * 16 + m;
 
-  const uint8_t* W[NMAT];
-  float sc[NMAT];
+  // (a second column block past the matrix reads the first's weights and is
+  // not stored)
+  const uint8_t* W[NMAT][CPW];
+  float sc[NMAT][CPW];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt) {
     const void* base = (mt == 0) ? a.b0 : a.b1;
-    W[mt] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd * BW +
-            (size_t)(active ? cb : 0) * 1024 * BW + 16 * lane;
-    if constexpr (W16)
-      sc[mt] = 1.0f;
-    else
-      sc[mt] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + c] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int cbj = active ? min(cb0 + j, ncb - 1) : 0;
+      W[mt][j] = static_cast<const uint8_t*>(base) + (size_t)e * NC * Kd * BW +
+                 (size_t)cbj * 1024 * BW + 16 * lane;
+      if constexpr (W16)
+        sc[mt][j] = 1.0f;
+      else
+        sc[mt][j] = active ? ((mt == 0) ? a.scale0 : a.scale1)[(size_t)e * NC + cbj * 16 + m]
+                           : 0.0f;
+    }
   }
   const uint16_t* X = static_cast<const uint16_t*>(a.a);
   const size_t ldx = DOWN_SPLIT ? 2 * (size_t)Kd : (size_t)Kd;  // A row stride
 
-  u32x4_t wb[P][NMAT][NPC];
+  u32x4_t wb[P][NMAT][CPW][NPC];
   auto wload = [&](int s, int kbl) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-      for (int h = 0; h < NPC; ++h)
-        wb[s][mt][h] = MXM_WLD(W[mt] + (size_t)kbl * kstride + 1024 * h);
+      for (int j = 0; j < CPW; ++j)
+#pragma unroll
+        for (int h = 0; h < NPC; ++h)
+          wb[s][mt][j][h] = MXM_WLD(W[mt][j] + (size_t)kbl * kstride + 1024 * h);
   };
   auto prologue = [&]() {
 #pragma unroll
@@ -344,11 +373,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
   for (int rc = 0; rc < count; rc += ROWS_PER_PASS) {
     if (active && rc > 0) prologue();
 
-    f32x4_t acc[RG][NMAT];
+    f32x4_t acc[RG][NMAT][CPW];
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) acc[rg][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) acc[rg][mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
     for (int k0 = 0; k0 < kblocks; k0 += chunk) {
@@ -384,32 +415,39 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       a0[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);    \
       a1[rg] = __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);    \
     }                                                                                        \
-    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
-      const bf16x8_t b0 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                   \
-                              : s8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                \
-      const bf16x8_t b1 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])             \
-                              : s8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                \
+    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt)                                      \
+    _Pragma("unroll") for (int j = 0; j < CPW; ++j) {                                        \
+      const bf16x8_t b0 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][j][0])                \
+                              : s8x8_to_bf16(wb[s][mt][j][0].x, wb[s][mt][j][0].y);          \
+      const bf16x8_t b1 = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][j][NPC - 1])          \
+                              : s8x8_to_bf16(wb[s][mt][j][0].z, wb[s][mt][j][0].w);          \
       _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                    \
-        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt], 0, 0, 0); \
-        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt], 0, 0, 0); \
+        acc[rg][mt][j] =                                                                     \
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[rg], b0, acc[rg][mt][j], 0, 0, 0);    \
+        acc[rg][mt][j] =                                                                     \
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[rg], b1, acc[rg][mt][j], 0, 0, 0);    \
       }                                                                                      \
     }                                                                                        \
   } else {                                                                                   \
-    bf16x8_t b0[NMAT], b1[NMAT];                                                             \
-    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                    \
-      b0[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][0])                              \
-                   : s8x8_to_bf16(wb[s][mt][0].x, wb[s][mt][0].y);                           \
-      b1[mt] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][NPC - 1])                        \
-                   : s8x8_to_bf16(wb[s][mt][0].z, wb[s][mt][0].w);                           \
+    bf16x8_t b0[NMAT][CPW], b1[NMAT][CPW];                                                   \
+    _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt)                                      \
+    _Pragma("unroll") for (int j = 0; j < CPW; ++j) {                                        \
+      b0[mt][j] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][j][0])                        \
+                      : s8x8_to_bf16(wb[s][mt][j][0].x, wb[s][mt][j][0].y);                  \
+      b1[mt][j] = W16 ? __builtin_bit_cast(bf16x8_t, wb[s][mt][j][NPC - 1])                  \
+                      : s8x8_to_bf16(wb[s][mt][j][0].z, wb[s][mt][j][0].w);                  \
     }                                                                                        \
     _Pragma("unroll") for (int rg = 0; rg < RG; ++rg) {                                      \
       const bf16x8_t a0 =                                                                    \
           __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 0) * 64 + lane]);         \
       const bf16x8_t a1 =                                                                    \
           __builtin_bit_cast(bf16x8_t, ash[rg * ASZ + ((kbi) * 2 + 1) * 64 + lane]);         \
-      _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt) {                                  \
-        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[mt], acc[rg][mt], 0, 0, 0); \
-        acc[rg][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[mt], acc[rg][mt], 0, 0, 0); \
+      _Pragma("unroll") for (int mt = 0; mt < NMAT; ++mt)                                    \
+      _Pragma("unroll") for (int j = 0; j < CPW; ++j) {                                      \
+        acc[rg][mt][j] =                                                                     \
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[mt][j], acc[rg][mt][j], 0, 0, 0); \
+        acc[rg][mt][j] =                                                                     \
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[mt][j], acc[rg][mt][j], 0, 0, 0); \
       }                                                                                      \
     }                                                                                        \
   }
@@ -434,6 +472,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
 #undef MXM_Q8_STEP
 
     // 16x16 layout: lane l holds column l%16, rows 4*(l/16) + i.
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+    if (cb0 + j >= ncb) continue;  // (wave-uniform)
+    const int c = (cb0 + j) * 16 + m;
     if constexpr (DOWN_SPLIT) {
 #pragma unroll
       for (int pg = 0; pg < RG / 2; ++pg)
@@ -442,10 +484,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         const int r = rc + 16 * pg + 4 * g + i;
         if (r >= count) continue;
         const int h0 = 2 * pg, l0 = 2 * pg + 1;  // the hi and lo planes' row groups
-        const float hi = acc[h0][0][i];
-        const float lo = acc[l0][0][i];
+        const float hi = acc[h0][0][j][i];
+        const float lo = acc[l0][0][j][i];
         const int yr = TOPK ? s_ypos[r] : row_begin + r;
-        static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0];
+        static_cast<float*>(a.out)[(size_t)yr * NC + c] = (hi + lo) * sc[0][j];
       }
       continue;
     }
@@ -458,7 +500,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
       float v[NMAT];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        v[mt] = W16 ? acc[rg][mt][i] : acc[rg][mt][i] * sc[mt];
+        v[mt] = W16 ? acc[rg][mt][j][i] : acc[rg][mt][j][i] * sc[mt][j];
       float out;
       if (MODE == MXM_GEMM_GLU) {
         out = mxm_hidden_fast<true>(Epi<EPI>::ETYPE, Epi<EPI>::ACT, a.slope, mxm_rbf_fast(v[0]),
@@ -480,27 +522,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_q8_kernel(GemmArgs a, int groups
         H[(size_t)yr * NC + c] = mxm_f2bf_fast(out);
       }
     }
+    }  // column blocks
   }
 }
 
-template <int EPI, int P, int RG, bool W16>
+template <int EPI, int P, int RG, bool W16, int CPW>
 void launch_q8w(const GemmArgs& a, hipStream_t s) {
   const int ncb = a.Ncols / 16;
-  const int gpe = (ncb + NW - 1) / NW;
+  const int gpe = (ncb + NW * CPW - 1) / (NW * CPW);
   if (a.top_idx)
-    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, true, W16>),
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, true, W16, CPW>),
                        dim3(a.E * gpe + (a.daux.aux ? 1 : 0)), dim3(NW * 64), 0, s, a, gpe);
   else
-    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, false, W16>), dim3(a.E * gpe), dim3(NW * 64),
-                       0, s, a, gpe);
+    hipLaunchKernelGGL((gemm_q8_kernel<EPI, P, RG, false, W16, CPW>), dim3(a.E * gpe),
+                       dim3(NW * 64), 0, s, a, gpe);
 }
 // P int8 blocks in flight per matrix, or P16 bf16 blocks
 template <int EPI, int P, int P16, int RG>
 void launch_q8(const GemmArgs& a, hipStream_t s) {
   if (a.w_bf16)
-    launch_q8w<EPI, P16, RG, true>(a, s);
+    launch_q8w<EPI, P16, RG, true, 1>(a, s);
+  else if constexpr (RG == 1 && MXM_Q8_CPW == 2 && Epi<EPI>::MODE == MXM_GEMM_DOWN &&
+                     !Epi<EPI>::DOWN_SPLIT)
+    launch_q8w<EPI, (P + MXM_Q8_CPW_PDIV - 1) / MXM_Q8_CPW_PDIV, RG, false, 2>(a, s);
   else
-    launch_q8w<EPI, P, RG, false>(a, s);
+    launch_q8w<EPI, P, RG, false, 1>(a, s);
 }
 template <int EPI>
 void launch_epi(const GemmArgs& a, hipStream_t s) {
