@@ -402,6 +402,7 @@ FLOW_CASES = [
     (300, 256, 8, 2, 128, 0, 0),     # several row passes per expert
     (300, 256, 8, 2, 128, 1, 1),     # split hidden, 32-row passes of the down projection
     (48, 196, 8, 2, 128, 0, 0),      # D not a multiple of 8
+    (33, 300, 200, 6, 128, 0, 0),    # four expert groups per token, D past whole 64-d chunks
 ]
 
 
